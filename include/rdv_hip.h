@@ -1,0 +1,127 @@
+/*
+ * rdv_hip.h — C ABI of the MI355X (gfx950) small-network hot path.
+ *
+ * The reference (rendervous/rdv_project) has no native FFI: every hot-path
+ * kernel there is a GLSL snippet stitched into one compute shader and submitted
+ * through `dispatch()` (src/rdv/core/_core.py:2799-2886).  Each entry point below
+ * replaces one such dispatch for one node family; the comment on each names the
+ * reference node and shader it stands in for.  The Python package
+ * `rdv_project_amd` binds these with ctypes (see rdv_project_amd/_lib.py).
+ *
+ * Conventions
+ *  - Every tensor argument is a caller-owned DEVICE pointer (e.g. a torch
+ *    tensor's data_ptr()).  Nothing on a forward path allocates device memory;
+ *    scratch, where a kernel needs it, is passed in by the caller.
+ *  - `stream` is a hipStream_t (NULL = the legacy default stream).  Launches are
+ *    stream-ordered and asynchronous; the caller synchronises if it needs to.
+ *  - Every function returns RDV_OK (0) or a negative rdv_status.  The message of
+ *    the last failure on the calling thread is returned by rdv_last_error().
+ *  - Shapes are validated on the host before anything is launched, so a bad
+ *    descriptor is an error code, never a GPU fault (the reference's equivalent
+ *    checks are host asserts, e.g. src/rdv/domain/nn.py:37-39, 1064-1078).
+ */
+#ifndef RDV_HIP_H
+#define RDV_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ------------------------------------------------------------------ status */
+typedef enum rdv_status {
+  RDV_OK = 0,
+  RDV_ERR_INVALID = -1,     /* bad descriptor / shape / pointer (reference: AssertionError) */
+  RDV_ERR_UNSUPPORTED = -2, /* valid request this build does not implement               */
+  RDV_ERR_HIP = -3,         /* a HIP runtime call failed                                  */
+  RDV_ERR_WORKSPACE = -4    /* caller-provided workspace too small                        */
+} rdv_status;
+
+/* Message of the last failing call on this thread ("" if none). */
+const char* rdv_last_error(void);
+/* ABI version of this library (major * 100 + minor). */
+int rdv_version(void);
+/* Number of compute units of the current device (0 if no device). */
+int rdv_device_cu_count(void);
+
+/* --------------------------------------------------------------- fused MLP */
+#define RDV_MLP_MAX_LAYERS 16
+#define RDV_MLP_MAX_WIDTH 256
+
+/* Activation applied to a layer's output. RELU is the reference's ReLU map
+ * (src/rdv/shaders/maps/relu.h:1-5); the others are build-defined heads for
+ * the emission-absorption renderer (no counterpart in the reference). */
+enum {
+  RDV_ACT_NONE = 0,
+  RDV_ACT_RELU = 1,
+  RDV_ACT_SOFTPLUS = 2,   /* log(1 + exp(x))                                   */
+  RDV_ACT_SIGMOID = 3,    /* 1 / (1 + exp(-x))                                 */
+  RDV_ACT_DENSITY_RGB = 4 /* channel 0 softplus, channels 1.. sigmoid          */
+};
+
+/* Arithmetic of a layer.
+ * F16: LinearFast (src/rdv/shaders/maps/linear_fast.h:39-100): input and weight
+ *      rounded to fp16, products accumulated in fp32, fp32 bias added after.
+ * F32: Linear (src/rdv/shaders/maps/linear.h:15-44): exact fp32,
+ *      acc = bias; acc += x[k] * W[o][k] for k ascending. */
+enum { RDV_PREC_F32 = 0, RDV_PREC_F16 = 1 };
+
+/* Input encoding applied to each row of x before layer 0 (build-defined; the
+ * reference has no encoding node).  FREQ with L octaves maps p[0..D) to
+ *   [p_0..p_{D-1}, for k in 0..L-1: sin(2^k pi p_0..D-1), cos(2^k pi p_0..D-1)]
+ * followed by zeros up to enc_width. */
+enum { RDV_ENC_NONE = 0, RDV_ENC_FREQ = 1 };
+
+typedef struct rdv_mlp_desc {
+  int32_t n_layers;                       /* 1..RDV_MLP_MAX_LAYERS                     */
+  int32_t in_features;                    /* width of each row of x                    */
+  int32_t encoding;                       /* RDV_ENC_*                                 */
+  int32_t enc_octaves;                    /* FREQ: number of octaves L                 */
+  int32_t dims[RDV_MLP_MAX_LAYERS + 1];   /* dims[0] = layer-0 input width (= encoded  */
+                                          /* width), dims[i+1] = output width of i     */
+  int32_t act[RDV_MLP_MAX_LAYERS];        /* RDV_ACT_* after layer i                   */
+  int32_t prec[RDV_MLP_MAX_LAYERS];       /* RDV_PREC_* of layer i                     */
+} rdv_mlp_desc;
+
+/* Host-only shape check of a descriptor; launches nothing. */
+int rdv_mlp_validate(const rdv_mlp_desc* desc);
+
+/* Size in bytes of the packed parameter block for `desc` (< 0 on error). */
+int64_t rdv_mlp_packed_bytes(const rdv_mlp_desc* desc);
+
+/* Packs the layers' parameters into `packed` (device, rdv_mlp_packed_bytes
+ * bytes, 256-byte aligned).  weights[i] points to layer i's fp32 weight,
+ * row-major [dims[i+1], dims[i]] (PyTorch nn.Linear layout), biases[i] to its
+ * fp32 bias [dims[i+1]]; both arrays hold DEVICE pointers and live on the host.
+ * Replaces the per-node weight/bias upload of _LinearBase.__init__
+ * (src/rdv/domain/nn.py:34-54). */
+int rdv_mlp_pack(const rdv_mlp_desc* desc, const float* const* weights,
+                 const float* const* biases, void* packed, void* stream);
+
+/* y[n, dims[L]] = chain(x[n, in_features]) for fp32 row-major x and y.
+ * Replaces Map.__call__ -> dispatch(MapEvaluator) over a chain of
+ * LinearFast / Linear / ReLU maps (src/rdv/maths/__init__.py:1451-1487,
+ * src/rdv/shaders/maps/map_evaluator.h:1-5, composite.h:8-12).
+ * Rows are processed in groups of 32 as the reference's workgroups are; when n
+ * is not a multiple of 32 the last partial group is evaluated in exact fp32,
+ * which is what the reference's LinearFast does for a partial workgroup
+ * (linear_fast.h:102-108 behind all_thread_sync,
+ * src/rdv/shaders/libraries/cooperative_library.h:20-33). */
+int rdv_mlp_forward(const rdv_mlp_desc* desc, const void* packed, const float* x,
+                    float* y, int64_t n, void* stream);
+
+/* Same as rdv_mlp_forward but evaluates every row (tail included) on the fp16
+ * matrix-core path; exposed for benchmarking the kernel alone. */
+int rdv_mlp_forward_f16_all(const rdv_mlp_desc* desc, const void* packed,
+                            const float* x, float* y, int64_t n, void* stream);
+
+/* Name of the kernel rdv_mlp_forward would launch for `desc` (for profiling
+ * reports); "" if the descriptor is invalid. */
+const char* rdv_mlp_kernel_name(const rdv_mlp_desc* desc);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* RDV_HIP_H */

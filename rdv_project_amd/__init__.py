@@ -1,0 +1,38 @@
+"""rdv_project_amd — MI355X-native (gfx950) implementation of rdv's small-network
+hot path, behind rdv's own Python API.
+
+    import rdv_project_amd as rdv
+    m = rdv.linear(W0, b0, f16=True) >> rdv.relu >> rdv.linear(W1, b1, f16=True)
+    y = m(rdv.wrap(x)).as_tensor('torch')
+
+Public names follow the reference's curated surface (src/rdv/__init__.py) for
+the parts this build implements.  Compute runs only through the HIP library
+(librdv_hip.so); there is no CPU fallback.
+"""
+from .core import (
+    RDVObject,
+    ensure_on_rdv,
+    is_on_rdv,
+    profiling,
+    profiling_submit_times,
+    reset_submit_times,
+    set_synchronous,
+    wrap,
+)
+from .maths import Composite, Grid, Identity, Map, Sensor, TensorOperation, X, e, pi
+from .nn import (
+    DensityRGB,
+    FrequencyEncoding,
+    Linear,
+    LinearFast,
+    ReLU,
+    Sigmoid,
+    Softplus,
+    density_rgb,
+    linear,
+    relu,
+    sigmoid,
+    softplus,
+)
+
+__version__ = "0.1.0"

@@ -1,0 +1,138 @@
+"""Lowers a composed Map onto the fused MLP kernels (rdv_mlp_* in the C ABI).
+
+A composition is accepted when its stages, in application order, are
+  [FrequencyEncoding]? (Linear | LinearFast) [activation]? ( (Linear | LinearFast) [activation]? )*
+which is what the reference's MapEvaluator runs for a chain of
+`linear(...) >> relu >> ...` (src/rdv/maths/__init__.py:1451-1487,
+src/rdv/shaders/maps/composite.h:8-12).  Anything else raises
+NotImplementedError: this build has no general Map code generator.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import math
+
+import torch
+
+from . import _lib
+from .core import RDVObject, current_stream_handle, device, launch_scope, wrap
+from .maths import Identity, Map
+from .nn import FrequencyEncoding, _Activation, _LinearBase
+
+
+class ChainPlan:
+    __slots__ = ("desc", "layers", "signature", "in_features", "out_features")
+
+    def __init__(self, desc, layers, signature, in_features, out_features):
+        self.desc = desc
+        self.layers = layers
+        self.signature = signature
+        self.in_features = in_features
+        self.out_features = out_features
+
+
+def plan_chain(m: Map, in_width: int) -> ChainPlan:
+    stages = [s for s in m.stages() if not isinstance(s, Identity)]
+    enc, octaves, i, cur = _lib.ENC_NONE, 0, 0, in_width
+    if stages and isinstance(stages[0], FrequencyEncoding):
+        e = stages[0]
+        if e.in_features != cur:
+            raise TypeError(f"encoding expects {e.in_features} input features, x has {cur}")
+        enc, octaves, cur, i = _lib.ENC_FREQ, e.octaves, e.OUT, 1
+    enc_width = cur
+    layers: list[_LinearBase] = []
+    acts: list[int] = []
+    for s in stages[i:]:
+        if isinstance(s, _LinearBase):
+            if s.IN != cur:
+                raise TypeError(f"layer expects {s.IN} input features, the chain provides {cur}")
+            layers.append(s)
+            acts.append(_lib.ACT_NONE)
+            cur = s.OUT
+        elif isinstance(s, _Activation):
+            if not layers:
+                raise NotImplementedError("an activation before the first linear layer has no HIP lowering")
+            if acts[-1] == _lib.ACT_NONE:
+                acts[-1] = s._act
+            elif acts[-1] == _lib.ACT_RELU and s._act == _lib.ACT_RELU:
+                pass  # relu(relu(x)) == relu(x)
+            else:
+                raise NotImplementedError("two different activations in a row have no HIP lowering")
+        elif isinstance(s, FrequencyEncoding):
+            raise NotImplementedError("FrequencyEncoding is only supported as the first stage of a chain")
+        else:
+            raise NotImplementedError(f"{type(s).__name__} has no HIP lowering in this build")
+    if not layers:
+        raise NotImplementedError("a chain needs at least one Linear / LinearFast layer")
+    if len(layers) > _lib.MLP_MAX_LAYERS:
+        raise NotImplementedError(f"chains longer than {_lib.MLP_MAX_LAYERS} layers are not supported")
+    d = _lib.MlpDesc()
+    d.n_layers = len(layers)
+    d.in_features = in_width
+    d.encoding = enc
+    d.enc_octaves = octaves
+    d.dims[0] = enc_width
+    for k, (lay, a) in enumerate(zip(layers, acts)):
+        d.dims[k + 1] = lay.OUT
+        d.act[k] = a
+        d.prec[k] = lay._precision
+    sig = (enc, octaves, in_width, tuple(d.dims[: d.n_layers + 1]), tuple(acts),
+           tuple(l._precision for l in layers))
+    _lib.check(_lib.load().rdv_mlp_validate(C.byref(d)), "mlp")
+    return ChainPlan(d, layers, sig, in_width, cur)
+
+
+def packed_params(m: Map, p: ChainPlan) -> torch.Tensor:
+    """Packed parameter block of `m`, rebuilt when a weight changed in place
+    (the reference reads weights through pointers at every dispatch)."""
+    key = (p.signature,
+           tuple((l.weight.device_ptr, l.bias.device_ptr) for l in p.layers),
+           tuple((l.weight._t._version, l.bias._t._version) for l in p.layers))
+    cached = getattr(m, "_rdv_packed", None)
+    if cached is not None and cached[0] == key:
+        return cached[1]
+    lib = _lib.load()
+    nbytes = lib.rdv_mlp_packed_bytes(C.byref(p.desc))
+    if nbytes < 0:
+        _lib.check(int(nbytes), "mlp")
+    buf = torch.empty(int(nbytes) + 256, dtype=torch.uint8, device=device())
+    off = (-buf.data_ptr()) % 256
+    buf = buf[off: off + int(nbytes)]
+    ws = _lib.void_ptr_array([l.weight.device_ptr for l in p.layers])
+    bs = _lib.void_ptr_array([l.bias.device_ptr for l in p.layers])
+    _lib.check(lib.rdv_mlp_pack(C.byref(p.desc), ws, bs, C.c_void_p(buf.data_ptr()),
+                                C.c_void_p(current_stream_handle())), "mlp pack")
+    m._rdv_packed = (key, buf)
+    return buf
+
+
+_OUTPUT_CACHE: dict = {}
+
+
+def _cached_output(sig, shape) -> RDVObject:
+    """One output buffer per chain structure, reallocated only when the row shape
+    changes (reference: Map.__call__'s per-class evaluator cache)."""
+    hit = _OUTPUT_CACHE.get(sig)
+    if hit is not None and hit[0] == shape:
+        return hit[1]
+    out = RDVObject(torch.empty(shape, dtype=torch.float32, device=device()))
+    _OUTPUT_CACHE[sig] = (shape, out)
+    return out
+
+
+def evaluate_map(m: Map, x) -> RDVObject:
+    x = wrap(x)
+    if x.scalar_type != torch.float32:
+        raise TypeError(f"Map input must be float32, got {x.scalar_type}")
+    if len(x.shape) < 1:
+        raise AssertionError("Map input needs a trailing feature dimension")
+    p = plan_chain(m, int(x.shape[-1]))
+    packed = packed_params(m, p)
+    rows = math.prod(x.shape[:-1])
+    out = _cached_output(p.signature, (*x.shape[:-1], p.out_features))
+    lib = _lib.load()
+    with launch_scope():
+        _lib.check(lib.rdv_mlp_forward(C.byref(p.desc), C.c_void_p(packed.data_ptr()), C.c_void_p(x.device_ptr),
+                                       C.c_void_p(out.device_ptr), C.c_int64(rows),
+                                       C.c_void_p(current_stream_handle())), "mlp forward")
+    return out

@@ -1,0 +1,130 @@
+// Packed parameter block of a fused MLP, shared by the packer and every MLP kernel.
+//
+// Matrix-core formulation.  Each layer is evaluated transposed, H^T = W . X^T,
+// with v_mfma_f32_32x32x16_f16: A = a 32x16 tile of W (output features x input
+// features), B = a 16x32 tile of X^T (input features x 32 points), D = 32 output
+// features x 32 points in fp32.  Per lane l (h = l / 32):
+//   A operand: W[32t + l%32][virtual k = 16c + 8h + j], j = 0..7
+//   B operand: X^T[virtual k = 16c + 8h + j][point l%32]
+//   D result : row 32t + 8(j/4) + 4h + (j%4) of point l%32, j = 0..15
+// The D registers of one 32-row tile, converted to fp16, ARE the B operands of
+// the next layer's two 16-wide K chunks (registers 0..7 -> chunk 2t, 8..15 ->
+// chunk 2t+1), with virtual k = 16c + v holding actual feature
+// 16c + sigma(v), where sigma swaps the middle two quartets of a 16-chunk.
+// The next layer's weight columns are permuted by the same sigma when packed,
+// so activations never leave registers between layers.
+//
+// Layout (every section 256-byte aligned), for layer i with KC = K chunks of 16
+// and MT = M tiles of 32:
+//   frag[i] : MT x KC x 64 lanes x 8 fp16   (A fragments in lane order)
+//   bias[i] : MT*32 fp32                      (zero padded)
+//   w32[i]  : dims[i+1] x dims[i] fp32        (row-major copy, for fp32 paths)
+//   b32[i]  : dims[i+1] fp32
+#pragma once
+
+#include <stdint.h>
+
+#include "../../include/rdv_hip.h"
+
+namespace rdv {
+
+struct MlpLayout {
+  int n_layers;
+  int in_w[RDV_MLP_MAX_LAYERS];   // actual input width of layer i
+  int out_w[RDV_MLP_MAX_LAYERS];  // actual output width of layer i
+  int kc[RDV_MLP_MAX_LAYERS];     // K chunks of 16 (virtual, after slot mapping)
+  int mt[RDV_MLP_MAX_LAYERS];     // M tiles of 32
+  int64_t frag_off[RDV_MLP_MAX_LAYERS];
+  int64_t bias_off[RDV_MLP_MAX_LAYERS];
+  int64_t w32_off[RDV_MLP_MAX_LAYERS];
+  int64_t b32_off[RDV_MLP_MAX_LAYERS];
+  int64_t total_bytes;
+};
+
+__host__ __device__ inline int div_up(int a, int b) { return (a + b - 1) / b; }
+__host__ __device__ inline int64_t align256(int64_t v) { return (v + 255) & ~int64_t(255); }
+
+// Octaves of a FREQ encoding evaluated by lane half 0 (the rest go to half 1).
+__host__ __device__ inline int freq_octaves_half0(int L) { return (L + 1) / 2; }
+
+// K chunks layer 0 needs on the matrix-core path.
+__host__ __device__ inline int layer0_kc(int encoding, int D, int L, int enc_width) {
+  if (encoding == RDV_ENC_FREQ) {
+    int h0 = freq_octaves_half0(L);
+    int need0 = 2 * D * h0 + D;  // half 0: trig slots of its octaves, then the raw input
+    int need1 = 2 * D * (L - h0);
+    int need = need0 > need1 ? need0 : need1;
+    return div_up(need, 8);
+  }
+  return div_up(enc_width, 16);
+}
+
+// Actual feature index (column of layer 0's weight) that virtual K slot kv of
+// layer 0 carries, or -1 for a zero slot.
+//  NONE: identity.
+//  FREQ: within each lane half, slot s = 8c + j holds, for the half's octaves
+//        k (half 0: [0, h0), half 1: [h0, L)), in order: sin(2^k pi p_d) for
+//        d < D, then cos(2^k pi p_d); half 0 then holds p_d itself.  Both halves
+//        therefore evaluate the same function kind in the same slot.
+__host__ __device__ inline int layer0_slot_feature(int encoding, int D, int L, int kv) {
+  if (encoding != RDV_ENC_FREQ) return kv;
+  const int c = kv >> 4, h = (kv >> 3) & 1, j = kv & 7;
+  const int s = c * 8 + j;
+  const int h0 = freq_octaves_half0(L);
+  const int nh = h == 0 ? h0 : L - h0;
+  const int kbase = h == 0 ? 0 : h0;
+  if (s < 2 * D * nh) {
+    const int i = s / (2 * D), r = s % (2 * D);
+    const int k = kbase + i;
+    const bool is_cos = r >= D;
+    const int d = is_cos ? r - D : r;
+    return D + 2 * D * k + (is_cos ? D : 0) + d;
+  }
+  if (h == 0 && s >= 2 * D * h0 && s < 2 * D * h0 + D) return s - 2 * D * h0;
+  return -1;
+}
+
+// sigma: swaps quartets 1 and 2 of a 16-chunk (self-inverse).
+__host__ __device__ inline int chunk_sigma(int v) {
+  const int q = v >> 2;
+  const int q2 = (q == 1) ? 2 : (q == 2 ? 1 : q);
+  return (q2 << 2) | (v & 3);
+}
+
+// Feature of layer i >= 1 carried by virtual K slot kv.
+__host__ __device__ inline int hidden_slot_feature(int kv) { return (kv & ~15) | chunk_sigma(kv & 15); }
+
+// Fills `lay` from `d`; returns false if d is not a valid chain.
+inline bool mlp_layout(const rdv_mlp_desc& d, MlpLayout* lay) {
+  const int L = d.n_layers;
+  if (L < 1 || L > RDV_MLP_MAX_LAYERS) return false;
+  lay->n_layers = L;
+  int64_t off = 0;
+  for (int i = 0; i < L; ++i) {
+    lay->in_w[i] = d.dims[i];
+    lay->out_w[i] = d.dims[i + 1];
+    lay->mt[i] = div_up(d.dims[i + 1], 32);
+    lay->kc[i] = i == 0 ? layer0_kc(d.encoding, d.in_features, d.enc_octaves, d.dims[0])
+                        : 2 * lay->mt[i - 1];
+  }
+  for (int i = 0; i < L; ++i) {
+    lay->frag_off[i] = off;
+    off = align256(off + int64_t(lay->mt[i]) * lay->kc[i] * 64 * 8 * 2);
+  }
+  for (int i = 0; i < L; ++i) {
+    lay->bias_off[i] = off;
+    off = align256(off + int64_t(lay->mt[i]) * 32 * 4);
+  }
+  for (int i = 0; i < L; ++i) {
+    lay->w32_off[i] = off;
+    off = align256(off + int64_t(lay->out_w[i]) * lay->in_w[i] * 4);
+  }
+  for (int i = 0; i < L; ++i) {
+    lay->b32_off[i] = off;
+    off = align256(off + int64_t(lay->out_w[i]) * 4);
+  }
+  lay->total_bytes = off;
+  return true;
+}
+
+}  // namespace rdv

@@ -1,0 +1,209 @@
+"""Map / Grid / TensorOperation families of the rdv API, for the hot path.
+
+Reference: src/rdv/maths/__init__.py.  A Map is a per-row function
+[..., IN] -> [..., OUT]; `a >> b` composes (b after a) into a Composite
+(maths:1489-1498, 1700-1728); calling a Map evaluates it over every row of its
+input (maths:1451-1487).  The reference lowers a composition to one GLSL
+shader; here a composition is pattern-matched onto the fused HIP kernels
+(see _chain.py), and anything that does not match raises NotImplementedError.
+"""
+from __future__ import annotations
+
+import math as _math
+
+from .core import RDVObject, wrap
+
+
+class Map:
+    """Base of every per-row map.  IN / OUT are None while generic."""
+
+    IN: int | None = None
+    OUT: int | None = None
+
+    # ---------------------------------------------------------- composition
+    def __rshift__(self, m: "Map") -> "Map":
+        """self, then m (reference: Map.__rshift__, maths:1489-1498)."""
+        if not isinstance(m, Map):
+            return NotImplemented
+        if isinstance(m, Identity):
+            return self
+        if isinstance(self, Identity):
+            return m
+        _check_link(self, m)
+        return Composite(m, self)
+
+    def __lshift__(self, m: "Map") -> "Map":
+        """m, then self (reference: Map.__lshift__)."""
+        if not isinstance(m, Map):
+            return NotImplemented
+        return m >> self
+
+    def stages(self) -> list["Map"]:
+        """Primitive maps in application order."""
+        return [self]
+
+    def __call__(self, x, **kwargs):
+        """Evaluates the map over every row of x; returns a cached output object
+        (same buffer when the same structure is called with the same row shape,
+        as the reference's per-class evaluator cache does, maths:1466-1476)."""
+        if kwargs:
+            raise NotImplementedError("deferred bindings (Map.__call__(**kwargs)) are outside this build")
+        from . import _chain
+        return _chain.evaluate_map(self, x)
+
+
+def _check_link(g: Map, f: Map) -> None:
+    """g's OUT must equal f's IN once both are known (reference: Composite.__init__
+    asserts it; a generic cast that cannot bind raises TypeError)."""
+    go, fi = g.OUT, f.IN
+    if go is not None and fi is not None and go != fi:
+        raise TypeError(f"cannot compose: output width {go} does not match input width {fi}")
+
+
+class Identity(Map):
+    """f(x) = x (reference: maths:1671-1684)."""
+
+
+X = Identity()
+
+
+class Composite(Map):
+    """f(g(x)) (reference: maths:1700-1728)."""
+
+    def __init__(self, f: Map, g: Map) -> None:
+        self.f = f
+        self.g = g
+        st = self.stages()
+        self.IN = _infer_in(st)
+        self.OUT = _infer_out(st)
+
+    def stages(self) -> list[Map]:
+        return self.g.stages() + self.f.stages()
+
+
+def _infer_in(stages: list[Map]) -> int | None:
+    for s in stages:
+        if s.IN is not None:
+            return s.IN
+        if s.OUT is not None and not getattr(s, "_shape_preserving", False):
+            return None
+    return None
+
+
+def _infer_out(stages: list[Map]) -> int | None:
+    for s in reversed(stages):
+        if s.OUT is not None:
+            return s.OUT
+        if not getattr(s, "_shape_preserving", False):
+            return None
+    return None
+
+
+# ================================================================= GRIDS
+
+
+class Grid:
+    """Index space [0..shape[i]) -> float vectors of width OUT (reference: maths:42-225).
+
+    Calling a grid with no arguments evaluates every cell in row-major order
+    into a [*shape, OUT] tensor (maths:77-103)."""
+
+    IN: int | None = None
+    OUT: int | None = None
+
+    def __init__(self, shape: list[int]) -> None:
+        self._shape = list(shape)
+        self.shape = list(shape)
+
+    def __rshift__(self, m):
+        if isinstance(m, Identity):
+            return self
+        if isinstance(m, Map):
+            return Sensor(self, m)
+        return NotImplemented
+
+    def __call__(self, *args, **kwargs):
+        if args or kwargs:
+            raise NotImplementedError("batched grid evaluation is outside this build")
+        from . import _render
+        return _render.evaluate_grid(self)
+
+
+class Sensor(Grid):
+    """map(grid(idx)) for every cell (reference: maths:252-271)."""
+
+    def __init__(self, grid: Grid, map: Map) -> None:
+        if map.IN is not None and grid.OUT is not None and map.IN != grid.OUT:
+            raise TypeError(f"cannot compose: grid output width {grid.OUT} does not match map input {map.IN}")
+        super().__init__(grid.shape)
+        self.grid = grid
+        self.map = map
+        self.IN = grid.IN
+        self.OUT = map.OUT
+
+
+# ======================================================== TENSOR OPERATIONS
+
+
+class TensorOperation:
+    """Self-materialising 2-D op, dispatched eagerly at construction
+    (reference: maths:1251-1380).  Subclasses set up their inputs and call
+    super().__init__(shape); `result` then holds the [rows, cols] fp32 output."""
+
+    _upstream = None
+    _extra_upstreams = ()
+
+    def __init__(self, shape: list[int]) -> None:
+        import torch
+        from .core import device
+        assert len(shape) == 2, "TensorOperation only supports 2D (rows, channels) shapes"
+        self._shape = list(shape)
+        self.shape = list(shape)
+        self._result_t = torch.empty(self._shape, dtype=torch.float32, device=device())
+        self.result = RDVObject(self._result_t)
+        self.evaluate()
+
+    def _forward(self) -> None:  # launches this op's kernel into self._result_t
+        raise NotImplementedError
+
+    def as_type(self, backend: str):
+        """This op's result in `backend` ('torch' view or 'numpy' copy)."""
+        return self.result.as_tensor(backend).reshape(self._shape)
+
+    def evaluate(self) -> None:
+        """Re-dispatches this op over its own result buffer (maths:1360-1366)."""
+        from .core import launch_scope
+        with launch_scope():
+            self._forward()
+
+    def evaluate_chain(self) -> None:
+        """Re-dispatches this op and every upstream op, in dependency order
+        (maths:1368-1379)."""
+        ops: list[TensorOperation] = []
+        _collect_tensor_ops(self, set(), ops)
+        for op in ops:
+            op.evaluate()
+
+
+def _as_op_input(x):
+    """(buffer, shape, upstream op or None) of an op input (maths:1402-1415)."""
+    if isinstance(x, TensorOperation):
+        return x.result, list(x._shape), x
+    data = wrap(x)
+    return data, list(data.shape), None
+
+
+def _collect_tensor_ops(node, seen_ids, out) -> None:
+    """Postorder walk of upstream ops (maths:1418-1430)."""
+    if id(node) in seen_ids:
+        return
+    if node._upstream is not None:
+        _collect_tensor_ops(node._upstream, seen_ids, out)
+    for up in node._extra_upstreams:
+        _collect_tensor_ops(up, seen_ids, out)
+    seen_ids.add(id(node))
+    out.append(node)
+
+
+pi = _math.pi
+e = _math.e
