@@ -1,0 +1,234 @@
+#!/usr/bin/env python
+"""Benchmark of the rdv small-network hot path on one MI355X.
+
+Headline (the JSON line's `value`): configuration C2 of BASELINE.json — the
+encoded coordinate MLP, 2^20 points, FREQ(6 octaves) 39 -> pad 48 -> 64 -> 64 ->
+64 -> 4, fp16 matrix cores with fp32 accumulation, one fused kernel per call.
+A step is one call over the 2^20 points with inputs already resident in HBM
+(buffer sets rotate so the 256 MB MALL does not serve them).
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1]
+
+Prints ONE JSON line.  `roofline` is computed live from HIP events recorded on
+the stream the kernels run on; `cpu_baseline` times this repo's numpy
+restatement (oracle/) on a bounded sample on the host cores.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "fused-MLP Mpoints/s (w64, 2^20 pts) + % fp16 MFMA peak; Winograd conv TFLOP/s"
+PEAK_FP16_TFLOPS = 2500.0  # MI355X dense fp16 MFMA
+PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
+C2_FLOP_PER_POINT = 2 * (48 * 64 + 64 * 64 + 64 * 64 + 64 * 4)  # 23,040 (declared padded shapes)
+C1_FLOP_PER_POINT = 2 * (3 * 64 + 3 * 64 * 64 + 64 * 4)          # 25,472
+ROTATE = 12
+
+
+def _log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def _mlp_setup(x_cpu, layers, acts, enc=None):
+    """Builds the rdv chain, packs it, and returns (desc, packed, rotating x/y sets)."""
+    import torch
+    import rdv_project_amd as rdv
+    from rdv_project_amd import _chain
+
+    m = enc
+    for (w, b), a in zip(layers, acts):
+        lin = rdv.linear(w.cuda(), b.cuda(), f16=True)
+        m = lin if m is None else m >> lin
+        if a == "relu":
+            m = m >> rdv.relu
+    p = _chain.plan_chain(m, x_cpu.shape[1])
+    packed = _chain.packed_params(m, p)
+    xd = x_cpu.cuda()
+    xs = [xd] + [xd.clone() for _ in range(ROTATE - 1)]
+    ys = [torch.empty(x_cpu.shape[0], p.out_features, device="cuda") for _ in range(ROTATE)]
+    return m, p, packed, xs, ys
+
+
+def _time_launches(launch, steps: int, warmup: int):
+    """Returns (wall ms per step, event ms per step) for `steps` back-to-back launches."""
+    import torch
+    for i in range(warmup):
+        launch(i)
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record()
+    for i in range(steps):
+        launch(i)
+    end.record()
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) * 1e3 / steps
+    ev = start.elapsed_time(end) / steps
+    return wall, ev
+
+
+def bench_mlp(x_cpu, layers, acts, enc, steps, warmup):
+    import torch
+    from rdv_project_amd import _lib
+    lib = _lib.load()
+    m, p, packed, xs, ys = _mlp_setup(x_cpu, layers, acts, enc)
+    n = x_cpu.shape[0]
+    stream = C.c_void_p(torch.cuda.current_stream().cuda_stream)
+    dptr = C.byref(p.desc)
+    pk = C.c_void_p(packed.data_ptr())
+    xp = [C.c_void_p(t.data_ptr()) for t in xs]
+    yp = [C.c_void_p(t.data_ptr()) for t in ys]
+    nn = C.c_int64(n)
+    fwd = lib.rdv_mlp_forward
+
+    def launch(i):
+        k = i % ROTATE
+        rc = fwd(dptr, pk, xp[k], yp[k], nn, stream)
+        if rc != 0:
+            _lib.check(rc, "mlp forward")
+
+    wall, ev = _time_launches(launch, steps, warmup)
+    name = lib.rdv_mlp_kernel_name(dptr).decode()
+    return wall, ev, name
+
+
+def cpu_baseline_c2(sample: int = 1 << 16):
+    """The oracle's C2 forward on `sample` points: 3 warm-ups, median of 5."""
+    import numpy as np
+    from oracle import mlp as O
+    from rdv_project_amd import workloads as WL
+    cores = len(os.sched_getaffinity(0))
+    try:
+        from threadpoolctl import threadpool_limits
+        limiter = threadpool_limits(limits=cores)
+    except Exception:  # noqa: BLE001 - threadpoolctl is optional
+        limiter = None
+    x, layers = WL.c2(sample)
+    L = [(w.numpy(), b.numpy()) for w, b in layers]
+    xn = x.numpy()
+    acts = ["relu"] * 3 + ["none"]
+    times = []
+    for i in range(8):
+        t = time.perf_counter()
+        O.mlp_forward(xn, L, acts, ["f16"] * 4, encoding=(WL.C2_OCTAVES, WL.C2_PAD))
+        if i >= 3:
+            times.append(time.perf_counter() - t)
+    if limiter is not None:
+        limiter.unregister() if hasattr(limiter, "unregister") else None
+    med = statistics.median(times)
+    return {"value": round(sample / med / 1e6, 4), "unit": "Mpoints/s", "cores": cores, "kind": "port",
+            "sample": f"C2 forward on {sample} of the 2^20 points (numpy oracle: fp16-rounded operands, "
+                      f"float64 sums), median of 5 after 3 warm-ups; BLAS threads = {cores}"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=1000)
+    ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU baseline (profiling runs)")
+    ap.add_argument("--no-extras", action="store_true", help="only the headline configuration")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one GPU: every box of this run has a single MI355X, and the hot path "
+              "(independent points / rays / image tiles) needs no collective. Run with --gpus 1.",
+              file=sys.stderr)
+        return 2
+
+    import torch
+    import rdv_project_amd as rdv
+    from rdv_project_amd import workloads as WL
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 2
+    torch.cuda.set_device(0)
+    rdv.set_synchronous(False)
+
+    # ---------------------------------------------------------------- C2 headline
+    _log("C2 setup")
+    x, layers = WL.c2()
+    enc = rdv.FrequencyEncoding(3, WL.C2_OCTAVES, pad_to=WL.C2_PAD)
+    acts = ["relu"] * 3 + ["none"]
+    wall, ev, kname = bench_mlp(x, layers, acts, enc, args.steps, args.warmup)
+    n = x.shape[0]
+    mpts = n / (wall * 1e-3) / 1e6
+    achieved = C2_FLOP_PER_POINT * n / (ev * 1e-3) / 1e12
+    _log(f"C2 {kname}: wall {wall * 1e3:.2f} us/step, events {ev * 1e3:.2f} us/launch, "
+         f"{mpts:.0f} Mpts/s, {achieved:.1f} TFLOP/s")
+
+    extras = {}
+    if not args.no_extras:
+        _log("C1")
+        x1, l1 = WL.c1()
+        w1, e1, k1 = bench_mlp(x1, l1, ["relu"] * 4 + ["none"], None, max(args.steps // 2, 10), args.warmup)
+        extras["C1_fused_mlp"] = {
+            "Mpoints_per_s": round(x1.shape[0] / (w1 * 1e-3) / 1e6, 1),
+            "us_per_call": round(w1 * 1e3, 3),
+            "kernel_us": round(e1 * 1e3, 3),
+            "TFLOP_s": round(C1_FLOP_PER_POINT * x1.shape[0] / (e1 * 1e-3) / 1e12, 2),
+            "kernel": k1,
+        }
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        _log("CPU baseline (oracle, bounded sample)")
+        cpu = cpu_baseline_c2()
+
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "mlp_fused_c2_traffic.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            traffic = json.load(f).get("hbm_bytes_per_launch")
+
+    line = {
+        "metric": METRIC,
+        "value": round(mpts, 1),
+        "unit": "Mpoints/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic",
+        "config": {
+            "workload": "C2 encoded coordinate MLP: 2^20 points U[-1,1]^3 (seed 0), FREQ 6 octaves "
+                        "(39 features, zero padded to 48) -> 64 -> 64 -> 64 -> 4, ReLU, Kaiming-uniform fp16 "
+                        "weights (seed 1), fp32 accumulate, one fused kernel",
+            "points": n,
+            "kernel": kname,
+        },
+        "roofline": {
+            "bound": "mfma",
+            "achieved": round(achieved, 2),
+            "peak": PEAK_FP16_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / PEAK_FP16_TFLOPS, 4),
+            "traffic": traffic,
+        },
+        "mfma_peak_pct": round(100.0 * achieved / PEAK_FP16_TFLOPS, 2),
+        "cpu_baseline": cpu,
+        "extras": extras,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
