@@ -16,6 +16,7 @@
 //
 // Layout (every section 256-byte aligned), for layer i with KC = K chunks of 16
 // and MT = M tiles of 32:
+//   header  : MlpPackHeader, 256 bytes (flags computed by the packer)
 //   frag[i] : MT x KC x 64 lanes x 8 fp16   (A fragments in lane order)
 //   bias[i] : MT*32 fp32                      (zero padded)
 //   w32[i]  : dims[i+1] x dims[i] fp32        (row-major copy, for fp32 paths)
@@ -27,6 +28,15 @@
 #include "../../include/rdv_hip.h"
 
 namespace rdv {
+
+// First 256 bytes of a packed block.
+struct MlpPackHeader {
+  uint32_t magic;  // kMlpPackMagic once packed
+  uint32_t flags;  // kMlpHasBias: some bias element is non-zero
+};
+constexpr uint32_t kMlpPackMagic = 0x52445631u;  // "RDV1"
+constexpr uint32_t kMlpHasBias = 1u;
+constexpr int64_t kMlpHeaderBytes = 256;
 
 struct MlpLayout {
   int n_layers;
@@ -99,7 +109,7 @@ inline bool mlp_layout(const rdv_mlp_desc& d, MlpLayout* lay) {
   const int L = d.n_layers;
   if (L < 1 || L > RDV_MLP_MAX_LAYERS) return false;
   lay->n_layers = L;
-  int64_t off = 0;
+  int64_t off = kMlpHeaderBytes;
   for (int i = 0; i < L; ++i) {
     lay->in_w[i] = d.dims[i];
     lay->out_w[i] = d.dims[i + 1];

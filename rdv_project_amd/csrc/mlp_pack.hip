@@ -4,6 +4,14 @@
 
 namespace rdv {
 
+__global__ void mlp_pack_header_kernel(uint8_t* __restrict__ packed) {
+  if (threadIdx.x == 0) {
+    MlpPackHeader* hdr = reinterpret_cast<MlpPackHeader*>(packed);
+    hdr->magic = kMlpPackMagic;
+    hdr->flags = 0;
+  }
+}
+
 // One thread per element of the largest region of layer `li`.
 __global__ void mlp_pack_layer_kernel(const float* __restrict__ W, const float* __restrict__ b,
                                       uint8_t* __restrict__ packed, MlpLayout lay, int li,
@@ -28,7 +36,9 @@ __global__ void mlp_pack_layer_kernel(const float* __restrict__ W, const float* 
   }
   // padded fp32 bias
   if (e < int64_t(mt) * 32) {
-    reinterpret_cast<float*>(packed + lay.bias_off[li])[e] = e < out_w ? b[e] : 0.0f;
+    const float bv = e < out_w ? b[e] : 0.0f;
+    reinterpret_cast<float*>(packed + lay.bias_off[li])[e] = bv;
+    if (bv != 0.0f) atomicOr(&reinterpret_cast<MlpPackHeader*>(packed)->flags, kMlpHasBias);
   }
   // fp32 copies
   if (e < int64_t(out_w) * in_w) reinterpret_cast<float*>(packed + lay.w32_off[li])[e] = W[e];
@@ -37,6 +47,8 @@ __global__ void mlp_pack_layer_kernel(const float* __restrict__ W, const float* 
 
 int launch_mlp_pack(const rdv_mlp_desc& d, const MlpLayout& lay, const float* const* W,
                     const float* const* b, void* packed, hipStream_t stream) {
+  mlp_pack_header_kernel<<<1, 64, 0, stream>>>(static_cast<uint8_t*>(packed));
+  RDV_HIP_TRY(hipGetLastError());
   for (int i = 0; i < lay.n_layers; ++i) {
     int64_t n = int64_t(lay.mt[i]) * lay.kc[i] * 64 * 8;
     const int64_t nw = int64_t(lay.out_w[i]) * lay.in_w[i];

@@ -88,7 +88,7 @@ def test_packed_bytes_layout():
                 64 * 4, 32 * 4,              # padded fp32 biases
                 64 * 3 * 4, 4 * 64 * 4,      # fp32 weight copies
                 64 * 4, 4 * 4]               # fp32 bias copies
-    off = 0
+    off = 256  # header (magic, flags)
     for s in sections:  # every section starts 256-byte aligned
         off = (off + s + 255) // 256 * 256
     assert n == off

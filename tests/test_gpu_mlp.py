@@ -76,6 +76,28 @@ def test_c4_mlp_density_rgb_head():
     _assert_fp16_parity(y, ref, "C4 mlp")
 
 
+@pytest.mark.parametrize("cfg", ["c1", "c2", "c4"])
+def test_fused_kernels_with_nonzero_bias(cfg):
+    """The benchmark configurations have zero biases (the packer then selects the
+    bias-free path); this runs the same fused kernels with biases seeded."""
+    g = WL.gen(31)
+    if cfg == "c2":
+        x, layers = WL.c2(20000)
+        enc = rdv.FrequencyEncoding(3, WL.C2_OCTAVES, pad_to=WL.C2_PAD)
+        acts, encoding = ["relu"] * 3 + ["none"], (WL.C2_OCTAVES, WL.C2_PAD)
+    elif cfg == "c1":
+        x, layers = WL.c1(20000)
+        enc, acts, encoding = None, ["relu"] * 4 + ["none"], None
+    else:
+        x = torch.rand(20000, 3, generator=g) * 2 - 1
+        layers = WL.c4_mlp()
+        enc, acts, encoding = None, ["relu"] * 3 + ["density_rgb"], None
+    layers = [(w, torch.rand(w.shape[0], generator=g) * 0.5 - 0.25) for w, _ in layers]
+    y = _chain(layers, acts, enc=enc)(x.cuda()).as_tensor("torch").cpu().numpy()
+    ref = O.mlp_forward(x.numpy(), _np_layers(layers), acts, ["f16"] * len(layers), encoding=encoding)
+    _assert_fp16_parity(y, ref, f"{cfg} with bias")
+
+
 @pytest.mark.parametrize("n", [1, 17, 31, 32, 33, 65, 4096 + 19])
 def test_row_counts_and_fp32_tail(n):
     x, layers = WL.c1(n)
