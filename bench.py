@@ -139,6 +139,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU baseline (profiling runs)")
     ap.add_argument("--no-extras", action="store_true", help="only the headline configuration")
+    ap.add_argument("--calib-copy", action="store_true",
+                    help="first run 5 plain 64 MiB device copies (known HBM bytes) so that a rocprofv3 --pmc "
+                         "FETCH_SIZE / WRITE_SIZE run can scale the counters")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -157,6 +160,14 @@ def main() -> int:
         return 2
     torch.cuda.set_device(0)
     rdv.set_synchronous(False)
+
+    if args.calib_copy:
+        src = torch.empty(64 << 20, dtype=torch.uint8, device="cuda").fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
 
     # ---------------------------------------------------------------- C2 headline
     _log("C2 setup")
