@@ -121,6 +121,47 @@ int rdv_mlp_forward_f16_all(const rdv_mlp_desc* desc, const void* packed,
  * reports); "" if the descriptor is invalid. */
 const char* rdv_mlp_kernel_name(const rdv_mlp_desc* desc);
 
+/* ------------------------------------------------- Winograd F(2x2,3x3) conv */
+/* Image layouts (one image = batch element): HWC is the reference's
+ * channels-last [H*W, C] (src/rdv/domain/nn.py:1018-1024); CHW is NCHW. */
+enum { RDV_LAYOUT_HWC = 0, RDV_LAYOUT_CHW = 1 };
+enum { RDV_DTYPE_F32 = 0, RDV_DTYPE_F16 = 1 };
+/* Filter layouts: RSCK is the reference's [3][3][CIN][COUT]; KCRS is PyTorch OIHW. */
+enum { RDV_WLAYOUT_RSCK = 0, RDV_WLAYOUT_KCRS = 1 };
+
+typedef struct rdv_conv_desc {
+  int32_t batch;               /* images, stored back to back          */
+  int32_t H, W;                /* even                                  */
+  int32_t cin;                 /* 1..64                                 */
+  int32_t cout;                /* multiple of 16, <= 1024               */
+  int32_t in_layout, in_dtype; /* RDV_LAYOUT_*, RDV_DTYPE_*             */
+  int32_t out_layout, out_dtype;
+  int32_t relu;                /* 1: max(y, 0) after the bias           */
+} rdv_conv_desc;
+
+/* Host-only shape check; launches nothing. */
+int rdv_winograd3x3_validate(const rdv_conv_desc* desc);
+
+/* Bytes of the transformed filter bank for (cin, cout). */
+int64_t rdv_winograd3x3_weight_bytes(int32_t cin, int32_t cout);
+
+/* U = G g G^T per (cin, cout) filter in fp32, rounded to fp16, packed for the
+ * matrix cores (rdv_winograd3x3_weight_bytes bytes, 16-byte aligned).  w is a
+ * device pointer to the 3x3 filters in w_layout / w_dtype.
+ * Replaces _winograd_transform_weight (src/rdv/domain/nn.py:525-538). */
+int rdv_winograd3x3_transform_weight(const void* w, int32_t w_layout, int32_t w_dtype, int32_t cin,
+                                     int32_t cout, void* U, void* stream);
+
+/* 'same'-padded stride-1 3x3 convolution y = conv(x, w) + bias (optionally
+ * ReLU), via F(2x2,3x3) with fp16 operands and fp32 accumulation.  bias is an
+ * fp32 device pointer [cout] or NULL (zero).
+ * Replaces Conv2DTensorOpWinograd3x3's dispatch (src/rdv/domain/nn.py:1002-1087,
+ * src/rdv/shaders/tensors/conv2d_tensor_op_winograd3x3.h:95-178).  Unlike the
+ * reference (CIN, COUT <= 48, (H/2)(W/2) % 32 == 0, nn.py:1066-1078) any even
+ * H, W and CIN <= 64 are accepted. */
+int rdv_winograd3x3_forward(const rdv_conv_desc* desc, const void* x, const void* U, const float* bias,
+                            void* y, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -20,7 +20,9 @@ from .core import (
     wrap,
 )
 from .maths import Composite, Grid, Identity, Map, Sensor, TensorOperation, X, e, pi
+from ._conv import Winograd3x3Conv2d, winograd3x3_conv2d
 from .nn import (
+    Conv2DTensorOpWinograd3x3,
     DensityRGB,
     FrequencyEncoding,
     Linear,

@@ -25,6 +25,9 @@ MLP_MAX_WIDTH = 256
 ACT_NONE, ACT_RELU, ACT_SOFTPLUS, ACT_SIGMOID, ACT_DENSITY_RGB = 0, 1, 2, 3, 4
 PREC_F32, PREC_F16 = 0, 1
 ENC_NONE, ENC_FREQ = 0, 1
+LAYOUT_HWC, LAYOUT_CHW = 0, 1
+DTYPE_F32, DTYPE_F16 = 0, 1
+WLAYOUT_RSCK, WLAYOUT_KCRS = 0, 1
 
 
 class MlpDesc(C.Structure):
@@ -37,6 +40,22 @@ class MlpDesc(C.Structure):
         ("dims", C.c_int32 * (MLP_MAX_LAYERS + 1)),
         ("act", C.c_int32 * MLP_MAX_LAYERS),
         ("prec", C.c_int32 * MLP_MAX_LAYERS),
+    ]
+
+
+class ConvDesc(C.Structure):
+    """Mirror of rdv_conv_desc."""
+    _fields_ = [
+        ("batch", C.c_int32),
+        ("H", C.c_int32),
+        ("W", C.c_int32),
+        ("cin", C.c_int32),
+        ("cout", C.c_int32),
+        ("in_layout", C.c_int32),
+        ("in_dtype", C.c_int32),
+        ("out_layout", C.c_int32),
+        ("out_dtype", C.c_int32),
+        ("relu", C.c_int32),
     ]
 
 
@@ -56,6 +75,12 @@ _SIGNATURES = {
     "rdv_mlp_forward_f16_all": (C.c_int, [C.POINTER(MlpDesc), C.c_void_p, C.c_void_p, C.c_void_p, C.c_int64,
                                           C.c_void_p]),
     "rdv_mlp_kernel_name": (C.c_char_p, [C.POINTER(MlpDesc)]),
+    "rdv_winograd3x3_validate": (C.c_int, [C.POINTER(ConvDesc)]),
+    "rdv_winograd3x3_weight_bytes": (C.c_int64, [C.c_int32, C.c_int32]),
+    "rdv_winograd3x3_transform_weight": (C.c_int, [C.c_void_p, C.c_int32, C.c_int32, C.c_int32, C.c_int32,
+                                                   C.c_void_p, C.c_void_p]),
+    "rdv_winograd3x3_forward": (C.c_int, [C.POINTER(ConvDesc), C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
+                                          C.c_void_p]),
 }
 
 _lib = None

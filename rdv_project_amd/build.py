@@ -25,6 +25,7 @@ SOURCES = [
     "mlp_pack.hip",
     "mlp_f32.hip",
     "mlp_fused.hip",
+    "winograd.hip",
 ]
 
 ARCH = os.environ.get("RDV_OFFLOAD_ARCH", "gfx950")

@@ -53,6 +53,35 @@ int launch_mlp_chain_f32(const rdv_mlp_desc& d, const MlpLayout& lay, const void
 int launch_mlp_pack(const rdv_mlp_desc& d, const MlpLayout& lay, const float* const* W, const float* const* b,
                     void* packed, hipStream_t stream);
 int prepare_chain_f32(const rdv_mlp_desc& d);
+int64_t winograd_weight_bytes(int cin, int cout);
+int launch_winograd_transform_weight(const void* w, int w_layout, int w_dtype, int cin, int cout, void* U,
+                                     hipStream_t stream);
+int launch_winograd3x3(const rdv_conv_desc& d, const void* x, const void* U, const float* bias, void* y,
+                       hipStream_t stream);
+
+static int check_conv(const rdv_conv_desc* d) {
+  if (!d) return fail(RDV_ERR_INVALID, "conv descriptor is NULL");
+  if (d->batch < 1) return fail(RDV_ERR_INVALID, "batch must be >= 1");
+  if (d->H < 2 || d->W < 2 || d->H % 2 || d->W % 2)
+    return fail(RDV_ERR_INVALID, "H (" + std::to_string(d->H) + ") and W (" + std::to_string(d->W) +
+                                     ") must be even and >= 2");
+  if (d->cin < 1 || d->cin > 64)
+    return fail(RDV_ERR_INVALID, "in_channels (" + std::to_string(d->cin) + ") must be in [1, 64]");
+  if (d->cout < 16 || d->cout > 1024 || d->cout % 16)
+    return fail(RDV_ERR_INVALID, "out_channels (" + std::to_string(d->cout) + ") must be a multiple of 16 in [16, 1024]");
+  if ((d->in_layout != RDV_LAYOUT_HWC && d->in_layout != RDV_LAYOUT_CHW) ||
+      (d->out_layout != RDV_LAYOUT_HWC && d->out_layout != RDV_LAYOUT_CHW))
+    return fail(RDV_ERR_INVALID, "unknown image layout");
+  if ((d->in_dtype != RDV_DTYPE_F32 && d->in_dtype != RDV_DTYPE_F16) ||
+      (d->out_dtype != RDV_DTYPE_F32 && d->out_dtype != RDV_DTYPE_F16))
+    return fail(RDV_ERR_INVALID, "unknown element type");
+  // per-image element offsets are 32-bit in the kernel
+  if (int64_t(d->H) * d->W * d->cin >= (int64_t(1) << 31))
+    return fail(RDV_ERR_INVALID, "H * W * in_channels must be < 2^31");
+  const int64_t px = int64_t(d->batch) * d->H * d->W;
+  if (px > (int64_t(1) << 40)) return fail(RDV_ERR_INVALID, "image too large");
+  return RDV_OK;
+}
 
 static int check_mlp(const rdv_mlp_desc* d, MlpLayout* lay) {
   if (!d) return fail(RDV_ERR_INVALID, "mlp descriptor is NULL");
@@ -166,6 +195,36 @@ int rdv_mlp_forward(const rdv_mlp_desc* desc, const void* packed, const float* x
 int rdv_mlp_forward_f16_all(const rdv_mlp_desc* desc, const void* packed, const float* x, float* y, int64_t n,
                             void* stream) {
   return mlp_forward_impl(desc, packed, x, y, n, stream, false);
+}
+
+int rdv_winograd3x3_validate(const rdv_conv_desc* desc) { return check_conv(desc); }
+
+int64_t rdv_winograd3x3_weight_bytes(int32_t cin, int32_t cout) {
+  if (cin < 1 || cin > 64 || cout < 16 || cout > 1024 || cout % 16)
+    return fail(RDV_ERR_INVALID, "in_channels must be in [1, 64], out_channels a multiple of 16 in [16, 1024]");
+  return winograd_weight_bytes(cin, cout);
+}
+
+int rdv_winograd3x3_transform_weight(const void* w, int32_t w_layout, int32_t w_dtype, int32_t cin, int32_t cout,
+                                     void* U, void* stream) {
+  const int64_t nb = rdv_winograd3x3_weight_bytes(cin, cout);
+  if (nb < 0) return int(nb);
+  if (!w || !U) return fail(RDV_ERR_INVALID, "rdv_winograd3x3_transform_weight: NULL pointer argument");
+  if (w_layout != RDV_WLAYOUT_RSCK && w_layout != RDV_WLAYOUT_KCRS) return fail(RDV_ERR_INVALID, "unknown filter layout");
+  if (w_dtype != RDV_DTYPE_F32 && w_dtype != RDV_DTYPE_F16) return fail(RDV_ERR_INVALID, "unknown filter type");
+  if (reinterpret_cast<uintptr_t>(U) % 16) return fail(RDV_ERR_INVALID, "U must be 16-byte aligned");
+  return launch_winograd_transform_weight(w, w_layout, w_dtype, cin, cout, U, static_cast<hipStream_t>(stream));
+}
+
+int rdv_winograd3x3_forward(const rdv_conv_desc* desc, const void* x, const void* U, const float* bias, void* y,
+                            void* stream) {
+  int rc = check_conv(desc);
+  if (rc != RDV_OK) return rc;
+  if (!x || !U || !y) return fail(RDV_ERR_INVALID, "rdv_winograd3x3_forward: NULL pointer argument");
+  if (reinterpret_cast<uintptr_t>(U) % 16) return fail(RDV_ERR_INVALID, "U must be 16-byte aligned");
+  const size_t oal = desc->out_dtype == RDV_DTYPE_F16 ? 8 : 16;
+  if (reinterpret_cast<uintptr_t>(y) % oal) return fail(RDV_ERR_INVALID, "y is not aligned for vector stores");
+  return launch_winograd3x3(*desc, x, U, bias, y, static_cast<hipStream_t>(stream));
 }
 
 const char* rdv_mlp_kernel_name(const rdv_mlp_desc* desc) {

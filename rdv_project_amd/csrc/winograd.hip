@@ -1,0 +1,400 @@
+// Winograd F(2x2, 3x3) convolution on the fp16 matrix cores.
+//
+// Replaces Conv2DTensorOpWinograd3x3 (src/rdv/domain/nn.py:1002-1087,
+// src/rdv/shaders/tensors/conv2d_tensor_op_winograd3x3.h:95-178) with the same
+// numerics: U = G g G^T in fp32 rounded to fp16 (nn.py:522-538); per tile and
+// input channel V = B^T d B in fp32 rounded to fp16 (.h:59-78, 136); 16
+// channel-reduction GEMMs with fp32 accumulation (.h:142-161); Y = A^T M A in
+// fp32 plus the fp32 bias (.h:80-93, 169-173); optional ReLU epilogue.
+//
+// MI355X mapping (v_mfma_f32_16x16x32_f16: A 16x32, B 32x16, D 16x16):
+//   M = 16 output channels (one wave per 16-channel group), N = 16 Winograd
+//   tiles, K = 32 input channels.  Lane l holds
+//     A: U[p][ci = 32 kc + 8 (l/16) + j][co = 16 g + l%16]          (VGPRs, packed)
+//     B: V[p][tile l%16][ci = 32 kc + 8 (l/16) + j]                 (LDS, ds_read_b128)
+//     D: M[p][co = 16 g + 4 (l/16) + j][tile l%16], j = 0..3
+//   so every lane holds all 16 domain positions of its (tile, 4 channels) and
+//   the inverse transform runs in registers: for each row a of the 4x4 domain,
+//   the four M[a][b] are reduced over b and folded into the 2x2 output.
+//   The reference's structure (one lane per tile re-reading its 4x4xCIN patch
+//   from global memory for every (position, channel block) pair, .h:113-137) is
+//   replaced by one staging of the haloed input in LDS per tile group.
+//
+// Work decomposition: a tile group is 16 consecutive tiles of one tile row (2
+// output rows x 32 output columns).  Each block owns a contiguous range of
+// groups; per group it stages the 4 x 34 x CIN input region in LDS (fp32),
+// transforms it to V in B-fragment order (fp16), then every wave evaluates its
+// 16 output channels for the 16 tiles.
+#include <type_traits>
+
+#include "rdv_common.h"
+
+namespace rdv {
+
+constexpr int kWgTiles = 16;               // tiles per group (MFMA N)
+constexpr int kWgCols = 2 * kWgTiles + 2;  // staged input columns (34)
+
+// ---------------------------------------------------------------- weights
+// U for (p, ci, co) following nn.py:532-538: T = G g (3 terms per element),
+// then U = T G^T (3 terms), in fp32, rounded to fp16.  g[r][s] = w(ci, co, r, s).
+__device__ __forceinline__ float winograd_u(const float g[3][3], int a, int b) {
+  const float G[4][3] = {{1.0f, 0.0f, 0.0f}, {0.5f, 0.5f, 0.5f}, {0.5f, -0.5f, 0.5f}, {0.0f, 0.0f, 1.0f}};
+  float t[3];
+#pragma unroll
+  for (int s = 0; s < 3; ++s) t[s] = G[a][0] * g[0][s] + G[a][1] * g[1][s] + G[a][2] * g[2][s];
+  return t[0] * G[b][0] + t[1] * G[b][1] + t[2] * G[b][2];
+}
+
+// One thread per packed element: Upk[p][kc][g][lane][j] (fp16), zero for padded channels.
+__global__ void winograd_transform_weight_kernel(const void* __restrict__ w, int w_layout, int w_dtype, int cin,
+                                                 int cout, int kc_n, int g_n, half_t* __restrict__ U) {
+  const int64_t e = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t total = int64_t(16) * kc_n * g_n * 64 * 8;
+  if (e >= total) return;
+  const int j = int(e & 7);
+  const int lane = int((e >> 3) & 63);
+  int64_t r = e >> 9;
+  const int g = int(r % g_n);
+  r /= g_n;
+  const int kc = int(r % kc_n);
+  const int p = int(r / kc_n);
+  const int ci = 32 * kc + 8 * (lane >> 4) + j;
+  const int co = 16 * g + (lane & 15);
+  float v = 0.0f;
+  if (ci < cin && co < cout) {
+    float gm[3][3];
+#pragma unroll
+    for (int rr = 0; rr < 3; ++rr)
+#pragma unroll
+      for (int ss = 0; ss < 3; ++ss) {
+        // reference layout [3][3][CIN][COUT]; KCRS = PyTorch OIHW [COUT][CIN][3][3]
+        const int64_t idx = w_layout == RDV_WLAYOUT_RSCK ? ((int64_t(rr) * 3 + ss) * cin + ci) * cout + co
+                                                         : ((int64_t(co) * cin + ci) * 3 + rr) * 3 + ss;
+        gm[rr][ss] = w_dtype == RDV_DTYPE_F16 ? float(reinterpret_cast<const half_t*>(w)[idx])
+                                              : reinterpret_cast<const float*>(w)[idx];
+      }
+    v = winograd_u(gm, p >> 2, p & 3);
+  }
+  // Round to fp32 first, as the reference does: without this barrier the
+  // compiler fuses the last fma with the fp16 conversion (v_fma_mix, one
+  // rounding), which differs from fp32-then-fp16 on exact fp16 ties.
+  asm volatile("" : "+v"(v));
+  U[e] = half_t(v);
+}
+
+// ---------------------------------------------------------------- forward
+struct WinogradArgs {
+  const void* x;
+  const half_t* U;
+  const float* bias;  // may be null
+  void* y;
+  int batch, H, W, cin, cout;
+  int in_layout, in_dtype, out_layout, out_dtype;
+  int relu;
+  int th, seg;        // tile rows per image, 16-tile segments per tile row
+  int64_t ngroups;    // batch * th * seg
+};
+
+// Block: 4 waves; wave w owns output channels 16 (4 blockIdx.y + w) + 0..15
+// (waves past COUT only help with staging).  IN_F16 / IN_CHW select the input
+// element type and layout at compile time.
+template <int KC, bool IN_F16, bool IN_CHW>
+__global__ __launch_bounds__(256, 2) void winograd3x3_kernel(WinogradArgs a) {
+  using in_t = typename std::conditional<IN_F16, half_t, float>::type;
+  constexpr int CINP = 32 * KC;                          // padded input channels
+  constexpr int XS = CINP + 4;                           // LDS pixel stride (floats): 8-byte aligned, fewer bank conflicts
+  constexpr int kRegion = 4 * kWgCols * CINP;            // staged elements per group
+  constexpr int kPer = (kRegion + 255) / 256;            // per thread
+  __shared__ float sin_[4 * kWgCols * XS];
+  __shared__ half8 sv[16 * KC * 64];                     // V fragments [p][kc][lane]
+  const int lane = threadIdx.x & 63;
+  const int g = blockIdx.y * 4 + (threadIdx.x >> 6);     // output channel group (16 channels)
+  const bool active = 16 * g < a.cout;
+  const int hw = a.H * a.W;
+  const in_t* __restrict__ x = static_cast<const in_t*>(a.x);
+
+  // this wave's U fragments, resident for the whole block
+  half8 u[16][KC];
+  const int g_n = (a.cout + 15) / 16;
+  const int gu = active ? g : 0;
+#pragma unroll
+  for (int p = 0; p < 16; ++p)
+#pragma unroll
+    for (int kc = 0; kc < KC; ++kc)
+      u[p][kc] = reinterpret_cast<const half8*>(a.U)[((int64_t(p) * KC + kc) * g_n + gu) * 64 + lane];
+
+  const int64_t per_block = (a.ngroups + gridDim.x - 1) / gridDim.x;
+  const int64_t g_begin = int64_t(blockIdx.x) * per_block;
+  const int64_t g_end = g_begin + per_block < a.ngroups ? g_begin + per_block : a.ngroups;
+
+  // Loads of group grp's 4 x 34 x CINP input region into registers: every load
+  // is unconditional (clamped offset from the image's base) so that all are in
+  // flight at once; the zero padding is applied by a select.
+  auto load_region = [&](int64_t grp, float (&v)[kPer]) {
+    const int seg = int(grp % a.seg);
+    const int64_t rest = grp / a.seg;
+    const int tr = int(rest % a.th);
+    const int img = int(rest / a.th);
+    const int ih0 = 2 * tr - 1, iw0 = 2 * (seg * kWgTiles) - 1;
+    const in_t* __restrict__ base = x + int64_t(img) * a.cin * hw;
+    // opaque copy of the thread index: keeps the compiler from hoisting kPer
+    // per-element index decompositions out of the group loop into registers
+    int tid = int(threadIdx.x);
+    asm volatile("" : "+v"(tid));
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+      const int i = k * 256 + tid;
+      int ci, c, r;
+      if constexpr (IN_CHW) {  // consecutive threads walk a row segment of one channel
+        c = i % kWgCols;
+        r = (i / kWgCols) % 4;
+        ci = i / (4 * kWgCols);
+      } else {                 // consecutive threads walk the channels of one pixel
+        ci = i % CINP;
+        c = (i / CINP) % kWgCols;
+        r = i / (CINP * kWgCols);
+      }
+      const int ih = ih0 + r, iw = iw0 + c;
+      const bool ok = i < kRegion && ci < a.cin && ih >= 0 && ih < a.H && iw >= 0 && iw < a.W;
+      int off = IN_CHW ? ci * hw + ih * a.W + iw : (ih * a.W + iw) * a.cin + ci;
+      off = ok ? off : 0;
+      const float val = float(base[off]);
+      v[k] = ok ? val : 0.0f;
+    }
+  };
+  auto park_region = [&](const float (&v)[kPer]) {
+    int tid = int(threadIdx.x);
+    asm volatile("" : "+v"(tid));
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+      const int i = k * 256 + tid;
+      if (i < kRegion) {
+        int ci, c, r;
+        if constexpr (IN_CHW) {
+          c = i % kWgCols;
+          r = (i / kWgCols) % 4;
+          ci = i / (4 * kWgCols);
+        } else {
+          ci = i % CINP;
+          c = (i / CINP) % kWgCols;
+          r = i / (CINP * kWgCols);
+        }
+        sin_[(r * kWgCols + c) * XS + ci] = v[k];
+      }
+    }
+  };
+
+  if (g_begin < g_end) {
+    float v[kPer];
+    load_region(g_begin, v);
+    park_region(v);
+  }
+  __syncthreads();
+
+  for (int64_t grp = g_begin; grp < g_end; ++grp) {
+    const int seg = int(grp % a.seg);
+    const int64_t rest = grp / a.seg;
+    const int tr = int(rest % a.th);
+    const int img = int(rest / a.th);
+
+    // ---- V = B^T d B per (tile, 2 channels), fp32 -> fp16, B-fragment order
+    for (int unit = threadIdx.x; unit < kWgTiles * (CINP / 2); unit += 256) {
+      const int n = unit % kWgTiles;
+      const int q = unit / kWgTiles;  // channel pair
+      // rows first, exactly as _winograd_fwd: m = B^T d (per column), then V = m B
+      f32x2 m[4][4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        f32x2 d[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) d[r] = *reinterpret_cast<const f32x2*>(&sin_[(r * kWgCols + 2 * n + c) * XS + 2 * q]);
+        m[0][c] = d[0] - d[2];
+        m[1][c] = d[1] + d[2];
+        m[2][c] = d[2] - d[1];
+        m[3][c] = d[1] - d[3];
+      }
+      const int ci0 = 2 * q;
+      const int kc = ci0 / 32, k = ci0 % 32;
+      const int flane = (k / 8) * 16 + n, j0 = k % 8;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        f32x2 vv[4];
+        vv[0] = m[r][0] - m[r][2];
+        vv[1] = m[r][1] + m[r][2];
+        vv[2] = m[r][2] - m[r][1];
+        vv[3] = m[r][1] - m[r][3];
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+          half2v hv = {half_t(vv[b][0]), half_t(vv[b][1])};
+          half_t* dst = reinterpret_cast<half_t*>(&sv[((4 * r + b) * KC + kc) * 64 + flane]) + j0;
+          *reinterpret_cast<half2v*>(dst) = hv;
+        }
+      }
+    }
+    __syncthreads();  // sv complete; sin_ free
+
+    // next group's input: in flight while this group's GEMMs run
+    const bool more = grp + 1 < g_end;
+    float vn[kPer];
+    load_region(more ? grp + 1 : grp, vn);
+
+    if (active) {
+      // ---- 16 channel-reduction GEMMs, inverse transform folded column by
+      // column in the reference's order (_winograd_inv, .h:80-93):
+      //   t0[b] = (M[0][b] + M[1][b]) + M[2][b],  t1[b] = (M[1][b] - M[2][b]) - M[3][b]
+      //   Y[i][0] = (t_i[0] + t_i[1]) + t_i[2],   Y[i][1] = (t_i[1] - t_i[2]) - t_i[3]
+      f32x4 y00, y01, y10, y11;
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        f32x4 ma[4];
+#pragma unroll
+        for (int ra = 0; ra < 4; ++ra) {
+          const int p = 4 * ra + b;
+          f32x4 acc = {};
+#pragma unroll
+          for (int kc = 0; kc < KC; ++kc)
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(u[p][kc], sv[(p * KC + kc) * 64 + lane], acc, 0, 0, 0);
+          ma[ra] = acc;
+        }
+        const f32x4 t0 = ma[0] + ma[1] + ma[2];
+        const f32x4 t1 = ma[1] - ma[2] - ma[3];
+        if (b == 0) {
+          y00 = t0;
+          y10 = t1;
+        } else if (b == 1) {
+          y00 += t0;
+          y01 = t0;
+          y10 += t1;
+          y11 = t1;
+        } else if (b == 2) {
+          y00 += t0;
+          y01 -= t0;
+          y10 += t1;
+          y11 -= t1;
+        } else {
+          y01 -= t0;
+          y11 -= t1;
+        }
+      }
+      // ---- bias, ReLU, store: lane holds channels 16g + 4(l/16) + jj of tile l%16
+      const int n = lane & 15;
+      const int tc = seg * kWgTiles + n;
+      const int co0 = 16 * g + 4 * (lane >> 4);
+      if (tc < a.W / 2 && co0 < a.cout) {
+        const int oh = 2 * tr, ow = 2 * tc;
+        f32x4 yv[2][2] = {{y00, y01}, {y10, y11}};
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+          const float bb = a.bias ? a.bias[co0 + jj] : 0.0f;
+#pragma unroll
+          for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+              float val = yv[i][j][jj] + bb;
+              if (a.relu) val = fmaxf(val, 0.0f);
+              yv[i][j][jj] = val;
+            }
+        }
+        if (a.out_layout == RDV_LAYOUT_CHW) {
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj) {
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+              const int64_t o = (int64_t(img) * a.cout + co0 + jj) * hw + int64_t(oh + i) * a.W + ow;
+              if (a.out_dtype == RDV_DTYPE_F16) {
+                half2v hv = {half_t(yv[i][0][jj]), half_t(yv[i][1][jj])};
+                __builtin_nontemporal_store(hv, reinterpret_cast<half2v*>(static_cast<half_t*>(a.y) + o));
+              } else {
+                f32x2 fv = {yv[i][0][jj], yv[i][1][jj]};
+                __builtin_nontemporal_store(fv, reinterpret_cast<f32x2*>(static_cast<float*>(a.y) + o));
+              }
+            }
+          }
+        } else {
+#pragma unroll
+          for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+              const int64_t o = (int64_t(img) * hw + int64_t(oh + i) * a.W + ow + j) * a.cout + co0;
+              if (a.out_dtype == RDV_DTYPE_F16) {
+                half4 hv = {half_t(yv[i][j][0]), half_t(yv[i][j][1]), half_t(yv[i][j][2]), half_t(yv[i][j][3])};
+                __builtin_nontemporal_store(hv, reinterpret_cast<half4*>(static_cast<half_t*>(a.y) + o));
+              } else {
+                __builtin_nontemporal_store(yv[i][j], reinterpret_cast<f32x4*>(static_cast<float*>(a.y) + o));
+              }
+            }
+        }
+      }
+    }
+    if (more) park_region(vn);
+    __syncthreads();  // sin_ holds the next region; every wave is done with sv
+  }
+}
+
+int64_t winograd_weight_bytes(int cin, int cout) {
+  const int kc_n = (cin + 31) / 32, g_n = (cout + 15) / 16;
+  return int64_t(16) * kc_n * g_n * 64 * 8 * 2;
+}
+
+int launch_winograd_transform_weight(const void* w, int w_layout, int w_dtype, int cin, int cout, void* U,
+                                     hipStream_t stream) {
+  const int kc_n = (cin + 31) / 32, g_n = (cout + 15) / 16;
+  const int64_t total = int64_t(16) * kc_n * g_n * 64 * 8;
+  winograd_transform_weight_kernel<<<dim3(unsigned((total + 255) / 256)), dim3(256), 0, stream>>>(
+      w, w_layout, w_dtype, cin, cout, kc_n, g_n, static_cast<half_t*>(U));
+  RDV_HIP_TRY(hipGetLastError());
+  return RDV_OK;
+}
+
+int launch_winograd3x3(const rdv_conv_desc& d, const void* x, const void* U, const float* bias, void* y,
+                       hipStream_t stream) {
+  DeviceInfo di;
+  int rc = device_info(&di);
+  if (rc != RDV_OK) return rc;
+  WinogradArgs a;
+  a.x = x;
+  a.U = static_cast<const half_t*>(U);
+  a.bias = bias;
+  a.y = y;
+  a.batch = d.batch;
+  a.H = d.H;
+  a.W = d.W;
+  a.cin = d.cin;
+  a.cout = d.cout;
+  a.in_layout = d.in_layout;
+  a.in_dtype = d.in_dtype;
+  a.out_layout = d.out_layout;
+  a.out_dtype = d.out_dtype;
+  a.relu = d.relu;
+  a.th = d.H / 2;
+  a.seg = (d.W / 2 + kWgTiles - 1) / kWgTiles;
+  a.ngroups = int64_t(d.batch) * a.th * a.seg;
+  if (a.ngroups == 0) return RDV_OK;
+  const int groups16 = (d.cout + 15) / 16;
+  const int slices = (groups16 + 3) / 4;  // 64-channel slices (grid y)
+  int64_t blocks = (2 * int64_t(di.cu_count) + slices - 1) / slices;  // ~2 resident blocks per CU
+  if (a.ngroups < blocks) blocks = a.ngroups;
+  const dim3 grid(static_cast<unsigned>(blocks), static_cast<unsigned>(slices)), block(256);
+  const bool f16 = d.in_dtype == RDV_DTYPE_F16, chw = d.in_layout == RDV_LAYOUT_CHW;
+  if (d.cin <= 32) {
+    if (f16) {
+      if (chw) winograd3x3_kernel<1, true, true><<<grid, block, 0, stream>>>(a);
+      else winograd3x3_kernel<1, true, false><<<grid, block, 0, stream>>>(a);
+    } else {
+      if (chw) winograd3x3_kernel<1, false, true><<<grid, block, 0, stream>>>(a);
+      else winograd3x3_kernel<1, false, false><<<grid, block, 0, stream>>>(a);
+    }
+  } else {
+    if (f16) {
+      if (chw) winograd3x3_kernel<2, true, true><<<grid, block, 0, stream>>>(a);
+      else winograd3x3_kernel<2, true, false><<<grid, block, 0, stream>>>(a);
+    } else {
+      if (chw) winograd3x3_kernel<2, false, true><<<grid, block, 0, stream>>>(a);
+      else winograd3x3_kernel<2, false, false><<<grid, block, 0, stream>>>(a);
+    }
+  }
+  RDV_HIP_TRY(hipGetLastError());
+  return RDV_OK;
+}
+
+}  // namespace rdv

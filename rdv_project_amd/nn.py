@@ -3,6 +3,7 @@
 Map nodes compose with `>>` and are evaluated by the fused HIP MLP kernels:
   Linear / LinearFast / linear   nn.py:25-104
   ReLU / relu                    nn.py:107-119
+  Conv2DTensorOpWinograd3x3      nn.py:1002-1087
 Build-defined additions (no reference counterpart, needed by the benchmark
 configurations): FrequencyEncoding, Softplus, Sigmoid, DensityRGB.
 """
@@ -10,9 +11,9 @@ from __future__ import annotations
 
 import torch
 
-from . import _lib
+from . import _conv, _lib
 from .core import RDVObject, wrap
-from .maths import Map
+from .maths import Map, TensorOperation, _as_op_input
 
 
 class _LinearBase(Map):
@@ -125,3 +126,59 @@ class FrequencyEncoding(Map):
         self.octaves = int(octaves)
         self.IN = self.in_features
         self.OUT = int(width)
+
+
+# ============================================================ TENSOR OPERATIONS
+
+
+class Conv2DTensorOpWinograd3x3(TensorOperation):
+    """'same'-padded (zero border), stride-1 3x3 convolution via Winograd
+    F(2x2, 3x3) (reference: nn.py:1002-1087,
+    shaders/tensors/conv2d_tensor_op_winograd3x3.h).
+
+    x: [H*W, in_channels] channels-last (a buffer or an upstream
+    TensorOperation), weight: [3, 3, in_channels, out_channels], bias:
+    [out_channels] fp32.  result: [H*W, out_channels] fp32.  The filters are
+    transformed once, at construction (U = G g G^T in fp32, rounded to fp16,
+    nn.py:522-538); per 2x2 output tile the 4x4 input patch is transformed
+    (V = B^T d B, rounded to fp16), the 16 channel reductions accumulate in
+    fp32 and Y = A^T M A + bias.
+
+    Shape rules follow the reference (H, W even; channels multiples of 16)
+    except for its shared-memory limits (in/out channels <= 48 and
+    (H/2)(W/2) % 32 == 0, nn.py:1066-1078), which this kernel does not have:
+    in_channels may be up to 64 and out_channels up to 1024."""
+
+    def __init__(self, x, weight, bias, H: int, W: int) -> None:
+        data, shape, upstream = _as_op_input(x)
+        assert len(shape) == 2, "Conv2DTensorOpWinograd3x3 requires a 2D (H*W, in_channels) input"
+        hw, in_channels = shape
+        assert hw == H * W, f"H*W ({H * W}) must match x's own row count ({hw})"
+        weight = weight if isinstance(weight, RDVObject) else wrap(weight)
+        bias = bias if isinstance(bias, RDVObject) else wrap(_float32(bias))
+        assert tuple(weight.shape[:2]) == (3, 3), "weight must be [3, 3, in_channels, out_channels]"
+        _, _, weight_in_channels, out_channels = weight.shape
+        assert weight_in_channels == in_channels, "weight's own in_channels must match x's own trailing dim"
+        assert tuple(bias.shape) == (out_channels,), "bias must be [out_channels]"
+        assert H % 2 == 0, f"H ({H}) must be even"
+        assert W % 2 == 0, f"W ({W}) must be even"
+        assert in_channels % 16 == 0, f"in_channels ({in_channels}) must be a multiple of 16"
+        assert out_channels % 16 == 0, f"out_channels ({out_channels}) must be a multiple of 16"
+        assert in_channels <= 64, f"in_channels ({in_channels}) must be at most 64"
+        assert out_channels <= 1024, f"out_channels ({out_channels}) must be at most 1024"
+        if bias.scalar_type != torch.float32:
+            raise TypeError("bias must be a float32 buffer (reference field is Buffer[FLOAT32])")
+        self.CIN, self.COUT, self.H, self.W = int(in_channels), int(out_channels), int(H), int(W)
+        self.x_buf = data
+        self.bias = bias
+        self._desc = _conv.conv_desc(1, self.H, self.W, self.CIN, self.COUT, _lib.LAYOUT_HWC,
+                                     _conv._dtype_code(data.as_tensor("torch"), "x"), _lib.LAYOUT_HWC,
+                                     _lib.DTYPE_F32, False)
+        _conv.validate(self._desc)
+        self.weight_u = _conv.transform_weight(weight.as_tensor("torch"), _lib.WLAYOUT_RSCK)
+        self._upstream = upstream
+        super().__init__([hw, out_channels])
+
+    def _forward(self) -> None:
+        _conv.forward(self._desc, self.x_buf.as_tensor("torch"), self.weight_u, self.bias.as_tensor("torch"),
+                      self._result_t)

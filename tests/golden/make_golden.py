@@ -110,6 +110,84 @@ def make_freq_case():
     return {"p": np.array(P, np.float32), "features": np.array(F, np.float64), "octaves": np.array(L)}
 
 
+WG_G = [[1.0, 0.0, 0.0], [0.5, 0.5, 0.5], [0.5, -0.5, 0.5], [0.0, 0.0, 1.0]]
+
+
+def winograd_u_scalar(w, cin, cout):
+    """_winograd_transform_weight (nn.py:525-538) per element: T = G g, U = T G^T,
+    each a left-to-right fp32 sum of three products, then fp16.  w[r][s][ci][co]."""
+    U = [[[0.0] * cout for _ in range(cin)] for _ in range(16)]
+    for ci in range(cin):
+        for co in range(cout):
+            g = [[w[r][s][ci][co] for s in range(3)] for r in range(3)]
+            T = [[r32(r32(r32(WG_G[a][0] * g[0][s]) + r32(WG_G[a][1] * g[1][s])) + r32(WG_G[a][2] * g[2][s]))
+                  for s in range(3)] for a in range(4)]
+            for a in range(4):
+                for b in range(4):
+                    v = r32(r32(r32(T[a][0] * WG_G[b][0]) + r32(T[a][1] * WG_G[b][1])) + r32(T[a][2] * WG_G[b][2]))
+                    U[4 * a + b][ci][co] = r16(v)
+    return U
+
+
+def winograd_conv_scalar(x, w, bias, H, W, cin, cout):
+    """conv2d_tensor_op_winograd3x3.h:95-178 for every tile, written as the
+    shader's per-lane loops: d from x (0 outside), _winograd_fwd in fp32, V[p]
+    to fp16, M[p] = sum over ci of V*U (exact in binary64, one fp32 rounding),
+    _winograd_inv in fp32, + bias.  x[(h * W + w) * cin + c], result likewise."""
+    U = winograd_u_scalar(w, cin, cout)
+    y = [0.0] * (H * W * cout)
+    for tr in range(H // 2):
+        for tc in range(W // 2):
+            oh0, ow0 = 2 * tr, 2 * tc
+            Vall = []
+            for c in range(cin):
+                d = [0.0] * 16
+                for dr in range(4):
+                    for dc in range(4):
+                        gh, gw = oh0 - 1 + dr, ow0 - 1 + dc
+                        d[dr * 4 + dc] = x[(gh * W + gw) * cin + c] if 0 <= gh < H and 0 <= gw < W else 0.0
+                m = [0.0] * 16
+                for j in range(4):
+                    d0, d1, d2, d3 = d[j], d[4 + j], d[8 + j], d[12 + j]
+                    m[j], m[4 + j], m[8 + j], m[12 + j] = r32(d0 - d2), r32(d1 + d2), r32(d2 - d1), r32(d1 - d3)
+                V = [0.0] * 16
+                for i in range(4):
+                    m0, m1, m2, m3 = m[4 * i], m[4 * i + 1], m[4 * i + 2], m[4 * i + 3]
+                    V[4 * i], V[4 * i + 1], V[4 * i + 2], V[4 * i + 3] = (r32(m0 - m2), r32(m1 + m2), r32(m2 - m1),
+                                                                          r32(m1 - m3))
+                Vall.append([r16(v) for v in V])
+            for co in range(cout):
+                M = [r32(sum(Vall[c][p] * U[p][c][co] for c in range(cin))) for p in range(16)]
+                t = [0.0] * 8
+                for j in range(4):
+                    t[j] = r32(r32(M[j] + M[4 + j]) + M[8 + j])
+                    t[4 + j] = r32(r32(M[4 + j] - M[8 + j]) - M[12 + j])
+                Y = [0.0] * 4
+                for i in range(2):
+                    Y[2 * i] = r32(r32(t[4 * i] + t[4 * i + 1]) + t[4 * i + 2])
+                    Y[2 * i + 1] = r32(r32(t[4 * i + 1] - t[4 * i + 2]) - t[4 * i + 3])
+                for k, (dh, dw) in enumerate(((0, 0), (0, 1), (1, 0), (1, 1))):
+                    y[((oh0 + dh) * W + ow0 + dw) * cout + co] = r32(Y[k] + bias[co])
+    return U, y
+
+
+def make_winograd_case(seed, H, W, cin, cout):
+    g = lcg(seed)
+    x = [r32(v) for v in take(g, H * W * cin)]
+    wf = [r32(0.3 * v) for v in take(g, 9 * cin * cout)]
+    w = [[[[wf[((r * 3 + s) * cin + ci) * cout + co] for co in range(cout)] for ci in range(cin)] for s in range(3)]
+         for r in range(3)]
+    bias = [r32(0.1 * v) for v in take(g, cout)]
+    U, y = winograd_conv_scalar(x, w, bias, H, W, cin, cout)
+    return {
+        "x": np.array(x, np.float32).reshape(H, W, cin),
+        "w": np.array(wf, np.float32).reshape(3, 3, cin, cout),
+        "b": np.array(bias, np.float32),
+        "U": np.array(U, np.float32),
+        "y": np.array(y, np.float32).reshape(H, W, cout),
+    }
+
+
 def main():
     cases = {
         # 40 rows: one full group of 32 (fp16 path) + a partial group of 8 (fp32 rule)
@@ -122,7 +200,13 @@ def main():
     for name, arrays in cases.items():
         np.savez(os.path.join(HERE, f"{name}.npz"), **arrays)
     np.savez(os.path.join(HERE, "freq_encoding.npz"), **make_freq_case())
-    print("wrote", len(cases) + 1, "fixtures to", HERE)
+    wcases = {
+        "winograd_6x8_5_16": make_winograd_case(21, 6, 8, 5, 16),
+        "winograd_4x4_16_32": make_winograd_case(22, 4, 4, 16, 32),
+    }
+    for name, arrays in wcases.items():
+        np.savez(os.path.join(HERE, f"{name}.npz"), **arrays)
+    print("wrote", len(cases) + 1 + len(wcases), "fixtures to", HERE)
 
 
 if __name__ == "__main__":

@@ -104,3 +104,48 @@ def test_kernel_selection_names():
     # fp32 layers and unlisted shapes go to the generic kernel
     assert lib.rdv_mlp_kernel_name(C.byref(_desc([3, 64, 4], precs=[0, 0]))).decode() == "mlp_chain_f32_kernel"
     assert lib.rdv_mlp_kernel_name(C.byref(_desc([5, 37, 19]))).decode() == "mlp_chain_f32_kernel"
+
+
+def _conv(**kw):
+    d = _lib.ConvDesc()
+    vals = dict(batch=1, H=256, W=256, cin=64, cout=64, in_layout=_lib.LAYOUT_CHW, in_dtype=_lib.DTYPE_F16,
+                out_layout=_lib.LAYOUT_CHW, out_dtype=_lib.DTYPE_F16, relu=1)
+    vals.update(kw)
+    for k, v in vals.items():
+        setattr(d, k, v)
+    return d
+
+
+def test_winograd_validate_accepts_benchmark_and_reference_shapes():
+    lib = _lib.load()
+    assert lib.rdv_winograd3x3_validate(_conv()) == 0
+    assert lib.rdv_winograd3x3_validate(_conv(H=16, W=16, cin=48, cout=48, in_layout=_lib.LAYOUT_HWC,
+                                              in_dtype=_lib.DTYPE_F32, out_layout=_lib.LAYOUT_HWC,
+                                              out_dtype=_lib.DTYPE_F32, relu=0)) == 0
+    assert lib.rdv_winograd3x3_validate(_conv(H=2, W=2, cin=1, cout=16)) == 0
+
+
+@pytest.mark.parametrize("kw,fragment", [
+    (dict(H=255), "even"),
+    (dict(W=0), "even"),
+    (dict(cin=65), "in_channels"),
+    (dict(cin=0), "in_channels"),
+    (dict(cout=40), "out_channels"),
+    (dict(cout=2048), "out_channels"),
+    (dict(batch=0), "batch"),
+    (dict(in_layout=7), "layout"),
+    (dict(out_dtype=5), "element type"),
+    (dict(H=8192, W=8192), "2^31"),
+])
+def test_winograd_validate_rejects(kw, fragment):
+    lib = _lib.load()
+    assert lib.rdv_winograd3x3_validate(_conv(**kw)) == _lib.RDV_ERR_INVALID
+    assert fragment in _lib.last_error()
+
+
+def test_winograd_weight_bytes():
+    lib = _lib.load()
+    # [16 positions][ceil(cin/32)][cout/16][64 lanes][8] fp16
+    assert lib.rdv_winograd3x3_weight_bytes(64, 64) == 16 * 2 * 4 * 64 * 8 * 2
+    assert lib.rdv_winograd3x3_weight_bytes(5, 16) == 16 * 1 * 1 * 64 * 8 * 2
+    assert lib.rdv_winograd3x3_weight_bytes(64, 40) == _lib.RDV_ERR_INVALID
