@@ -33,6 +33,13 @@ PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
 C2_FLOP_PER_POINT = 2 * (48 * 64 + 64 * 64 + 64 * 64 + 64 * 4)  # 23,040 (declared padded shapes)
 C1_FLOP_PER_POINT = 2 * (3 * 64 + 3 * 64 * 64 + 64 * 4)          # 25,472
 ROTATE = 12
+# C3: direct-equivalent work 2 H W CIN COUT 9 (the convention for reporting
+# convolution TFLOP/s); Winograd-domain MFMA work 2 * 16 * tiles * CIN * COUT;
+# algorithmic HBM bytes: fp16 x + fp16 y + packed fp16 U.
+C3_DIRECT_FLOP = 2 * 256 * 256 * 64 * 64 * 9                     # 4.832 GFLOP
+C3_WINO_FLOP = 2 * 16 * (128 * 128) * 64 * 64                     # 2.147 GFLOP
+C3_BYTES = 2 * 64 * 256 * 256 * 2 + 16 * 2 * 4 * 64 * 8 * 2       # 16,908,288 B
+C3_ROTATE = 24  # 24 x (8 + 8) MiB of x / y: more than the 256 MB MALL
 
 
 def _log(msg: str) -> None:
@@ -101,6 +108,47 @@ def bench_mlp(x_cpu, layers, acts, enc, steps, warmup):
     wall, ev = _time_launches(launch, steps, warmup)
     name = lib.rdv_mlp_kernel_name(dptr).decode()
     return wall, ev, name
+
+
+def bench_winograd(steps, warmup):
+    """C3 through the C ABI: NCHW fp16 in / out, ReLU, rotating x / y sets."""
+    import torch
+    import rdv_project_amd as rdv
+    from rdv_project_amd import _conv, _lib
+    from rdv_project_amd import workloads as WL
+    lib = _lib.load()
+    x, w, b = WL.c3()
+    conv = rdv.Winograd3x3Conv2d(w.cuda(), b.cuda())
+    xd = x.cuda()
+    xs = [xd] + [xd.clone() for _ in range(C3_ROTATE - 1)]
+    ys = [torch.empty(1, 64, 256, 256, dtype=torch.float16, device="cuda") for _ in range(C3_ROTATE)]
+    d = _conv.conv_desc(1, 256, 256, 64, 64, _lib.LAYOUT_CHW, _lib.DTYPE_F16, _lib.LAYOUT_CHW, _lib.DTYPE_F16, True)
+    stream = C.c_void_p(torch.cuda.current_stream().cuda_stream)
+    dptr = C.byref(d)
+    up = C.c_void_p(conv.U.data_ptr())
+    bp = C.c_void_p(conv.bias.data_ptr())
+    xp = [C.c_void_p(t.data_ptr()) for t in xs]
+    yp = [C.c_void_p(t.data_ptr()) for t in ys]
+    fwd = lib.rdv_winograd3x3_forward
+
+    def launch(i):
+        k = i % C3_ROTATE
+        rc = fwd(dptr, xp[k], up, bp, yp[k], stream)
+        if rc != 0:
+            _lib.check(rc, "winograd forward")
+
+    wall, ev = _time_launches(launch, steps, warmup)
+    return {
+        "us_per_call": round(wall * 1e3, 3),
+        "kernel_us": round(ev * 1e3, 3),
+        "TFLOP_s_direct_equiv": round(C3_DIRECT_FLOP / (ev * 1e-3) / 1e12, 2),
+        "TFLOP_s_winograd_mfma": round(C3_WINO_FLOP / (ev * 1e-3) / 1e12, 2),
+        "hbm_GB_s": round(C3_BYTES / (ev * 1e-3) / 1e9, 1),
+        "hbm_frac": round(C3_BYTES / (ev * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+        "workload": "C3 Winograd F(2x2,3x3): NCHW fp16 1x64x256x256 U[0,1] (seed 3), 64 -> 64, "
+                    "w ~ N(0, sqrt(2/576)) fp16 (seed 4), zero bias, ReLU, fp16 out",
+        "kernel": "winograd3x3_strip_kernel<2>",
+    }
 
 
 def cpu_baseline_c2(sample: int = 1 << 16):
@@ -193,6 +241,9 @@ def main() -> int:
             "TFLOP_s": round(C1_FLOP_PER_POINT * x1.shape[0] / (e1 * 1e-3) / 1e12, 2),
             "kernel": k1,
         }
+        _log("C3")
+        extras["C3_winograd"] = bench_winograd(max(args.steps // 2, 10), args.warmup)
+        _log(f"C3 {extras['C3_winograd']}")
 
     cpu = None
     if not args.no_cpu_baseline:

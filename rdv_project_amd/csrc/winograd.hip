@@ -25,6 +25,7 @@
 // groups; per group it stages the 4 x 34 x CIN input region in LDS (fp32),
 // transforms it to V in B-fragment order (fp16), then every wave evaluates its
 // 16 output channels for the 16 tiles.
+#include <algorithm>
 #include <type_traits>
 
 #include "rdv_common.h"
@@ -93,7 +94,122 @@ struct WinogradArgs {
   int relu;
   int th, seg;        // tile rows per image, 16-tile segments per tile row
   int64_t ngroups;    // batch * th * seg
+  int rows_per_item;  // strip kernel: tile rows per work item
+  int chunks;         // strip kernel: work items per strip (ceil(th / rows_per_item))
+  int64_t items;      // strip kernel: batch * seg * chunks
 };
+
+// The 16 channel-reduction GEMMs of one 16-tile group for this wave's 16
+// output channels (A = U from registers, B = V fragments from LDS), the
+// inverse transform folded column by column in the reference's order
+// (_winograd_inv, .h:80-93):
+//   t0[b] = (M[0][b] + M[1][b]) + M[2][b],  t1[b] = (M[1][b] - M[2][b]) - M[3][b]
+//   Y[i][0] = (t_i[0] + t_i[1]) + t_i[2],   Y[i][1] = (t_i[1] - t_i[2]) - t_i[3]
+// then + bias, optional ReLU, and the store of the 2x2 outputs of tile
+// lane % 16 for channels 16 g + 4 (lane / 16) + 0..3 (`bias` holds those
+// four channels' biases).
+template <int KC>
+__device__ __forceinline__ void wg_gemm(const half8 (&u)[16][KC], const half8* sv, int lane, f32x4 (&yv)[2][2]) {
+  f32x4 y00, y01, y10, y11;
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    f32x4 ma[4];
+#pragma unroll
+    for (int ra = 0; ra < 4; ++ra) {
+      const int p = 4 * ra + b;
+      f32x4 acc = {};
+#pragma unroll
+      for (int kc = 0; kc < KC; ++kc)
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(u[p][kc], sv[(p * KC + kc) * 64 + lane], acc, 0, 0, 0);
+      ma[ra] = acc;
+    }
+    const f32x4 t0 = ma[0] + ma[1] + ma[2];
+    const f32x4 t1 = ma[1] - ma[2] - ma[3];
+    if (b == 0) {
+      y00 = t0;
+      y10 = t1;
+    } else if (b == 1) {
+      y00 += t0;
+      y01 = t0;
+      y10 += t1;
+      y11 = t1;
+    } else if (b == 2) {
+      y00 += t0;
+      y01 -= t0;
+      y10 += t1;
+      y11 -= t1;
+    } else {
+      y01 -= t0;
+      y11 -= t1;
+    }
+  }
+  yv[0][0] = y00;
+  yv[0][1] = y01;
+  yv[1][0] = y10;
+  yv[1][1] = y11;
+}
+
+template <int KC>
+__device__ __forceinline__ void wg_gemm_store(const half8 (&u)[16][KC], const half8* sv, int lane, int g,
+                                              const f32x4& bias, const WinogradArgs& a, int img, int tr, int seg) {
+  f32x4 yv[2][2];
+  wg_gemm(u, sv, lane, yv);
+  const int hw = a.H * a.W;
+  const int n = lane & 15;
+  const int tc = seg * kWgTiles + n;
+  const int co0 = 16 * g + 4 * (lane >> 4);
+  if (tc >= a.W / 2 || co0 >= a.cout) return;
+  const int oh = 2 * tr, ow = 2 * tc;
+#pragma unroll
+  for (int jj = 0; jj < 4; ++jj) {
+    const float bb = bias[jj];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        float val = yv[i][j][jj] + bb;
+        if (a.relu) val = fmaxf(val, 0.0f);
+        yv[i][j][jj] = val;
+      }
+  }
+  if (a.out_layout == RDV_LAYOUT_CHW) {
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int64_t o = (int64_t(img) * a.cout + co0 + jj) * hw + int64_t(oh + i) * a.W + ow;
+        if (a.out_dtype == RDV_DTYPE_F16) {
+          half2v hv = {half_t(yv[i][0][jj]), half_t(yv[i][1][jj])};
+          __builtin_nontemporal_store(hv, reinterpret_cast<half2v*>(static_cast<half_t*>(a.y) + o));
+        } else {
+          f32x2 fv = {yv[i][0][jj], yv[i][1][jj]};
+          __builtin_nontemporal_store(fv, reinterpret_cast<f32x2*>(static_cast<float*>(a.y) + o));
+        }
+      }
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int64_t o = (int64_t(img) * hw + int64_t(oh + i) * a.W + ow + j) * a.cout + co0;
+        if (a.out_dtype == RDV_DTYPE_F16) {
+          half4 hv = {half_t(yv[i][j][0]), half_t(yv[i][j][1]), half_t(yv[i][j][2]), half_t(yv[i][j][3])};
+          __builtin_nontemporal_store(hv, reinterpret_cast<half4*>(static_cast<half_t*>(a.y) + o));
+        } else {
+          __builtin_nontemporal_store(yv[i][j], reinterpret_cast<f32x4*>(static_cast<float*>(a.y) + o));
+        }
+      }
+  }
+}
+
+// The four biases of this lane's output channels 16 g + 4 (lane / 16) + 0..3.
+__device__ __forceinline__ f32x4 wg_lane_bias(const WinogradArgs& a, int g, int lane) {
+  const int co0 = 16 * g + 4 * (lane >> 4);
+  f32x4 b = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (a.bias && co0 < a.cout) b = *reinterpret_cast<const f32x4*>(a.bias + co0);
+  return b;
+}
 
 // Block: 4 waves; wave w owns output channels 16 (4 blockIdx.y + w) + 0..15
 // (waves past COUT only help with staging).  IN_F16 / IN_CHW select the input
@@ -123,6 +239,7 @@ __global__ __launch_bounds__(256, 2) void winograd3x3_kernel(WinogradArgs a) {
     for (int kc = 0; kc < KC; ++kc)
       u[p][kc] = reinterpret_cast<const half8*>(a.U)[((int64_t(p) * KC + kc) * g_n + gu) * 64 + lane];
 
+  const f32x4 bias = wg_lane_bias(a, gu, lane);
   const int64_t per_block = (a.ngroups + gridDim.x - 1) / gridDim.x;
   const int64_t g_begin = int64_t(blockIdx.x) * per_block;
   const int64_t g_end = g_begin + per_block < a.ngroups ? g_begin + per_block : a.ngroups;
@@ -238,96 +355,313 @@ __global__ __launch_bounds__(256, 2) void winograd3x3_kernel(WinogradArgs a) {
     float vn[kPer];
     load_region(more ? grp + 1 : grp, vn);
 
-    if (active) {
-      // ---- 16 channel-reduction GEMMs, inverse transform folded column by
-      // column in the reference's order (_winograd_inv, .h:80-93):
-      //   t0[b] = (M[0][b] + M[1][b]) + M[2][b],  t1[b] = (M[1][b] - M[2][b]) - M[3][b]
-      //   Y[i][0] = (t_i[0] + t_i[1]) + t_i[2],   Y[i][1] = (t_i[1] - t_i[2]) - t_i[3]
-      f32x4 y00, y01, y10, y11;
+    if (active) wg_gemm_store<KC>(u, sv, lane, g, bias, a, img, tr, seg);
+
+    if (more) park_region(vn);
+    __syncthreads();  // sin_ holds the next region; every wave is done with sv
+  }
+}
+
+
+// ------------------------------------------------------------ strip kernel
+// Fast path for NCHW fp16 input with W % 8 == 0 (the benchmark layout).
+//
+// Each block (4 waves, two per CU) walks a vertical strip of one image: 32 output
+// columns (16 tiles) by `rows_per_item` tile rows, top to bottom.  Input rows
+// arrive in LDS by direct global->LDS DMA (global_load_lds_dwordx4: lane l of
+// an instruction writes its 16 bytes at M0 + 16 l) into a ring of 4 row-pair
+// slots (pair k = input rows 2k-1 and 2k, fp16, 48 columns [32 s - 8, 32 s + 40)
+// per channel row); tile row tr reads pairs tr and tr+1, so every input row of
+// the strip is fetched from HBM once, and pairs are requested 3 tile rows
+// ahead without occupying registers.  Chunks outside the image are fetched
+// from a 16-byte zero block.
+//
+// The DMA and the output stores are issued from inline assembly, so the wave's
+// vector-memory stream inside the loop is exactly: the DMAs of one pair (Ld
+// instructions) and the stores of one step (St instructions) per step; the
+// wait for a pair is then an exact s_waitcnt vmcnt(N) for the number of
+// operations issued after it (loads and stores retire in order on gfx9).
+//
+// The V transform is one (tile, 4-channel) unit per thread: 4 x 4 patch reads
+// from the ring (fp16 -> fp32), the reference's fp32 operation order, fp16
+// rounding, and 16 8-byte writes in B-fragment order.
+constexpr int kStripSlots = 3;                 // row-pair ring = prefetch distance
+constexpr int kRowBytes = 96;                  // 48 fp16 columns per staged channel row
+
+__device__ __attribute__((aligned(16))) uint32_t g_wg_zero16[4] = {0u, 0u, 0u, 0u};
+
+// 16-byte global -> LDS DMA for this lane; lds_wave is the wave's LDS base
+// (lane l lands at lds_wave + 16 l).  M0 is saved and restored around it.
+__device__ __forceinline__ void wg_dma16(const void* src, uint32_t lds_wave) {
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %2\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %1, off\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(src), "s"(__builtin_amdgcn_readfirstlane(lds_wave))
+      : "memory");
+}
+
+__device__ __forceinline__ void wg_st32(void* p, uint32_t v) {
+  asm volatile("global_store_dword %0, %1, off nt" ::"v"(p), "v"(v) : "memory");
+}
+__device__ __forceinline__ void wg_st64(void* p, f32x2 v) {
+  asm volatile("global_store_dwordx2 %0, %1, off nt" ::"v"(p), "v"(v) : "memory");
+}
+__device__ __forceinline__ void wg_st128(void* p, f32x4 v) {
+  asm volatile("global_store_dwordx4 %0, %1, off nt\n\ts_nop 0" ::"v"(p), "v"(v) : "memory");
+}
+
+// s_waitcnt vmcnt(n) for a run-time n (clamped to 63); expcnt / lgkmcnt untouched.
+__device__ __forceinline__ void wg_wait_vmcnt(int n) {
+  switch (n < 63 ? (n < 0 ? 0 : n) : 63) {
+#define RDV_WG_CASE(k) \
+  case k:              \
+    asm volatile("s_waitcnt vmcnt(" #k ")" ::: "memory"); \
+    break;
+    RDV_WG_CASE(0) RDV_WG_CASE(1) RDV_WG_CASE(2) RDV_WG_CASE(3) RDV_WG_CASE(4) RDV_WG_CASE(5) RDV_WG_CASE(6)
+    RDV_WG_CASE(7) RDV_WG_CASE(8) RDV_WG_CASE(9) RDV_WG_CASE(10) RDV_WG_CASE(11) RDV_WG_CASE(12) RDV_WG_CASE(13)
+    RDV_WG_CASE(14) RDV_WG_CASE(15) RDV_WG_CASE(16) RDV_WG_CASE(17) RDV_WG_CASE(18) RDV_WG_CASE(19)
+    RDV_WG_CASE(20) RDV_WG_CASE(21) RDV_WG_CASE(22) RDV_WG_CASE(23) RDV_WG_CASE(24) RDV_WG_CASE(25)
+    RDV_WG_CASE(26) RDV_WG_CASE(27) RDV_WG_CASE(28) RDV_WG_CASE(29) RDV_WG_CASE(30) RDV_WG_CASE(31)
+    RDV_WG_CASE(32) RDV_WG_CASE(33) RDV_WG_CASE(34) RDV_WG_CASE(35) RDV_WG_CASE(36) RDV_WG_CASE(37)
+    RDV_WG_CASE(38) RDV_WG_CASE(39) RDV_WG_CASE(40) RDV_WG_CASE(41) RDV_WG_CASE(42) RDV_WG_CASE(43)
+    RDV_WG_CASE(44) RDV_WG_CASE(45) RDV_WG_CASE(46) RDV_WG_CASE(47) RDV_WG_CASE(48) RDV_WG_CASE(49)
+    RDV_WG_CASE(50) RDV_WG_CASE(51) RDV_WG_CASE(52) RDV_WG_CASE(53) RDV_WG_CASE(54) RDV_WG_CASE(55)
+    RDV_WG_CASE(56) RDV_WG_CASE(57) RDV_WG_CASE(58) RDV_WG_CASE(59) RDV_WG_CASE(60) RDV_WG_CASE(61)
+    RDV_WG_CASE(62)
+#undef RDV_WG_CASE
+    default:
+      asm volatile("s_waitcnt vmcnt(63)" ::: "memory");
+      break;
+  }
+}
+
+// Stores of one tile's 2x2 outputs for this lane's 4 channels (after bias /
+// ReLU) through wg_st*: CHW issues 8 instructions, HWC 4.
+__device__ __forceinline__ void wg_store_asm(const f32x4 (&yv)[2][2], const WinogradArgs& a, int img, int co0,
+                                             int oh, int ow) {
+  const int hw = a.H * a.W;
+  if (a.out_layout == RDV_LAYOUT_CHW) {
 #pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        f32x4 ma[4];
+    for (int jj = 0; jj < 4; ++jj)
 #pragma unroll
-        for (int ra = 0; ra < 4; ++ra) {
-          const int p = 4 * ra + b;
-          f32x4 acc = {};
-#pragma unroll
-          for (int kc = 0; kc < KC; ++kc)
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(u[p][kc], sv[(p * KC + kc) * 64 + lane], acc, 0, 0, 0);
-          ma[ra] = acc;
-        }
-        const f32x4 t0 = ma[0] + ma[1] + ma[2];
-        const f32x4 t1 = ma[1] - ma[2] - ma[3];
-        if (b == 0) {
-          y00 = t0;
-          y10 = t1;
-        } else if (b == 1) {
-          y00 += t0;
-          y01 = t0;
-          y10 += t1;
-          y11 = t1;
-        } else if (b == 2) {
-          y00 += t0;
-          y01 -= t0;
-          y10 += t1;
-          y11 -= t1;
+      for (int i = 0; i < 2; ++i) {
+        const int64_t o = (int64_t(img) * a.cout + co0 + jj) * hw + int64_t(oh + i) * a.W + ow;
+        if (a.out_dtype == RDV_DTYPE_F16) {
+          const half2v hv = {half_t(yv[i][0][jj]), half_t(yv[i][1][jj])};
+          wg_st32(static_cast<half_t*>(a.y) + o, __builtin_bit_cast(uint32_t, hv));
         } else {
-          y01 -= t0;
-          y11 -= t1;
+          const f32x2 fv = {yv[i][0][jj], yv[i][1][jj]};
+          wg_st64(static_cast<float*>(a.y) + o, fv);
         }
       }
-      // ---- bias, ReLU, store: lane holds channels 16g + 4(l/16) + jj of tile l%16
-      const int n = lane & 15;
-      const int tc = seg * kWgTiles + n;
-      const int co0 = 16 * g + 4 * (lane >> 4);
-      if (tc < a.W / 2 && co0 < a.cout) {
-        const int oh = 2 * tr, ow = 2 * tc;
-        f32x4 yv[2][2] = {{y00, y01}, {y10, y11}};
+  } else {
 #pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
-          const float bb = a.bias ? a.bias[co0 + jj] : 0.0f;
+    for (int i = 0; i < 2; ++i)
 #pragma unroll
-          for (int i = 0; i < 2; ++i)
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-              float val = yv[i][j][jj] + bb;
-              if (a.relu) val = fmaxf(val, 0.0f);
-              yv[i][j][jj] = val;
-            }
+      for (int j = 0; j < 2; ++j) {
+        const int64_t o = (int64_t(img) * hw + int64_t(oh + i) * a.W + ow + j) * a.cout + co0;
+        if (a.out_dtype == RDV_DTYPE_F16) {
+          const half4 hv = {half_t(yv[i][j][0]), half_t(yv[i][j][1]), half_t(yv[i][j][2]), half_t(yv[i][j][3])};
+          wg_st64(static_cast<half_t*>(a.y) + o, __builtin_bit_cast(f32x2, hv));
+        } else {
+          wg_st128(static_cast<float*>(a.y) + o, yv[i][j]);
         }
-        if (a.out_layout == RDV_LAYOUT_CHW) {
+      }
+  }
+}
+
+template <int KC>
+__global__ __launch_bounds__(256, 2) void winograd3x3_strip_kernel(WinogradArgs a) {
+  constexpr int CH = 32 * KC;                          // staged channels
+  constexpr int kPairChunks = 2 * CH * 6;              // 16-byte chunks per row pair (multiple of 64)
+  constexpr int kLoads = (kPairChunks + 255) / 256;    // DMA rounds per pair
+  constexpr int kSlotBytes = 2 * CH * kRowBytes;
+  constexpr int D = kStripSlots;
+  __shared__ __attribute__((aligned(16))) uint32_t ring[kStripSlots * kSlotBytes / 4];
+  __shared__ half8 sv[16 * KC * 64];
+  const int tid = int(threadIdx.x);
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int g = blockIdx.y * 4 + wave;
+  const bool active = 16 * g < a.cout;
+  const int hw = a.H * a.W;
+  const half_t* __restrict__ x = static_cast<const half_t*>(a.x);
+  const uint32_t ring_lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(ring));
+
+  // this wave's vector-memory operations per pair (DMA) and per step (stores)
+  int Ld = 0;
 #pragma unroll
-          for (int jj = 0; jj < 4; ++jj) {
+  for (int i = 0; i < kLoads; ++i) Ld += (i * 256 + wave * 64 < kPairChunks) ? 1 : 0;
+  const int St = active ? (a.out_layout == RDV_LAYOUT_CHW ? 8 : 4) : 0;
+
+  // DMA of row pair k of strip (img, seg) into ring slot `slot`
+  auto dma_pair = [&](int img, int seg, int k, int slot) {
+    const half_t* base = x + int64_t(img) * a.cin * hw;
 #pragma unroll
-            for (int i = 0; i < 2; ++i) {
-              const int64_t o = (int64_t(img) * a.cout + co0 + jj) * hw + int64_t(oh + i) * a.W + ow;
-              if (a.out_dtype == RDV_DTYPE_F16) {
-                half2v hv = {half_t(yv[i][0][jj]), half_t(yv[i][1][jj])};
-                __builtin_nontemporal_store(hv, reinterpret_cast<half2v*>(static_cast<half_t*>(a.y) + o));
-              } else {
-                f32x2 fv = {yv[i][0][jj], yv[i][1][jj]};
-                __builtin_nontemporal_store(fv, reinterpret_cast<f32x2*>(static_cast<float*>(a.y) + o));
+    for (int i = 0; i < kLoads; ++i) {
+      const int first = i * 256 + wave * 64;  // wave-uniform
+      if (first < kPairChunks) {
+        const int lin = first + lane;
+        const int cc = lin % 6;
+        const int rest = lin / 6;
+        const int ci = rest % CH;
+        const int row = 2 * k - 1 + rest / CH;
+        const int col = 32 * seg - 8 + 8 * cc;
+        const bool ok = (ci < a.cin) & (row >= 0) & (row < a.H) & (col >= 0) & (col < a.W);
+        const void* src = ok ? static_cast<const void*>(base + (ci * a.H + row) * a.W + col)
+                             : static_cast<const void*>(g_wg_zero16);
+        wg_dma16(src, ring_lds + uint32_t(slot * kSlotBytes + first * 16));
+      }
+    }
+  };
+
+  auto decode = [&](int64_t item, int& img, int& seg, int& tr0) {
+    const int chunk = int(item % a.chunks);
+    const int64_t strip = item / a.chunks;
+    seg = int(strip % a.seg);
+    img = int(strip / a.seg);
+    tr0 = chunk * a.rows_per_item;
+  };
+
+  // U and the bias, resident for the whole block, and the first item's first
+  // row pairs; all waited for before the loop so that no compiler-generated
+  // vector-memory wait is left inside it
+  half8 u[16][KC];
+  const int g_n = (a.cout + 15) / 16;
+  const int gu = active ? g : 0;
+#pragma unroll
+  for (int p = 0; p < 16; ++p)
+#pragma unroll
+    for (int kc = 0; kc < KC; ++kc)
+      u[p][kc] = reinterpret_cast<const half8*>(a.U)[((int64_t(p) * KC + kc) * g_n + gu) * 64 + lane];
+  const f32x4 bias = wg_lane_bias(a, gu, lane);
+  if (int64_t(blockIdx.x) < a.items) {
+    int img, seg, tr0;
+    decode(blockIdx.x, img, seg, tr0);
+    const int R = min(a.rows_per_item, a.th - tr0);
+    for (int q = 0; q < min(D, R + 1); ++q) dma_pair(img, seg, tr0 + q, q);
+  }
+#pragma unroll
+  for (int p = 0; p < 16; ++p)
+#pragma unroll
+    for (int kc = 0; kc < KC; ++kc) asm volatile("" ::"v"(u[p][kc]));
+  asm volatile("" ::"v"(bias));
+  wg_wait_vmcnt(0);
+  __syncthreads();
+
+  for (int64_t item = blockIdx.x; item < a.items; item += gridDim.x) {
+    int img, seg, tr0;
+    decode(item, img, seg, tr0);
+    const int R = min(a.rows_per_item, a.th - tr0);  // tile rows of this item (>= 1); pairs 0..R
+    const int P = min(D, R + 1);                     // pairs requested up front
+    if (item != int64_t(blockIdx.x))
+      for (int q = 0; q < P; ++q) dma_pair(img, seg, tr0 + q, q);
+
+    for (int j = 0; j < R; ++j) {
+      const int tr = tr0 + j;
+      // ---- wait until pairs j and j+1 are in LDS (this wave's DMAs), then for every wave
+      {
+        int after;
+        if (j + 1 < P) {
+          const int hi = min(j - 1, R - D);
+          after = Ld * (P - j - 2) + St * j + Ld * (hi >= 0 ? hi + 1 : 0);
+        } else {
+          const int lo = j + 2 - D, hi = min(j - 1, R - D);
+          after = St * (D - 1) + Ld * (hi >= lo ? hi - lo + 1 : 0);
+        }
+        wg_wait_vmcnt(after);
+      }
+      __syncthreads();
+
+      // ---- V = B^T d B per (tile, 4 channels)
+      {
+        const int n = tid & 15;
+        const int qd = tid >> 4;
+        if (qd < CH / 4) {
+          const int sa = j % D, sb = (j + 1) % D;
+          half4 hv[16];
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            const int ci = 4 * qd + c;
+            float d[4][4];
+#pragma unroll
+            for (int dr = 0; dr < 4; ++dr) {
+              const uint32_t* row = ring + ((dr < 2 ? sa : sb) * kSlotBytes + ((dr & 1) * CH + ci) * kRowBytes) / 4;
+              // columns 2n-1 .. 2n+2 of the tile = halves 2n+7 .. 2n+10 of the staged row
+              const uint32_t w0 = row[n + 3], w1 = row[n + 4], w2 = row[n + 5];
+              const half2v h0 = __builtin_bit_cast(half2v, w0);
+              const half2v h1 = __builtin_bit_cast(half2v, w1);
+              const half2v h2 = __builtin_bit_cast(half2v, w2);
+              d[dr][0] = float(h0[1]);
+              d[dr][1] = float(h1[0]);
+              d[dr][2] = float(h1[1]);
+              d[dr][3] = float(h2[0]);
+            }
+            float m[4][4];
+#pragma unroll
+            for (int cj = 0; cj < 4; ++cj) {
+              m[0][cj] = d[0][cj] - d[2][cj];
+              m[1][cj] = d[1][cj] + d[2][cj];
+              m[2][cj] = d[2][cj] - d[1][cj];
+              m[3][cj] = d[1][cj] - d[3][cj];
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              float vv[4];
+              vv[0] = m[r][0] - m[r][2];
+              vv[1] = m[r][1] + m[r][2];
+              vv[2] = m[r][2] - m[r][1];
+              vv[3] = m[r][1] - m[r][3];
+#pragma unroll
+              for (int b = 0; b < 4; ++b) {
+                float v = vv[b];
+                asm volatile("" : "+v"(v));  // fp32 result first, then fp16 (no fused fma_mix rounding)
+                hv[4 * r + b][c] = half_t(v);
               }
             }
           }
-        } else {
+          const int ci0 = 4 * qd;
+          const int kc = ci0 / 32, k = ci0 % 32;
+          const int flane = (k / 8) * 16 + n, j0 = k % 8;
+#pragma unroll
+          for (int p = 0; p < 16; ++p)
+            *reinterpret_cast<half4*>(reinterpret_cast<half_t*>(&sv[(p * KC + kc) * 64 + flane]) + j0) = hv[p];
+        }
+      }
+      __syncthreads();  // sv complete; every wave is done with the slot of pair j
+
+      // ---- request pair j + D into the slot pair j used
+      if (j + D <= R) dma_pair(img, seg, tr0 + j + D, j % D);
+
+      // ---- GEMMs, inverse transform, bias / ReLU, stores
+      if (active) {
+        f32x4 yv[2][2];
+        wg_gemm(u, sv, lane, yv);
+        const int n = lane & 15;
+        const int tc = seg * kWgTiles + n;
+        const int co0 = 16 * g + 4 * (lane >> 4);
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj)
 #pragma unroll
           for (int i = 0; i < 2; ++i)
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
-              const int64_t o = (int64_t(img) * hw + int64_t(oh + i) * a.W + ow + j) * a.cout + co0;
-              if (a.out_dtype == RDV_DTYPE_F16) {
-                half4 hv = {half_t(yv[i][j][0]), half_t(yv[i][j][1]), half_t(yv[i][j][2]), half_t(yv[i][j][3])};
-                __builtin_nontemporal_store(hv, reinterpret_cast<half4*>(static_cast<half_t*>(a.y) + o));
-              } else {
-                __builtin_nontemporal_store(yv[i][j], reinterpret_cast<f32x4*>(static_cast<float*>(a.y) + o));
-              }
+            for (int jx = 0; jx < 2; ++jx) {
+              float val = yv[i][jx][jj] + bias[jj];
+              if (a.relu) val = fmaxf(val, 0.0f);
+              yv[i][jx][jj] = val;
             }
-        }
+        if (tc < a.W / 2) wg_store_asm(yv, a, img, co0, 2 * tr, 2 * tc);
       }
     }
-    if (more) park_region(vn);
-    __syncthreads();  // sin_ holds the next region; every wave is done with sv
+    // all of this item's DMAs have landed (the last step waited for pair R)
+    // and every wave is past its last read of the ring before the next item's
+    // DMAs overwrite it
+    __syncthreads();
   }
 }
 
@@ -372,10 +706,25 @@ int launch_winograd3x3(const rdv_conv_desc& d, const void* x, const void* U, con
   if (a.ngroups == 0) return RDV_OK;
   const int groups16 = (d.cout + 15) / 16;
   const int slices = (groups16 + 3) / 4;  // 64-channel slices (grid y)
+  const bool f16 = d.in_dtype == RDV_DTYPE_F16, chw = d.in_layout == RDV_LAYOUT_CHW;
+  if (f16 && chw && d.W % 8 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0) {
+    // strip kernel: one block per CU, each walking rows_per_item tile rows of a strip
+    const int64_t strips = int64_t(d.batch) * a.seg;
+    const int64_t target = std::max<int64_t>(1, 2 * di.cu_count / slices);  // two blocks per CU
+    const int64_t per_strip = std::max<int64_t>(1, target / strips);
+    a.rows_per_item = int((a.th + per_strip - 1) / per_strip);
+    a.chunks = (a.th + a.rows_per_item - 1) / a.rows_per_item;
+    a.items = strips * a.chunks;
+    const int64_t blocks = std::min<int64_t>(a.items, std::max<int64_t>(target, 1));
+    const dim3 grid(static_cast<unsigned>(blocks), static_cast<unsigned>(slices)), block(256);
+    if (d.cin <= 32) winograd3x3_strip_kernel<1><<<grid, block, 0, stream>>>(a);
+    else winograd3x3_strip_kernel<2><<<grid, block, 0, stream>>>(a);
+    RDV_HIP_TRY(hipGetLastError());
+    return RDV_OK;
+  }
   int64_t blocks = (2 * int64_t(di.cu_count) + slices - 1) / slices;  // ~2 resident blocks per CU
   if (a.ngroups < blocks) blocks = a.ngroups;
   const dim3 grid(static_cast<unsigned>(blocks), static_cast<unsigned>(slices)), block(256);
-  const bool f16 = d.in_dtype == RDV_DTYPE_F16, chw = d.in_layout == RDV_LAYOUT_CHW;
   if (d.cin <= 32) {
     if (f16) {
       if (chw) winograd3x3_kernel<1, true, true><<<grid, block, 0, stream>>>(a);

@@ -164,6 +164,26 @@ def test_shapes_layouts_and_types(N, H, W, C, K, inl, ind, outl, outd, relu, bia
         _check_direct(y[i], O.direct_conv(x[i], w, b, relu=relu), f"image {i}")
 
 
+@pytest.mark.parametrize("N,H,W,C,K,outl,outd,relu", [
+    (2, 10, 40, 64, 48, _lib.LAYOUT_CHW, _lib.DTYPE_F16, True),
+    (1, 2, 8, 17, 16, _lib.LAYOUT_CHW, _lib.DTYPE_F32, False),
+    (3, 6, 72, 40, 112, _lib.LAYOUT_HWC, _lib.DTYPE_F16, True),
+    (1, 34, 24, 64, 80, _lib.LAYOUT_HWC, _lib.DTYPE_F32, False),
+    (1, 130, 16, 32, 64, _lib.LAYOUT_CHW, _lib.DTYPE_F16, False),
+])
+def test_strip_path_nchw_f16(N, H, W, C, K, outl, outd, relu):
+    """NCHW fp16 input with W % 8 == 0 (the path of the benchmark configuration):
+    partial strips, several images, one-row items, channel padding, every output form."""
+    rng = np.random.default_rng(N * 131 + H * 17 + W + C + K)
+    x = O.f16(rng.uniform(-1, 1, (N, H, W, C)).astype(np.float32))
+    w = rng.normal(0, 0.1, (3, 3, C, K)).astype(np.float32)
+    b = rng.normal(0, 0.5, K).astype(np.float32)
+    y = _run(x, w, b, _lib.LAYOUT_CHW, _lib.DTYPE_F16, outl, outd, relu, batch=N)
+    for i in range(N):
+        ref = O.winograd_conv(x[i], w, b, relu=relu)
+        _check_close(y[i], ref, f"image {i}", f16_out=outd == _lib.DTYPE_F16)
+
+
 def test_c3_full_config():
     """The benchmark configuration: NCHW fp16 1x64x256x256, 64 -> 64, zero bias, ReLU, fp16 out."""
     x, w, b = WL.c3()
