@@ -162,6 +162,50 @@ int rdv_winograd3x3_transform_weight(const void* w, int32_t w_layout, int32_t w_
 int rdv_winograd3x3_forward(const rdv_conv_desc* desc, const void* x, const void* U, const float* bias,
                             void* y, void* stream);
 
+/* ------------------------------------------------ cameras and volume rendering */
+typedef struct rdv_camera_desc {
+  int32_t n_cams;       /* poses rows                                             */
+  int32_t width, height;
+  float aspect_ratio;   /* reference default width / height                       */
+  float fov;            /* vertical field of view in radians (reference default pi/4) */
+} rdv_camera_desc;
+
+/* rays[n, H, W, 6] = (origin, unit direction) of the pinhole camera ray through
+ * each pixel centre; poses is a device [n, 9] fp32 array (origin | target | up).
+ * Replaces Cameras' grid dispatch (src/rdv/domain/rendering.py:10-42,
+ * src/rdv/shaders/rendering/cameras.h:1-20); pixel jitter is not supported. */
+int rdv_cameras_rays(const rdv_camera_desc* cam, const float* poses, float* rays, void* stream);
+
+/* Emission-absorption render of a density / RGB field (build-defined; no
+ * reference counterpart): for every pixel ray of `cam` that meets [-1,1]^3 on
+ * [t0, t1] (t0 >= 0), `samples` points t_i = t0 + (i + 1/2) dt, dt = (t1 - t0) /
+ * samples, are evaluated by `field` (3 -> 64 -> 64 -> 64 -> 4 LinearFast chain,
+ * ReLU hidden, raw head; sigma = softplus(o0), c = sigmoid(o1..3)) and composited
+ * front to back: alpha_i = 1 - exp(-sigma_i dt), T_i = prod_{j<i} (1 - alpha_j),
+ * image = sum_i T_i alpha_i c_i (0 for rays that miss).  image: device
+ * [n, H, W, 3] fp32.  samples: a positive multiple of 32. */
+int rdv_render_emission_absorption(const rdv_camera_desc* cam, const float* poses, const rdv_mlp_desc* field,
+                                   const void* packed, int32_t samples, float* image, void* stream);
+
+/* The same compositing over precomputed samples (build-defined):
+ * sigma_rgb[n_rays, samples, 4] = (sigma, r, g, b), dt[n_rays] the sample
+ * spacing of each ray (0 for rays that miss), out[n_rays, 3]. */
+int rdv_composite(const float* sigma_rgb, const float* dt, int64_t n_rays, int32_t samples, float* out,
+                  void* stream);
+
+/* out[n] = transmittance along each ray rays[n, 6] = (x, w) through the box
+ * [-1,1]^3 in the object space of transform (mat4x3, column-major: three linear
+ * columns then the translation, 12 floats on the host), marched with fixed
+ * steps of step_size: tau += extinction(x) * density_scale * step_size, 0 once
+ * tau > 16, exp(-tau) at the end (1 for rays that miss).  extinction: a
+ * 3 -> 64 -> 64 -> 64 -> 1 LinearFast chain with ReLU hidden activations.
+ * Replaces RaymarchingTransmittance (src/rdv/domain/volumes.py:124-141,
+ * src/rdv/shaders/volumes/raymarching_transmittance.h:1-22,
+ * raymarching_transmittance_trait.h:1-14, libraries/math_library.h:48-57). */
+int rdv_raymarch_transmittance(const rdv_mlp_desc* extinction, const void* packed, const float* rays,
+                               int64_t n_rays, const float* transform12, float step_size, float density_scale,
+                               float* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

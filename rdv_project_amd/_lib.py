@@ -59,6 +59,17 @@ class ConvDesc(C.Structure):
     ]
 
 
+class CameraDesc(C.Structure):
+    """Mirror of rdv_camera_desc."""
+    _fields_ = [
+        ("n_cams", C.c_int32),
+        ("width", C.c_int32),
+        ("height", C.c_int32),
+        ("aspect_ratio", C.c_float),
+        ("fov", C.c_float),
+    ]
+
+
 class RDVError(RuntimeError):
     """A HIP runtime failure reported by the library."""
 
@@ -75,6 +86,12 @@ _SIGNATURES = {
     "rdv_mlp_forward_f16_all": (C.c_int, [C.POINTER(MlpDesc), C.c_void_p, C.c_void_p, C.c_void_p, C.c_int64,
                                           C.c_void_p]),
     "rdv_mlp_kernel_name": (C.c_char_p, [C.POINTER(MlpDesc)]),
+    "rdv_cameras_rays": (C.c_int, [C.POINTER(CameraDesc), C.c_void_p, C.c_void_p, C.c_void_p]),
+    "rdv_render_emission_absorption": (C.c_int, [C.POINTER(CameraDesc), C.c_void_p, C.POINTER(MlpDesc), C.c_void_p,
+                                                 C.c_int32, C.c_void_p, C.c_void_p]),
+    "rdv_composite": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int64, C.c_int32, C.c_void_p, C.c_void_p]),
+    "rdv_raymarch_transmittance": (C.c_int, [C.POINTER(MlpDesc), C.c_void_p, C.c_void_p, C.c_int64,
+                                             C.POINTER(C.c_float), C.c_float, C.c_float, C.c_void_p, C.c_void_p]),
     "rdv_winograd3x3_validate": (C.c_int, [C.POINTER(ConvDesc)]),
     "rdv_winograd3x3_weight_bytes": (C.c_int64, [C.c_int32, C.c_int32]),
     "rdv_winograd3x3_transform_weight": (C.c_int, [C.c_void_p, C.c_int32, C.c_int32, C.c_int32, C.c_int32,

@@ -26,6 +26,7 @@ SOURCES = [
     "mlp_f32.hip",
     "mlp_fused.hip",
     "winograd.hip",
+    "render.hip",
 ]
 
 ARCH = os.environ.get("RDV_OFFLOAD_ARCH", "gfx950")

@@ -56,6 +56,14 @@ int prepare_chain_f32(const rdv_mlp_desc& d);
 int64_t winograd_weight_bytes(int cin, int cout);
 int launch_winograd_transform_weight(const void* w, int w_layout, int w_dtype, int cin, int cout, void* U,
                                      hipStream_t stream);
+int launch_camera_rays(const rdv_camera_desc& c, const float* poses, float* rays, hipStream_t stream);
+int launch_render_ea(const rdv_camera_desc& c, const float* poses, const rdv_mlp_desc& d, const MlpLayout& lay,
+                     const void* packed, int samples, float* image, hipStream_t stream);
+int launch_composite(const float* sigma_rgb, const float* dts, int64_t nrays, int samples, float* out,
+                     hipStream_t stream);
+int launch_raymarch_transmittance(const rdv_mlp_desc& d, const MlpLayout& lay, const void* packed, const float* rays,
+                                  int64_t nrays, const float* transform12, float step, float density_scale,
+                                  float* out, hipStream_t stream);
 int launch_winograd3x3(const rdv_conv_desc& d, const void* x, const void* U, const float* bias, void* y,
                        hipStream_t stream);
 
@@ -225,6 +233,60 @@ int rdv_winograd3x3_forward(const rdv_conv_desc* desc, const void* x, const void
   const size_t oal = desc->out_dtype == RDV_DTYPE_F16 ? 8 : 16;
   if (reinterpret_cast<uintptr_t>(y) % oal) return fail(RDV_ERR_INVALID, "y is not aligned for vector stores");
   return launch_winograd3x3(*desc, x, U, bias, y, static_cast<hipStream_t>(stream));
+}
+
+static int check_camera(const rdv_camera_desc* c) {
+  if (!c) return fail(RDV_ERR_INVALID, "camera descriptor is NULL");
+  if (c->n_cams < 1 || c->width < 1 || c->height < 1)
+    return fail(RDV_ERR_INVALID, "cameras need n_cams, width and height >= 1");
+  if (int64_t(c->n_cams) * c->width * c->height > (int64_t(1) << 40)) return fail(RDV_ERR_INVALID, "too many rays");
+  if (!(c->fov > 0.0f && c->fov < 3.14159265f)) return fail(RDV_ERR_INVALID, "fov must be in (0, pi)");
+  if (!(c->aspect_ratio > 0.0f)) return fail(RDV_ERR_INVALID, "aspect_ratio must be > 0");
+  return RDV_OK;
+}
+
+int rdv_cameras_rays(const rdv_camera_desc* cam, const float* poses, float* rays, void* stream) {
+  int rc = check_camera(cam);
+  if (rc != RDV_OK) return rc;
+  if (!poses || !rays) return fail(RDV_ERR_INVALID, "rdv_cameras_rays: NULL pointer argument");
+  return launch_camera_rays(*cam, poses, rays, static_cast<hipStream_t>(stream));
+}
+
+int rdv_render_emission_absorption(const rdv_camera_desc* cam, const float* poses, const rdv_mlp_desc* field,
+                                   const void* packed, int32_t samples, float* image, void* stream) {
+  int rc = check_camera(cam);
+  if (rc != RDV_OK) return rc;
+  MlpLayout lay;
+  rc = check_mlp(field, &lay);
+  if (rc != RDV_OK) return rc;
+  if (samples < 32 || samples % 32 || samples > (1 << 20))
+    return fail(RDV_ERR_INVALID, "samples must be a positive multiple of 32 (at most 2^20)");
+  if (!poses || !packed || !image) return fail(RDV_ERR_INVALID, "rdv_render_emission_absorption: NULL pointer argument");
+  return launch_render_ea(*cam, poses, *field, lay, packed, samples, image, static_cast<hipStream_t>(stream));
+}
+
+int rdv_composite(const float* sigma_rgb, const float* dt, int64_t n_rays, int32_t samples, float* out,
+                  void* stream) {
+  if (n_rays < 0 || samples < 1) return fail(RDV_ERR_INVALID, "rdv_composite: n_rays >= 0 and samples >= 1 required");
+  if (n_rays == 0) return RDV_OK;
+  if (!sigma_rgb || !dt || !out) return fail(RDV_ERR_INVALID, "rdv_composite: NULL pointer argument");
+  if (reinterpret_cast<uintptr_t>(sigma_rgb) % 16) return fail(RDV_ERR_INVALID, "sigma_rgb must be 16-byte aligned");
+  return launch_composite(sigma_rgb, dt, n_rays, samples, out, static_cast<hipStream_t>(stream));
+}
+
+int rdv_raymarch_transmittance(const rdv_mlp_desc* extinction, const void* packed, const float* rays,
+                               int64_t n_rays, const float* transform12, float step_size, float density_scale,
+                               float* out, void* stream) {
+  MlpLayout lay;
+  int rc = check_mlp(extinction, &lay);
+  if (rc != RDV_OK) return rc;
+  if (n_rays < 0) return fail(RDV_ERR_INVALID, "n_rays must be >= 0");
+  if (!(step_size > 0.0f)) return fail(RDV_ERR_INVALID, "step_size must be > 0");
+  if (!transform12) return fail(RDV_ERR_INVALID, "transform is NULL");
+  if (n_rays == 0) return RDV_OK;
+  if (!packed || !rays || !out) return fail(RDV_ERR_INVALID, "rdv_raymarch_transmittance: NULL pointer argument");
+  return launch_raymarch_transmittance(*extinction, lay, packed, rays, n_rays, transform12, step_size, density_scale,
+                                       out, static_cast<hipStream_t>(stream));
 }
 
 const char* rdv_mlp_kernel_name(const rdv_mlp_desc* desc) {

@@ -1,0 +1,240 @@
+// Device-side core of the fused fp16 MLP: the compile-time network shape, the
+// layer-0 input fragments (raw or frequency-encoded), the MFMA layer chain with
+// the D -> B fragment hand-off, and the output heads.  Shared by the fused MLP
+// kernel (mlp_fused.hip) and the MLP-in-the-loop renderer (render.hip).
+//
+// Fragment layout (mlp_layout.h): v_mfma_f32_32x32x16_f16 with the transposed
+// formulation H^T = W X^T, 32 points per N block; lane l holds point l % 32 and
+// feature half h = l / 32 of every K chunk.
+#ifndef RDV_MLP_CORE_H
+#define RDV_MLP_CORE_H
+
+#include "mlp_layout.h"
+#include "rdv_common.h"
+
+namespace rdv {
+
+template <int ENC, int IN, int OCT, int OUT, int KC0, int... MT>
+struct Net {
+  static constexpr int kEnc = ENC, kIn = IN, kOct = OCT, kOut = OUT;
+  static constexpr int kL = sizeof...(MT);
+  static constexpr int kMT[kL] = {MT...};
+  static constexpr int mt(int l) { return kMT[l]; }
+  static constexpr int kc(int l) { return l == 0 ? KC0 : 2 * kMT[l - 1]; }
+  static constexpr int frag_base(int l) {
+    int s = 0;
+    for (int i = 0; i < l; ++i) s += kc(i) * mt(i);
+    return s;
+  }
+  static constexpr int bias_base(int l) {
+    int s = 0;
+    for (int i = 0; i < l; ++i) s += 32 * mt(i);
+    return s;
+  }
+  static constexpr int max_mt() {
+    int m = 0;
+    for (int i = 0; i < kL; ++i) m = mt(i) > m ? mt(i) : m;
+    return m;
+  }
+  static constexpr int max_kc() {
+    int m = 0;
+    for (int i = 0; i < kL; ++i) m = kc(i) > m ? kc(i) : m;
+    return m;
+  }
+  static constexpr int kFrags = frag_base(kL);
+  static constexpr int kBias = bias_base(kL);
+  static constexpr int kMaxMT = max_mt();
+  static constexpr int kMaxKC = max_kc();
+};
+
+// ----------------------------------------------------------------- input
+// Builds layer 0's B fragments for this lane's point from its raw input p.
+template <class N>
+__device__ __forceinline__ void build_input(const float (&p)[N::kIn], int h, half8 (&b)[N::kMaxKC]) {
+  constexpr int D = N::kIn;
+  if constexpr (N::kEnc == RDV_ENC_FREQ) {
+    constexpr int L = N::kOct;
+    constexpr int H0 = (L + 1) / 2;  // octaves of half 0 (freq_octaves_half0)
+    constexpr int H1 = L - H0;
+    // First octave of this lane half from the hardware sine/cosine, the rest by
+    // the double-angle recurrence sin 2x = 2 sin x cos x, cos 2x = 1 - 2 sin^2 x
+    // (3 VALU ops per octave instead of two quarter-rate transcendentals).
+    // v_sin/v_cos take revolutions: sin(2^k pi p) = sin(2 pi * 2^(k-1) p), and
+    // the power-of-two scale is exact.  Two doublings grow the ~1e-7 absolute
+    // error of v_sin/v_cos to a few 1e-7, far below the fp16 rounding applied next.
+    float sn[D][H0], cs[D][H0];
+    const float scale = h ? __builtin_ldexpf(1.0f, H0 - 1) : 0.5f;
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      const float arg = scale * p[d];
+      sn[d][0] = __builtin_amdgcn_sinf(arg);
+      cs[d][0] = __builtin_amdgcn_cosf(arg);
+#pragma unroll
+      for (int i = 1; i < H0; ++i) {
+        const float u = sn[d][i - 1] + sn[d][i - 1];
+        sn[d][i] = u * cs[d][i - 1];
+        cs[d][i] = __builtin_fmaf(-u, sn[d][i - 1], 1.0f);
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < N::kc(0); ++c) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int s = 8 * c + j;
+        float v = 0.0f;
+        if (s < 2 * D * H0) {
+          const int i = s / (2 * D), r = s % (2 * D);
+          const bool is_cos = r >= D;
+          const int d = is_cos ? r - D : r;
+          v = is_cos ? cs[d][i] : sn[d][i];
+          if (i >= H1) v = h ? 0.0f : v;
+        } else if (s < 2 * D * H0 + D) {
+          v = h ? 0.0f : p[s - 2 * D * H0];
+        }
+        b[c][j] = half_t(v);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int c = 0; c < N::kc(0); ++c) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int f0 = 16 * c + j, f1 = 16 * c + 8 + j;
+        const float v0 = f0 < D ? p[f0 < D ? f0 : 0] : 0.0f;
+        const float v1 = f1 < D ? p[f1 < D ? f1 : 0] : 0.0f;
+        b[c][j] = half_t(h ? v1 : v0);
+      }
+    }
+  }
+}
+
+// ----------------------------------------------------------------- layers
+// Accumulators of layer l start at its bias: rows 32t + 8q + 4h + 0..3 of D are
+// contiguous in the padded bias, one ds_read_b128 each.
+template <class N, int l>
+__device__ __forceinline__ void load_bias(f32x16 (&acc)[N::kMaxMT], const float* sb, int h) {
+#pragma unroll
+  for (int t = 0; t < N::mt(l); ++t) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const f32x4 bv = *reinterpret_cast<const f32x4*>(sb + N::bias_base(l) + 32 * t + 8 * q + 4 * h);
+      acc[t][4 * q + 0] = bv[0];
+      acc[t][4 * q + 1] = bv[1];
+      acc[t][4 * q + 2] = bv[2];
+      acc[t][4 * q + 3] = bv[3];
+    }
+  }
+}
+
+// Where a wave's A fragments live: VGPRs for the life of the wave, or the
+// block's LDS copy (fragment f is a conflict-free 1 KiB line, one
+// ds_read_b128 per lane, read right before its MFMA).
+template <class N>
+struct RegWeights {
+  half8 w[N::kFrags];
+  __device__ __forceinline__ half8 get(int f) const { return w[f]; }
+};
+struct LdsWeights {
+  const half8* sw;  // fragment f at sw[f * 64 + lane]
+  int lane;
+  __device__ __forceinline__ half8 get(int f) const { return sw[f * 64 + lane]; }
+};
+
+// BIAS: the accumulators were seeded with the bias; otherwise the first K
+// chunk starts from MFMA's zero C operand (all biases zero: nothing to load).
+template <class N, int l, bool BIAS, class WS>
+__device__ __forceinline__ void mfma_layer(const WS& ws, const half8 (&b)[N::kMaxKC], f32x16 (&acc)[N::kMaxMT]) {
+  const f32x16 zero = {};
+#pragma unroll
+  for (int c = 0; c < N::kc(l); ++c) {
+#pragma unroll
+    for (int t = 0; t < N::mt(l); ++t) {
+      const f32x16& cin = (BIAS || c > 0) ? acc[t] : zero;
+      acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ws.get(N::frag_base(l) + t * N::kc(l) + c), b[c], cin, 0, 0, 0);
+    }
+  }
+}
+
+// D registers of layer l -> B fragments of layer l + 1 (hidden activations are
+// all ReLU or all none on this path; the dispatcher routes anything else to the
+// generic kernel).
+template <class N, int l, bool RELU>
+__device__ __forceinline__ void to_next(const f32x16 (&acc)[N::kMaxMT], half8 (&b)[N::kMaxKC]) {
+  const half8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+  for (int t = 0; t < N::mt(l); ++t) {
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      half8 v;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = half_t(acc[t][8 * q + j]);
+      // max after the fp16 rounding equals rounding after max (rounding is monotone)
+      if constexpr (RELU) v = __builtin_elementwise_max(v, zero);
+      b[2 * t + q] = v;
+    }
+  }
+}
+
+// Layer l accumulates into `cur` (already holding its bias) while the next
+// layer's bias is read into `nxt`; the two sets alternate down the chain, so
+// every LDS read has a whole layer of matrix work to hide behind.  The last
+// layer's result ends in acc set (kL - 1) % 2.
+template <class N, int l, bool RELU, bool BIAS, class WS>
+__device__ __forceinline__ void run_chain(const WS& ws, half8 (&b)[N::kMaxKC], f32x16 (&cur)[N::kMaxMT],
+                                          f32x16 (&nxt)[N::kMaxMT], const float* sb, int h) {
+  if constexpr (BIAS) {
+    if constexpr (l + 1 < N::kL) load_bias<N, l + 1>(nxt, sb, h);
+    // keep the machine scheduler from sinking those reads back to their use
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  mfma_layer<N, l, BIAS>(ws, b, cur);
+  if constexpr (l + 1 < N::kL) {
+    to_next<N, l, RELU>(cur, b);
+    run_chain<N, l + 1, RELU, BIAS>(ws, b, nxt, cur, sb, h);
+  }
+}
+
+// Output activation of the last layer (compile-time so that the unused heads
+// cost nothing).  The transcendental heads use the hardware exp2/log2/rcp.
+template <int ACT>
+__device__ __forceinline__ float head_act(int channel, float v) {
+  if constexpr (ACT == RDV_ACT_RELU) return fmaxf(v, 0.0f);
+  else if constexpr (ACT == RDV_ACT_SOFTPLUS) return fast_softplus(v);
+  else if constexpr (ACT == RDV_ACT_SIGMOID) return fast_sigmoid(v);
+  else if constexpr (ACT == RDV_ACT_DENSITY_RGB) return channel == 0 ? fast_softplus(v) : fast_sigmoid(v);
+  else return v;
+}
+
+// Stores the head values of one row (rows 32t + 8q + 4h + 0..3 of the last D).
+template <class N>
+__device__ __forceinline__ void store_head(float* __restrict__ yr, const f32x4 (&v)[N::mt(N::kL - 1)][4], int h) {
+#pragma unroll
+  for (int t = 0; t < N::mt(N::kL - 1); ++t) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int r0 = 32 * t + 8 * q + 4 * h;
+      if (r0 < N::kOut) {
+        if constexpr (N::kOut % 4 == 0) {
+          // streaming (non-temporal) store: the output is not re-read by this kernel
+          __builtin_nontemporal_store(v[t][q], reinterpret_cast<f32x4*>(yr + r0));
+        } else {
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj)
+            if (r0 + jj < N::kOut) __builtin_nontemporal_store(v[t][q][jj], yr + r0 + jj);
+        }
+      }
+    }
+  }
+}
+
+// ----------------------------------------------------------------- kernel
+// A zero the compiler cannot see through, re-materialised per loop iteration.
+__device__ __forceinline__ int opaque_zero() {
+  int z = 0;
+  asm volatile("" : "+s"(z));
+  return z;
+}
+
+}  // namespace rdv
+
+#endif  // RDV_MLP_CORE_H

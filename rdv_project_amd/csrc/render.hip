@@ -1,0 +1,517 @@
+// Camera rays, MLP-in-the-loop volume rendering and compositing.
+//
+//  - camera_rays_kernel: Cameras (src/rdv/domain/rendering.py:10-42,
+//    src/rdv/shaders/rendering/cameras.h:1-20), one thread per (cam, y, x).
+//  - render_ea_kernel: build-defined emission-absorption renderer of the
+//    benchmark configuration: per pixel ray through the box [-1,1]^3, S samples
+//    t_i = t0 + (i + 1/2) dt, dt = (t1 - t0) / S, each fed through the fused
+//    fp16 MLP (density / RGB head), composited front to back in fp32:
+//    alpha_i = 1 - exp(-sigma_i dt), T_i = prod_{j<i} (1 - alpha_j),
+//    C = sum_i T_i alpha_i c_i.
+//  - composite_kernel: the same compositing over precomputed samples
+//    (sigma, r, g, b) streamed from HBM.
+//  - raymarch_transmittance_kernel: RaymarchingTransmittance
+//    (src/rdv/domain/volumes.py:124-141, shaders/volumes/raymarching_transmittance.h,
+//    raymarching_transmittance_trait.h, libraries/math_library.h:48-57) with
+//    the extinction map evaluated on the matrix cores 32 march steps at a time.
+//
+// MLP-in-the-loop mapping: one wave owns one ray at a time; a 32-sample chunk
+// of the ray is one MFMA N block (lane l evaluates sample l % 32, both feature
+// halves), so the layer chain is exactly the fused MLP kernel's.  The samples'
+// positions are generated in registers and the head values never leave the
+// wave: transmittance along the chunk is an inclusive wavefront scan of
+// sigma * dt (T_i = T_in exp(-sum_{j<i} sigma_j dt)), the colour a per-lane
+// partial sum reduced once per ray.
+#include "mlp_core.h"
+
+namespace rdv {
+
+struct CameraParams {
+  const float* poses;  // [n, 9]: origin, target, up
+  int n, H, W;
+  float aspect, fov;
+};
+
+// cameras.h: pixel centre p = ((x, y) + 0.5) / (W, H) * 2 - 1, s = (p.x * aspect,
+// p.y, 1 / tan(fov / 2)), frame z = normalize(target - origin),
+// x = normalize(cross(up, z)), y = cross(z, x), w = normalize(s.x x + s.y y + s.z z).
+__device__ __forceinline__ void camera_ray(const CameraParams& c, int cam, int y, int x, float (&o)[3],
+                                           float (&w)[3]) {
+  const float* P = c.poses + int64_t(cam) * 9;
+  float t[3], n[3];
+#pragma unroll
+  for (int i = 0; i < 3; ++i) {
+    o[i] = P[i];
+    t[i] = P[3 + i];
+    n[i] = P[6 + i];
+  }
+  const float px = (float(x) + 0.5f) / float(c.W) * 2.0f - 1.0f;
+  const float py = (float(y) + 0.5f) / float(c.H) * 2.0f - 1.0f;
+  const float sx = px * c.aspect, sy = py, sz = 1.0f / tanf(c.fov * 0.5f);
+  float z[3] = {t[0] - o[0], t[1] - o[1], t[2] - o[2]};
+  float inv = 1.0f / sqrtf(z[0] * z[0] + z[1] * z[1] + z[2] * z[2]);
+#pragma unroll
+  for (int i = 0; i < 3; ++i) z[i] *= inv;
+  float xa[3] = {n[1] * z[2] - n[2] * z[1], n[2] * z[0] - n[0] * z[2], n[0] * z[1] - n[1] * z[0]};
+  inv = 1.0f / sqrtf(xa[0] * xa[0] + xa[1] * xa[1] + xa[2] * xa[2]);
+#pragma unroll
+  for (int i = 0; i < 3; ++i) xa[i] *= inv;
+  const float ya[3] = {z[1] * xa[2] - z[2] * xa[1], z[2] * xa[0] - z[0] * xa[2], z[0] * xa[1] - z[1] * xa[0]};
+#pragma unroll
+  for (int i = 0; i < 3; ++i) w[i] = xa[i] * sx + ya[i] * sy + z[i] * sz;
+  inv = 1.0f / sqrtf(w[0] * w[0] + w[1] * w[1] + w[2] * w[2]);
+#pragma unroll
+  for (int i = 0; i < 3; ++i) w[i] *= inv;
+}
+
+// math_library.h:48-57: slab test against [-1, 1]^3.
+__device__ __forceinline__ void ray_box(const float (&x)[3], const float (&w)[3], float& tmin, float& tmax) {
+  float c0[3], c1[3];
+#pragma unroll
+  for (int i = 0; i < 3; ++i) {
+    const float inv = 1.0f / w[i];
+    const float xc = -x[i] * inv;
+    const float s = fabsf(inv);
+    c0[i] = xc - s;
+    c1[i] = xc + s;
+  }
+  tmin = fmaxf(fmaxf(c0[0], c0[1]), c0[2]);
+  tmax = fminf(fminf(c1[0], c1[1]), c1[2]);
+}
+
+__global__ void camera_rays_kernel(CameraParams c, float* __restrict__ rays) {
+  const int64_t total = int64_t(c.n) * c.H * c.W;
+  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < total; i += int64_t(gridDim.x) * blockDim.x) {
+    const int x = int(i % c.W);
+    const int64_t r = i / c.W;
+    const int y = int(r % c.H);
+    const int cam = int(r / c.H);
+    float o[3], w[3];
+    camera_ray(c, cam, y, x, o, w);
+    float* dst = rays + i * 6;
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+      dst[k] = o[k];
+      dst[3 + k] = w[k];
+    }
+  }
+}
+
+// ------------------------------------------------------------ wave helpers
+// Inclusive prefix sum over the 64 lanes of a wave.
+__device__ __forceinline__ float wave_scan_incl(float v, int lane) {
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const float u = __shfl_up(v, d, 64);
+    if (lane >= d) v += u;
+  }
+  return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d, 64);
+  return v;
+}
+
+// The MLP of one 32-sample chunk: p is this lane's sample (lanes l and l + 32
+// hold the same sample), fin the last layer's accumulators.
+template <class N, bool RELU>
+__device__ __forceinline__ void eval_chunk(const half8* sw, const float* sb, bool has_bias, int lane, int h,
+                                           const float (&p)[N::kIn], f32x16 (&fin)[N::kMaxMT]) {
+  constexpr int LL = N::kL - 1;
+  f32x16 accA[N::kMaxMT], accB[N::kMaxMT];
+  half8 b[N::kMaxKC];
+  const LdsWeights ws{sw + opaque_zero(), lane};
+  if (has_bias) {
+    const float* sbt = sb + opaque_zero();
+    load_bias<N, 0>(accA, sbt, h);
+    build_input<N>(p, h, b);
+    run_chain<N, 0, RELU, true>(ws, b, accA, accB, sbt, h);
+  } else {
+    build_input<N>(p, h, b);
+    run_chain<N, 0, RELU, false>(ws, b, accA, accB, sb, h);
+  }
+#pragma unroll
+  for (int t = 0; t < N::kMaxMT; ++t) fin[t] = (LL % 2 == 0) ? accA[t] : accB[t];
+}
+
+constexpr int kRenderWaves = 16;
+constexpr int kRenderThreads = 64 * kRenderWaves;
+
+// Weights and biases of the packed MLP into LDS (block-wide), counter reset.
+template <class N>
+__device__ __forceinline__ void stage_weights(const uint8_t* packed, const MlpLayout& lay, float* sb, half8* sw,
+                                              int* s_next) {
+#pragma unroll
+  for (int l = 0; l < N::kL; ++l) {
+    const float* src = reinterpret_cast<const float*>(packed + lay.bias_off[l]);
+    for (int i = threadIdx.x; i < 32 * N::mt(l); i += blockDim.x) sb[N::bias_base(l) + i] = src[i];
+    const half8* fsrc = reinterpret_cast<const half8*>(packed + lay.frag_off[l]);
+    for (int i = threadIdx.x; i < N::kc(l) * N::mt(l) * 64; i += blockDim.x) sw[N::frag_base(l) * 64 + i] = fsrc[i];
+  }
+  if (threadIdx.x == 0) *s_next = 0;
+  __syncthreads();
+}
+
+// ------------------------------------------------------ emission-absorption
+struct RenderArgs {
+  CameraParams cam;
+  const uint8_t* packed;
+  MlpLayout lay;
+  float* image;  // [n, H, W, 3]
+  int samples;   // multiple of 32
+};
+
+template <class N>
+__global__ __launch_bounds__(kRenderThreads, 1) void render_ea_kernel(RenderArgs a) {
+  static_assert(N::kIn == 3 && N::kOut == 4, "the renderer evaluates a 3 -> 4 (density, RGB) field");
+  __shared__ float sb[N::kBias];
+  __shared__ half8 sw[N::kFrags * 64];
+  __shared__ int s_next;
+  const int lane = threadIdx.x & 63;
+  const int h = lane >> 5, col = lane & 31;
+  const int64_t nrays = int64_t(a.cam.n) * a.cam.H * a.cam.W;
+  const int64_t per_block = (nrays + gridDim.x - 1) / gridDim.x;
+  const int64_t r_begin = int64_t(blockIdx.x) * per_block;
+  const int64_t r_end = r_begin + per_block < nrays ? r_begin + per_block : nrays;
+  const int nr = int(r_end > r_begin ? r_end - r_begin : 0);
+  const bool has_bias = (reinterpret_cast<const MlpPackHeader*>(a.packed)->flags & kMlpHasBias) != 0;
+  stage_weights<N>(a.packed, a.lay, sb, sw, &s_next);
+
+  auto claim = [&]() {
+    int t = 0;
+    if (lane == 0) t = atomicAdd(&s_next, 1);
+    return __builtin_amdgcn_readfirstlane(t);
+  };
+  const int chunks = a.samples / 32;
+  for (int r = claim(); r < nr; r = claim()) {
+    const int64_t ray = r_begin + r;
+    const int x = int(ray % a.cam.W);
+    const int64_t rest = ray / a.cam.W;
+    const int y = int(rest % a.cam.H);
+    const int cam = int(rest / a.cam.H);
+    float o[3], w[3];
+    camera_ray(a.cam, cam, y, x, o, w);
+    float t0, t1;
+    ray_box(o, w, t0, t1);
+    float cr = 0.0f, cg = 0.0f, cb = 0.0f;
+    if (!(t1 <= 0.0f || t0 > t1)) {
+      t0 = fmaxf(t0, 0.0f);
+      const float dt = (t1 - t0) / float(a.samples);
+      float Tin = 1.0f;
+      for (int c = 0; c < chunks; ++c) {
+        const float ts = t0 + (float(32 * c + col) + 0.5f) * dt;
+        const float p[3] = {o[0] + ts * w[0], o[1] + ts * w[1], o[2] + ts * w[2]};
+        f32x16 fin[N::kMaxMT];
+        eval_chunk<N, true>(sw, sb, has_bias, lane, h, p, fin);
+        // lanes 0..31 hold rows 0..3 = (density, r, g, b) of sample col
+        const float sigma = fast_softplus(fin[0][0]);
+        const float ad = h == 0 ? sigma * dt : 0.0f;
+        const float incl = wave_scan_incl(ad, lane);
+        const float total = __shfl(incl, 31, 64);
+        const float wgt = h == 0 ? Tin * __expf(-(incl - ad)) * (1.0f - __expf(-ad)) : 0.0f;
+        cr += wgt * fast_sigmoid(fin[0][1]);
+        cg += wgt * fast_sigmoid(fin[0][2]);
+        cb += wgt * fast_sigmoid(fin[0][3]);
+        Tin *= __expf(-total);
+      }
+      cr = wave_sum(cr);
+      cg = wave_sum(cg);
+      cb = wave_sum(cb);
+    }
+    if (lane == 0) {
+      float* dst = a.image + ray * 3;
+      dst[0] = cr;
+      dst[1] = cg;
+      dst[2] = cb;
+    }
+  }
+}
+
+// --------------------------------------------------------------- compositing
+// One wave per ray, 64 samples per step: s[ray][i] = (sigma, r, g, b).
+__global__ __launch_bounds__(256) void composite_kernel(const f32x4* __restrict__ s, const float* __restrict__ dts,
+                                                        int64_t nrays, int samples, float* __restrict__ out) {
+  const int lane = threadIdx.x & 63;
+  const int64_t wave0 = (int64_t(blockIdx.x) * blockDim.x + threadIdx.x) >> 6;
+  const int64_t nwaves = (int64_t(gridDim.x) * blockDim.x) >> 6;
+  for (int64_t ray = wave0; ray < nrays; ray += nwaves) {
+    const float dt = dts[ray];
+    const f32x4* src = s + ray * samples;
+    float Tin = 1.0f, cr = 0.0f, cg = 0.0f, cb = 0.0f;
+    for (int k = 0; k < samples; k += 64) {
+      const int i = k + lane;
+      f32x4 v = {0.0f, 0.0f, 0.0f, 0.0f};
+      if (i < samples) v = __builtin_nontemporal_load(src + i);
+      const float ad = v[0] * dt;
+      const float incl = wave_scan_incl(ad, lane);
+      const float total = __shfl(incl, 63, 64);
+      const float wgt = Tin * __expf(-(incl - ad)) * (1.0f - __expf(-ad));
+      cr += wgt * v[1];
+      cg += wgt * v[2];
+      cb += wgt * v[3];
+      Tin *= __expf(-total);
+    }
+    cr = wave_sum(cr);
+    cg = wave_sum(cg);
+    cb = wave_sum(cb);
+    if (lane == 0) {
+      out[ray * 3 + 0] = cr;
+      out[ray * 3 + 1] = cg;
+      out[ray * 3 + 2] = cb;
+    }
+  }
+}
+
+// ------------------------------------------------ raymarching transmittance
+struct TransmittanceArgs {
+  const float* rays;  // [n, 6]: x, w (world)
+  int64_t nrays;
+  const uint8_t* packed;
+  MlpLayout lay;
+  float M[12];        // mat4x3, column-major: linear columns 0..2, translation column 3
+  float step, density_scale;
+  float* out;         // [n]
+};
+
+// GLSL inverse() of the 3x3 linear part by the adjugate (columns c0, c1, c2).
+__device__ __forceinline__ void inverse3(const float (&M)[12], float (&L)[9]) {
+  const float a00 = M[0], a01 = M[1], a02 = M[2];  // column 0
+  const float a10 = M[3], a11 = M[4], a12 = M[5];  // column 1
+  const float a20 = M[6], a21 = M[7], a22 = M[8];  // column 2
+  const float b01 = a22 * a11 - a12 * a21;
+  const float b11 = -a22 * a10 + a12 * a20;
+  const float b21 = a21 * a10 - a11 * a20;
+  const float det = a00 * b01 + a01 * b11 + a02 * b21;
+  const float id = 1.0f / det;
+  L[0] = b01 * id;
+  L[1] = (-a22 * a01 + a02 * a21) * id;
+  L[2] = (a12 * a01 - a02 * a11) * id;
+  L[3] = b11 * id;
+  L[4] = (a22 * a00 - a02 * a20) * id;
+  L[5] = (-a12 * a00 + a02 * a10) * id;
+  L[6] = b21 * id;
+  L[7] = (-a21 * a00 + a01 * a20) * id;
+  L[8] = (a11 * a00 - a01 * a10) * id;
+}
+
+// The reference marches sequentially (transmittance_rm):
+//   for (k = 0; d > 0 && k < 4096; k++) { tau += extinction(x) * density * step;
+//     if (tau > 16) return 0; d -= step; x += step * w; }   return exp(-tau)
+// with every update rounded to fp32.  Here a chunk of 32 consecutive steps is
+// one MFMA block: lane c reproduces x_{k0+c} and d_{k0+c} by applying the same
+// fp32 updates c times (so the sample positions and the step count are the
+// reference's, bit for bit), the 32 extinctions are evaluated together, and tau
+// is an inclusive wavefront scan of the increments (the order of that fp32 sum
+// is the only difference from the reference).
+template <class N, int HEAD_ACT>
+__global__ __launch_bounds__(kRenderThreads, 1) void raymarch_transmittance_kernel(TransmittanceArgs a) {
+  static_assert(N::kIn == 3 && N::kOut == 1, "the extinction is a Map[3, 1]");
+  __shared__ float sb[N::kBias];
+  __shared__ half8 sw[N::kFrags * 64];
+  __shared__ int s_next;
+  const int lane = threadIdx.x & 63;
+  const int h = lane >> 5, col = lane & 31;
+  const int64_t per_block = (a.nrays + gridDim.x - 1) / gridDim.x;
+  const int64_t r_begin = int64_t(blockIdx.x) * per_block;
+  const int64_t r_end = r_begin + per_block < a.nrays ? r_begin + per_block : a.nrays;
+  const int nr = int(r_end > r_begin ? r_end - r_begin : 0);
+  const bool has_bias = (reinterpret_cast<const MlpPackHeader*>(a.packed)->flags & kMlpHasBias) != 0;
+  stage_weights<N>(a.packed, a.lay, sb, sw, &s_next);
+  float L[9];
+  inverse3(a.M, L);
+
+  auto claim = [&]() {
+    int t = 0;
+    if (lane == 0) t = atomicAdd(&s_next, 1);
+    return __builtin_amdgcn_readfirstlane(t);
+  };
+  for (int r = claim(); r < nr; r = claim()) {
+    const int64_t ray = r_begin + r;
+    const float* rr = a.rays + ray * 6;
+    const float xw[3] = {rr[0] - a.M[9], rr[1] - a.M[10], rr[2] - a.M[11]};
+    float x[3], w[3];
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {  // L * v with L column-major
+      x[i] = L[i] * xw[0] + L[3 + i] * xw[1] + L[6 + i] * xw[2];
+      w[i] = L[i] * rr[3] + L[3 + i] * rr[4] + L[6 + i] * rr[5];
+    }
+    float tmin, tmax;
+    ray_box(x, w, tmin, tmax);
+    float T = 1.0f;
+    if (!(tmax <= 0.0f || tmin > tmax)) {
+      tmin = fmaxf(0.0f, tmin);
+      float sws[3];
+#pragma unroll
+      for (int i = 0; i < 3; ++i) {
+        float wt = w[i] * tmin;
+        asm volatile("" : "+v"(wt));  // x += w * tMin: product and sum rounded separately
+        x[i] = x[i] + wt;
+        sws[i] = a.step * w[i];
+        asm volatile("" : "+v"(sws[i]));  // the product is rounded on its own, as x += step * w
+      }
+      float d = tmax - tmin;
+      float tau = 0.0f;
+      bool dead = false;
+      for (int k0 = 0; k0 < 4096 && d > 0.0f; k0 += 32) {
+        // lane c: position and remaining distance after c more steps
+        float xc[3] = {x[0], x[1], x[2]}, dc = d;
+        for (int it = 0; it < 31; ++it) {
+          if (it < col) {
+            dc = dc - a.step;
+#pragma unroll
+            for (int i = 0; i < 3; ++i) xc[i] = xc[i] + sws[i];
+          }
+        }
+        const bool valid = dc > 0.0f && k0 + col < 4096;
+        // every lane in [0, c) was valid when lane c is (d only decreases)
+        f32x16 fin[N::kMaxMT];
+        eval_chunk<N, true>(sw, sb, has_bias, lane, h, xc, fin);
+        const float sigma = head_act<HEAD_ACT>(0, fin[0][0]);
+        const float ce = sigma * a.density_scale;
+        float inc = ce * a.step;
+        asm volatile("" : "+v"(inc));
+        inc = (h == 0 && valid) ? inc : 0.0f;
+        const float incl = tau + wave_scan_incl(inc, lane);
+        const bool over = h == 0 && valid && incl > 16.0f;
+        if (__builtin_amdgcn_ballot_w64(over) != 0) {
+          dead = true;
+          break;
+        }
+        const uint64_t vmask = __builtin_amdgcn_ballot_w64(h == 0 && valid);
+        const int last = 63 - __builtin_clzll(vmask);  // highest valid lane (lane 0 is valid here)
+        tau = __shfl(incl, last, 64);
+        if (last < 31) break;  // the march ended inside this chunk
+        // state after step k0 + 31, then one more step: the next chunk's start
+        float nd = __shfl(dc, 31, 64);
+        float nx[3];
+#pragma unroll
+        for (int i = 0; i < 3; ++i) nx[i] = __shfl(xc[i], 31, 64);
+        d = nd - a.step;
+#pragma unroll
+        for (int i = 0; i < 3; ++i) x[i] = nx[i] + sws[i];
+      }
+      T = dead ? 0.0f : expf(-tau);
+    }
+    if (lane == 0) a.out[ray] = T;
+  }
+}
+
+// ---------------------------------------------------------- instantiations
+using RenderNet64x3 = Net<RDV_ENC_NONE, 3, 0, 4, 1, 2, 2, 2, 1>;   // 3->64->64->64->4
+using ExtinctionNet64x3 = Net<RDV_ENC_NONE, 3, 0, 1, 1, 2, 2, 2, 1>;  // 3->64->64->64->1
+
+// Is `d` the renderer's field network: 3 -> 64 -> 64 -> 64 -> 4, fp16, ReLU
+// hidden activations, raw (no-activation) head (softplus / sigmoid are applied
+// by the renderer)?
+static bool is_render_field(const rdv_mlp_desc& d, const MlpLayout& lay) {
+  if (d.encoding != RDV_ENC_NONE || d.in_features != 3 || d.n_layers != 4) return false;
+  const int dims[5] = {3, 64, 64, 64, 4};
+  for (int i = 0; i <= 4; ++i)
+    if (d.dims[i] != dims[i]) return false;
+  for (int i = 0; i < 4; ++i)
+    if (d.prec[i] != RDV_PREC_F16) return false;
+  for (int i = 0; i < 3; ++i)
+    if (d.act[i] != RDV_ACT_RELU) return false;
+  return d.act[3] == RDV_ACT_NONE && lay.kc[0] == 1;
+}
+
+static bool is_extinction_field(const rdv_mlp_desc& d, const MlpLayout& lay) {
+  if (d.encoding != RDV_ENC_NONE || d.in_features != 3 || d.n_layers != 4) return false;
+  const int dims[5] = {3, 64, 64, 64, 1};
+  for (int i = 0; i <= 4; ++i)
+    if (d.dims[i] != dims[i]) return false;
+  for (int i = 0; i < 4; ++i)
+    if (d.prec[i] != RDV_PREC_F16) return false;
+  for (int i = 0; i < 3; ++i)
+    if (d.act[i] != RDV_ACT_RELU) return false;
+  return (d.act[3] == RDV_ACT_NONE || d.act[3] == RDV_ACT_SOFTPLUS || d.act[3] == RDV_ACT_RELU) && lay.kc[0] == 1;
+}
+
+int launch_camera_rays(const rdv_camera_desc& c, const float* poses, float* rays, hipStream_t stream) {
+  CameraParams p{poses, c.n_cams, c.height, c.width, c.aspect_ratio, c.fov};
+  const int64_t total = int64_t(c.n_cams) * c.height * c.width;
+  int64_t blocks = (total + 255) / 256;
+  if (blocks > 65536) blocks = 65536;
+  camera_rays_kernel<<<dim3(unsigned(blocks)), dim3(256), 0, stream>>>(p, rays);
+  RDV_HIP_TRY(hipGetLastError());
+  return RDV_OK;
+}
+
+int launch_render_ea(const rdv_camera_desc& c, const float* poses, const rdv_mlp_desc& d, const MlpLayout& lay,
+                     const void* packed, int samples, float* image, hipStream_t stream) {
+  if (!is_render_field(d, lay))
+    return fail(RDV_ERR_UNSUPPORTED,
+                "the renderer's field must be a 3 -> 64 -> 64 -> 64 -> 4 LinearFast chain with ReLU hidden "
+                "activations and no head activation");
+  DeviceInfo di;
+  int rc = device_info(&di);
+  if (rc != RDV_OK) return rc;
+  RenderArgs a;
+  a.cam = CameraParams{poses, c.n_cams, c.height, c.width, c.aspect_ratio, c.fov};
+  a.packed = static_cast<const uint8_t*>(packed);
+  a.lay = lay;
+  a.image = image;
+  a.samples = samples;
+  const int64_t nrays = int64_t(c.n_cams) * c.height * c.width;
+  int64_t blocks = di.cu_count;
+  const int64_t need = (nrays + kRenderWaves - 1) / kRenderWaves;
+  if (need < blocks) blocks = need;
+  render_ea_kernel<RenderNet64x3><<<dim3(unsigned(blocks)), dim3(kRenderThreads), 0, stream>>>(a);
+  RDV_HIP_TRY(hipGetLastError());
+  return RDV_OK;
+}
+
+int launch_composite(const float* sigma_rgb, const float* dts, int64_t nrays, int samples, float* out,
+                     hipStream_t stream) {
+  DeviceInfo di;
+  int rc = device_info(&di);
+  if (rc != RDV_OK) return rc;
+  int64_t blocks = (nrays + 3) / 4;  // 4 waves (rays) per block
+  const int64_t cap = int64_t(di.cu_count) * 16;
+  if (blocks > cap) blocks = cap;
+  composite_kernel<<<dim3(unsigned(blocks)), dim3(256), 0, stream>>>(reinterpret_cast<const f32x4*>(sigma_rgb), dts,
+                                                                     nrays, samples, out);
+  RDV_HIP_TRY(hipGetLastError());
+  return RDV_OK;
+}
+
+int launch_raymarch_transmittance(const rdv_mlp_desc& d, const MlpLayout& lay, const void* packed, const float* rays,
+                                  int64_t nrays, const float* transform12, float step, float density_scale,
+                                  float* out, hipStream_t stream) {
+  if (!is_extinction_field(d, lay))
+    return fail(RDV_ERR_UNSUPPORTED,
+                "the extinction field must be a 3 -> 64 -> 64 -> 64 -> 1 LinearFast chain with ReLU hidden "
+                "activations (head: none, relu or softplus)");
+  DeviceInfo di;
+  int rc = device_info(&di);
+  if (rc != RDV_OK) return rc;
+  TransmittanceArgs a;
+  a.rays = rays;
+  a.nrays = nrays;
+  a.packed = static_cast<const uint8_t*>(packed);
+  a.lay = lay;
+  for (int i = 0; i < 12; ++i) a.M[i] = transform12[i];
+  a.step = step;
+  a.density_scale = density_scale;
+  a.out = out;
+  int64_t blocks = di.cu_count;
+  const int64_t need = (nrays + kRenderWaves - 1) / kRenderWaves;
+  if (need < blocks) blocks = need;
+  const dim3 grid(static_cast<unsigned>(blocks)), block(static_cast<unsigned>(kRenderThreads));
+  switch (d.act[3]) {
+    case RDV_ACT_SOFTPLUS:
+      raymarch_transmittance_kernel<ExtinctionNet64x3, RDV_ACT_SOFTPLUS><<<grid, block, 0, stream>>>(a);
+      break;
+    case RDV_ACT_RELU:
+      raymarch_transmittance_kernel<ExtinctionNet64x3, RDV_ACT_RELU><<<grid, block, 0, stream>>>(a);
+      break;
+    default:
+      raymarch_transmittance_kernel<ExtinctionNet64x3, RDV_ACT_NONE><<<grid, block, 0, stream>>>(a);
+      break;
+  }
+  RDV_HIP_TRY(hipGetLastError());
+  return RDV_OK;
+}
+
+}  // namespace rdv

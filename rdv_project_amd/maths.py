@@ -48,6 +48,9 @@ class Map:
         as the reference's per-class evaluator cache does, maths:1466-1476)."""
         if kwargs:
             raise NotImplementedError("deferred bindings (Map.__call__(**kwargs)) are outside this build")
+        ev = getattr(self, "_evaluate_rows", None)
+        if ev is not None:  # maps with a kernel of their own (rendering nodes)
+            return ev(x)
         from . import _chain
         return _chain.evaluate_map(self, x)
 

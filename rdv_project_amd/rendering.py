@@ -1,0 +1,98 @@
+"""Camera, transmittance and volume-rendering nodes of the rdv API.
+
+  Cameras                    reference domain/rendering.py:10-42 (Grid[3, 6])
+  RaymarchingTransmittance   reference domain/volumes.py:124-141 (Map[6, 1])
+  EmissionAbsorption         build-defined (Map[6, 3]): the MLP-in-the-loop
+                             renderer of the benchmark configuration
+Grids compose with maps (`Cameras(...) >> RaymarchingTransmittance(m)`) into a
+Sensor; calling the sensor renders every pixel on the GPU.
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+from .core import RDVObject, wrap
+from .maths import Grid, Map
+
+
+class Cameras(Grid):
+    """Pinhole cameras: cell (c, y, x) -> (origin, unit direction) of the ray
+    through pixel (x, y) of camera c (reference: rendering.py:10-42,
+    shaders/rendering/cameras.h).  poses: [num_cameras, 9] = origin | target | up.
+    aspect_ratio defaults to width / height and fov (vertical, radians) to pi / 4."""
+
+    IN = 3
+    OUT = 6
+
+    def __init__(self, width: int, height: int, poses, aspect_ratio: float | None = None, fov: float | None = None,
+                 jitter: bool = False) -> None:
+        if aspect_ratio is None:
+            aspect_ratio = width / height
+        if fov is None:
+            fov = math.pi / 4
+        if not isinstance(poses, RDVObject):
+            poses = wrap(torch.as_tensor(poses, dtype=torch.float32))
+        assert poses.shape[1] == 9, "poses must be a [num_cameras, 9] tensor (ori | target | up)"
+        if jitter:
+            raise NotImplementedError("pixel jitter (RandomLibrary) is outside this build")
+        super().__init__([poses.shape[0], height, width])
+        self.poses = poses
+        self.width = int(width)
+        self.height = int(height)
+        self.aspect_ratio = float(aspect_ratio)
+        self.fov = float(fov)
+        self.pixel_jitter = 0
+
+
+def _identity_transform() -> list[float]:
+    return [1.0, 0.0, 0.0, 0.0, 1.0, 0.0, 0.0, 0.0, 1.0, 0.0, 0.0, 0.0]
+
+
+class RaymarchingTransmittance(Map):
+    """T(x, w) along a ray through the box [-1,1]^3 of the object space given by
+    `transform` (mat4x3, column-major: three linear columns, then the translation),
+    marched with fixed steps: tau += extinction(x) * density_scale * step_size,
+    0 once tau > 16, exp(-tau) at the end; 1 when the ray misses
+    (reference: volumes.py:124-141, shaders/volumes/raymarching_transmittance.h).
+    extinction: a Map[3, 1] (here a 3 -> 64 -> 64 -> 64 -> 1 LinearFast chain)."""
+
+    IN = 6
+    OUT = 1
+
+    def __init__(self, extinction: Map, transform=None, step_size: float = 0.002, density_scale: float = 1.0) -> None:
+        if extinction.IN not in (None, 3) or extinction.OUT not in (None, 1):
+            raise TypeError("extinction must be a Map[3, 1]")
+        self.extinction = extinction
+        self.transform = _identity_transform() if transform is None else [float(v) for v in
+                                                                          torch.as_tensor(transform).reshape(-1)]
+        assert len(self.transform) == 12, "transform must be a mat4x3 (12 values)"
+        self.step_size = float(step_size)
+        self.density_scale = float(density_scale)
+
+    def _evaluate_rows(self, x) -> RDVObject:
+        from . import _render
+        return _render.raymarch_rows(self, x)
+
+
+class EmissionAbsorption(Map):
+    """Build-defined volume renderer (no reference counterpart): along each ray
+    (origin, direction) through [-1,1]^3, `samples` points t_i = t0 + (i + 1/2) dt
+    are fed through `field` (Map[3, 4]: density logit, RGB logits), with
+    sigma = softplus, c = sigmoid, and composited front to back:
+    alpha_i = 1 - exp(-sigma_i dt), T_i = prod_{j<i} (1 - alpha_j),
+    C = sum_i T_i alpha_i c_i (0 for rays that miss)."""
+
+    IN = 6
+    OUT = 3
+
+    def __init__(self, field: Map, samples: int = 128) -> None:
+        if field.IN not in (None, 3) or field.OUT not in (None, 4):
+            raise TypeError("field must be a Map[3, 4]")
+        assert samples >= 32 and samples % 32 == 0, "samples must be a positive multiple of 32"
+        self.field = field
+        self.samples = int(samples)
+
+    def _evaluate_rows(self, x) -> RDVObject:
+        raise NotImplementedError("EmissionAbsorption renders camera rays: call (Cameras(...) >> it)()")
