@@ -40,6 +40,10 @@ C3_DIRECT_FLOP = 2 * 256 * 256 * 64 * 64 * 9                     # 4.832 GFLOP
 C3_WINO_FLOP = 2 * 16 * (128 * 128) * 64 * 64                     # 2.147 GFLOP
 C3_BYTES = 2 * 64 * 256 * 256 * 2 + 16 * 2 * 4 * 64 * 8 * 2       # 16,908,288 B
 C3_ROTATE = 24  # 24 x (8 + 8) MiB of x / y: more than the 256 MB MALL
+# C4: per-sample work of the 3 -> 64 -> 64 -> 64 -> 4 field; compositing kernel
+# traffic per ray: 128 samples x 16 B read, 4 B dt read, 12 B colour written.
+C4_FLOP_PER_SAMPLE = 2 * (3 * 64 + 64 * 64 + 64 * 64 + 64 * 4)   # 17,280
+C4_COMPOSITE_BYTES_PER_RAY = 128 * 16 + 4 + 12
 
 
 def _log(msg: str) -> None:
@@ -151,6 +155,79 @@ def bench_winograd(steps, warmup):
     }
 
 
+def bench_render(steps, warmup):
+    """C4: the fused MLP-in-the-loop renderer (one frame per step) and the
+    HBM-streaming compositing kernel on C4-sized samples."""
+    import torch
+    import rdv_project_amd as rdv
+    from rdv_project_amd import _chain, _lib, _render
+    from rdv_project_amd import workloads as WL
+    lib = _lib.load()
+    m = None
+    for i, (w, b) in enumerate(WL.c4_mlp()):
+        lin = rdv.linear(w.cuda(), b.cuda(), f16=True)
+        m = lin if m is None else m >> lin
+        if i < 3:
+            m = m >> rdv.relu
+    p = _chain.plan_chain(m, 3)
+    packed = _chain.packed_params(m, p)
+    cam = rdv.Cameras(WL.C4_WIDTH, WL.C4_HEIGHT, WL.c4_pose().cuda())
+    d = _render.camera_desc(cam)
+    poses = cam.poses.as_tensor("torch")
+    img = torch.empty(1, WL.C4_HEIGHT, WL.C4_WIDTH, 3, device="cuda")
+    stream = C.c_void_p(torch.cuda.current_stream().cuda_stream)
+    dp, pp, pk, ip = C.byref(d), C.c_void_p(poses.data_ptr()), C.c_void_p(packed.data_ptr()), C.c_void_p(img.data_ptr())
+    desc = C.byref(p.desc)
+
+    def launch(i):
+        rc = lib.rdv_render_emission_absorption(dp, pp, desc, pk, WL.C4_SAMPLES, ip, stream)
+        if rc != 0:
+            _lib.check(rc, "render")
+
+    wall, ev = _time_launches(launch, steps, warmup)
+    # samples actually evaluated: 128 per ray that meets the box
+    r = cam().as_tensor("torch").reshape(-1, 6)
+    inv = 1.0 / r[:, 3:]
+    xc, sa = -r[:, :3] * inv, inv.abs()
+    tmin = (xc - sa).max(dim=1).values
+    tmax = (xc + sa).min(dim=1).values
+    hits = int((~((tmax <= 0) | (tmin > tmax))).sum())
+    samples = hits * WL.C4_SAMPLES
+    tflops = C4_FLOP_PER_SAMPLE * samples / (ev * 1e-3) / 1e12
+    out = {
+        "ms_per_frame": round(wall, 4),
+        "kernel_ms": round(ev, 4),
+        "Msamples_per_s": round(samples / (ev * 1e-3) / 1e6, 1),
+        "TFLOP_s": round(tflops, 1),
+        "mfma_peak_pct": round(100 * tflops / PEAK_FP16_TFLOPS, 2),
+        "hit_rays": hits,
+        "workload": "C4 emission-absorption render: 512x512 pinhole rays (origin (0,0,-3.5), target 0, fov pi/4) "
+                    "through [-1,1]^3, 128 samples per ray, MLP 3->64->64->64->4 (Kaiming-uniform fp16, seed 2), "
+                    "softplus density + sigmoid RGB, front-to-back fp32 compositing, one fused kernel",
+        "kernel": "render_ea_kernel",
+    }
+    # compositing kernel alone over C4-sized samples (262,144 rays x 128)
+    nr = WL.C4_WIDTH * WL.C4_HEIGHT
+    g = torch.Generator(device="cpu").manual_seed(9)
+    sets = [torch.rand(nr, WL.C4_SAMPLES, 4, generator=g).cuda() for _ in range(2)]
+    dts = (torch.rand(nr, generator=g) * 0.02).cuda()
+    cout = torch.empty(nr, 3, device="cuda")
+    sp = [C.c_void_p(t.data_ptr()) for t in sets]
+    dtp, cop = C.c_void_p(dts.data_ptr()), C.c_void_p(cout.data_ptr())
+
+    def launch_c(i):
+        rc = lib.rdv_composite(sp[i % 2], dtp, C.c_int64(nr), WL.C4_SAMPLES, cop, stream)
+        if rc != 0:
+            _lib.check(rc, "composite")
+
+    _, cev = _time_launches(launch_c, max(steps, 20), warmup)
+    gbs = C4_COMPOSITE_BYTES_PER_RAY * nr / (cev * 1e-3) / 1e9
+    out["composite"] = {"kernel_us": round(cev * 1e3, 2), "hbm_GB_s": round(gbs, 1),
+                        "hbm_frac": round(gbs / PEAK_HBM_GBS, 4), "bytes_per_ray": C4_COMPOSITE_BYTES_PER_RAY,
+                        "rays": nr, "kernel": "composite_kernel<2>"}
+    return out
+
+
 def cpu_baseline_c2(sample: int = 1 << 16):
     """The oracle's C2 forward on `sample` points: 3 warm-ups, median of 5."""
     import numpy as np
@@ -244,6 +321,9 @@ def main() -> int:
         _log("C3")
         extras["C3_winograd"] = bench_winograd(max(args.steps // 2, 10), args.warmup)
         _log(f"C3 {extras['C3_winograd']}")
+        _log("C4")
+        extras["C4_render"] = bench_render(max(args.steps // 50, 10), 3)
+        _log(f"C4 {extras['C4_render']}")
 
     cpu = None
     if not args.no_cpu_baseline:

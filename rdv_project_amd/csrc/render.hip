@@ -9,7 +9,8 @@
 //    alpha_i = 1 - exp(-sigma_i dt), T_i = prod_{j<i} (1 - alpha_j),
 //    C = sum_i T_i alpha_i c_i.
 //  - composite_kernel: the same compositing over precomputed samples
-//    (sigma, r, g, b) streamed from HBM.
+//    (sigma, r, g, b) streamed from HBM (exclusive optical depth per sample from
+//    a per-lane partial sum and one wavefront scan).
 //  - raymarch_transmittance_kernel: RaymarchingTransmittance
 //    (src/rdv/domain/volumes.py:124-141, shaders/volumes/raymarching_transmittance.h,
 //    raymarching_transmittance_trait.h, libraries/math_library.h:48-57) with
@@ -98,19 +99,31 @@ __global__ void camera_rays_kernel(CameraParams c, float* __restrict__ rays) {
 }
 
 // ------------------------------------------------------------ wave helpers
-// Inclusive prefix sum over the 64 lanes of a wave.
-__device__ __forceinline__ float wave_scan_incl(float v, int lane) {
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    const float u = __shfl_up(v, d, 64);
-    if (lane >= d) v += u;
-  }
+// Inclusive prefix sum over the 64 lanes of a wave with DPP lane moves (no LDS
+// traffic): shifts by 1, 2, 4, 8 inside each 16-lane row, then row 0's / 1's
+// last lane broadcast into rows 1 / 3 (row_bcast:15) and lane 31 into rows 2, 3
+// (row_bcast:31).  Out-of-row sources read 0 (bound_ctrl).
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_move(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROW_MASK, 0xF, true));
+}
+__device__ __forceinline__ float wave_scan_incl(float v, int /*lane*/) {
+  v += dpp_move<0x111, 0xF>(v);  // row_shr:1
+  v += dpp_move<0x112, 0xF>(v);  // row_shr:2
+  v += dpp_move<0x114, 0xF>(v);  // row_shr:4
+  v += dpp_move<0x118, 0xF>(v);  // row_shr:8
+  v += dpp_move<0x142, 0xA>(v);  // row_bcast:15 into rows 1, 3
+  v += dpp_move<0x143, 0xC>(v);  // row_bcast:31 into rows 2, 3
   return v;
 }
+// Sum over the wave, returned in every lane.
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d, 64);
-  return v;
+  const float incl = wave_scan_incl(v, 0);
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, incl), 63));
+}
+// Value of lane `src` (wave-uniform) in every lane.
+__device__ __forceinline__ float lane_value(float v, int src) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), src));
 }
 
 // The MLP of one 32-sample chunk: p is this lane's sample (lanes l and l + 32
@@ -208,7 +221,7 @@ __global__ __launch_bounds__(kRenderThreads, 1) void render_ea_kernel(RenderArgs
         const float sigma = fast_softplus(fin[0][0]);
         const float ad = h == 0 ? sigma * dt : 0.0f;
         const float incl = wave_scan_incl(ad, lane);
-        const float total = __shfl(incl, 31, 64);
+        const float total = lane_value(incl, 31);
         const float wgt = h == 0 ? Tin * __expf(-(incl - ad)) * (1.0f - __expf(-ad)) : 0.0f;
         cr += wgt * fast_sigmoid(fin[0][1]);
         cg += wgt * fast_sigmoid(fin[0][2]);
@@ -229,9 +242,71 @@ __global__ __launch_bounds__(kRenderThreads, 1) void render_ea_kernel(RenderArgs
 }
 
 // --------------------------------------------------------------- compositing
-// One wave per ray, 64 samples per step: s[ray][i] = (sigma, r, g, b).
+// One wave per ray.  SPL <= 4 samples per lane: lane l owns the SPL consecutive
+// samples l SPL .. l SPL + SPL - 1 (one contiguous 16 SPL-byte read, the wave's
+// reads one contiguous block), combines them locally and joins the wave scan
+// with its partial sum; the next ray's samples are loaded before this ray is
+// composited.  Longer rays go through the 64-sample loop.
+template <int SPL>
+__device__ __forceinline__ void load_ray(const f32x4* __restrict__ src, int samples, int lane, f32x4 (&v)[SPL]) {
+#pragma unroll
+  for (int j = 0; j < SPL; ++j) {
+    const int i = lane * SPL + j;
+    v[j] = i < samples ? __builtin_nontemporal_load(src + i) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  }
+}
+
+template <int SPL>
+__device__ __forceinline__ void composite_ray(const f32x4 (&v)[SPL], float dt, int lane, float* __restrict__ dst) {
+  float a[SPL], part = 0.0f;
+#pragma unroll
+  for (int j = 0; j < SPL; ++j) {
+    a[j] = v[j][0] * dt;
+    part += a[j];
+  }
+  float run = wave_scan_incl(part, lane) - part;  // optical depth in front of this lane's first sample
+  float cr = 0.0f, cg = 0.0f, cb = 0.0f;
+#pragma unroll
+  for (int j = 0; j < SPL; ++j) {
+    const float wgt = __expf(-run) * (1.0f - __expf(-a[j]));
+    cr += wgt * v[j][1];
+    cg += wgt * v[j][2];
+    cb += wgt * v[j][3];
+    run += a[j];
+  }
+  cr = wave_sum(cr);
+  cg = wave_sum(cg);
+  cb = wave_sum(cb);
+  if (lane == 0) {
+    dst[0] = cr;
+    dst[1] = cg;
+    dst[2] = cb;
+  }
+}
+
+template <int SPL>
 __global__ __launch_bounds__(256) void composite_kernel(const f32x4* __restrict__ s, const float* __restrict__ dts,
                                                         int64_t nrays, int samples, float* __restrict__ out) {
+  const int lane = threadIdx.x & 63;
+  const int64_t wave0 = (int64_t(blockIdx.x) * blockDim.x + threadIdx.x) >> 6;
+  const int64_t nwaves = (int64_t(gridDim.x) * blockDim.x) >> 6;
+  if (wave0 >= nrays) return;
+  // two register sets, alternating: each ray's samples are requested one ray
+  // ahead of its compositing
+  f32x4 va[SPL], vb[SPL];
+  load_ray<SPL>(s + wave0 * samples, samples, lane, va);
+  for (int64_t ray = wave0; ray < nrays; ray += 2 * nwaves) {
+    const int64_t rb = ray + nwaves, ra2 = ray + 2 * nwaves;
+    if (rb < nrays) load_ray<SPL>(s + rb * samples, samples, lane, vb);
+    composite_ray<SPL>(va, dts[ray], lane, out + ray * 3);
+    if (ra2 < nrays) load_ray<SPL>(s + ra2 * samples, samples, lane, va);
+    if (rb < nrays) composite_ray<SPL>(vb, dts[rb], lane, out + rb * 3);
+  }
+}
+
+__global__ __launch_bounds__(256) void composite_long_kernel(const f32x4* __restrict__ s,
+                                                             const float* __restrict__ dts, int64_t nrays,
+                                                             int samples, float* __restrict__ out) {
   const int lane = threadIdx.x & 63;
   const int64_t wave0 = (int64_t(blockIdx.x) * blockDim.x + threadIdx.x) >> 6;
   const int64_t nwaves = (int64_t(gridDim.x) * blockDim.x) >> 6;
@@ -245,7 +320,7 @@ __global__ __launch_bounds__(256) void composite_kernel(const f32x4* __restrict_
       if (i < samples) v = __builtin_nontemporal_load(src + i);
       const float ad = v[0] * dt;
       const float incl = wave_scan_incl(ad, lane);
-      const float total = __shfl(incl, 63, 64);
+      const float total = lane_value(incl, 63);
       const float wgt = Tin * __expf(-(incl - ad)) * (1.0f - __expf(-ad));
       cr += wgt * v[1];
       cg += wgt * v[2];
@@ -380,13 +455,13 @@ __global__ __launch_bounds__(kRenderThreads, 1) void raymarch_transmittance_kern
         }
         const uint64_t vmask = __builtin_amdgcn_ballot_w64(h == 0 && valid);
         const int last = 63 - __builtin_clzll(vmask);  // highest valid lane (lane 0 is valid here)
-        tau = __shfl(incl, last, 64);
+        tau = lane_value(incl, last);
         if (last < 31) break;  // the march ended inside this chunk
         // state after step k0 + 31, then one more step: the next chunk's start
-        float nd = __shfl(dc, 31, 64);
+        float nd = lane_value(dc, 31);
         float nx[3];
 #pragma unroll
-        for (int i = 0; i < 3; ++i) nx[i] = __shfl(xc[i], 31, 64);
+        for (int i = 0; i < 3; ++i) nx[i] = lane_value(xc[i], 31);
         d = nd - a.step;
 #pragma unroll
         for (int i = 0; i < 3; ++i) x[i] = nx[i] + sws[i];
@@ -468,10 +543,14 @@ int launch_composite(const float* sigma_rgb, const float* dts, int64_t nrays, in
   int rc = device_info(&di);
   if (rc != RDV_OK) return rc;
   int64_t blocks = (nrays + 3) / 4;  // 4 waves (rays) per block
-  const int64_t cap = int64_t(di.cu_count) * 16;
+  const int64_t cap = int64_t(di.cu_count) * 8;
   if (blocks > cap) blocks = cap;
-  composite_kernel<<<dim3(unsigned(blocks)), dim3(256), 0, stream>>>(reinterpret_cast<const f32x4*>(sigma_rgb), dts,
-                                                                     nrays, samples, out);
+  const dim3 grid(static_cast<unsigned>(blocks)), block(256);
+  const f32x4* s = reinterpret_cast<const f32x4*>(sigma_rgb);
+  if (samples <= 64) composite_kernel<1><<<grid, block, 0, stream>>>(s, dts, nrays, samples, out);
+  else if (samples <= 128) composite_kernel<2><<<grid, block, 0, stream>>>(s, dts, nrays, samples, out);
+  else if (samples <= 256) composite_kernel<4><<<grid, block, 0, stream>>>(s, dts, nrays, samples, out);
+  else composite_long_kernel<<<grid, block, 0, stream>>>(s, dts, nrays, samples, out);
   RDV_HIP_TRY(hipGetLastError());
   return RDV_OK;
 }

@@ -54,7 +54,7 @@ def test_camera_rays(W, H, fov):
     np.testing.assert_allclose(rays, ref, atol=2e-6, rtol=0)
 
 
-@pytest.mark.parametrize("n,S", [(1000, 128), (37, 100), (5, 1)])
+@pytest.mark.parametrize("n,S", [(1000, 128), (37, 100), (5, 1), (300, 64), (77, 256), (20, 300)])
 def test_composite_kernel(n, S):
     g = torch.Generator().manual_seed(n + S)
     s = torch.rand(n, S, 4, generator=g)
