@@ -162,6 +162,24 @@ int rdv_winograd3x3_transform_weight(const void* w, int32_t w_layout, int32_t w_
 int rdv_winograd3x3_forward(const rdv_conv_desc* desc, const void* x, const void* U, const float* bias,
                             void* y, void* stream);
 
+/* ------------------------------------------------- MLP training step (C5) */
+/* Bytes of workspace rdv_mlp_train_step needs for `desc` and n points (< 0 if
+ * the chain is not supported by the training kernels). */
+int64_t rdv_mlp_train_workspace_bytes(const rdv_mlp_desc* desc, int64_t n);
+
+/* Forward + MSE loss + backward of a LinearFast / ReLU chain (build-defined;
+ * the reference has no backward pass).  x: device [n, dims[0]] fp16; target:
+ * device [n, dims[L]] fp32; loss: device fp32 scalar = mean over n x dims[L] of
+ * (y - target)^2; dW[i] / db[i] (host arrays of device pointers): fp32
+ * [dims[i+1], dims[i]] / [dims[i+1]] gradients of the loss, reduced over every
+ * point in fp32.  Supported chains: ReLU hidden layers, linear head, input
+ * width a multiple of 16 and hidden widths multiples of 32 (all <= 128), head
+ * width a multiple of 8 (<= 128).  workspace: rdv_mlp_train_workspace_bytes
+ * bytes, 256-byte aligned. */
+int rdv_mlp_train_step(const rdv_mlp_desc* desc, const void* packed, const void* x, const float* target, int64_t n,
+                       void* workspace, int64_t workspace_bytes, float* loss, float* const* dW, float* const* db,
+                       void* stream);
+
 /* ------------------------------------------------ cameras and volume rendering */
 typedef struct rdv_camera_desc {
   int32_t n_cams;       /* poses rows                                             */

@@ -22,6 +22,7 @@ from .core import (
 from .maths import Composite, Grid, Identity, Map, Sensor, TensorOperation, X, e, pi
 from ._conv import Winograd3x3Conv2d, winograd3x3_conv2d
 from ._render import composite
+from ._train import mse_backward
 from .rendering import Cameras, EmissionAbsorption, RaymarchingTransmittance
 from .nn import (
     Conv2DTensorOpWinograd3x3,

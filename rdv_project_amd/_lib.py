@@ -86,6 +86,10 @@ _SIGNATURES = {
     "rdv_mlp_forward_f16_all": (C.c_int, [C.POINTER(MlpDesc), C.c_void_p, C.c_void_p, C.c_void_p, C.c_int64,
                                           C.c_void_p]),
     "rdv_mlp_kernel_name": (C.c_char_p, [C.POINTER(MlpDesc)]),
+    "rdv_mlp_train_workspace_bytes": (C.c_int64, [C.POINTER(MlpDesc), C.c_int64]),
+    "rdv_mlp_train_step": (C.c_int, [C.POINTER(MlpDesc), C.c_void_p, C.c_void_p, C.c_void_p, C.c_int64, C.c_void_p,
+                                     C.c_int64, C.c_void_p, C.POINTER(C.c_void_p), C.POINTER(C.c_void_p),
+                                     C.c_void_p]),
     "rdv_cameras_rays": (C.c_int, [C.POINTER(CameraDesc), C.c_void_p, C.c_void_p, C.c_void_p]),
     "rdv_render_emission_absorption": (C.c_int, [C.POINTER(CameraDesc), C.c_void_p, C.POINTER(MlpDesc), C.c_void_p,
                                                  C.c_int32, C.c_void_p, C.c_void_p]),

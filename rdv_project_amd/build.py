@@ -27,6 +27,7 @@ SOURCES = [
     "mlp_fused.hip",
     "winograd.hip",
     "render.hip",
+    "train.hip",
 ]
 
 ARCH = os.environ.get("RDV_OFFLOAD_ARCH", "gfx950")

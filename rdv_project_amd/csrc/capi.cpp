@@ -56,6 +56,11 @@ int prepare_chain_f32(const rdv_mlp_desc& d);
 int64_t winograd_weight_bytes(int cin, int cout);
 int launch_winograd_transform_weight(const void* w, int w_layout, int w_dtype, int cin, int cout, void* U,
                                      hipStream_t stream);
+int train_check(const rdv_mlp_desc& d, const MlpLayout& lay);
+int64_t train_workspace_bytes(const rdv_mlp_desc& d, const MlpLayout& lay, int64_t n, int cu);
+int launch_train_step(const rdv_mlp_desc& d, const MlpLayout& lay, const void* packed, const void* x,
+                      const float* target, int64_t n, void* workspace, int64_t ws_bytes, float* loss,
+                      float* const* dW, float* const* db, hipStream_t stream);
 int launch_camera_rays(const rdv_camera_desc& c, const float* poses, float* rays, hipStream_t stream);
 int launch_render_ea(const rdv_camera_desc& c, const float* poses, const rdv_mlp_desc& d, const MlpLayout& lay,
                      const void* packed, int samples, float* image, hipStream_t stream);
@@ -233,6 +238,39 @@ int rdv_winograd3x3_forward(const rdv_conv_desc* desc, const void* x, const void
   const size_t oal = desc->out_dtype == RDV_DTYPE_F16 ? 8 : 16;
   if (reinterpret_cast<uintptr_t>(y) % oal) return fail(RDV_ERR_INVALID, "y is not aligned for vector stores");
   return launch_winograd3x3(*desc, x, U, bias, y, static_cast<hipStream_t>(stream));
+}
+
+int64_t rdv_mlp_train_workspace_bytes(const rdv_mlp_desc* desc, int64_t n) {
+  MlpLayout lay;
+  int rc = check_mlp(desc, &lay);
+  if (rc != RDV_OK) return rc;
+  rc = train_check(*desc, lay);
+  if (rc != RDV_OK) return rc;
+  if (n < 1) return fail(RDV_ERR_INVALID, "n must be >= 1");
+  DeviceInfo di;
+  rc = device_info(&di);
+  if (rc != RDV_OK) return rc;
+  return train_workspace_bytes(*desc, lay, n, di.cu_count);
+}
+
+int rdv_mlp_train_step(const rdv_mlp_desc* desc, const void* packed, const void* x, const float* target, int64_t n,
+                       void* workspace, int64_t workspace_bytes, float* loss, float* const* dW, float* const* db,
+                       void* stream) {
+  MlpLayout lay;
+  int rc = check_mlp(desc, &lay);
+  if (rc != RDV_OK) return rc;
+  rc = train_check(*desc, lay);
+  if (rc != RDV_OK) return rc;
+  if (n < 1) return fail(RDV_ERR_INVALID, "n must be >= 1");
+  if (!packed || !x || !target || !workspace || !loss || !dW || !db)
+    return fail(RDV_ERR_INVALID, "rdv_mlp_train_step: NULL pointer argument");
+  for (int i = 0; i < desc->n_layers; ++i)
+    if (!dW[i] || !db[i]) return fail(RDV_ERR_INVALID, "rdv_mlp_train_step: NULL gradient pointer");
+  if (reinterpret_cast<uintptr_t>(x) % 16 || reinterpret_cast<uintptr_t>(target) % 16 ||
+      reinterpret_cast<uintptr_t>(workspace) % 256)
+    return fail(RDV_ERR_INVALID, "x and target must be 16-byte aligned, the workspace 256-byte aligned");
+  return launch_train_step(*desc, lay, packed, x, target, n, workspace, workspace_bytes, loss, dW, db,
+                           static_cast<hipStream_t>(stream));
 }
 
 static int check_camera(const rdv_camera_desc* c) {

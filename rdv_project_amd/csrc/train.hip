@@ -1,0 +1,538 @@
+// MLP training step on the matrix cores: forward, MSE loss, backward with fp32
+// weight gradients reduced over every point (build-defined; the reference has
+// no backward pass).
+//
+// Numerics.  Forward = the LinearFast chain (fp16 inputs and weights, fp32
+// accumulation, fp32 bias, ReLU); hidden activations are kept in fp16 exactly
+// as they feed the next layer.  Loss = mean over n x out of (y - t)^2.  The
+// backward carries the unscaled gradient g = 2 (y - t) (fp16, O(1) values, no
+// underflow); dz_l = (dz_{l+1} W_l) masked by h_l > 0 in fp32, rounded to fp16;
+// dW_l = sum_p dz_{l+1}[p]^T h_l[p] and db_l = sum_p dz_{l+1}[p] accumulated in
+// fp32; dW and db are finally scaled by 1 / (n out) in fp32.
+//
+// Kernels.
+//  - train_fwd_kernel: a group of consecutive layers whose A fragments fit in
+//    LDS, per wave 32-point tiles, the same register layer hand-off as the
+//    fused MLP (mlp_layout.h); every hidden output is also stored (fp16, row
+//    major) for the backward pass; the group that ends the chain computes
+//    g = 2 (y - t) and per-block partial sums of (y - t)^2.
+//  - train_bwd_kernel: one layer; a block of 4 waves stages a 32-point tile of
+//    dz_{l+1} and h_l in LDS, then wave w computes one 32-row tile of
+//    dz_l^T = W^T dz_{l+1}^T (v_mfma_f32_32x32x16_f16 with packed W^T fragments)
+//    and one 32-row tile of dW (K = the tile's points, operands
+//    gathered from the LDS tile); dW stays in registers across the block's whole
+//    point range and is written once as a per-block partial.
+//  - train_reduce_kernel: sums the per-block partials in a fixed order.
+#include <algorithm>
+
+#include "mlp_core.h"
+
+namespace rdv {
+
+constexpr int kTrMT = 4;      // 32-row M tiles per layer (widths <= 128)
+constexpr int kTrKC = 8;      // 16-wide K chunks per layer
+constexpr int kTrWaves = 8;   // forward block
+constexpr int kTrFwdThreads = 64 * kTrWaves;
+constexpr int kTrBwdThreads = 256;
+
+struct TrainFwdArgs {
+  const uint8_t* packed;
+  MlpLayout lay;
+  int L, l0, l1;                        // layers [l0, l1) of an L-layer chain
+  const half_t* in;                     // layer l0's input [n, in_w[l0]] fp16
+  half_t* hout[RDV_MLP_MAX_LAYERS];     // hout[l]: output of layer l (l < L - 1) [n, out_w[l]]
+  const float* target;                  // [n, out] fp32 (l1 == L)
+  half_t* g;                            // [n, out] fp16 2 (y - t) (l1 == L)
+  float* loss_partial;                  // [gridDim.x] (l1 == L)
+  int64_t n;
+  int has_bias;
+};
+
+// Sum over a wave (every lane gets it): DPP row shifts + row broadcasts.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float tr_dpp(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROW_MASK, 0xF, true));
+}
+__device__ __forceinline__ float tr_wave_sum(float v) {
+  v += tr_dpp<0x111, 0xF>(v);
+  v += tr_dpp<0x112, 0xF>(v);
+  v += tr_dpp<0x114, 0xF>(v);
+  v += tr_dpp<0x118, 0xF>(v);
+  v += tr_dpp<0x142, 0xA>(v);
+  v += tr_dpp<0x143, 0xC>(v);
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+
+typedef half_t half4v __attribute__((ext_vector_type(4)));
+
+__global__ __launch_bounds__(kTrFwdThreads, 1) void train_fwd_kernel(TrainFwdArgs a) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  __shared__ float s_loss[kTrWaves];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int h = lane >> 5, col = lane & 31;
+  const MlpLayout& lay = a.lay;
+  // stage the group's fragments and biases: [frag bytes of l0..l1-1][bias floats]
+  const int64_t fbase = lay.frag_off[a.l0];
+  const int64_t fend = lay.frag_off[a.l1 - 1] + int64_t(lay.mt[a.l1 - 1]) * lay.kc[a.l1 - 1] * 1024;
+  const int64_t bbase = lay.bias_off[a.l0];
+  const int64_t bend = lay.bias_off[a.l1 - 1] + int64_t(lay.mt[a.l1 - 1]) * 128;
+  {
+    const uint4* src = reinterpret_cast<const uint4*>(a.packed + fbase);
+    uint4* dst = reinterpret_cast<uint4*>(smem);
+    for (int64_t i = threadIdx.x; i < (fend - fbase) / 16; i += blockDim.x) dst[i] = src[i];
+    const uint4* bsrc = reinterpret_cast<const uint4*>(a.packed + bbase);
+    uint4* bdst = reinterpret_cast<uint4*>(smem + (fend - fbase));
+    for (int64_t i = threadIdx.x; i < (bend - bbase) / 16; i += blockDim.x) bdst[i] = bsrc[i];
+  }
+  __syncthreads();
+  const half8* sw = reinterpret_cast<const half8*>(smem);
+  const float* sb = reinterpret_cast<const float*>(smem + (fend - fbase));
+
+  const int64_t ntiles = (a.n + 31) / 32;
+  const int64_t per_block = (ntiles + gridDim.x - 1) / gridDim.x;
+  const int64_t t_begin = int64_t(blockIdx.x) * per_block;
+  const int64_t t_end = t_begin + per_block < ntiles ? t_begin + per_block : ntiles;
+  const bool last_group = a.l1 == a.L;
+  float loss = 0.0f;
+
+  for (int64_t tile = t_begin + wave; tile < t_end; tile += kTrWaves) {
+    const int64_t p = tile * 32 + col;            // this lane's point
+    const bool pv = p < a.n;
+    const int64_t pc = pv ? p : a.n - 1;          // clamped row for loads
+    half8 b[kTrKC];
+    {
+      const int w0 = lay.in_w[a.l0];
+      const half_t* row = a.in + pc * w0;
+      const int kc0 = lay.kc[a.l0];
+#pragma unroll
+      for (int c = 0; c < kTrKC; ++c) {
+        if (c < kc0) {
+          if (a.l0 == 0) {
+            // natural order: features 16c + 8h + 0..7
+            b[c] = *reinterpret_cast<const half8*>(row + 16 * c + 8 * h);
+          } else {
+            // hidden slot order (chunk_sigma): 16c + 4h + 0..3, then 16c + 8 + 4h + 0..3
+            const half4v lo = *reinterpret_cast<const half4v*>(row + 16 * c + 4 * h);
+            const half4v hi = *reinterpret_cast<const half4v*>(row + 16 * c + 8 + 4 * h);
+            b[c] = half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+          }
+        }
+      }
+    }
+    for (int l = a.l0; l < a.l1; ++l) {
+      const int mt = lay.mt[l], kc = lay.kc[l];
+      const int frag = int((lay.frag_off[l] - fbase) / 16) / 64;  // first fragment of layer l in LDS
+      const int boff = int((lay.bias_off[l] - bbase) / 4);        // first bias of layer l in LDS
+      f32x16 acc[kTrMT];
+#pragma unroll
+      for (int t = 0; t < kTrMT; ++t) {
+        if (t < mt) {
+          if (a.has_bias) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const f32x4 bv = *reinterpret_cast<const f32x4*>(sb + boff + 32 * t + 8 * q + 4 * h);
+#pragma unroll
+              for (int jj = 0; jj < 4; ++jj) acc[t][4 * q + jj] = bv[jj];
+            }
+          } else {
+            acc[t] = f32x16{};
+          }
+        }
+      }
+#pragma unroll
+      for (int c = 0; c < kTrKC; ++c) {
+        if (c < kc) {
+#pragma unroll
+          for (int t = 0; t < kTrMT; ++t)
+            if (t < mt)
+              acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(sw[(frag + t * kc + c) * 64 + lane], b[c], acc[t], 0, 0, 0);
+        }
+      }
+      if (l == a.L - 1) {
+        // head: y = acc rows (32t + 8q + 4h + jj) < out; g = 2 (y - t), loss += (y - t)^2
+        const int out = lay.out_w[l];
+#pragma unroll
+        for (int t = 0; t < kTrMT; ++t) {
+          if (t < mt) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const int r = 32 * t + 8 * q + 4 * h;
+              if (r < out && pv) {
+                const f32x4 tv = *reinterpret_cast<const f32x4*>(a.target + p * out + r);
+                half4v gv;
+#pragma unroll
+                for (int jj = 0; jj < 4; ++jj) {
+                  const float d = acc[t][4 * q + jj] - tv[jj];
+                  loss += d * d;
+                  gv[jj] = half_t(d + d);
+                }
+                *reinterpret_cast<half4v*>(a.g + p * out + r) = gv;
+              }
+            }
+          }
+        }
+      } else {
+        // ReLU, fp16: store the hidden output and hand it to the next layer
+        const int out = lay.out_w[l];
+        half_t* dst = a.hout[l] + p * out;
+#pragma unroll
+        for (int t = 0; t < kTrMT; ++t) {
+          if (t < mt) {
+#pragma unroll
+            for (int qq = 0; qq < 2; ++qq) {
+              half8 v;
+#pragma unroll
+              for (int j = 0; j < 8; ++j) v[j] = half_t(acc[t][8 * qq + j]);
+              v = __builtin_elementwise_max(v, half8{0, 0, 0, 0, 0, 0, 0, 0});
+              b[2 * t + qq] = v;
+              if (pv) {
+                // registers 8qq + 0..3 are rows 32t + 16qq + 4h + 0..3, 8qq + 4..7 rows 32t + 16qq + 8 + 4h + 0..3
+                *reinterpret_cast<half4v*>(dst + 32 * t + 16 * qq + 4 * h) = half4v{v[0], v[1], v[2], v[3]};
+                *reinterpret_cast<half4v*>(dst + 32 * t + 16 * qq + 8 + 4 * h) = half4v{v[4], v[5], v[6], v[7]};
+              }
+            }
+          }
+        }
+      }
+    }
+  }
+  if (last_group) {
+    loss = tr_wave_sum(loss);
+    if (lane == 0) s_loss[wave] = loss;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      float s = 0.0f;
+      for (int w = 0; w < kTrWaves; ++w) s += s_loss[w];
+      a.loss_partial[blockIdx.x] = s;
+    }
+  }
+}
+
+// --------------------------------------------------------------- backward
+struct TrainBwdArgs {
+  const half_t* dz;   // [n, out] gradient of layer l's output (pre-activation)
+  const half_t* hin;  // [n, in] layer l's input
+  const half_t* wt;   // W^T A fragments [in / 32][ceil(out / 16)][64][8]
+  half_t* dzin;       // [n, in] gradient of the input's pre-activation (masked), or null
+  float* dw_part;     // [gridDim.x][out][in]
+  float* db_part;     // [gridDim.x][out]
+  int in, out;
+  int64_t n;
+};
+
+constexpr int kTrPad = 8;  // LDS row padding (halves): rows 8 points apart fall in different banks
+
+__global__ __launch_bounds__(kTrBwdThreads, 2) void train_bwd_kernel(TrainBwdArgs a) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int h = lane >> 5, col = lane & 31;
+  const int mto = (a.out + 31) / 32;       // dW row tiles (o)
+  const int mti = (a.in + 31) / 32;        // dW column tiles (i)
+  const int mtx = a.dzin != nullptr ? a.in / 32 : 0;  // dX row tiles (hidden inputs: multiples of 32)
+  const int kco = (a.out + 15) / 16;       // K chunks of the dX product
+  const int OP = 32 * mto + kTrPad;        // LDS dz row stride (halves), columns >= out stay 0
+  const int IP = 32 * mti + kTrPad;        // LDS h row stride (halves), columns >= in stay 0
+  half8* swt = reinterpret_cast<half8*>(smem);
+  half_t* sdz = reinterpret_cast<half_t*>(smem + int64_t(mtx) * kco * 1024);
+  half_t* sh = sdz + 32 * OP;
+  // W^T fragments -> LDS, zero both tiles (their padding columns stay zero)
+  for (int i = threadIdx.x; i < mtx * kco * 64; i += blockDim.x) swt[i] = reinterpret_cast<const half8*>(a.wt)[i];
+  for (int i = threadIdx.x; i < 32 * (OP + IP); i += blockDim.x) sdz[i] = half_t(0.0f);
+  __syncthreads();
+
+  const int64_t ntiles = (a.n + 31) / 32;
+  const int64_t per_block = (ntiles + gridDim.x - 1) / gridDim.x;
+  const int64_t t_begin = int64_t(blockIdx.x) * per_block;
+  const int64_t t_end = t_begin + per_block < ntiles ? t_begin + per_block : ntiles;
+
+  const int to = wave;            // this wave's dW row tile (if < mto)
+  const int ti = wave;            // this wave's dX row tile (if < mti)
+  f32x16 accw[kTrMT];
+#pragma unroll
+  for (int t = 0; t < kTrMT; ++t) accw[t] = f32x16{};
+  float dbs = 0.0f;               // db of row 32 to + col, this lane's half of the points
+
+  const int dz_chunks = 32 * a.out / 8;   // 16-byte chunks per tile
+  const int h_chunks = 32 * a.in / 8;
+  for (int64_t tile = t_begin; tile < t_end; ++tile) {
+    // ---- stage the tile (rows past n read as zero)
+    for (int i = threadIdx.x; i < dz_chunks + h_chunks; i += blockDim.x) {
+      if (i < dz_chunks) {
+        const int r = i / (a.out / 8), c8 = i % (a.out / 8);
+        const int64_t p = tile * 32 + r;
+        half8 v = {};
+        if (p < a.n) v = *reinterpret_cast<const half8*>(a.dz + p * a.out + 8 * c8);
+        *reinterpret_cast<half8*>(sdz + r * OP + 8 * c8) = v;
+      } else {
+        const int k = i - dz_chunks;
+        const int r = k / (a.in / 8), c8 = k % (a.in / 8);
+        const int64_t p = tile * 32 + r;
+        half8 v = {};
+        if (p < a.n) v = *reinterpret_cast<const half8*>(a.hin + p * a.in + 8 * c8);
+        *reinterpret_cast<half8*>(sh + r * IP + 8 * c8) = v;
+      }
+    }
+    __syncthreads();
+
+    // ---- dz_in^T tile ti = W^T[32 ti .. +31][:] . dz^T, masked by h > 0
+    if (ti < mtx) {
+      f32x16 acc = {};
+      for (int c = 0; c < kco; ++c) {
+        const half8 bf = *reinterpret_cast<const half8*>(sdz + col * OP + 16 * c + 8 * h);
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(swt[(ti * kco + c) * 64 + lane], bf, acc, 0, 0, 0);
+      }
+      const int64_t p = tile * 32 + col;
+      if (p < a.n) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int i0 = 32 * ti + 8 * q + 4 * h;
+          const half4v hv = *reinterpret_cast<const half4v*>(sh + col * IP + i0);
+          half4v o;
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj) o[jj] = float(hv[jj]) > 0.0f ? half_t(acc[4 * q + jj]) : half_t(0.0f);
+          *reinterpret_cast<half4v*>(a.dzin + p * a.in + i0) = o;
+        }
+      }
+    }
+    // ---- dW rows tile to += dz^T[32 to .. +31][tile points] . h[tile points][:]
+    if (to < mto) {
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        half8 af;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) af[j] = sdz[(16 * ks + 8 * h + j) * OP + 32 * to + col];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) dbs += float(af[j]);
+#pragma unroll
+        for (int t = 0; t < kTrMT; ++t) {
+          if (t < mti) {
+            half8 bf;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) bf[j] = sh[(16 * ks + 8 * h + j) * IP + 32 * t + col];
+            accw[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf, accw[t], 0, 0, 0);
+          }
+        }
+      }
+    }
+    __syncthreads();  // before the next tile overwrites the LDS tile
+  }
+
+  // ---- per-block partials: dW rows 32 to + 8q + 4h + jj, column 32 t + col
+  if (to < mto) {
+    float* dst = a.dw_part + int64_t(blockIdx.x) * a.out * a.in;
+#pragma unroll
+    for (int t = 0; t < kTrMT; ++t) {
+      if (t < mti) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj) {
+            const int o = 32 * to + 8 * q + 4 * h + jj;
+            if (o < a.out && 32 * t + col < a.in) dst[int64_t(o) * a.in + 32 * t + col] = accw[t][4 * q + jj];
+          }
+      }
+    }
+    const float other = __shfl_xor(dbs, 32, 64);
+    const int o = 32 * to + col;
+    if (h == 0 && o < a.out) a.db_part[int64_t(blockIdx.x) * a.out + o] = dbs + other;
+  }
+}
+
+// out[i] = scale * sum over b < nb of part[b * count + i], in order of b.
+__global__ void train_reduce_kernel(const float* __restrict__ part, int nb, int64_t count, float scale,
+                                    float* __restrict__ out) {
+  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < count; i += int64_t(gridDim.x) * blockDim.x) {
+    float s = 0.0f;
+    for (int b = 0; b < nb; ++b) s += part[int64_t(b) * count + i];
+    out[i] = s * scale;
+  }
+}
+
+// W^T A fragments of layer li from the fp32 copy: element
+// ((ti * kco + c) * 64 + lane) * 8 + j = W[16c + 8 (lane / 32) + j][32 ti + lane % 32].
+__global__ void train_pack_wt_kernel(const float* __restrict__ w32, int in, int out, half_t* __restrict__ wt) {
+  const int kco = (out + 15) / 16;
+  const int64_t total = int64_t(in / 32) * kco * 64 * 8;
+  const int64_t e = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (e >= total) return;
+  const int j = int(e & 7);
+  const int lane = int((e >> 3) & 63);
+  const int64_t r = e >> 9;
+  const int c = int(r % kco), ti = int(r / kco);
+  const int o = 16 * c + 8 * (lane >> 5) + j;
+  const int i = 32 * ti + (lane & 31);
+  wt[e] = half_t(o < out ? w32[int64_t(o) * in + i] : 0.0f);
+}
+
+// ------------------------------------------------------------------- host
+struct TrainPlan {
+  int groups;
+  int g0[RDV_MLP_MAX_LAYERS + 1];  // group k = layers [g0[k], g0[k + 1])
+  int blocks_fwd, blocks_bwd;
+  int64_t wt_off[RDV_MLP_MAX_LAYERS], h_off[RDV_MLP_MAX_LAYERS], g_off, dz_off[2], dw_off, db_off, loss_off;
+  int64_t total;
+};
+
+static constexpr int64_t kTrFwdLdsCap = 150 * 1024;
+
+static int64_t group_lds(const MlpLayout& lay, int l0, int l1) {
+  int64_t f = 0, b = 0;
+  for (int l = l0; l < l1; ++l) {
+    f += int64_t(lay.mt[l]) * lay.kc[l] * 1024;
+    b += int64_t(lay.mt[l]) * 128;
+  }
+  return f + b;
+}
+
+int train_check(const rdv_mlp_desc& d, const MlpLayout& lay) {
+  const int L = d.n_layers;
+  if (L < 2) return fail(RDV_ERR_UNSUPPORTED, "the training step needs at least two layers");
+  if (d.encoding != RDV_ENC_NONE) return fail(RDV_ERR_UNSUPPORTED, "the training step takes raw (unencoded) inputs");
+  for (int l = 0; l < L; ++l) {
+    if (d.prec[l] != RDV_PREC_F16) return fail(RDV_ERR_UNSUPPORTED, "the training step runs LinearFast (fp16) layers");
+    if (d.act[l] != (l + 1 < L ? RDV_ACT_RELU : RDV_ACT_NONE))
+      return fail(RDV_ERR_UNSUPPORTED, "the training step needs ReLU hidden layers and a linear head");
+  }
+  if (d.dims[0] % 16 || d.dims[0] > 128) return fail(RDV_ERR_UNSUPPORTED, "input width must be a multiple of 16, <= 128");
+  for (int l = 1; l < L; ++l)
+    if (d.dims[l] % 32 || d.dims[l] > 128)
+      return fail(RDV_ERR_UNSUPPORTED, "hidden widths must be multiples of 32, <= 128");
+  if (d.dims[L] % 8 || d.dims[L] > 128) return fail(RDV_ERR_UNSUPPORTED, "output width must be a multiple of 8, <= 128");
+  for (int l = 0; l < L; ++l)
+    if (group_lds(lay, l, l + 1) > kTrFwdLdsCap) return fail(RDV_ERR_UNSUPPORTED, "layer too large for LDS");
+  return RDV_OK;
+}
+
+static void train_plan(const rdv_mlp_desc& d, const MlpLayout& lay, int64_t n, int cu, TrainPlan* p) {
+  const int L = d.n_layers;
+  p->groups = 0;
+  int l = 0;
+  while (l < L) {
+    int e = l + 1;
+    while (e < L && group_lds(lay, l, e + 1) <= kTrFwdLdsCap) ++e;
+    p->g0[p->groups++] = l;
+    l = e;
+  }
+  p->g0[p->groups] = L;
+  const int64_t ntiles = (n + 31) / 32;
+  p->blocks_fwd = int(std::min<int64_t>(cu, (ntiles + kTrWaves - 1) / kTrWaves));
+  p->blocks_bwd = int(std::min<int64_t>(2 * int64_t(cu), ntiles));
+  int64_t off = 0;
+  auto take = [&](int64_t bytes) {
+    const int64_t o = off;
+    off = align256(off + bytes);
+    return o;
+  };
+  int maxw = 0, maxoi = 0, maxo = 0;
+  for (int i = 0; i < L; ++i) {
+    p->wt_off[i] = take(int64_t(d.dims[i] / 32 > 0 ? d.dims[i] / 32 : 1) * ((d.dims[i + 1] + 15) / 16) * 1024);
+    maxw = std::max(maxw, d.dims[i]);
+    maxoi = std::max(maxoi, d.dims[i] * d.dims[i + 1]);
+    maxo = std::max(maxo, d.dims[i + 1]);
+  }
+  p->h_off[0] = 0;
+  for (int i = 1; i < L; ++i) p->h_off[i] = take(n * d.dims[i] * 2);
+  p->g_off = take(n * d.dims[L] * 2);
+  p->dz_off[0] = take(n * maxw * 2);
+  p->dz_off[1] = take(n * maxw * 2);
+  p->dw_off = take(int64_t(p->blocks_bwd) * maxoi * 4);
+  p->db_off = take(int64_t(p->blocks_bwd) * maxo * 4);
+  p->loss_off = take(int64_t(p->blocks_fwd) * 4);
+  p->total = off;
+}
+
+int64_t train_workspace_bytes(const rdv_mlp_desc& d, const MlpLayout& lay, int64_t n, int cu) {
+  TrainPlan p;
+  train_plan(d, lay, n, cu, &p);
+  return p.total;
+}
+
+int launch_train_step(const rdv_mlp_desc& d, const MlpLayout& lay, const void* packed, const void* x,
+                      const float* target, int64_t n, void* workspace, int64_t ws_bytes, float* loss,
+                      float* const* dW, float* const* db, hipStream_t stream) {
+  DeviceInfo di;
+  int rc = device_info(&di);
+  if (rc != RDV_OK) return rc;
+  TrainPlan p;
+  train_plan(d, lay, n, di.cu_count, &p);
+  if (ws_bytes < p.total) return fail(RDV_ERR_WORKSPACE, "training workspace too small");
+  uint8_t* ws = static_cast<uint8_t*>(workspace);
+  const int L = d.n_layers;
+  const uint8_t* pk = static_cast<const uint8_t*>(packed);
+  // forward groups
+  static bool attr_set = false;
+  if (!attr_set) {
+    RDV_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&train_fwd_kernel),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, int(kTrFwdLdsCap)));
+    RDV_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&train_bwd_kernel),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, 64 * 1024));
+    attr_set = true;
+  }
+  TrainFwdArgs fa;
+  fa.packed = pk;
+  fa.lay = lay;
+  fa.L = L;
+  fa.target = target;
+  fa.g = reinterpret_cast<half_t*>(ws + p.g_off);
+  fa.loss_partial = reinterpret_cast<float*>(ws + p.loss_off);
+  fa.n = n;
+  fa.has_bias = 1;  // the packed header's flag is on the device; biases are staged either way
+  for (int i = 0; i < RDV_MLP_MAX_LAYERS; ++i) fa.hout[i] = nullptr;
+  for (int i = 0; i + 1 < L; ++i) fa.hout[i] = reinterpret_cast<half_t*>(ws + p.h_off[i + 1]);
+  for (int k = 0; k < p.groups; ++k) {
+    fa.l0 = p.g0[k];
+    fa.l1 = p.g0[k + 1];
+    fa.in = fa.l0 == 0 ? static_cast<const half_t*>(x) : reinterpret_cast<const half_t*>(ws + p.h_off[fa.l0]);
+    const int64_t lds = group_lds(lay, fa.l0, fa.l1);
+    train_fwd_kernel<<<dim3(unsigned(p.blocks_fwd)), dim3(kTrFwdThreads), size_t(lds), stream>>>(fa);
+    RDV_HIP_TRY(hipGetLastError());
+  }
+  const float scale = 1.0f / float(double(n) * d.dims[L]);
+  train_reduce_kernel<<<1, 64, 0, stream>>>(reinterpret_cast<float*>(ws + p.loss_off), p.blocks_fwd, 1, scale, loss);
+  RDV_HIP_TRY(hipGetLastError());
+  // backward, last layer first; dz ping-pongs between dz_off[0] and dz_off[1]
+  int src = -1;  // -1: g
+  for (int l = L - 1; l >= 0; --l) {
+    const int in = d.dims[l], out = d.dims[l + 1];
+    const int kco = (out + 15) / 16;
+    const int mtx = l == 0 ? 0 : in / 32, mti = (in + 31) / 32;
+    half_t* wt = reinterpret_cast<half_t*>(ws + p.wt_off[l]);
+    {
+      const int64_t total = int64_t(in / 32) * kco * 64 * 8;
+      if (total > 0) {
+        train_pack_wt_kernel<<<dim3(unsigned((total + 255) / 256)), dim3(256), 0, stream>>>(
+            reinterpret_cast<const float*>(pk + lay.w32_off[l]), in, out, wt);
+        RDV_HIP_TRY(hipGetLastError());
+      }
+    }
+    TrainBwdArgs ba;
+    const int dst = src < 0 ? 0 : src ^ 1;
+    ba.dz = src < 0 ? reinterpret_cast<const half_t*>(ws + p.g_off) : reinterpret_cast<const half_t*>(ws + p.dz_off[src]);
+    ba.hin = l == 0 ? static_cast<const half_t*>(x) : reinterpret_cast<const half_t*>(ws + p.h_off[l]);
+    ba.wt = wt;
+    ba.dzin = l == 0 ? nullptr : reinterpret_cast<half_t*>(ws + p.dz_off[dst]);
+    ba.dw_part = reinterpret_cast<float*>(ws + p.dw_off);
+    ba.db_part = reinterpret_cast<float*>(ws + p.db_off);
+    ba.in = in;
+    ba.out = out;
+    ba.n = n;
+    const int mto = (out + 31) / 32;
+    const size_t lds = size_t(mtx) * kco * 1024 + size_t(32) * (32 * mto + kTrPad) * 2 +
+                       size_t(32) * (32 * mti + kTrPad) * 2;
+    train_bwd_kernel<<<dim3(unsigned(p.blocks_bwd)), dim3(kTrBwdThreads), lds, stream>>>(ba);
+    RDV_HIP_TRY(hipGetLastError());
+    const int64_t cw = int64_t(out) * in;
+    train_reduce_kernel<<<dim3(unsigned(std::min<int64_t>((cw + 255) / 256, 4096))), dim3(256), 0, stream>>>(
+        ba.dw_part, p.blocks_bwd, cw, scale, dW[l]);
+    RDV_HIP_TRY(hipGetLastError());
+    train_reduce_kernel<<<dim3(unsigned((out + 255) / 256)), dim3(256), 0, stream>>>(ba.db_part, p.blocks_bwd, out,
+                                                                                    scale, db[l]);
+    RDV_HIP_TRY(hipGetLastError());
+    src = dst;
+  }
+  return RDV_OK;
+}
+
+}  // namespace rdv
