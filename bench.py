@@ -44,6 +44,8 @@ C3_ROTATE = 24  # 24 x (8 + 8) MiB of x / y: more than the 256 MB MALL
 # traffic per ray: 128 samples x 16 B read, 4 B dt read, 12 B colour written.
 C4_FLOP_PER_SAMPLE = 2 * (3 * 64 + 64 * 64 + 64 * 64 + 64 * 4)   # 17,280
 C4_COMPOSITE_BYTES_PER_RAY = 128 * 16 + 4 + 12
+# C5: forward 2 (32 128 + 7 128^2 + 128 16), dW the same, dX of layers 2..9
+C5_FLOP_PER_POINT = 241664 + 241664 + 233472                        # 716,800
 
 
 def _log(msg: str) -> None:
@@ -228,6 +230,40 @@ def bench_render(steps, warmup):
     return out
 
 
+def bench_train(steps, warmup):
+    """C5: one training step (forward, MSE, backward, fp32 dW) over 4,194,304 points."""
+    import torch
+    import rdv_project_amd as rdv
+    from rdv_project_amd import workloads as WL
+    x, t, layers = WL.c5()
+    m = None
+    for i, (w, b) in enumerate(layers):
+        lin = rdv.linear(w.cuda(), b.cuda(), f16=True)
+        m = lin if m is None else m >> lin
+        if i + 1 < len(layers):
+            m = m >> rdv.relu
+    xd, td = x.cuda(), t.cuda()
+    loss, grads = rdv.mse_backward(m, xd, td)
+
+    def launch(i):
+        rdv.mse_backward(m, xd, td, grads)
+
+    wall, ev = _time_launches(launch, steps, warmup)
+    n = x.shape[0]
+    tflops = C5_FLOP_PER_POINT * n / (ev * 1e-3) / 1e12
+    return {
+        "ms_per_step": round(wall, 3),
+        "kernel_ms": round(ev, 3),
+        "TFLOP_s": round(tflops, 1),
+        "mfma_peak_pct": round(100 * tflops / PEAK_FP16_TFLOPS, 2),
+        "loss": round(float(loss.item()), 5),
+        "workload": "C5 MLP training step: 4,194,304 points x ~ N(0,1) fp16 (seed 5), 32 -> 128 x 8 -> 16, ReLU, "
+                    "MSE against N(0,1) targets (seed 6), Kaiming-uniform fp16 weights (seed 7); forward, loss, "
+                    "backward with fp32 dW / db reduced over all points",
+        "kernels": "train_fwd_kernel x2 + train_bwd_kernel x9 + reductions",
+    }
+
+
 def cpu_baseline_c2(sample: int = 1 << 16):
     """The oracle's C2 forward on `sample` points: 3 warm-ups, median of 5."""
     import numpy as np
@@ -324,6 +360,10 @@ def main() -> int:
         _log("C4")
         extras["C4_render"] = bench_render(max(args.steps // 50, 10), 3)
         _log(f"C4 {extras['C4_render']}")
+        _log("C5")
+        rdv.set_synchronous(False)
+        extras["C5_train"] = bench_train(5, 2)
+        _log(f"C5 {extras['C5_train']}")
 
     cpu = None
     if not args.no_cpu_baseline:

@@ -16,13 +16,14 @@
 //    fused MLP (mlp_layout.h); every hidden output is also stored (fp16, row
 //    major) for the backward pass; the group that ends the chain computes
 //    g = 2 (y - t) and per-block partial sums of (y - t)^2.
-//  - train_bwd_kernel: one layer; a block of 4 waves stages a 32-point tile of
-//    dz_{l+1} and h_l in LDS, then wave w computes one 32-row tile of
+//  - train_bwd_kernel: one layer; a block of 4 waves stages 32-point tiles of
+//    dz_{l+1} and h_l in two LDS buffers (the next tile's loads in flight while
+//    the current one is computed), then wave w computes one 32-row tile of
 //    dz_l^T = W^T dz_{l+1}^T (v_mfma_f32_32x32x16_f16 with packed W^T fragments)
 //    and one 32-row tile of dW (K = the tile's points, operands
 //    gathered from the LDS tile); dW stays in registers across the block's whole
 //    point range and is written once as a per-block partial.
-//  - train_reduce_kernel: sums the per-block partials in a fixed order.
+//  - train_reduce1/2_kernel: sum the per-block partials in a fixed order.
 #include <algorithm>
 
 #include "mlp_core.h"
@@ -222,6 +223,7 @@ struct TrainBwdArgs {
 };
 
 constexpr int kTrPad = 8;  // LDS row padding (halves): rows 8 points apart fall in different banks
+constexpr int kTrLoads = 4;  // 16-byte loads per thread per tile: 32 x (128 + 128) halves / 256 threads
 
 __global__ __launch_bounds__(kTrBwdThreads, 2) void train_bwd_kernel(TrainBwdArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -236,10 +238,9 @@ __global__ __launch_bounds__(kTrBwdThreads, 2) void train_bwd_kernel(TrainBwdArg
   const int IP = 32 * mti + kTrPad;        // LDS h row stride (halves), columns >= in stay 0
   half8* swt = reinterpret_cast<half8*>(smem);
   half_t* sdz = reinterpret_cast<half_t*>(smem + int64_t(mtx) * kco * 1024);
-  half_t* sh = sdz + 32 * OP;
-  // W^T fragments -> LDS, zero both tiles (their padding columns stay zero)
+  // W^T fragments -> LDS, zero both tile buffers (their padding columns stay zero)
   for (int i = threadIdx.x; i < mtx * kco * 64; i += blockDim.x) swt[i] = reinterpret_cast<const half8*>(a.wt)[i];
-  for (int i = threadIdx.x; i < 32 * (OP + IP); i += blockDim.x) sdz[i] = half_t(0.0f);
+  for (int i = threadIdx.x; i < 2 * 32 * (OP + IP); i += blockDim.x) sdz[i] = half_t(0.0f);
   __syncthreads();
 
   const int64_t ntiles = (a.n + 31) / 32;
@@ -256,31 +257,60 @@ __global__ __launch_bounds__(kTrBwdThreads, 2) void train_bwd_kernel(TrainBwdArg
 
   const int dz_chunks = 32 * a.out / 8;   // 16-byte chunks per tile
   const int h_chunks = 32 * a.in / 8;
-  for (int64_t tile = t_begin; tile < t_end; ++tile) {
-    // ---- stage the tile (rows past n read as zero)
-    for (int i = threadIdx.x; i < dz_chunks + h_chunks; i += blockDim.x) {
+  const int tile_halves = 32 * (OP + IP);
+  // this thread's share of a tile's chunks (at most kTrLoads: widths <= 128)
+  auto load_tile = [&](int64_t tile, half8 (&r)[kTrLoads]) {
+#pragma unroll
+    for (int k = 0; k < kTrLoads; ++k) {
+      const int i = k * kTrBwdThreads + int(threadIdx.x);
+      half8 v = {};
       if (i < dz_chunks) {
-        const int r = i / (a.out / 8), c8 = i % (a.out / 8);
-        const int64_t p = tile * 32 + r;
-        half8 v = {};
+        const int rr = i / (a.out / 8), c8 = i % (a.out / 8);
+        const int64_t p = tile * 32 + rr;
         if (p < a.n) v = *reinterpret_cast<const half8*>(a.dz + p * a.out + 8 * c8);
-        *reinterpret_cast<half8*>(sdz + r * OP + 8 * c8) = v;
-      } else {
-        const int k = i - dz_chunks;
-        const int r = k / (a.in / 8), c8 = k % (a.in / 8);
-        const int64_t p = tile * 32 + r;
-        half8 v = {};
+      } else if (i < dz_chunks + h_chunks) {
+        const int kk = i - dz_chunks;
+        const int rr = kk / (a.in / 8), c8 = kk % (a.in / 8);
+        const int64_t p = tile * 32 + rr;
         if (p < a.n) v = *reinterpret_cast<const half8*>(a.hin + p * a.in + 8 * c8);
-        *reinterpret_cast<half8*>(sh + r * IP + 8 * c8) = v;
+      }
+      r[k] = v;
+    }
+  };
+  auto park_tile = [&](half_t* buf, const half8 (&r)[kTrLoads]) {
+#pragma unroll
+    for (int k = 0; k < kTrLoads; ++k) {
+      const int i = k * kTrBwdThreads + int(threadIdx.x);
+      if (i < dz_chunks) {
+        const int rr = i / (a.out / 8), c8 = i % (a.out / 8);
+        *reinterpret_cast<half8*>(buf + rr * OP + 8 * c8) = r[k];
+      } else if (i < dz_chunks + h_chunks) {
+        const int kk = i - dz_chunks;
+        const int rr = kk / (a.in / 8), c8 = kk % (a.in / 8);
+        *reinterpret_cast<half8*>(buf + 32 * OP + rr * IP + 8 * c8) = r[k];
       }
     }
-    __syncthreads();
+  };
+  if (t_begin < t_end) {
+    half8 r[kTrLoads];
+    load_tile(t_begin, r);
+    park_tile(sdz, r);
+  }
+  __syncthreads();
+  for (int64_t tile = t_begin; tile < t_end; ++tile) {
+    const int cur = int((tile - t_begin) & 1);
+    const half_t* tdz = sdz + cur * tile_halves;
+    const half_t* th = tdz + 32 * OP;
+    // the next tile's loads are in flight while this tile is computed
+    half8 r[kTrLoads];
+    const bool more = tile + 1 < t_end;
+    if (more) load_tile(tile + 1, r);
 
     // ---- dz_in^T tile ti = W^T[32 ti .. +31][:] . dz^T, masked by h > 0
     if (ti < mtx) {
       f32x16 acc = {};
       for (int c = 0; c < kco; ++c) {
-        const half8 bf = *reinterpret_cast<const half8*>(sdz + col * OP + 16 * c + 8 * h);
+        const half8 bf = *reinterpret_cast<const half8*>(tdz + col * OP + 16 * c + 8 * h);
         acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(swt[(ti * kco + c) * 64 + lane], bf, acc, 0, 0, 0);
       }
       const int64_t p = tile * 32 + col;
@@ -288,7 +318,7 @@ __global__ __launch_bounds__(kTrBwdThreads, 2) void train_bwd_kernel(TrainBwdArg
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           const int i0 = 32 * ti + 8 * q + 4 * h;
-          const half4v hv = *reinterpret_cast<const half4v*>(sh + col * IP + i0);
+          const half4v hv = *reinterpret_cast<const half4v*>(th + col * IP + i0);
           half4v o;
 #pragma unroll
           for (int jj = 0; jj < 4; ++jj) o[jj] = float(hv[jj]) > 0.0f ? half_t(acc[4 * q + jj]) : half_t(0.0f);
@@ -302,7 +332,7 @@ __global__ __launch_bounds__(kTrBwdThreads, 2) void train_bwd_kernel(TrainBwdArg
       for (int ks = 0; ks < 2; ++ks) {
         half8 af;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) af[j] = sdz[(16 * ks + 8 * h + j) * OP + 32 * to + col];
+        for (int j = 0; j < 8; ++j) af[j] = tdz[(16 * ks + 8 * h + j) * OP + 32 * to + col];
 #pragma unroll
         for (int j = 0; j < 8; ++j) dbs += float(af[j]);
 #pragma unroll
@@ -310,13 +340,14 @@ __global__ __launch_bounds__(kTrBwdThreads, 2) void train_bwd_kernel(TrainBwdArg
           if (t < mti) {
             half8 bf;
 #pragma unroll
-            for (int j = 0; j < 8; ++j) bf[j] = sh[(16 * ks + 8 * h + j) * IP + 32 * t + col];
+            for (int j = 0; j < 8; ++j) bf[j] = th[(16 * ks + 8 * h + j) * IP + 32 * t + col];
             accw[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf, accw[t], 0, 0, 0);
           }
         }
       }
     }
-    __syncthreads();  // before the next tile overwrites the LDS tile
+    if (more) park_tile(sdz + (cur ^ 1) * tile_halves, r);  // the other buffer: last read a tile ago
+    __syncthreads();
   }
 
   // ---- per-block partials: dW rows 32 to + 8q + 4h + jj, column 32 t + col
@@ -340,13 +371,24 @@ __global__ __launch_bounds__(kTrBwdThreads, 2) void train_bwd_kernel(TrainBwdArg
   }
 }
 
-// out[i] = scale * sum over b < nb of part[b * count + i], in order of b.
-__global__ void train_reduce_kernel(const float* __restrict__ part, int nb, int64_t count, float scale,
-                                    float* __restrict__ out) {
+// Deterministic two-stage sum over nb partials part[b][count]:
+//  stage 1: mid[s][i] = sum of part[b][i] for b = s, s + S, s + 2S, ... (in order)
+//  stage 2: out[i] = scale * sum over s < S of mid[s][i] (in order)
+constexpr int kTrSplit = 32;
+__global__ void train_reduce1_kernel(const float* __restrict__ part, int nb, int64_t count, float* __restrict__ mid) {
+  const int s = blockIdx.y;
   for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < count; i += int64_t(gridDim.x) * blockDim.x) {
-    float s = 0.0f;
-    for (int b = 0; b < nb; ++b) s += part[int64_t(b) * count + i];
-    out[i] = s * scale;
+    float acc = 0.0f;
+    for (int b = s; b < nb; b += kTrSplit) acc += part[int64_t(b) * count + i];
+    mid[int64_t(s) * count + i] = acc;
+  }
+}
+__global__ void train_reduce2_kernel(const float* __restrict__ mid, int64_t count, float scale, float* __restrict__ out) {
+  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < count; i += int64_t(gridDim.x) * blockDim.x) {
+    float acc = 0.0f;
+#pragma unroll 8
+    for (int s = 0; s < kTrSplit; ++s) acc += mid[int64_t(s) * count + i];
+    out[i] = acc * scale;
   }
 }
 
@@ -371,7 +413,7 @@ struct TrainPlan {
   int groups;
   int g0[RDV_MLP_MAX_LAYERS + 1];  // group k = layers [g0[k], g0[k + 1])
   int blocks_fwd, blocks_bwd;
-  int64_t wt_off[RDV_MLP_MAX_LAYERS], h_off[RDV_MLP_MAX_LAYERS], g_off, dz_off[2], dw_off, db_off, loss_off;
+  int64_t wt_off[RDV_MLP_MAX_LAYERS], h_off[RDV_MLP_MAX_LAYERS], g_off, dz_off[2], dw_off, db_off, loss_off, mid_off;
   int64_t total;
 };
 
@@ -440,6 +482,7 @@ static void train_plan(const rdv_mlp_desc& d, const MlpLayout& lay, int64_t n, i
   p->dw_off = take(int64_t(p->blocks_bwd) * maxoi * 4);
   p->db_off = take(int64_t(p->blocks_bwd) * maxo * 4);
   p->loss_off = take(int64_t(p->blocks_fwd) * 4);
+  p->mid_off = take(int64_t(kTrSplit) * std::max(maxoi, p->blocks_fwd) * 4);
   p->total = off;
 }
 
@@ -467,7 +510,7 @@ int launch_train_step(const rdv_mlp_desc& d, const MlpLayout& lay, const void* p
     RDV_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&train_fwd_kernel),
                                     hipFuncAttributeMaxDynamicSharedMemorySize, int(kTrFwdLdsCap)));
     RDV_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&train_bwd_kernel),
-                                    hipFuncAttributeMaxDynamicSharedMemorySize, 64 * 1024));
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, 80 * 1024));
     attr_set = true;
   }
   TrainFwdArgs fa;
@@ -490,8 +533,17 @@ int launch_train_step(const rdv_mlp_desc& d, const MlpLayout& lay, const void* p
     RDV_HIP_TRY(hipGetLastError());
   }
   const float scale = 1.0f / float(double(n) * d.dims[L]);
-  train_reduce_kernel<<<1, 64, 0, stream>>>(reinterpret_cast<float*>(ws + p.loss_off), p.blocks_fwd, 1, scale, loss);
-  RDV_HIP_TRY(hipGetLastError());
+  float* mid = reinterpret_cast<float*>(ws + p.mid_off);
+  auto reduce = [&](const float* part, int nb, int64_t count, float* out) -> int {
+    const unsigned gx = unsigned(std::min<int64_t>((count + 255) / 256, 1024));
+    train_reduce1_kernel<<<dim3(gx, kTrSplit), dim3(256), 0, stream>>>(part, nb, count, mid);
+    RDV_HIP_TRY(hipGetLastError());
+    train_reduce2_kernel<<<dim3(gx), dim3(256), 0, stream>>>(mid, count, scale, out);
+    RDV_HIP_TRY(hipGetLastError());
+    return RDV_OK;
+  };
+  rc = reduce(reinterpret_cast<float*>(ws + p.loss_off), p.blocks_fwd, 1, loss);
+  if (rc != RDV_OK) return rc;
   // backward, last layer first; dz ping-pongs between dz_off[0] and dz_off[1]
   int src = -1;  // -1: g
   for (int l = L - 1; l >= 0; --l) {
@@ -519,17 +571,14 @@ int launch_train_step(const rdv_mlp_desc& d, const MlpLayout& lay, const void* p
     ba.out = out;
     ba.n = n;
     const int mto = (out + 31) / 32;
-    const size_t lds = size_t(mtx) * kco * 1024 + size_t(32) * (32 * mto + kTrPad) * 2 +
-                       size_t(32) * (32 * mti + kTrPad) * 2;
+    const size_t lds = size_t(mtx) * kco * 1024 + 2 * (size_t(32) * (32 * mto + kTrPad) * 2 +
+                                                        size_t(32) * (32 * mti + kTrPad) * 2);
     train_bwd_kernel<<<dim3(unsigned(p.blocks_bwd)), dim3(kTrBwdThreads), lds, stream>>>(ba);
     RDV_HIP_TRY(hipGetLastError());
-    const int64_t cw = int64_t(out) * in;
-    train_reduce_kernel<<<dim3(unsigned(std::min<int64_t>((cw + 255) / 256, 4096))), dim3(256), 0, stream>>>(
-        ba.dw_part, p.blocks_bwd, cw, scale, dW[l]);
-    RDV_HIP_TRY(hipGetLastError());
-    train_reduce_kernel<<<dim3(unsigned((out + 255) / 256)), dim3(256), 0, stream>>>(ba.db_part, p.blocks_bwd, out,
-                                                                                    scale, db[l]);
-    RDV_HIP_TRY(hipGetLastError());
+    rc = reduce(ba.dw_part, p.blocks_bwd, int64_t(out) * in, dW[l]);
+    if (rc != RDV_OK) return rc;
+    rc = reduce(ba.db_part, p.blocks_bwd, out, db[l]);
+    if (rc != RDV_OK) return rc;
     src = dst;
   }
   return RDV_OK;
