@@ -162,6 +162,47 @@ int rdv_winograd3x3_transform_weight(const void* w, int32_t w_layout, int32_t w_
 int rdv_winograd3x3_forward(const rdv_conv_desc* desc, const void* x, const void* U, const float* bias,
                             void* y, void* stream);
 
+/* ------------------------------------------------------ tensor operations */
+/* Storage of a linear tensor op's weight:
+ *   F32        fp32 [out][in] (PyTorch nn.Linear layout), read at every dispatch;
+ *   F16        fp16 [out][in] (LinearTensorOpSimple's pre-cast copy, nn.py:493-501);
+ *   F16_TILED16 fp16 [out/16][in/16][16 k][16 n] (LinearTensorOpFast's pre-tiled
+ *              copy, nn.py:472-490). */
+enum { RDV_WKIND_F32 = 0, RDV_WKIND_F16 = 1, RDV_WKIND_F16_TILED16 = 2 };
+
+typedef struct rdv_linear_op_desc {
+  int64_t rows;          /* batch rows of x and y (>= 0)                            */
+  int32_t in_features;   /* multiple of 8                                           */
+  int32_t out_features;  /* multiple of 4                                           */
+  int32_t precision;     /* RDV_PREC_F16: x and W rounded to fp16, fp32 accumulation
+                            (LinearTensorOp{Small,Simple,Fast,Mine}); RDV_PREC_F32:
+                            fp32 throughout (LinearTensorOp)                        */
+  int32_t wkind;         /* RDV_WKIND_*; F16 kinds need RDV_PREC_F16                */
+  int32_t relu;          /* 1: y = max(y, 0) after the bias (build-defined fusion; the
+                            reference's tensor-op path has a separate ReLUTensorOp)  */
+  int32_t reserved;      /* 0                                                       */
+} rdv_linear_op_desc;
+
+/* Host-only shape check; launches nothing. */
+int rdv_linear_op_validate(const rdv_linear_op_desc* desc);
+
+/* y[rows, out] = x[rows, in] W^T + bias, fp32 x / bias / y (16-byte aligned device
+ * pointers), weight per desc->wkind (16-byte aligned for F32 and F16).
+ * Replaces the dispatch of LinearTensorOp (src/rdv/domain/nn.py:377-411,
+ * src/rdv/shaders/tensors/linear_tensor_op.h:8-51), LinearTensorOpSmall
+ * (nn.py:1303-1411, linear_tensor_op_small.h:50-247), LinearTensorOpSimple
+ * (nn.py:1204-1300, linear_tensor_op_simple.h:49-116), LinearTensorOpFast
+ * (nn.py:541-605, linear_tensor_op_fast.h:37-122) and LinearTensorOpMine
+ * (nn.py:1153-1201, linear_tensor_op_mine.h:51-133), all through
+ * TensorOpEvaluator (src/rdv/maths/__init__.py:1382-1399). */
+int rdv_linear_op(const rdv_linear_op_desc* desc, const float* x, const void* weight, const float* bias, float* y,
+                  void* stream);
+
+/* y[i] = max(x[i], 0) for i < n (fp32, 16-byte aligned; a NaN maps to 0).
+ * Replaces ReLUTensorOp (src/rdv/domain/nn.py:362-374,
+ * src/rdv/shaders/tensors/relu_tensor_op.h:3-22). */
+int rdv_relu_op(const float* x, float* y, int64_t n, void* stream);
+
 /* ------------------------------------------------- MLP training step (C5) */
 /* Bytes of workspace rdv_mlp_train_step needs for `desc` and n points (< 0 if
  * the chain is not supported by the training kernels). */

@@ -27,6 +27,12 @@ from .rendering import Cameras, EmissionAbsorption, RaymarchingTransmittance
 from .nn import (
     Conv2DTensorOpWinograd3x3,
     DensityRGB,
+    LinearTensorOp,
+    LinearTensorOpFast,
+    LinearTensorOpMine,
+    LinearTensorOpSimple,
+    LinearTensorOpSmall,
+    ReLUTensorOp,
     FrequencyEncoding,
     Linear,
     LinearFast,

@@ -28,6 +28,7 @@ ENC_NONE, ENC_FREQ = 0, 1
 LAYOUT_HWC, LAYOUT_CHW = 0, 1
 DTYPE_F32, DTYPE_F16 = 0, 1
 WLAYOUT_RSCK, WLAYOUT_KCRS = 0, 1
+WKIND_F32, WKIND_F16, WKIND_F16_TILED16 = 0, 1, 2
 
 
 class MlpDesc(C.Structure):
@@ -70,6 +71,19 @@ class CameraDesc(C.Structure):
     ]
 
 
+class LinearOpDesc(C.Structure):
+    """Mirror of rdv_linear_op_desc."""
+    _fields_ = [
+        ("rows", C.c_int64),
+        ("in_features", C.c_int32),
+        ("out_features", C.c_int32),
+        ("precision", C.c_int32),
+        ("wkind", C.c_int32),
+        ("relu", C.c_int32),
+        ("reserved", C.c_int32),
+    ]
+
+
 class RDVError(RuntimeError):
     """A HIP runtime failure reported by the library."""
 
@@ -96,6 +110,10 @@ _SIGNATURES = {
     "rdv_composite": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int64, C.c_int32, C.c_void_p, C.c_void_p]),
     "rdv_raymarch_transmittance": (C.c_int, [C.POINTER(MlpDesc), C.c_void_p, C.c_void_p, C.c_int64,
                                              C.POINTER(C.c_float), C.c_float, C.c_float, C.c_void_p, C.c_void_p]),
+    "rdv_linear_op_validate": (C.c_int, [C.POINTER(LinearOpDesc)]),
+    "rdv_linear_op": (C.c_int, [C.POINTER(LinearOpDesc), C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
+                                C.c_void_p]),
+    "rdv_relu_op": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int64, C.c_void_p]),
     "rdv_winograd3x3_validate": (C.c_int, [C.POINTER(ConvDesc)]),
     "rdv_winograd3x3_weight_bytes": (C.c_int64, [C.c_int32, C.c_int32]),
     "rdv_winograd3x3_transform_weight": (C.c_int, [C.c_void_p, C.c_int32, C.c_int32, C.c_int32, C.c_int32,

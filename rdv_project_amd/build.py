@@ -28,6 +28,7 @@ SOURCES = [
     "winograd.hip",
     "render.hip",
     "train.hip",
+    "linear_op.hip",
 ]
 
 ARCH = os.environ.get("RDV_OFFLOAD_ARCH", "gfx950")

@@ -72,6 +72,20 @@ int launch_raymarch_transmittance(const rdv_mlp_desc& d, const MlpLayout& lay, c
 int launch_winograd3x3(const rdv_conv_desc& d, const void* x, const void* U, const float* bias, void* y,
                        hipStream_t stream);
 
+int linear_op_check(const rdv_linear_op_desc& d, std::string* why);
+int launch_linear_op(const rdv_linear_op_desc& d, const float* x, const void* w, const float* bias, float* y,
+                     hipStream_t stream);
+int launch_relu_op(const float* x, float* y, int64_t n, hipStream_t stream);
+
+static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+static int check_linear_op(const rdv_linear_op_desc* d) {
+  if (!d) return fail(RDV_ERR_INVALID, "linear op descriptor is NULL");
+  std::string why;
+  if (linear_op_check(*d, &why) != RDV_OK) return fail(RDV_ERR_INVALID, why);
+  return RDV_OK;
+}
+
 static int check_conv(const rdv_conv_desc* d) {
   if (!d) return fail(RDV_ERR_INVALID, "conv descriptor is NULL");
   if (d->batch < 1) return fail(RDV_ERR_INVALID, "batch must be >= 1");
@@ -238,6 +252,29 @@ int rdv_winograd3x3_forward(const rdv_conv_desc* desc, const void* x, const void
   const size_t oal = desc->out_dtype == RDV_DTYPE_F16 ? 8 : 16;
   if (reinterpret_cast<uintptr_t>(y) % oal) return fail(RDV_ERR_INVALID, "y is not aligned for vector stores");
   return launch_winograd3x3(*desc, x, U, bias, y, static_cast<hipStream_t>(stream));
+}
+
+int rdv_linear_op_validate(const rdv_linear_op_desc* desc) { return check_linear_op(desc); }
+
+int rdv_linear_op(const rdv_linear_op_desc* desc, const float* x, const void* weight, const float* bias, float* y,
+                  void* stream) {
+  if (int rc = check_linear_op(desc)) return rc;
+  if (desc->rows == 0) return RDV_OK;
+  if (!x || !weight || !bias || !y) return fail(RDV_ERR_INVALID, "linear op: NULL pointer");
+  if (!aligned16(x) || !aligned16(y)) return fail(RDV_ERR_INVALID, "linear op: x and y must be 16-byte aligned");
+  if (desc->wkind != RDV_WKIND_F16_TILED16 && !aligned16(weight))
+    return fail(RDV_ERR_INVALID, "linear op: weight must be 16-byte aligned");
+  if ((reinterpret_cast<uintptr_t>(weight) & 1) != 0) return fail(RDV_ERR_INVALID, "linear op: weight misaligned");
+  if ((reinterpret_cast<uintptr_t>(bias) & 3) != 0) return fail(RDV_ERR_INVALID, "linear op: bias misaligned");
+  return launch_linear_op(*desc, x, weight, bias, y, static_cast<hipStream_t>(stream));
+}
+
+int rdv_relu_op(const float* x, float* y, int64_t n, void* stream) {
+  if (n < 0) return fail(RDV_ERR_INVALID, "relu op: n must be >= 0");
+  if (n == 0) return RDV_OK;
+  if (!x || !y) return fail(RDV_ERR_INVALID, "relu op: NULL pointer");
+  if (!aligned16(x) || !aligned16(y)) return fail(RDV_ERR_INVALID, "relu op: x and y must be 16-byte aligned");
+  return launch_relu_op(x, y, n, static_cast<hipStream_t>(stream));
 }
 
 int64_t rdv_mlp_train_workspace_bytes(const rdv_mlp_desc* desc, int64_t n) {

@@ -151,15 +151,22 @@ class Sensor(Grid):
 class TensorOperation:
     """Self-materialising 2-D op, dispatched eagerly at construction
     (reference: maths:1251-1380).  Subclasses set up their inputs and call
-    super().__init__(shape); `result` then holds the [rows, cols] fp32 output."""
+    super().__init__(shape); `result` then holds the [rows, cols] fp32 output.
+    rows and cols must be multiples of the class's _TILE_ROWS / _TILE_COLS
+    (maths:1335-1337)."""
 
     _upstream = None
     _extra_upstreams = ()
+    _TILE_ROWS = 4  # BLOCK_ROWS (maths:945)
+    _TILE_COLS = 8  # BLOCK_CHANNELS (maths:946)
 
     def __init__(self, shape: list[int]) -> None:
         import torch
         from .core import device
+        cls = type(self)
         assert len(shape) == 2, "TensorOperation only supports 2D (rows, channels) shapes"
+        assert shape[0] % cls._TILE_ROWS == 0, f"rows ({shape[0]}) must be a multiple of {cls._TILE_ROWS}"
+        assert shape[1] % cls._TILE_COLS == 0, f"channels ({shape[1]}) must be a multiple of {cls._TILE_COLS}"
         self._shape = list(shape)
         self.shape = list(shape)
         self._result_t = torch.empty(self._shape, dtype=torch.float32, device=device())

@@ -3,6 +3,13 @@
 Map nodes compose with `>>` and are evaluated by the fused HIP MLP kernels:
   Linear / LinearFast / linear   nn.py:25-104
   ReLU / relu                    nn.py:107-119
+TensorOperation nodes dispatch eagerly, one kernel per op:
+  ReLUTensorOp                   nn.py:362-374
+  LinearTensorOp                 nn.py:377-411
+  LinearTensorOpFast             nn.py:541-605
+  LinearTensorOpMine             nn.py:1153-1201
+  LinearTensorOpSimple           nn.py:1204-1300
+  LinearTensorOpSmall            nn.py:1303-1411
   Conv2DTensorOpWinograd3x3      nn.py:1002-1087
 Build-defined additions (no reference counterpart, needed by the benchmark
 configurations): FrequencyEncoding, Softplus, Sigmoid, DensityRGB.
@@ -11,7 +18,7 @@ from __future__ import annotations
 
 import torch
 
-from . import _conv, _lib
+from . import _conv, _lib, _tensor_ops
 from .core import RDVObject, wrap
 from .maths import Map, TensorOperation, _as_op_input
 
@@ -131,6 +138,180 @@ class FrequencyEncoding(Map):
 # ============================================================ TENSOR OPERATIONS
 
 
+def _op_float32(data: RDVObject, what: str) -> RDVObject:
+    """The reference binds these inputs as Buffer[FLOAT32]; other float
+    buffers are converted (a copy, so later in-place updates of the original
+    are not seen)."""
+    if data.scalar_type == torch.float32:
+        return data
+    if not data.scalar_type.is_floating_point:
+        raise TypeError(f"{what} must be a floating-point buffer, got {data.scalar_type}")
+    return wrap(data.as_tensor("torch").to(torch.float32))
+
+
+class ReLUTensorOp(TensorOperation):
+    """f(x) = max(x, 0), elementwise (reference: nn.py:362-374,
+    shaders/tensors/relu_tensor_op.h:3-22).  x may be another TensorOperation
+    or raw data; a NaN input gives 0."""
+
+    def __init__(self, x) -> None:
+        data, shape, upstream = _as_op_input(x)
+        self.x_buf = _op_float32(data, "x")
+        self._upstream = upstream
+        super().__init__(shape)
+
+    def _forward(self) -> None:
+        _tensor_ops.relu(self.x_buf.as_tensor("torch"), self._result_t)
+
+
+class _LinearTensorOpBase(TensorOperation):
+    """y = x W^T + b for x [batch, in_features], weight [out_features,
+    in_features] (PyTorch nn.Linear layout), bias [out_features]; result
+    [batch, out_features] fp32.  Shared argument handling of the reference's
+    linear tensor ops (nn.py:377-411, 541-605, 1153-1411)."""
+
+    _precision = _lib.PREC_F16
+    _wkind = _lib.WKIND_F32
+
+    def _bind(self, x, weight, bias):
+        name = type(self).__name__
+        data, shape, upstream = _as_op_input(x)
+        assert len(shape) == 2, f"{name} requires a 2D (BATCH, in_features) input"
+        batch, in_features = shape
+        weight = weight if isinstance(weight, RDVObject) else wrap(weight)
+        bias = bias if isinstance(bias, RDVObject) else wrap(bias)
+        assert len(weight.shape) == 2, "weight must be [out_features, in_features]"
+        out_features, weight_in_features = weight.shape
+        assert weight_in_features == in_features, "weight's own in_features must match x's own trailing dim"
+        assert tuple(bias.shape) == (out_features,), "bias must be [out_features]"
+        self.x_buf = _op_float32(data, "x")
+        self.bias = _op_float32(bias, "bias")
+        self._upstream = upstream
+        self.INF, self.OUTF = int(in_features), int(out_features)
+        return int(batch), int(in_features), int(out_features), weight
+
+    def _finish(self, batch: int) -> None:
+        self._desc = _tensor_ops.linear_desc(batch, self.INF, self.OUTF, self._precision, self._wkind)
+        _tensor_ops.validate(self._desc, type(self).__name__)
+        super().__init__([batch, self.OUTF])
+
+    def _weight_buffer(self) -> torch.Tensor:
+        return self.weight.as_tensor("torch")
+
+    def _forward(self) -> None:
+        _tensor_ops.linear(self._desc, self.x_buf.as_tensor("torch"), self._weight_buffer(),
+                           self.bias.as_tensor("torch"), self._result_t, type(self).__name__)
+
+
+class LinearTensorOp(_LinearTensorOpBase):
+    """y = W @ x + b in fp32 (reference: nn.py:377-411,
+    shaders/tensors/linear_tensor_op.h:8-51).  batch must be a multiple of 4,
+    in_features and out_features multiples of 8.  The fp32 weight is read at
+    every dispatch, so in-place updates of it are seen by evaluate()."""
+
+    _precision = _lib.PREC_F32
+    _wkind = _lib.WKIND_F32
+
+    def __init__(self, x, weight, bias) -> None:
+        batch, in_features, out_features, weight = self._bind(x, weight, bias)
+        assert in_features % 8 == 0, f"in_features ({in_features}) must be a multiple of 8"
+        assert out_features % 8 == 0, f"out_features ({out_features}) must be a multiple of 8"
+        self.weight = _op_float32(weight, "weight")
+        self._finish(batch)
+
+
+class LinearTensorOpSmall(_LinearTensorOpBase):
+    """y = W @ x + b with x and W rounded to fp16 and fp32 accumulation
+    (reference: nn.py:1303-1411, shaders/tensors/linear_tensor_op_small.h:50-247).
+    batch must be a multiple of 32, in_features and out_features multiples of
+    16 and at most 128.  The fp32 weight is read (and rounded) at every
+    dispatch.  SPT is the reference's subgroups-per-workgroup choice; the HIP
+    kernel stages the whole weight block in LDS regardless."""
+
+    _TILE_ROWS = 32
+    _TILE_COLS = 16
+
+    def __init__(self, x, weight, bias) -> None:
+        batch, in_features, out_features, weight = self._bind(x, weight, bias)
+        assert batch % 32 == 0, f"batch ({batch}) must be a multiple of 32"
+        assert in_features % 16 == 0, f"in_features ({in_features}) must be a multiple of 16"
+        assert out_features % 16 == 0, f"out_features ({out_features}) must be a multiple of 16"
+        assert in_features <= 128, f"in_features ({in_features}) must be at most 128 (see this op's own docstring)"
+        assert out_features <= 128, f"out_features ({out_features}) must be at most 128 (see this op's own docstring)"
+        self.SPT = _tensor_ops.max_subgroups(fixed_bytes=out_features * in_features * 2,
+                                             per_subgroup_bytes=32 * in_features * 2,
+                                             divides=lambda s: batch % (32 * s) == 0)
+        self.weight = _op_float32(weight, "weight")
+        self._finish(batch)
+
+
+class LinearTensorOpSimple(_LinearTensorOpBase):
+    """y = W @ x + b with x and W rounded to fp16 and fp32 accumulation
+    (reference: nn.py:1204-1300, shaders/tensors/linear_tensor_op_simple.h:49-116).
+    batch must be a multiple of 32, in_features a multiple of 16 and
+    out_features a multiple of 16 * SPT.  The weight is cast to fp16 once, at
+    construction (_cast_fp16, nn.py:493-501)."""
+
+    _TILE_ROWS = 32
+    _TILE_COLS = 16
+    _wkind = _lib.WKIND_F16
+
+    def __init__(self, x, weight, bias) -> None:
+        batch, in_features, out_features, weight = self._bind(x, weight, bias)
+        assert batch % 32 == 0, f"batch ({batch}) must be a multiple of 32"
+        assert in_features % 16 == 0, f"in_features ({in_features}) must be a multiple of 16"
+        spt = _tensor_ops.max_subgroups(fixed_bytes=32 * in_features * 2,
+                                        per_subgroup_bytes=16 * in_features * 2,
+                                        divides=lambda s: out_features % (16 * s) == 0)
+        out_tile = 16 * spt
+        assert out_features % out_tile == 0, f"out_features ({out_features}) must be a multiple of {out_tile}"
+        self.SPT = spt
+        self.weight = wrap(_tensor_ops.cast_fp16(weight.as_tensor("torch")))
+        self._finish(batch)
+
+
+class LinearTensorOpFast(_LinearTensorOpBase):
+    """y = W @ x + b with x and W rounded to fp16 and fp32 accumulation
+    (reference: nn.py:541-605, shaders/tensors/linear_tensor_op_fast.h:37-122).
+    batch must be a multiple of 64, in_features a multiple of 16, out_features a
+    multiple of 32.  The weight is rearranged once, at construction, into the
+    reference's fp16 tile layout weight_tiled (_tile_weight_fp16,
+    nn.py:472-490), which the kernel reads directly."""
+
+    _TILE_ROWS = 64
+    _TILE_COLS = 32
+    _wkind = _lib.WKIND_F16_TILED16
+
+    def __init__(self, x, weight, bias) -> None:
+        batch, in_features, out_features, weight = self._bind(x, weight, bias)
+        assert batch % 64 == 0, f"batch ({batch}) must be a multiple of 64"
+        assert in_features % 16 == 0, f"in_features ({in_features}) must be a multiple of 16"
+        assert out_features % 32 == 0, f"out_features ({out_features}) must be a multiple of 32"
+        self.weight_tiled = wrap(_tensor_ops.tile_weight_fp16(weight.as_tensor("torch")))
+        self._finish(batch)
+
+    def _weight_buffer(self) -> torch.Tensor:
+        return self.weight_tiled.as_tensor("torch")
+
+
+class LinearTensorOpMine(_LinearTensorOpBase):
+    """y = W @ x + b with x and W rounded to fp16 and fp32 accumulation
+    (reference: nn.py:1153-1201, shaders/tensors/linear_tensor_op_mine.h:51-133).
+    batch must be a multiple of 32, in_features and out_features multiples of
+    16.  The fp32 weight is read (and rounded) at every dispatch."""
+
+    _TILE_ROWS = 32
+    _TILE_COLS = 16
+
+    def __init__(self, x, weight, bias) -> None:
+        batch, in_features, out_features, weight = self._bind(x, weight, bias)
+        assert batch % 32 == 0, f"batch ({batch}) must be a multiple of 32"
+        assert in_features % 16 == 0, f"in_features ({in_features}) must be a multiple of 16"
+        assert out_features % 16 == 0, f"out_features ({out_features}) must be a multiple of 16"
+        self.weight = _op_float32(weight, "weight")
+        self._finish(batch)
+
+
 class Conv2DTensorOpWinograd3x3(TensorOperation):
     """'same'-padded (zero border), stride-1 3x3 convolution via Winograd
     F(2x2, 3x3) (reference: nn.py:1002-1087,
@@ -148,6 +329,9 @@ class Conv2DTensorOpWinograd3x3(TensorOperation):
     except for its shared-memory limits (in/out channels <= 48 and
     (H/2)(W/2) % 32 == 0, nn.py:1066-1078), which this kernel does not have:
     in_channels may be up to 64 and out_channels up to 1024."""
+
+    _TILE_ROWS = 1
+    _TILE_COLS = 16
 
     def __init__(self, x, weight, bias, H: int, W: int) -> None:
         data, shape, upstream = _as_op_input(x)

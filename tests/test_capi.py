@@ -149,3 +149,47 @@ def test_winograd_weight_bytes():
     assert lib.rdv_winograd3x3_weight_bytes(64, 64) == 16 * 2 * 4 * 64 * 8 * 2
     assert lib.rdv_winograd3x3_weight_bytes(5, 16) == 16 * 1 * 1 * 64 * 8 * 2
     assert lib.rdv_winograd3x3_weight_bytes(64, 40) == _lib.RDV_ERR_INVALID
+
+
+def _lin(rows=4096, inf=128, outf=128, prec=_lib.PREC_F16, wkind=_lib.WKIND_F32, relu=0):
+    d = _lib.LinearOpDesc()
+    d.rows, d.in_features, d.out_features, d.precision, d.wkind, d.relu, d.reserved = rows, inf, outf, prec, wkind, relu, 0
+    return d
+
+
+def test_linear_op_validate_accepts_reference_shapes():
+    lib = _lib.load()
+    for d in (_lin(), _lin(rows=4, inf=8, outf=8, prec=_lib.PREC_F32), _lin(inf=4096, outf=1000),
+              _lin(inf=32, outf=16, wkind=_lib.WKIND_F16), _lin(rows=64, inf=64, outf=96, wkind=_lib.WKIND_F16_TILED16),
+              _lin(rows=0)):
+        assert lib.rdv_linear_op_validate(C.byref(d)) == 0, _lib.last_error()
+
+
+@pytest.mark.parametrize("kw,fragment", [
+    (dict(inf=12), "in_features"),
+    (dict(inf=0), "in_features"),
+    (dict(outf=6), "out_features"),
+    (dict(rows=-1), "rows"),
+    (dict(prec=7), "precision"),
+    (dict(wkind=9), "weight kind"),
+    (dict(prec=_lib.PREC_F32, wkind=_lib.WKIND_F16), "fp32 weight"),
+    (dict(inf=24, wkind=_lib.WKIND_F16_TILED16), "tiled"),
+])
+def test_linear_op_validate_rejects(kw, fragment):
+    lib = _lib.load()
+    assert lib.rdv_linear_op_validate(C.byref(_lin(**kw))) == _lib.RDV_ERR_INVALID
+    assert fragment in _lib.last_error()
+
+
+def test_linear_op_host_errors_need_no_device():
+    lib = _lib.load()
+    # invalid descriptor, NULL and misaligned pointers are refused before any HIP call
+    assert lib.rdv_linear_op(C.byref(_lin(inf=12)), None, None, None, None, None) == _lib.RDV_ERR_INVALID
+    assert lib.rdv_linear_op(C.byref(_lin()), None, None, None, None, None) == _lib.RDV_ERR_INVALID
+    assert "NULL" in _lib.last_error()
+    assert lib.rdv_linear_op(C.byref(_lin()), 0x1004, 0x2000, 0x3000, 0x4000, None) == _lib.RDV_ERR_INVALID
+    assert "aligned" in _lib.last_error()
+    assert lib.rdv_linear_op(C.byref(_lin(rows=0)), None, None, None, None, None) == 0
+    assert lib.rdv_relu_op(None, None, -1, None) == _lib.RDV_ERR_INVALID
+    assert lib.rdv_relu_op(None, None, 0, None) == 0
+    assert lib.rdv_relu_op(0x1008, 0x2000, 16, None) == _lib.RDV_ERR_INVALID
