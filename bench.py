@@ -264,6 +264,44 @@ def bench_train(steps, warmup):
     }
 
 
+def bench_tensor_ops(steps, warmup):
+    """TensorOperation path at the C5 layer shape: LinearTensorOpSmall over
+    4,194,304 x 128 -> 128 fp32 rows (x and y each 2 GiB, far beyond the MALL)
+    and ReLUTensorOp over the same 4,194,304 x 128 buffer."""
+    import torch
+    import rdv_project_amd as rdv
+    n, inf, outf = 4_194_304, 128, 128
+    g = torch.Generator(device="cuda").manual_seed(12)
+    x = torch.randn(n, inf, device="cuda", generator=g)
+    W = torch.randn(outf, inf, device="cuda", generator=g) / inf ** 0.5
+    b = torch.randn(outf, device="cuda", generator=g)
+    op = rdv.LinearTensorOpSmall(x, W, b)
+    wall, ev = _time_launches(lambda i: op.evaluate(), steps, warmup)
+    nbytes = n * (inf + outf) * 4
+    relu = rdv.ReLUTensorOp(x)
+    rwall, rev = _time_launches(lambda i: relu.evaluate(), steps, warmup)
+    rbytes = n * inf * 8
+    return {
+        "LinearTensorOpSmall": {
+            "workload": "4,194,304 x 128 -> 128, fp32 x / y, fp16 operands, fp32 accumulate (seed 12)",
+            "ms_per_call": round(wall, 4),
+            "kernel_ms": round(ev, 4),
+            "GB_s": round(nbytes / (ev * 1e-3) / 1e9, 1),
+            "hbm_peak_pct": round(100 * nbytes / (ev * 1e-3) / 1e9 / PEAK_HBM_GBS, 2),
+            "TFLOP_s": round(2.0 * n * inf * outf / (ev * 1e-3) / 1e12, 1),
+            "bytes_per_call": nbytes,
+            "kernel": "linear_op_kernel<true, 2, 4>",
+        },
+        "ReLUTensorOp": {
+            "workload": "4,194,304 x 128 fp32",
+            "kernel_ms": round(rev, 4),
+            "GB_s": round(rbytes / (rev * 1e-3) / 1e9, 1),
+            "hbm_peak_pct": round(100 * rbytes / (rev * 1e-3) / 1e9 / PEAK_HBM_GBS, 2),
+            "kernel": "relu_op_kernel",
+        },
+    }
+
+
 def cpu_baseline_c2(sample: int = 1 << 16):
     """The oracle's C2 forward on `sample` points: 3 warm-ups, median of 5."""
     import numpy as np
@@ -364,6 +402,9 @@ def main() -> int:
         rdv.set_synchronous(False)
         extras["C5_train"] = bench_train(5, 2)
         _log(f"C5 {extras['C5_train']}")
+        _log("tensor ops")
+        extras["tensor_ops"] = bench_tensor_ops(20, 3)
+        _log(f"tensor ops {extras['tensor_ops']}")
 
     cpu = None
     if not args.no_cpu_baseline:

@@ -252,7 +252,7 @@ __device__ __forceinline__ void load_ray(const f32x4* __restrict__ src, int samp
 #pragma unroll
   for (int j = 0; j < SPL; ++j) {
     const int i = lane * SPL + j;
-    v[j] = i < samples ? __builtin_nontemporal_load(src + i) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    v[j] = i < samples ? src[i] : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   }
 }
 
@@ -317,7 +317,7 @@ __global__ __launch_bounds__(256) void composite_long_kernel(const f32x4* __rest
     for (int k = 0; k < samples; k += 64) {
       const int i = k + lane;
       f32x4 v = {0.0f, 0.0f, 0.0f, 0.0f};
-      if (i < samples) v = __builtin_nontemporal_load(src + i);
+      if (i < samples) v = src[i];
       const float ad = v[0] * dt;
       const float incl = wave_scan_incl(ad, lane);
       const float total = lane_value(incl, 63);
