@@ -72,9 +72,23 @@ def _mlp_setup(x_cpu, layers, acts, enc=None):
     return m, p, packed, xs, ys
 
 
-def _time_launches(launch, steps: int, warmup: int):
-    """Returns (wall ms per step, event ms per step) for `steps` back-to-back launches."""
+PREWARM_S = 0.5  # seconds of untimed launches before the warm-up steps
+
+
+def _time_launches(launch, steps: int, warmup: int, prewarm_s: float = PREWARM_S):
+    """Returns (wall ms per step, event ms per step) for `steps` back-to-back
+    launches.  Before the `warmup` steps the same launches run, untimed, for
+    `prewarm_s` seconds: the GPU takes longer than a few hundred short launches
+    to reach its steady-state clock (the first 40 ms of C2 launches run ~7%
+    slower than the rest), and the benchmark reports the steady state."""
     import torch
+    t_end = time.perf_counter() + prewarm_s
+    i = 0
+    while time.perf_counter() < t_end:
+        for _ in range(64):
+            launch(i)
+            i += 1
+        torch.cuda.synchronize()
     for i in range(warmup):
         launch(i)
     torch.cuda.synchronize()

@@ -70,24 +70,11 @@ __global__ __launch_bounds__(kThreads, 1) void mlp_fused_f16_kernel(FusedArgs a)
   // all biases zero (flag computed by the packer): skip seeding the accumulators
   const bool has_bias = (reinterpret_cast<const MlpPackHeader*>(a.packed)->flags & kMlpHasBias) != 0;
 
-  // ---- start-up: biases and fragments -> LDS, counter reset
-#pragma unroll
-  for (int l = 0; l < N::kL; ++l) {
-    const float* src = reinterpret_cast<const float*>(a.packed + a.lay.bias_off[l]);
-    for (int i = threadIdx.x; i < 32 * N::mt(l); i += kThreads) sb[N::bias_base(l) + i] = src[i];
-    const half8* fsrc = reinterpret_cast<const half8*>(a.packed + a.lay.frag_off[l]);
-    for (int i = threadIdx.x; i < N::kc(l) * N::mt(l) * 64; i += kThreads) sw[N::frag_base(l) * 64 + i] = fsrc[i];
-  }
-  if (threadIdx.x == 0) s_next = 0;
-  __syncthreads();
-
-  auto claim = [&]() {
-    int t = 0;
-    if (lane == 0) t = atomicAdd(&s_next, 1);
-    return __builtin_amdgcn_readfirstlane(t);
-  };
-  // Rows of block tile lt (clamped to valid rows: tiles past the end are never
-  // computed, rows past the end of the last tile feed outputs that are not stored).
+  // ---- start-up.  Wave w's first tile is block tile w (the counter starts
+  // past them), so its input loads are issued before the weight staging and
+  // their latency overlaps it.
+  // Rows of block tile lt, clamped to valid rows: tiles past the end are never
+  // computed, and rows past the end of the last tile feed outputs never stored.
   const int64_t last = a.nrows - 1;
   auto load_tile = [&](int lt, float (&r)[D]) {
     int64_t row = (t_begin + (lt < nt ? lt : 0)) * 32 + col;
@@ -101,13 +88,27 @@ __global__ __launch_bounds__(kThreads, 1) void mlp_fused_f16_kernel(FusedArgs a)
       for (int d = 0; d < D; ++d) sx[wave][col * D + d] = r[d];
     }
   };
+  int cur = wave;
+  float r0[D];
+  load_tile(cur, r0);
 
-  int cur = claim();
-  {
-    float r[D];
-    load_tile(cur, r);
-    park(r);
+  // biases and fragments -> LDS, counter reset
+#pragma unroll
+  for (int l = 0; l < N::kL; ++l) {
+    const float* src = reinterpret_cast<const float*>(a.packed + a.lay.bias_off[l]);
+    for (int i = threadIdx.x; i < 32 * N::mt(l); i += kThreads) sb[N::bias_base(l) + i] = src[i];
+    const half8* fsrc = reinterpret_cast<const half8*>(a.packed + a.lay.frag_off[l]);
+    for (int i = threadIdx.x; i < N::kc(l) * N::mt(l) * 64; i += kThreads) sw[N::frag_base(l) * 64 + i] = fsrc[i];
   }
+  if (threadIdx.x == 0) s_next = kWaves;
+  __syncthreads();
+
+  auto claim = [&]() {
+    int t = 0;
+    if (lane == 0) t = atomicAdd(&s_next, 1);
+    return __builtin_amdgcn_readfirstlane(t);
+  };
+  park(r0);
 #if !RDV_MLP_WEIGHTS_IN_LDS
   RegWeights<N> rw;
 #pragma unroll
