@@ -75,14 +75,14 @@ def _mlp_setup(x_cpu, layers, acts, enc=None):
 PREWARM_S = 0.5  # seconds of untimed launches before the warm-up steps
 
 
-def _time_launches(launch, steps: int, warmup: int, prewarm_s: float = PREWARM_S):
+def _time_launches(launch, steps: int, warmup: int, prewarm_s: float | None = None):
     """Returns (wall ms per step, event ms per step) for `steps` back-to-back
     launches.  Before the `warmup` steps the same launches run, untimed, for
     `prewarm_s` seconds: the GPU takes longer than a few hundred short launches
     to reach its steady-state clock (the first 40 ms of C2 launches run ~7%
     slower than the rest), and the benchmark reports the steady state."""
     import torch
-    t_end = time.perf_counter() + prewarm_s
+    t_end = time.perf_counter() + (PREWARM_S if prewarm_s is None else prewarm_s)
     i = 0
     while time.perf_counter() < t_end:
         for _ in range(64):
@@ -346,16 +346,20 @@ def cpu_baseline_c2(sample: int = 1 << 16):
 
 
 def main() -> int:
+    global PREWARM_S
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=1000)
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU baseline (profiling runs)")
     ap.add_argument("--no-extras", action="store_true", help="only the headline configuration")
+    ap.add_argument("--prewarm", type=float, default=PREWARM_S,
+                    help="seconds of untimed launches before each configuration's warm-up (0 for counter runs)")
     ap.add_argument("--calib-copy", action="store_true",
                     help="first run 5 plain 64 MiB device copies (known HBM bytes) so that a rocprofv3 --pmc "
                          "FETCH_SIZE / WRITE_SIZE run can scale the counters")
     args = ap.parse_args()
+    PREWARM_S = max(0.0, args.prewarm)
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
