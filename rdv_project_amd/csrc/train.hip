@@ -16,9 +16,14 @@
 //    fused MLP (mlp_layout.h); every hidden output is also stored (fp16, row
 //    major) for the backward pass; the group that ends the chain computes
 //    g = 2 (y - t) and per-block partial sums of (y - t)^2.
-//  - train_bwd_kernel: one layer; a block of 4 waves stages 32-point tiles of
-//    dz_{l+1} and h_l in two LDS buffers (the next tile's loads in flight while
-//    the current one is computed), then wave w computes one 32-row tile of
+//  - train_pair_kernel: layers l and l - 1 in one pass (pairs from the head
+//    down): recomputes h_l from the stored h_{l-1}, keeps g_{l-1} in LDS, and
+//    accumulates dW of both layers; only g_{l-2} reaches HBM.  The forward
+//    therefore stores every other activation.
+//  - train_bwd_kernel: one layer (layer 0 when the chain has an odd number of
+//    layers); a block of 4 waves stages 32-point tiles of dz_{l+1} and h_l in
+//    two LDS buffers (the next tile's loads in flight while the current one is
+//    computed), then wave w computes one 32-row tile of
 //    dz_l^T = W^T dz_{l+1}^T (v_mfma_f32_32x32x16_f16 with packed W^T fragments)
 //    and one 32-row tile of dW (K = the tile's points, operands
 //    gathered from the LDS tile); dW stays in registers across the block's whole
@@ -41,7 +46,7 @@ struct TrainFwdArgs {
   MlpLayout lay;
   int L, l0, l1;                        // layers [l0, l1) of an L-layer chain
   const half_t* in;                     // layer l0's input [n, in_w[l0]] fp16
-  half_t* hout[RDV_MLP_MAX_LAYERS];     // hout[l]: output of layer l (l < L - 1) [n, out_w[l]]
+  half_t* hout[RDV_MLP_MAX_LAYERS];     // hout[l]: output of layer l (l < L - 1) [n, out_w[l]], or null (not kept)
   const float* target;                  // [n, out] fp32 (l1 == L)
   half_t* g;                            // [n, out] fp16 2 (y - t) (l1 == L)
   float* loss_partial;                  // [gridDim.x] (l1 == L)
@@ -176,7 +181,7 @@ __global__ __launch_bounds__(kTrFwdThreads, 1) void train_fwd_kernel(TrainFwdArg
       } else {
         // ReLU, fp16: store the hidden output and hand it to the next layer
         const int out = lay.out_w[l];
-        half_t* dst = a.hout[l] + p * out;
+        half_t* dst = a.hout[l] == nullptr ? nullptr : a.hout[l] + p * out;
 #pragma unroll
         for (int t = 0; t < kTrMT; ++t) {
           if (t < mt) {
@@ -187,7 +192,7 @@ __global__ __launch_bounds__(kTrFwdThreads, 1) void train_fwd_kernel(TrainFwdArg
               for (int j = 0; j < 8; ++j) v[j] = half_t(acc[t][8 * qq + j]);
               v = __builtin_elementwise_max(v, half8{0, 0, 0, 0, 0, 0, 0, 0});
               b[2 * t + qq] = v;
-              if (pv) {
+              if (pv && dst != nullptr) {
                 // registers 8qq + 0..3 are rows 32t + 16qq + 4h + 0..3, 8qq + 4..7 rows 32t + 16qq + 8 + 4h + 0..3
                 *reinterpret_cast<half4v*>(dst + 32 * t + 16 * qq + 4 * h) = half4v{v[0], v[1], v[2], v[3]};
                 *reinterpret_cast<half4v*>(dst + 32 * t + 16 * qq + 8 + 4 * h) = half4v{v[4], v[5], v[6], v[7]};
@@ -248,8 +253,9 @@ __global__ __launch_bounds__(kTrBwdThreads, 2) void train_bwd_kernel(TrainBwdArg
   const int64_t t_begin = int64_t(blockIdx.x) * per_block;
   const int64_t t_end = t_begin + per_block < ntiles ? t_begin + per_block : ntiles;
 
-  const int to = wave;            // this wave's dW row tile (if < mto)
-  const int ti = wave;            // this wave's dX row tile (if < mti)
+  const int to = __builtin_amdgcn_readfirstlane(wave);  // this wave's dW row tile (if < mto)
+  const int ti = to;              // this wave's dX row tile (if < mti)
+  __builtin_assume(to >= 0 && to < kTrBwdThreads / 64);
   f32x16 accw[kTrMT];
 #pragma unroll
   for (int t = 0; t < kTrMT; ++t) accw[t] = f32x16{};
@@ -371,6 +377,290 @@ __global__ __launch_bounds__(kTrBwdThreads, 2) void train_bwd_kernel(TrainBwdArg
   }
 }
 
+// ------------------------------------------------------- backward, layer pairs
+// Layers l and l - 1 in one pass over the points, so that neither the hidden
+// activation h_l between them nor the gradient g_{l-1} ever reaches HBM:
+//   h_l      = relu(fp16(W_{l-1} h_{l-1} + b_{l-1}))   recomputed, bit-identical to the forward
+//   g_{l-1}  = fp16((g_l W_l) * [h_l > 0])              kept in LDS
+//   dW_l    += g_l^T h_l,          db_l     += sum g_l
+//   dW_{l-1}+= g_{l-1}^T h_{l-1},  db_{l-1} += sum g_{l-1}
+//   g_{l-2}  = fp16((g_{l-1} W_{l-1}) * [h_{l-1} > 0])  written, unless l - 1 is the first layer
+// Per 32-point tile the block stages g_l and h_{l-1} into LDS (double buffered,
+// the next tile's loads in flight), and wave w computes the 32-row block w of
+// every 128-wide product: the recompute (forward A fragments of layer l - 1,
+// the same MFMA sequence as the forward), g_{l-1} (W_l^T fragments, masked
+// with its own recomputed rows), the dW row blocks (operands gathered from the
+// LDS tiles, K = the tile's points) and g_{l-2}.  dW of both layers stays in
+// registers over the block's point range and is written once as a partial.
+struct TrainPairArgs {
+  const half_t* g;       // [n, out] g_l
+  const half_t* hin;     // [n, in0] h_{l-1} (natural feature order)
+  const half_t* wf;      // layer l-1 forward A fragments [mid / 32][kc0][64][8] (packed layout)
+  const float* bias;     // layer l-1 padded bias [mid]
+  const half_t* wtl;     // W_l^T fragments [mid / 32][ceil(out / 16)][64][8]
+  const half_t* wtl1;    // W_{l-1}^T fragments [in0 / 32][mid / 16][64][8] (gout only)
+  half_t* gout;          // [n, in0] g_{l-2}, or null
+  float* dw_l;           // [gridDim.x][out][mid]
+  float* db_l;           // [gridDim.x][out]
+  float* dw_l1;          // [gridDim.x][mid][in0]
+  float* db_l1;          // [gridDim.x][mid]
+  int in0, mid, out;
+  int kc0;               // K chunks of layer l - 1's forward fragments
+  int natural0;          // layer l - 1 is layer 0: its K slots are in natural order (else chunk_sigma)
+  int64_t n;
+};
+
+constexpr int kTpThreads = 256;
+
+// IN0 / MID / OUT: the widths as compile-time constants (fully unrolled K loops,
+// so every LDS read of a product can be issued ahead of its MFMA chain), or 0
+// for the generic kernel that reads them from the arguments.  NAT0: the K order
+// of layer l - 1's forward fragments (natural for layer 0, chunk_sigma after).
+template <int IN0, int MID, int OUT, bool NAT0>
+__global__ __launch_bounds__(kTpThreads, 1) void train_pair_kernel(TrainPairArgs a) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int h = lane >> 5, col = lane & 31;
+  const int in0 = IN0 ? IN0 : a.in0;
+  const int mid = MID ? MID : a.mid;
+  const int out = OUT ? OUT : a.out;
+  const int mtm = mid / 32;              // row blocks of h_l and g_{l-1}
+  const int mto = (out + 31) / 32;       // row blocks of dW_l
+  const int mti = (in0 + 31) / 32;       // column blocks of dW_{l-1}
+  const int mtg = a.gout != nullptr ? in0 / 32 : 0;  // row blocks of g_{l-2}
+  const int kco = (out + 15) / 16;
+  const int kcm = mid / 16;
+  const int kc0 = IN0 ? (NAT0 ? (IN0 + 15) / 16 : IN0 / 16) : a.kc0;
+  const int OP = 32 * mto + kTrPad, IP = 32 * mti + kTrPad, MP = mid + kTrPad;
+  // LDS: fragments, bias, two (g_l, h_{l-1}) tile buffers, the h_l and g_{l-1} tiles
+  half8* swf = reinterpret_cast<half8*>(smem);
+  half8* swl = swf + mtm * kc0 * 64;
+  half8* swl1 = swl + mtm * kco * 64;
+  float* sbias = reinterpret_cast<float*>(swl1 + mtg * kcm * 64);
+  half_t* stile = reinterpret_cast<half_t*>(sbias + mid);
+  const int tile_halves = 32 * (OP + IP);
+  half_t* shl = stile + 2 * tile_halves;
+  half_t* sg1 = shl + 32 * MP;
+  for (int i = threadIdx.x; i < mtm * kc0 * 64; i += blockDim.x) swf[i] = reinterpret_cast<const half8*>(a.wf)[i];
+  for (int i = threadIdx.x; i < mtm * kco * 64; i += blockDim.x) swl[i] = reinterpret_cast<const half8*>(a.wtl)[i];
+  for (int i = threadIdx.x; i < mtg * kcm * 64; i += blockDim.x) swl1[i] = reinterpret_cast<const half8*>(a.wtl1)[i];
+  for (int i = threadIdx.x; i < mid; i += blockDim.x) sbias[i] = a.bias[i];
+  for (int i = threadIdx.x; i < 2 * tile_halves + 64 * MP; i += blockDim.x) stile[i] = half_t(0.0f);
+  __syncthreads();
+
+  const int64_t ntiles = (a.n + 31) / 32;
+  const int64_t per_block = (ntiles + gridDim.x - 1) / gridDim.x;
+  const int64_t t_begin = int64_t(blockIdx.x) * per_block;
+  const int64_t t_end = t_begin + per_block < ntiles ? t_begin + per_block : ntiles;
+  // wave-uniform in a scalar register, so that the per-wave role tests below are
+  // scalar branches and the dW accumulators stay put across the tile loop
+  const int w = __builtin_amdgcn_readfirstlane(wave);
+  __builtin_assume(w >= 0 && w < kTpThreads / 64);
+
+  f32x16 accl[kTrMT], accl1[kTrMT];
+#pragma unroll
+  for (int t = 0; t < kTrMT; ++t) {
+    accl[t] = f32x16{};
+    accl1[t] = f32x16{};
+  }
+  float dbl = 0.0f, dbl1 = 0.0f;
+
+  const int g_chunks = 32 * out / 8;
+  const int h_chunks = 32 * in0 / 8;
+  auto load_tile = [&](int64_t tile, half8 (&r)[kTrLoads]) {
+#pragma unroll
+    for (int k = 0; k < kTrLoads; ++k) {
+      const int i = k * kTpThreads + int(threadIdx.x);
+      half8 v = {};
+      if (i < g_chunks) {
+        const int rr = i / (out / 8), c8 = i % (out / 8);
+        const int64_t p = tile * 32 + rr;
+        if (p < a.n) v = *reinterpret_cast<const half8*>(a.g + p * out + 8 * c8);
+      } else if (i < g_chunks + h_chunks) {
+        const int kk = i - g_chunks;
+        const int rr = kk / (in0 / 8), c8 = kk % (in0 / 8);
+        const int64_t p = tile * 32 + rr;
+        if (p < a.n) v = *reinterpret_cast<const half8*>(a.hin + p * in0 + 8 * c8);
+      }
+      r[k] = v;
+    }
+  };
+  auto park_tile = [&](half_t* buf, const half8 (&r)[kTrLoads]) {
+#pragma unroll
+    for (int k = 0; k < kTrLoads; ++k) {
+      const int i = k * kTpThreads + int(threadIdx.x);
+      if (i < g_chunks) {
+        const int rr = i / (out / 8), c8 = i % (out / 8);
+        *reinterpret_cast<half8*>(buf + rr * OP + 8 * c8) = r[k];
+      } else if (i < g_chunks + h_chunks) {
+        const int kk = i - g_chunks;
+        const int rr = kk / (in0 / 8), c8 = kk % (in0 / 8);
+        *reinterpret_cast<half8*>(buf + 32 * OP + rr * IP + 8 * c8) = r[k];
+      }
+    }
+  };
+  if (t_begin < t_end) {
+    half8 r[kTrLoads];
+    load_tile(t_begin, r);
+    park_tile(stile, r);
+  }
+  __syncthreads();
+
+  for (int64_t tile = t_begin; tile < t_end; ++tile) {
+    const int cur = int((tile - t_begin) & 1);
+    const half_t* tg = stile + cur * tile_halves;
+    const half_t* th = tg + 32 * OP;
+    half8 r[kTrLoads];
+    const bool more = tile + 1 < t_end;
+    if (more) load_tile(tile + 1, r);
+
+    if (w < mtm) {
+      // ---- h_l rows 32w..32w+31 (the forward's MFMA sequence for layer l - 1)
+      f32x16 acc;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const f32x4 bv = *reinterpret_cast<const f32x4*>(sbias + 32 * w + 8 * q + 4 * h);
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) acc[4 * q + jj] = bv[jj];
+      }
+#pragma unroll
+      for (int c = 0; c < kc0; ++c) {
+        half8 bf;
+        if constexpr (NAT0) {
+          bf = *reinterpret_cast<const half8*>(th + col * IP + 16 * c + 8 * h);
+        } else {
+          const half4v lo = *reinterpret_cast<const half4v*>(th + col * IP + 16 * c + 4 * h);
+          const half4v hi = *reinterpret_cast<const half4v*>(th + col * IP + 16 * c + 8 + 4 * h);
+          bf = half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        }
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(swf[(w * kc0 + c) * 64 + lane], bf, acc, 0, 0, 0);
+      }
+      // D register 4q + jj is row 32w + 8q + 4h + jj: fp16, ReLU; into LDS row-major
+      half4v hv[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) hv[q][jj] = half_t(acc[4 * q + jj]);
+        hv[q] = __builtin_elementwise_max(hv[q], half4v{0, 0, 0, 0});
+        *reinterpret_cast<half4v*>(shl + col * MP + 32 * w + 8 * q + 4 * h) = hv[q];
+      }
+      // ---- g_{l-1} rows 32w.. = W_l^T[32w.., :] g_l^T, masked by h_l > 0
+      f32x16 accg = {};
+#pragma unroll
+      for (int c = 0; c < kco; ++c) {
+        const half8 bf = *reinterpret_cast<const half8*>(tg + col * OP + 16 * c + 8 * h);
+        accg = __builtin_amdgcn_mfma_f32_32x32x16_f16(swl[(w * kco + c) * 64 + lane], bf, accg, 0, 0, 0);
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        half4v o;
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) o[jj] = float(hv[q][jj]) > 0.0f ? half_t(accg[4 * q + jj]) : half_t(0.0f);
+        *reinterpret_cast<half4v*>(sg1 + col * MP + 32 * w + 8 * q + 4 * h) = o;
+      }
+    }
+    __syncthreads();  // h_l and g_{l-1} tiles complete
+
+    // ---- dW_l rows 32w.. += g_l^T[32w.., points] h_l[points, :]
+    if (w < mto) {
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        half8 af;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) af[j] = tg[(16 * ks + 8 * h + j) * OP + 32 * w + col];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) dbl += float(af[j]);
+#pragma unroll
+        for (int t = 0; t < kTrMT; ++t) {
+          if (t < mtm) {
+            half8 bf;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) bf[j] = shl[(16 * ks + 8 * h + j) * MP + 32 * t + col];
+            accl[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf, accl[t], 0, 0, 0);
+          }
+        }
+      }
+    }
+    if (w < mtm) {
+      // ---- dW_{l-1} rows 32w.. += g_{l-1}^T[32w.., points] h_{l-1}[points, :]
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        half8 af;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) af[j] = sg1[(16 * ks + 8 * h + j) * MP + 32 * w + col];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) dbl1 += float(af[j]);
+#pragma unroll
+        for (int t = 0; t < kTrMT; ++t) {
+          if (t < mti) {
+            half8 bf;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) bf[j] = th[(16 * ks + 8 * h + j) * IP + 32 * t + col];
+            accl1[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf, accl1[t], 0, 0, 0);
+          }
+        }
+      }
+    }
+    if (w < mtg) {
+      // ---- g_{l-2} rows 32w.. = W_{l-1}^T[32w.., :] g_{l-1}^T, masked by h_{l-1} > 0
+      f32x16 acc = {};
+#pragma unroll
+      for (int c = 0; c < kcm; ++c) {
+        const half8 bf = *reinterpret_cast<const half8*>(sg1 + col * MP + 16 * c + 8 * h);
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(swl1[(w * kcm + c) * 64 + lane], bf, acc, 0, 0, 0);
+      }
+      const int64_t p = tile * 32 + col;
+      if (p < a.n) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int i0 = 32 * w + 8 * q + 4 * h;
+          const half4v hv = *reinterpret_cast<const half4v*>(th + col * IP + i0);
+          half4v o;
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj) o[jj] = float(hv[jj]) > 0.0f ? half_t(acc[4 * q + jj]) : half_t(0.0f);
+          *reinterpret_cast<half4v*>(a.gout + p * in0 + i0) = o;
+        }
+      }
+    }
+    if (more) park_tile(stile + (cur ^ 1) * tile_halves, r);  // the other buffer: last read a tile ago
+    __syncthreads();
+  }
+
+  // ---- per-block partials (rows 32w + 8q + 4h + jj, column 32t + col)
+  if (w < mto) {
+    float* dst = a.dw_l + int64_t(blockIdx.x) * out * mid;
+#pragma unroll
+    for (int t = 0; t < kTrMT; ++t)
+      if (t < mtm)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj) {
+            const int o = 32 * w + 8 * q + 4 * h + jj;
+            if (o < out) dst[int64_t(o) * mid + 32 * t + col] = accl[t][4 * q + jj];
+          }
+    const float other = __shfl_xor(dbl, 32, 64);
+    const int o = 32 * w + col;
+    if (h == 0 && o < out) a.db_l[int64_t(blockIdx.x) * out + o] = dbl + other;
+  }
+  if (w < mtm) {
+    float* dst = a.dw_l1 + int64_t(blockIdx.x) * mid * in0;
+#pragma unroll
+    for (int t = 0; t < kTrMT; ++t)
+      if (t < mti)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj) {
+            const int o = 32 * w + 8 * q + 4 * h + jj;
+            if (32 * t + col < in0) dst[int64_t(o) * in0 + 32 * t + col] = accl1[t][4 * q + jj];
+          }
+    const float other = __shfl_xor(dbl1, 32, 64);
+    if (h == 0) a.db_l1[int64_t(blockIdx.x) * mid + 32 * w + col] = dbl1 + other;
+  }
+}
+
 // Deterministic two-stage sum over nb partials part[b][count]:
 //  stage 1: mid[s][i] = sum of part[b][i] for b = s, s + S, s + 2S, ... (in order)
 //  stage 2: out[i] = scale * sum over s < S of mid[s][i] (in order)
@@ -409,15 +699,47 @@ __global__ void train_pack_wt_kernel(const float* __restrict__ w32, int in, int 
 }
 
 // ------------------------------------------------------------------- host
+// Backward schedule: layer pairs (L-1, L-2), (L-3, L-4), ... through
+// train_pair_kernel, then layer 0 alone (train_bwd_kernel, dW only) when L is
+// odd.  The forward keeps h_i (the input of layer i) only where the backward
+// or a later forward group reads it: i = L-2, L-4, ... >= 1, and the first
+// layer of every forward group.
 struct TrainPlan {
   int groups;
   int g0[RDV_MLP_MAX_LAYERS + 1];  // group k = layers [g0[k], g0[k + 1])
-  int blocks_fwd, blocks_bwd;
-  int64_t wt_off[RDV_MLP_MAX_LAYERS], h_off[RDV_MLP_MAX_LAYERS], g_off, dz_off[2], dw_off, db_off, loss_off, mid_off;
+  int blocks_fwd, blocks_bwd, blocks_pair;
+  bool keep[RDV_MLP_MAX_LAYERS];   // h_i stored by the forward
+  int64_t wt_off[RDV_MLP_MAX_LAYERS], h_off[RDV_MLP_MAX_LAYERS], g_off, dz_off[2], dw_off[2], db_off[2], loss_off,
+      mid_off;
   int64_t total;
 };
 
 static constexpr int64_t kTrFwdLdsCap = 150 * 1024;
+static constexpr int64_t kTrPairLdsCap = 160 * 1024;
+
+// Specialisations of train_pair_kernel: the layer pairs of the benchmark chain
+// (128-wide hidden layers, a 16-wide head), then the generic kernel.
+static const void* const kPairKernels[] = {
+    reinterpret_cast<const void*>(&train_pair_kernel<128, 128, 128, false>),
+    reinterpret_cast<const void*>(&train_pair_kernel<128, 128, 16, false>),
+    reinterpret_cast<const void*>(&train_pair_kernel<0, 0, 0, false>),
+    reinterpret_cast<const void*>(&train_pair_kernel<0, 0, 0, true>),
+};
+
+static const void* pair_kernel(const TrainPairArgs& pa) {
+  if (!pa.natural0 && pa.in0 == 128 && pa.mid == 128 && pa.out == 128) return kPairKernels[0];
+  if (!pa.natural0 && pa.in0 == 128 && pa.mid == 128 && pa.out == 16) return kPairKernels[1];
+  return kPairKernels[pa.natural0 ? 3 : 2];
+}
+
+// LDS bytes of train_pair_kernel (same carve-up as the kernel).
+static int64_t pair_lds(int in0, int mid, int out, int kc0, bool gout) {
+  const int mtm = mid / 32, mto = (out + 31) / 32, mti = (in0 + 31) / 32;
+  const int kco = (out + 15) / 16, kcm = mid / 16;
+  const int64_t frags = int64_t(mtm) * kc0 + int64_t(mtm) * kco + (gout ? int64_t(in0 / 32) * kcm : 0);
+  const int64_t tiles = 2 * 32 * int64_t((32 * mto + kTrPad) + (32 * mti + kTrPad)) + 64 * int64_t(mid + kTrPad);
+  return frags * 1024 + int64_t(mid) * 4 + tiles * 2;
+}
 
 static int64_t group_lds(const MlpLayout& lay, int l0, int l1) {
   int64_t f = 0, b = 0;
@@ -444,6 +766,9 @@ int train_check(const rdv_mlp_desc& d, const MlpLayout& lay) {
   if (d.dims[L] % 8 || d.dims[L] > 128) return fail(RDV_ERR_UNSUPPORTED, "output width must be a multiple of 8, <= 128");
   for (int l = 0; l < L; ++l)
     if (group_lds(lay, l, l + 1) > kTrFwdLdsCap) return fail(RDV_ERR_UNSUPPORTED, "layer too large for LDS");
+  for (int l = L - 1; l >= 1; l -= 2)
+    if (pair_lds(d.dims[l - 1], d.dims[l], d.dims[l + 1], lay.kc[l - 1], l - 1 > 0) > kTrPairLdsCap)
+      return fail(RDV_ERR_UNSUPPORTED, "layer pair too large for LDS");
   return RDV_OK;
 }
 
@@ -461,6 +786,10 @@ static void train_plan(const rdv_mlp_desc& d, const MlpLayout& lay, int64_t n, i
   const int64_t ntiles = (n + 31) / 32;
   p->blocks_fwd = int(std::min<int64_t>(cu, (ntiles + kTrWaves - 1) / kTrWaves));
   p->blocks_bwd = int(std::min<int64_t>(2 * int64_t(cu), ntiles));
+  p->blocks_pair = int(std::max<int64_t>(1, std::min<int64_t>(cu, ntiles)));
+  for (int i = 0; i < RDV_MLP_MAX_LAYERS; ++i) p->keep[i] = false;
+  for (int i = L - 2; i >= 1; i -= 2) p->keep[i] = true;
+  for (int k = 1; k < p->groups; ++k) p->keep[p->g0[k]] = true;
   int64_t off = 0;
   auto take = [&](int64_t bytes) {
     const int64_t o = off;
@@ -474,13 +803,15 @@ static void train_plan(const rdv_mlp_desc& d, const MlpLayout& lay, int64_t n, i
     maxoi = std::max(maxoi, d.dims[i] * d.dims[i + 1]);
     maxo = std::max(maxo, d.dims[i + 1]);
   }
-  p->h_off[0] = 0;
-  for (int i = 1; i < L; ++i) p->h_off[i] = take(n * d.dims[i] * 2);
+  for (int i = 0; i < L; ++i) p->h_off[i] = (i >= 1 && p->keep[i]) ? take(n * d.dims[i] * 2) : -1;
   p->g_off = take(n * d.dims[L] * 2);
   p->dz_off[0] = take(n * maxw * 2);
   p->dz_off[1] = take(n * maxw * 2);
-  p->dw_off = take(int64_t(p->blocks_bwd) * maxoi * 4);
-  p->db_off = take(int64_t(p->blocks_bwd) * maxo * 4);
+  const int64_t parts = std::max(p->blocks_bwd, p->blocks_pair);
+  for (int k = 0; k < 2; ++k) {
+    p->dw_off[k] = take(parts * maxoi * 4);
+    p->db_off[k] = take(parts * maxo * 4);
+  }
   p->loss_off = take(int64_t(p->blocks_fwd) * 4);
   p->mid_off = take(int64_t(kTrSplit) * std::max(maxoi, p->blocks_fwd) * 4);
   p->total = off;
@@ -511,6 +842,8 @@ int launch_train_step(const rdv_mlp_desc& d, const MlpLayout& lay, const void* p
                                     hipFuncAttributeMaxDynamicSharedMemorySize, int(kTrFwdLdsCap)));
     RDV_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&train_bwd_kernel),
                                     hipFuncAttributeMaxDynamicSharedMemorySize, 80 * 1024));
+    for (const void* fn : kPairKernels)
+      RDV_HIP_TRY(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, int(kTrPairLdsCap)));
     attr_set = true;
   }
   TrainFwdArgs fa;
@@ -523,7 +856,8 @@ int launch_train_step(const rdv_mlp_desc& d, const MlpLayout& lay, const void* p
   fa.n = n;
   fa.has_bias = 1;  // the packed header's flag is on the device; biases are staged either way
   for (int i = 0; i < RDV_MLP_MAX_LAYERS; ++i) fa.hout[i] = nullptr;
-  for (int i = 0; i + 1 < L; ++i) fa.hout[i] = reinterpret_cast<half_t*>(ws + p.h_off[i + 1]);
+  for (int i = 0; i + 1 < L; ++i)
+    if (p.keep[i + 1]) fa.hout[i] = reinterpret_cast<half_t*>(ws + p.h_off[i + 1]);
   for (int k = 0; k < p.groups; ++k) {
     fa.l0 = p.g0[k];
     fa.l1 = p.g0[k + 1];
@@ -544,42 +878,83 @@ int launch_train_step(const rdv_mlp_desc& d, const MlpLayout& lay, const void* p
   };
   rc = reduce(reinterpret_cast<float*>(ws + p.loss_off), p.blocks_fwd, 1, loss);
   if (rc != RDV_OK) return rc;
-  // backward, last layer first; dz ping-pongs between dz_off[0] and dz_off[1]
-  int src = -1;  // -1: g
-  for (int l = L - 1; l >= 0; --l) {
+  // backward: layer pairs from the head down, then layer 0 alone if L is odd;
+  // gradients ping-pong between dz_off[0] and dz_off[1]
+  auto pack_wt = [&](int l) -> half_t* {
     const int in = d.dims[l], out = d.dims[l + 1];
-    const int kco = (out + 15) / 16;
-    const int mtx = l == 0 ? 0 : in / 32, mti = (in + 31) / 32;
     half_t* wt = reinterpret_cast<half_t*>(ws + p.wt_off[l]);
-    {
-      const int64_t total = int64_t(in / 32) * kco * 64 * 8;
-      if (total > 0) {
-        train_pack_wt_kernel<<<dim3(unsigned((total + 255) / 256)), dim3(256), 0, stream>>>(
-            reinterpret_cast<const float*>(pk + lay.w32_off[l]), in, out, wt);
-        RDV_HIP_TRY(hipGetLastError());
-      }
+    const int64_t total = int64_t(in / 32) * ((out + 15) / 16) * 64 * 8;
+    if (total > 0) {
+      train_pack_wt_kernel<<<dim3(unsigned((total + 255) / 256)), dim3(256), 0, stream>>>(
+          reinterpret_cast<const float*>(pk + lay.w32_off[l]), in, out, wt);
     }
+    return wt;
+  };
+  const half_t* gsrc = reinterpret_cast<const half_t*>(ws + p.g_off);
+  int dst = 0;
+  int l = L - 1;
+  for (; l >= 1; l -= 2) {
+    TrainPairArgs pa;
+    pa.in0 = d.dims[l - 1];
+    pa.mid = d.dims[l];
+    pa.out = d.dims[l + 1];
+    pa.kc0 = lay.kc[l - 1];
+    pa.natural0 = l - 1 == 0 ? 1 : 0;
+    pa.n = n;
+    pa.g = gsrc;
+    pa.hin = l - 1 == 0 ? static_cast<const half_t*>(x) : reinterpret_cast<const half_t*>(ws + p.h_off[l - 1]);
+    pa.wf = reinterpret_cast<const half_t*>(pk + lay.frag_off[l - 1]);
+    pa.bias = reinterpret_cast<const float*>(pk + lay.bias_off[l - 1]);
+    pa.wtl = pack_wt(l);
+    RDV_HIP_TRY(hipGetLastError());
+    pa.wtl1 = l - 1 > 0 ? pack_wt(l - 1) : nullptr;
+    RDV_HIP_TRY(hipGetLastError());
+    pa.gout = l - 1 > 0 ? reinterpret_cast<half_t*>(ws + p.dz_off[dst]) : nullptr;
+    pa.dw_l = reinterpret_cast<float*>(ws + p.dw_off[0]);
+    pa.db_l = reinterpret_cast<float*>(ws + p.db_off[0]);
+    pa.dw_l1 = reinterpret_cast<float*>(ws + p.dw_off[1]);
+    pa.db_l1 = reinterpret_cast<float*>(ws + p.db_off[1]);
+    const size_t lds = size_t(pair_lds(pa.in0, pa.mid, pa.out, pa.kc0, pa.gout != nullptr));
+    const void* fn = pair_kernel(pa);
+    void* args[] = {&pa};
+    RDV_HIP_TRY(hipLaunchKernel(fn, dim3(unsigned(p.blocks_pair)), dim3(kTpThreads), args, lds, stream));
+    RDV_HIP_TRY(hipGetLastError());
+    rc = reduce(pa.dw_l, p.blocks_pair, int64_t(pa.out) * pa.mid, dW[l]);
+    if (rc != RDV_OK) return rc;
+    rc = reduce(pa.db_l, p.blocks_pair, pa.out, db[l]);
+    if (rc != RDV_OK) return rc;
+    rc = reduce(pa.dw_l1, p.blocks_pair, int64_t(pa.mid) * pa.in0, dW[l - 1]);
+    if (rc != RDV_OK) return rc;
+    rc = reduce(pa.db_l1, p.blocks_pair, pa.mid, db[l - 1]);
+    if (rc != RDV_OK) return rc;
+    if (pa.gout != nullptr) {
+      gsrc = pa.gout;
+      dst ^= 1;
+    }
+  }
+  if (l == 0) {
+    // layer 0 alone: dW_0 = g_0^T x, no input gradient
+    const int in = d.dims[0], out = d.dims[1];
+    const int kco = (out + 15) / 16;
+    const int mti = (in + 31) / 32, mto = (out + 31) / 32;
     TrainBwdArgs ba;
-    const int dst = src < 0 ? 0 : src ^ 1;
-    ba.dz = src < 0 ? reinterpret_cast<const half_t*>(ws + p.g_off) : reinterpret_cast<const half_t*>(ws + p.dz_off[src]);
-    ba.hin = l == 0 ? static_cast<const half_t*>(x) : reinterpret_cast<const half_t*>(ws + p.h_off[l]);
-    ba.wt = wt;
-    ba.dzin = l == 0 ? nullptr : reinterpret_cast<half_t*>(ws + p.dz_off[dst]);
-    ba.dw_part = reinterpret_cast<float*>(ws + p.dw_off);
-    ba.db_part = reinterpret_cast<float*>(ws + p.db_off);
+    ba.dz = gsrc;
+    ba.hin = static_cast<const half_t*>(x);
+    ba.wt = reinterpret_cast<half_t*>(ws + p.wt_off[0]);
+    ba.dzin = nullptr;
+    ba.dw_part = reinterpret_cast<float*>(ws + p.dw_off[0]);
+    ba.db_part = reinterpret_cast<float*>(ws + p.db_off[0]);
     ba.in = in;
     ba.out = out;
     ba.n = n;
-    const int mto = (out + 31) / 32;
-    const size_t lds = size_t(mtx) * kco * 1024 + 2 * (size_t(32) * (32 * mto + kTrPad) * 2 +
-                                                        size_t(32) * (32 * mti + kTrPad) * 2);
+    const size_t lds = 2 * (size_t(32) * (32 * mto + kTrPad) * 2 + size_t(32) * (32 * mti + kTrPad) * 2);
+    (void)kco;
     train_bwd_kernel<<<dim3(unsigned(p.blocks_bwd)), dim3(kTrBwdThreads), lds, stream>>>(ba);
     RDV_HIP_TRY(hipGetLastError());
-    rc = reduce(ba.dw_part, p.blocks_bwd, int64_t(out) * in, dW[l]);
+    rc = reduce(ba.dw_part, p.blocks_bwd, int64_t(out) * in, dW[0]);
     if (rc != RDV_OK) return rc;
-    rc = reduce(ba.db_part, p.blocks_bwd, out, db[l]);
+    rc = reduce(ba.db_part, p.blocks_bwd, out, db[0]);
     if (rc != RDV_OK) return rc;
-    src = dst;
   }
   return RDV_OK;
 }
