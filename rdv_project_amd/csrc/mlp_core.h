@@ -126,14 +126,8 @@ __device__ __forceinline__ void load_bias(f32x16 (&acc)[N::kMaxMT], const float*
   }
 }
 
-// Where a wave's A fragments live: VGPRs for the life of the wave, or the
-// block's LDS copy (fragment f is a conflict-free 1 KiB line, one
-// ds_read_b128 per lane, read right before its MFMA).
-template <class N>
-struct RegWeights {
-  half8 w[N::kFrags];
-  __device__ __forceinline__ half8 get(int f) const { return w[f]; }
-};
+// A wave's view of the block's LDS copy of the A fragments: fragment f is a
+// conflict-free 1 KiB line, one ds_read_b128 per lane, read right before its MFMA.
 struct LdsWeights {
   const half8* sw;  // fragment f at sw[f * 64 + lane]
   int lane;
@@ -191,6 +185,86 @@ __device__ __forceinline__ void run_chain(const WS& ws, half8 (&b)[N::kMaxKC], f
   if constexpr (l + 1 < N::kL) {
     to_next<N, l, RELU>(cur, b);
     run_chain<N, l + 1, RELU, BIAS>(ws, b, nxt, cur, sb, h);
+  }
+}
+
+// ------------------------------------------------------------ tile pairs
+// Two 32-point tiles A and B per wave, staggered by half a layer: the MFMAs of
+// one tile's layer l are interleaved, in program order, with the other tile's
+// register hand-off (fp32 -> fp16 conversion and ReLU), which does not depend
+// on them.  MFMA and VALU time on a SIMD overlap only when independent VALU
+// work is ready while the matrix core is busy; this puts it right behind each
+// MFMA of the wave itself.
+//   stage l.a: layer l MFMAs of A  +  layer l-1 hand-off of B (B's input encoding at l = 0)
+//   stage l.b: layer l MFMAs of B  +  layer l hand-off of A
+
+// Hand-off slot s = 2t + q of layer lp: acc[t][8q .. 8q+7] -> b[s].
+template <class N, int lp, bool RELU>
+__device__ __forceinline__ void handoff_slot(int s, const f32x16 (&acc)[N::kMaxMT], half8 (&b)[N::kMaxKC]) {
+  const int t = s >> 1, q = s & 1;
+  half8 v;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) v[j] = half_t(acc[t][8 * q + j]);
+  // max after the fp16 rounding equals rounding after max (rounding is monotone)
+  if constexpr (RELU) v = __builtin_elementwise_max(v, half8{0, 0, 0, 0, 0, 0, 0, 0});
+  b[s] = v;
+}
+
+// Layer l MFMAs of tile X; hand-off slot s of tile Y's layer LP (LP < 0: none)
+// follows MFMA floor(s NM / NH).
+template <class N, int l, int LP, bool RELU, bool BIAS, class WS>
+__device__ __forceinline__ void stage_pair(const WS& ws, const half8 (&bX)[N::kMaxKC], f32x16 (&accX)[N::kMaxMT],
+                                           const f32x16 (&accY)[N::kMaxMT], half8 (&bY)[N::kMaxKC]) {
+  constexpr int NM = N::mt(l) * N::kc(l);
+  constexpr int NH = LP >= 0 ? 2 * N::mt(LP < 0 ? 0 : LP) : 0;
+  const f32x16 zero = {};
+#pragma unroll
+  for (int c = 0; c < N::kc(l); ++c) {
+#pragma unroll
+    for (int t = 0; t < N::mt(l); ++t) {
+      const int i = c * N::mt(l) + t;
+      const f32x16& cin = (BIAS || c > 0) ? accX[t] : zero;
+      accX[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ws.get(N::frag_base(l) + t * N::kc(l) + c), bX[c], cin, 0, 0, 0);
+      if constexpr (NH > 0) {
+#pragma unroll
+        for (int s = 0; s < NH; ++s)
+          if ((s * NM) / NH == i) handoff_slot<N, LP < 0 ? 0 : LP, RELU>(s, accY, bY);
+      }
+    }
+  }
+}
+
+// Layer 0 MFMAs of tile A, with tile B's input encoding right after the first.
+template <class N, bool BIAS, class WS>
+__device__ __forceinline__ void stage_pair_input(const WS& ws, const half8 (&bA)[N::kMaxKC], f32x16 (&accA)[N::kMaxMT],
+                                                 const float (&pB)[N::kIn], int h, half8 (&bB)[N::kMaxKC]) {
+  const f32x16 zero = {};
+#pragma unroll
+  for (int c = 0; c < N::kc(0); ++c) {
+#pragma unroll
+    for (int t = 0; t < N::mt(0); ++t) {
+      const f32x16& cin = (BIAS || c > 0) ? accA[t] : zero;
+      accA[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ws.get(N::frag_base(0) + t * N::kc(0) + c), bA[c], cin, 0, 0, 0);
+      if (c == 0 && t == 0) build_input<N>(pB, h, bB);
+    }
+  }
+}
+
+// The whole chain for tiles A (input fragments in bA) and B (raw input pB).
+// On return accA / accB hold the last layer's D of each tile.
+template <class N, int l, bool RELU, bool BIAS, class WS>
+__device__ __forceinline__ void run_pair(const WS& ws, const float (&pB)[N::kIn], int h, half8 (&bA)[N::kMaxKC],
+                                         half8 (&bB)[N::kMaxKC], f32x16 (&accA)[N::kMaxMT],
+                                         f32x16 (&accB)[N::kMaxMT], const float* sb) {
+  if constexpr (BIAS) load_bias<N, l>(accA, sb, h);
+  if constexpr (l == 0) stage_pair_input<N, BIAS>(ws, bA, accA, pB, h, bB);
+  else stage_pair<N, l, l - 1, RELU, BIAS>(ws, bA, accA, accB, bB);
+  if constexpr (BIAS) load_bias<N, l>(accB, sb, h);
+  if constexpr (l + 1 < N::kL) {
+    stage_pair<N, l, l, RELU, BIAS>(ws, bB, accB, accA, bA);
+    run_pair<N, l + 1, RELU, BIAS>(ws, pB, h, bA, bB, accA, accB, sb);
+  } else {
+    stage_pair<N, l, -1, RELU, BIAS>(ws, bB, accB, accA, bA);
   }
 }
 

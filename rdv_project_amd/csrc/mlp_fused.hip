@@ -1,5 +1,5 @@
 // Fused fp16 matrix-core MLP: the whole layer chain evaluated per wave, weights
-// resident in VGPRs for the life of the wave, activations passed from layer to
+// resident in LDS for the life of the block, activations passed from layer to
 // layer in registers (the D -> B fragment identity of mlp_layout.h).
 //
 // Replaces the reference's LinearFast / ReLU megakernel
@@ -10,8 +10,8 @@
 // weights in fp16, products accumulated in fp32, fp32 bias, activation in fp32
 // before the next rounding to fp16.
 //
-// Work decomposition: one 8-wave block per CU; each wave evaluates one 32-point
-// tile (one MFMA N block) at a time, claiming tiles dynamically (see the kernel).
+// Work decomposition: one block per CU; each wave evaluates two 32-point tiles
+// (two MFMA N blocks) at a time, claiming them dynamically (see the kernels).
 #include "mlp_core.h"
 
 namespace rdv {
@@ -26,81 +26,79 @@ struct FusedArgs {
 };
 
 // Work decomposition.  One 512-thread block (8 waves, 2 per SIMD) per CU owns a
-// contiguous range of 32-row tiles; its waves claim tiles one at a time from an
-// LDS counter, so the two waves of a SIMD finish together (with a static split
-// the SIMD arbiter's preference for older waves let one finish ~25% earlier,
-// leaving the tail at one wave per SIMD).
-//  - Weights: the block copies the packed A fragments into LDS once, and every
-//    wave then reads its copy into VGPRs.  (2048 waves each pulling the same
-//    26 KiB straight from L2 serialised on a few hot lines for ~3 us.)
-//  - Input: at the top of an iteration a wave claims its next tile and issues
-//    that tile's row loads into registers; at the bottom, a whole tile of work
-//    later, it parks them in a wave-private LDS slot, which the next iteration
-//    reads.  The wait for the load therefore lands where the data has long
-//    arrived, and no barrier is needed after start-up.
-//  - Output: each tile's store is issued after the next input has been parked,
-//    so the wait that precedes the parking never covers a store younger than
-//    a tile.
-#ifndef RDV_MLP_WEIGHTS_IN_LDS
-#define RDV_MLP_WEIGHTS_IN_LDS 1
-#endif
-// 4 waves per SIMD when the weights stay in LDS (<= 128 VGPRs), 2 when they
-// are held in VGPRs.
-constexpr int kWaves = RDV_MLP_WEIGHTS_IN_LDS ? 16 : 8;
-constexpr int kThreads = 64 * kWaves;
+// contiguous range of 64-row pair tiles; its waves claim them one at a time
+// from an LDS counter (wave w starts on pair tile w), so the waves of a SIMD
+// finish together.  Each wave evaluates a pair tile as two 32-point tiles
+// staggered by half a layer (run_pair, mlp_core.h): the fp32 -> fp16 hand-off
+// of one tile is interleaved with the MFMAs of the other, so VALU and matrix
+// work overlap within the wave.
+//  - Weights: the block copies the packed A fragments into LDS once; every MFMA
+//    reads its fragment with one conflict-free ds_read_b128.  (2048 waves each
+//    pulling the same 26 KiB straight from L2 serialised on a few hot lines for
+//    ~3 us.)
+//  - Input: at the top of an iteration a wave claims its next pair tile and
+//    issues that tile's row loads into registers; at the bottom, a whole
+//    iteration later, it parks them in a wave-private LDS slot, which the next
+//    iteration reads.  The wait for the load therefore lands where the data has
+//    long arrived, and no barrier is needed after start-up.  The first tile's
+//    loads are issued before the weight staging, so their latency overlaps it.
+//  - Output: each pair tile's stores are issued after the next input has been
+//    parked, so the wait that precedes the parking never covers a store younger
+//    than an iteration.
+constexpr int kWaves2 = 8;
+constexpr int kThreads2 = 64 * kWaves2;
 
 template <class N, bool RELU, int HEAD_ACT>
-__global__ __launch_bounds__(kThreads, 1) void mlp_fused_f16_kernel(FusedArgs a) {
+__global__ __launch_bounds__(kThreads2, 1) void mlp_fused_f16_kernel(FusedArgs a) {
   constexpr int D = N::kIn;
   constexpr int LL = N::kL - 1;
   constexpr int MTO = N::mt(LL);
   __shared__ float sb[N::kBias];
   __shared__ half8 sw[N::kFrags * 64];
-  __shared__ float sx[kWaves][32 * D];  // each wave's parked input tile
+  __shared__ float sx[kWaves2][64 * D];  // each wave's parked input pair tile
   __shared__ int s_next;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int h = lane >> 5, col = lane & 31;
 
-  const int64_t ntiles = (a.nrows + 31) >> 5;
+  const int64_t ntiles = (a.nrows + 63) >> 6;  // 64-row pair tiles
   const int64_t per_block = (ntiles + gridDim.x - 1) / gridDim.x;
   const int64_t t_begin = int64_t(blockIdx.x) * per_block;
   const int64_t t_end = t_begin + per_block < ntiles ? t_begin + per_block : ntiles;
-  const int nt = int(t_end > t_begin ? t_end - t_begin : 0);  // this block's tiles
-  // all biases zero (flag computed by the packer): skip seeding the accumulators
+  const int nt = int(t_end > t_begin ? t_end - t_begin : 0);
   const bool has_bias = (reinterpret_cast<const MlpPackHeader*>(a.packed)->flags & kMlpHasBias) != 0;
 
-  // ---- start-up.  Wave w's first tile is block tile w (the counter starts
-  // past them), so its input loads are issued before the weight staging and
-  // their latency overlaps it.
-  // Rows of block tile lt, clamped to valid rows: tiles past the end are never
-  // computed, and rows past the end of the last tile feed outputs never stored.
+  // Rows of pair tile lt, half s (0: rows 0-31, 1: rows 32-63), clamped to valid rows.
   const int64_t last = a.nrows - 1;
-  auto load_tile = [&](int lt, float (&r)[D]) {
-    int64_t row = (t_begin + (lt < nt ? lt : 0)) * 32 + col;
-    row = row < last ? row : last;
+  auto load_tile = [&](int lt, float (&r)[2][D]) {
 #pragma unroll
-    for (int d = 0; d < D; ++d) r[d] = __builtin_nontemporal_load(a.x + row * D + d);
+    for (int s2 = 0; s2 < 2; ++s2) {
+      int64_t row = (t_begin + (lt < nt ? lt : 0)) * 64 + 32 * s2 + col;
+      row = row < last ? row : last;
+#pragma unroll
+      for (int d = 0; d < D; ++d) r[s2][d] = __builtin_nontemporal_load(a.x + row * D + d);
+    }
   };
-  auto park = [&](const float (&r)[D]) {
+  auto park = [&](const float (&r)[2][D]) {
     if (h == 0) {
 #pragma unroll
-      for (int d = 0; d < D; ++d) sx[wave][col * D + d] = r[d];
+      for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+        for (int d = 0; d < D; ++d) sx[wave][(32 * s2 + col) * D + d] = r[s2][d];
     }
   };
   int cur = wave;
-  float r0[D];
+  float r0[2][D];
   load_tile(cur, r0);
 
-  // biases and fragments -> LDS, counter reset
 #pragma unroll
   for (int l = 0; l < N::kL; ++l) {
     const float* src = reinterpret_cast<const float*>(a.packed + a.lay.bias_off[l]);
-    for (int i = threadIdx.x; i < 32 * N::mt(l); i += kThreads) sb[N::bias_base(l) + i] = src[i];
+    for (int i = threadIdx.x; i < 32 * N::mt(l); i += kThreads2) sb[N::bias_base(l) + i] = src[i];
     const half8* fsrc = reinterpret_cast<const half8*>(a.packed + a.lay.frag_off[l]);
-    for (int i = threadIdx.x; i < N::kc(l) * N::mt(l) * 64; i += kThreads) sw[N::frag_base(l) * 64 + i] = fsrc[i];
+    for (int i = threadIdx.x; i < N::kc(l) * N::mt(l) * 64; i += kThreads2) sw[N::frag_base(l) * 64 + i] = fsrc[i];
   }
-  if (threadIdx.x == 0) s_next = kWaves;
+  if (threadIdx.x == 0) s_next = kWaves2;
   __syncthreads();
 
   auto claim = [&]() {
@@ -109,65 +107,58 @@ __global__ __launch_bounds__(kThreads, 1) void mlp_fused_f16_kernel(FusedArgs a)
     return __builtin_amdgcn_readfirstlane(t);
   };
   park(r0);
-#if !RDV_MLP_WEIGHTS_IN_LDS
-  RegWeights<N> rw;
-#pragma unroll
-  for (int f = 0; f < N::kFrags; ++f) rw.w[f] = sw[f * 64 + lane];
-#endif
 
-  // Each tile's output is stored one iteration late, after the next park: the
-  // wait preceding a park then never covers a store younger than a whole tile
-  // (write acknowledgements under load take longer than one tile).
-  f32x4 po[MTO][4];
+  f32x4 po[2][MTO][4];
   int64_t prow = -1;
   while (cur < nt) {
     const int nxt = claim();
-    float r[D];
+    float r[2][D];
     load_tile(nxt, r);
 
-    float p[D];
+    float pA[D], pB[D];
 #pragma unroll
-    for (int d = 0; d < D; ++d) p[d] = sx[wave][col * D + d];
-    // The bias reads are loop-invariant; left visible, the compiler hoists all
-    // of them out of the tile loop and pins 16 VGPRs per M tile.  A zero offset
-    // laundered through an empty asm each iteration keeps them as per-tile LDS
-    // reads straight into the accumulators.
-    f32x16 accA[N::kMaxMT], accB[N::kMaxMT];
-    half8 b[N::kMaxKC];
-#if RDV_MLP_WEIGHTS_IN_LDS
-    const LdsWeights ws{sw + opaque_zero(), lane};  // opaque offset keeps the reads in the loop
-#else
-    const RegWeights<N>& ws = rw;
-#endif
-    if (has_bias) {
-      const float* sbt = sb + opaque_zero();
-      load_bias<N, 0>(accA, sbt, h);
-      build_input<N>(p, h, b);
-      run_chain<N, 0, RELU, true>(ws, b, accA, accB, sbt, h);
-    } else {
-      build_input<N>(p, h, b);
-      run_chain<N, 0, RELU, false>(ws, b, accA, accB, sb, h);
+    for (int d = 0; d < D; ++d) {
+      pA[d] = sx[wave][col * D + d];
+      pB[d] = sx[wave][(32 + col) * D + d];
     }
-    const f32x16 (&fin)[N::kMaxMT] = (LL % 2 == 0) ? accA : accB;
-    f32x4 o[MTO][4];
+    f32x16 accA[N::kMaxMT], accB[N::kMaxMT];
+    half8 bA[N::kMaxKC], bB[N::kMaxKC];
+    const LdsWeights ws{sw + opaque_zero(), lane};
+    build_input<N>(pA, h, bA);
+    if (has_bias) {
+      run_pair<N, 0, RELU, true>(ws, pB, h, bA, bB, accA, accB, sb + opaque_zero());
+    } else {
+      run_pair<N, 0, RELU, false>(ws, pB, h, bA, bB, accA, accB, sb);
+    }
+    f32x4 o[2][MTO][4];
 #pragma unroll
     for (int t = 0; t < MTO; ++t)
 #pragma unroll
       for (int q = 0; q < 4; ++q)
 #pragma unroll
-        for (int jj = 0; jj < 4; ++jj)
-          o[t][q][jj] = head_act<HEAD_ACT>(32 * t + 8 * q + 4 * h + jj, fin[t][4 * q + jj]);
+        for (int jj = 0; jj < 4; ++jj) {
+          o[0][t][q][jj] = head_act<HEAD_ACT>(32 * t + 8 * q + 4 * h + jj, accA[t][4 * q + jj]);
+          o[1][t][q][jj] = head_act<HEAD_ACT>(32 * t + 8 * q + 4 * h + jj, accB[t][4 * q + jj]);
+        }
 
-    park(r);  // the next tile's input, loaded a whole tile ago
-    if (prow >= 0 && prow < a.nrows) store_head<N>(a.y + prow * N::kOut, po, h);
+    park(r);  // the next pair tile's input, loaded a whole iteration ago
+    if (prow >= 0) {
+      if (prow < a.nrows) store_head<N>(a.y + prow * N::kOut, po[0], h);
+      if (prow + 32 < a.nrows) store_head<N>(a.y + (prow + 32) * N::kOut, po[1], h);
+    }
 #pragma unroll
-    for (int t = 0; t < MTO; ++t)
+    for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
-      for (int q = 0; q < 4; ++q) po[t][q] = o[t][q];
-    prow = (t_begin + cur) * 32 + col;
+      for (int t = 0; t < MTO; ++t)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) po[s2][t][q] = o[s2][t][q];
+    prow = (t_begin + cur) * 64 + col;
     cur = nxt;
   }
-  if (prow >= 0 && prow < a.nrows) store_head<N>(a.y + prow * N::kOut, po, h);
+  if (prow >= 0) {
+    if (prow < a.nrows) store_head<N>(a.y + prow * N::kOut, po[0], h);
+    if (prow + 32 < a.nrows) store_head<N>(a.y + (prow + 32) * N::kOut, po[1], h);
+  }
 }
 
 // ---------------------------------------------------------- instantiations
@@ -186,12 +177,11 @@ int launch_fused(const FusedArgs& a, int64_t nrows, hipStream_t stream) {
   DeviceInfo di;
   int rc = device_info(&di);
   if (rc != RDV_OK) return rc;
-  const int64_t ntiles = (nrows + 31) / 32;
-  // one 8-wave block per CU; never more waves than tiles
+  // one block per CU; never more waves than pair tiles
   int64_t blocks = di.cu_count;
-  const int64_t need = (ntiles + kWaves - 1) / kWaves;
+  const int64_t need = ((nrows + 63) / 64 + kWaves2 - 1) / kWaves2;
   if (need < blocks) blocks = need;
-  mlp_fused_f16_kernel<N, RELU, HEAD_ACT><<<dim3(unsigned(blocks)), dim3(kThreads), 0, stream>>>(a);
+  mlp_fused_f16_kernel<N, RELU, HEAD_ACT><<<dim3(unsigned(blocks)), dim3(kThreads2), 0, stream>>>(a);
   RDV_HIP_TRY(hipGetLastError());
   return RDV_OK;
 }
