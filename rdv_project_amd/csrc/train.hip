@@ -385,13 +385,20 @@ __global__ __launch_bounds__(kTrBwdThreads, 2) void train_bwd_kernel(TrainBwdArg
 //   dW_l    += g_l^T h_l,          db_l     += sum g_l
 //   dW_{l-1}+= g_{l-1}^T h_{l-1},  db_{l-1} += sum g_{l-1}
 //   g_{l-2}  = fp16((g_{l-1} W_{l-1}) * [h_{l-1} > 0])  written, unless l - 1 is the first layer
-// Per 32-point tile the block stages g_l and h_{l-1} into LDS (double buffered,
-// the next tile's loads in flight), and wave w computes the 32-row block w of
-// every 128-wide product: the recompute (forward A fragments of layer l - 1,
-// the same MFMA sequence as the forward), g_{l-1} (W_l^T fragments, masked
-// with its own recomputed rows), the dW row blocks (operands gathered from the
-// LDS tiles, K = the tile's points) and g_{l-2}.  dW of both layers stays in
-// registers over the block's point range and is written once as a partial.
+// Per 32-point tile the block stages g_l and h_{l-1} into LDS (the next tile's
+// global loads in flight during the current one), and wave w computes the
+// 32-row block w of every 128-wide product: the recompute (forward A fragments
+// of layer l - 1, the same MFMA sequence as the forward), g_{l-1} (W_l^T
+// fragments, masked with its own recomputed rows), the dW row blocks (K = the
+// tile's points) and g_{l-2}.  dW of both layers stays in registers over the
+// block's point range and is written once as a partial.
+//
+// LDS holds every tile twice: row-major [point][feature] (the operands whose K
+// is a feature: 16-byte reads of 8 consecutive features of one point) and
+// feature-major [feature][point] (the dW operands, whose K is the point: 8-byte
+// reads of consecutive points of one feature).  Feature-major copies are written
+// with 2-byte stores as tiles are parked or produced; their 36-half rows make
+// both the stores and the 8-byte reads bank-conflict free.
 struct TrainPairArgs {
   const half_t* g;       // [n, out] g_l
   const half_t* hin;     // [n, in0] h_{l-1} (natural feature order)
@@ -410,17 +417,48 @@ struct TrainPairArgs {
   int64_t n;
 };
 
-constexpr int kTpThreads = 256;
+constexpr int kTpThreads = 512;  // 8 waves: two roles of 4
+constexpr int kTpT = 36;         // feature-major row stride (halves)
 
-// IN0 / MID / OUT: the widths as compile-time constants (fully unrolled K loops,
-// so every LDS read of a product can be issued ahead of its MFMA chain), or 0
-// for the generic kernel that reads them from the arguments.  NAT0: the K order
-// of layer l - 1's forward fragments (natural for layer 0, chunk_sigma after).
+// 8 consecutive halves of a feature-major row (8-byte aligned) as one fragment.
+__device__ __forceinline__ half8 tp_frag(const half_t* p) {
+  const half4v lo = *reinterpret_cast<const half4v*>(p);
+  const half4v hi = *reinterpret_cast<const half4v*>(p + 4);
+  return half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+
+// LDS carve-up of train_pair_kernel (halves; after the fp32 bias), per tile
+// parity b: the inputs of the tile (row-major g_l, h_{l-1}; feature-major g_l,
+// h_{l-1}) and the products (row-major g_{l-1}; feature-major g_{l-1}, h_l).
+struct PairLds {
+  int OP, IP, MP, in_halves, pr_halves;
+  __device__ __host__ PairLds(int in0, int mid, int out) {
+    const int mto = (out + 31) / 32, mti = (in0 + 31) / 32;
+    OP = 32 * mto + kTrPad;
+    IP = 32 * mti + kTrPad;
+    MP = mid + kTrPad;
+    in_halves = 32 * OP + 32 * IP + kTpT * (32 * mto + 32 * mti);
+    pr_halves = 32 * MP + kTpT * 2 * mid;
+  }
+  __device__ __host__ int total_halves() const { return 2 * (in_halves + pr_halves); }
+};
+
+// Two roles, software-pipelined over the block's tiles (tile parity selects the
+// LDS buffers):
+//   waves 0-3, tile i:    h_l rows 32w.. (recompute) and g_{l-1} rows 32w..
+//   waves 4-7, tile i-1:  dW_l, dW_{l-1} row blocks w, db, and g_{l-2} rows 32w..
+// so each SIMD runs one wave of each, and the dW accumulators live only in the
+// second role.  The weight fragments each wave needs (its 32-row blocks) sit in
+// its registers.  Every iteration ends with two barriers around the parking of
+// tile i+1 into the buffers tile i-1 used.
+//
+// IN0 / MID / OUT: the widths as compile-time constants (fully unrolled K loops),
+// or 0 for the generic kernel that reads them from the arguments.  NAT0: the K
+// order of layer l - 1's forward fragments (natural for layer 0, chunk_sigma after).
 template <int IN0, int MID, int OUT, bool NAT0>
 __global__ __launch_bounds__(kTpThreads, 1) void train_pair_kernel(TrainPairArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
   const int h = lane >> 5, col = lane & 31;
   const int in0 = IN0 ? IN0 : a.in0;
   const int mid = MID ? MID : a.mid;
@@ -432,32 +470,161 @@ __global__ __launch_bounds__(kTpThreads, 1) void train_pair_kernel(TrainPairArgs
   const int kco = (out + 15) / 16;
   const int kcm = mid / 16;
   const int kc0 = IN0 ? (NAT0 ? (IN0 + 15) / 16 : IN0 / 16) : a.kc0;
-  const int OP = 32 * mto + kTrPad, IP = 32 * mti + kTrPad, MP = mid + kTrPad;
-  // LDS: fragments, bias, two (g_l, h_{l-1}) tile buffers, the h_l and g_{l-1} tiles
-  half8* swf = reinterpret_cast<half8*>(smem);
-  half8* swl = swf + mtm * kc0 * 64;
-  half8* swl1 = swl + mtm * kco * 64;
-  float* sbias = reinterpret_cast<float*>(swl1 + mtg * kcm * 64);
-  half_t* stile = reinterpret_cast<half_t*>(sbias + mid);
-  const int tile_halves = 32 * (OP + IP);
-  half_t* shl = stile + 2 * tile_halves;
-  half_t* sg1 = shl + 32 * MP;
-  for (int i = threadIdx.x; i < mtm * kc0 * 64; i += blockDim.x) swf[i] = reinterpret_cast<const half8*>(a.wf)[i];
-  for (int i = threadIdx.x; i < mtm * kco * 64; i += blockDim.x) swl[i] = reinterpret_cast<const half8*>(a.wtl)[i];
-  for (int i = threadIdx.x; i < mtg * kcm * 64; i += blockDim.x) swl1[i] = reinterpret_cast<const half8*>(a.wtl1)[i];
+  constexpr int T = kTpT;
+  const PairLds L(in0, mid, out);
+  const int OP = L.OP, IP = L.IP, MP = L.MP;
+  float* sbias = reinterpret_cast<float*>(smem);
+  half_t* base = reinterpret_cast<half_t*>(sbias + mid);
+  auto rg = [&](int b) { return base + b * (L.in_halves + L.pr_halves); };  // g_l [32][OP]
+  auto rh = [&](int b) { return rg(b) + 32 * OP; };                         // h_{l-1} [32][IP]
+  auto tg = [&](int b) { return rh(b) + 32 * IP; };                         // g_l^T [32 mto][T]
+  auto th = [&](int b) { return tg(b) + T * 32 * mto; };                    // h_{l-1}^T [32 mti][T]
+  auto rg1 = [&](int b) { return th(b) + T * 32 * mti; };                   // g_{l-1} [32][MP]
+  auto tg1 = [&](int b) { return rg1(b) + 32 * MP; };                       // g_{l-1}^T [mid][T]
+  auto thl = [&](int b) { return tg1(b) + T * mid; };                       // h_l^T [mid][T]
   for (int i = threadIdx.x; i < mid; i += blockDim.x) sbias[i] = a.bias[i];
-  for (int i = threadIdx.x; i < 2 * tile_halves + 64 * MP; i += blockDim.x) stile[i] = half_t(0.0f);
-  __syncthreads();
+  for (int i = threadIdx.x; i < L.total_halves(); i += blockDim.x) base[i] = half_t(0.0f);  // padding stays zero
 
   const int64_t ntiles = (a.n + 31) / 32;
   const int64_t per_block = (ntiles + gridDim.x - 1) / gridDim.x;
   const int64_t t_begin = int64_t(blockIdx.x) * per_block;
   const int64_t t_end = t_begin + per_block < ntiles ? t_begin + per_block : ntiles;
-  // wave-uniform in a scalar register, so that the per-wave role tests below are
-  // scalar branches and the dW accumulators stay put across the tile loop
-  const int w = __builtin_amdgcn_readfirstlane(wave);
-  __builtin_assume(w >= 0 && w < kTpThreads / 64);
+  const int count = int(t_end > t_begin ? t_end - t_begin : 0);
+  // wave-uniform in scalar registers: role tests are scalar branches
+  const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
+  __builtin_assume(wave >= 0 && wave < kTpThreads / 64);
+  const int role = wave >> 2, w = wave & 3;
 
+  // Tile chunks (16 bytes, 8 features of one point): chunk i covers point i % 32
+  // and features 8 (i / 32) ..; g_l's chunks first, then h_{l-1}'s.  Consecutive
+  // lanes take consecutive points, so the feature-major stores of a chunk fill
+  // consecutive halves of a row.
+  constexpr int kLoads = 2;  // 16-byte chunks per thread: 32 x (128 + 128) halves / 512 threads
+  const int g_chunks = 32 * (out / 8);
+  const int h_chunks = 32 * (in0 / 8);
+  auto load_tile = [&](int64_t tile, half8 (&r)[kLoads]) {
+#pragma unroll
+    for (int k = 0; k < kLoads; ++k) {
+      const int i = k * kTpThreads + int(threadIdx.x);
+      half8 v = {};
+      if (i < g_chunks) {
+        const int64_t p = tile * 32 + (i & 31);
+        if (p < a.n) v = *reinterpret_cast<const half8*>(a.g + p * out + 8 * (i >> 5));
+      } else if (i < g_chunks + h_chunks) {
+        const int kk = i - g_chunks;
+        const int64_t p = tile * 32 + (kk & 31);
+        if (p < a.n) v = *reinterpret_cast<const half8*>(a.hin + p * in0 + 8 * (kk >> 5));
+      }
+      r[k] = v;
+    }
+  };
+  auto park_tile = [&](int b, const half8 (&r)[kLoads]) {
+#pragma unroll
+    for (int k = 0; k < kLoads; ++k) {
+      const int i = k * kTpThreads + int(threadIdx.x);
+      if (i < g_chunks) {
+        const int pp = i & 31, f0 = 8 * (i >> 5);
+        *reinterpret_cast<half8*>(rg(b) + pp * OP + f0) = r[k];
+        half_t* t = tg(b) + f0 * T + pp;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) t[j * T] = r[k][j];
+      } else if (i < g_chunks + h_chunks) {
+        const int kk = i - g_chunks;
+        const int pp = kk & 31, f0 = 8 * (kk >> 5);
+        *reinterpret_cast<half8*>(rh(b) + pp * IP + f0) = r[k];
+        half_t* t = th(b) + f0 * T + pp;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) t[j * T] = r[k][j];
+      }
+    }
+  };
+  __syncthreads();  // zeroed buffers before the first park
+  if (count > 0) {
+    half8 r[kLoads];
+    load_tile(t_begin, r);
+    park_tile(0, r);
+  }
+  __syncthreads();
+
+  if (role == 0) {
+    // ================= role 0: h_l and g_{l-1} of tile it (rows 32w..)
+    half8 wf[kTrKC], wl[kTrKC];
+#pragma unroll
+    for (int c = 0; c < kTrKC; ++c) {
+      wf[c] = (w < mtm && c < kc0) ? reinterpret_cast<const half8*>(a.wf)[(w * kc0 + c) * 64 + lane] : half8{};
+      wl[c] = (w < mtm && c < kco) ? reinterpret_cast<const half8*>(a.wtl)[(w * kco + c) * 64 + lane] : half8{};
+    }
+    for (int it = 0; it <= count; ++it) {
+      half8 r[kLoads];
+      const bool more = it + 1 < count;
+      if (more) load_tile(t_begin + it + 1, r);
+      if (it < count && w < mtm) {
+        const int b = it & 1;
+        const half_t* xh = rh(b);
+        const half_t* xg = rg(b);
+        f32x16 acc;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const f32x4 bv = *reinterpret_cast<const f32x4*>(sbias + 32 * w + 8 * q + 4 * h);
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj) acc[4 * q + jj] = bv[jj];
+        }
+        // the forward's MFMA sequence for layer l - 1: h_l bit-identical
+#pragma unroll
+        for (int c = 0; c < kTrKC; ++c) {
+          if (c < kc0) {
+            half8 bf;
+            if constexpr (NAT0) {
+              bf = *reinterpret_cast<const half8*>(xh + col * IP + 16 * c + 8 * h);
+            } else {
+              const half4v lo = *reinterpret_cast<const half4v*>(xh + col * IP + 16 * c + 4 * h);
+              const half4v hi = *reinterpret_cast<const half4v*>(xh + col * IP + 16 * c + 8 + 4 * h);
+              bf = half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            }
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(wf[c], bf, acc, 0, 0, 0);
+          }
+        }
+        f32x16 accg = {};
+#pragma unroll
+        for (int c = 0; c < kTrKC; ++c) {
+          if (c < kco) {
+            const half8 bf = *reinterpret_cast<const half8*>(xg + col * OP + 16 * c + 8 * h);
+            accg = __builtin_amdgcn_mfma_f32_32x32x16_f16(wl[c], bf, accg, 0, 0, 0);
+          }
+        }
+        // D register 4q + jj is feature 32w + 8q + 4h + jj of point col
+        half_t* ohl = thl(b);
+        half_t* og1 = rg1(b);
+        half_t* ot1 = tg1(b);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          half4v hv, o;
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj) hv[jj] = half_t(acc[4 * q + jj]);
+          hv = __builtin_elementwise_max(hv, half4v{0, 0, 0, 0});
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj) o[jj] = float(hv[jj]) > 0.0f ? half_t(accg[4 * q + jj]) : half_t(0.0f);
+          const int f = 32 * w + 8 * q + 4 * h;
+          *reinterpret_cast<half4v*>(og1 + col * MP + f) = o;
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj) {
+            ohl[(f + jj) * T + col] = hv[jj];
+            ot1[(f + jj) * T + col] = o[jj];
+          }
+        }
+      }
+      __syncthreads();  // tile it's products and tile it-1's reads complete
+      if (more) park_tile((it + 1) & 1, r);
+      __syncthreads();
+    }
+    return;
+  }
+
+  // ================= role 1: dW and g_{l-2} of tile it - 1 (row blocks w)
+  half8 wl1[kTrKC];
+#pragma unroll
+  for (int c = 0; c < kTrKC; ++c)
+    wl1[c] = (w < mtg && c < kcm) ? reinterpret_cast<const half8*>(a.wtl1)[(w * kcm + c) * 64 + lane] : half8{};
   f32x16 accl[kTrMT], accl1[kTrMT];
 #pragma unroll
   for (int t = 0; t < kTrMT; ++t) {
@@ -465,165 +632,77 @@ __global__ __launch_bounds__(kTpThreads, 1) void train_pair_kernel(TrainPairArgs
     accl1[t] = f32x16{};
   }
   float dbl = 0.0f, dbl1 = 0.0f;
-
-  const int g_chunks = 32 * out / 8;
-  const int h_chunks = 32 * in0 / 8;
-  auto load_tile = [&](int64_t tile, half8 (&r)[kTrLoads]) {
+  for (int it = 0; it <= count; ++it) {
+    half8 r[kLoads];
+    const bool more = it + 1 < count;
+    if (more) load_tile(t_begin + it + 1, r);
+    if (it >= 1) {
+      const int b = (it - 1) & 1;
+      const int64_t tile = t_begin + it - 1;
+      // ---- dW_l rows 32w.. += g_l^T[32w.., points] h_l[points, :]
+      if (w < mto) {
+        const half_t* xtg = tg(b);
+        const half_t* xhl = thl(b);
 #pragma unroll
-    for (int k = 0; k < kTrLoads; ++k) {
-      const int i = k * kTpThreads + int(threadIdx.x);
-      half8 v = {};
-      if (i < g_chunks) {
-        const int rr = i / (out / 8), c8 = i % (out / 8);
-        const int64_t p = tile * 32 + rr;
-        if (p < a.n) v = *reinterpret_cast<const half8*>(a.g + p * out + 8 * c8);
-      } else if (i < g_chunks + h_chunks) {
-        const int kk = i - g_chunks;
-        const int rr = kk / (in0 / 8), c8 = kk % (in0 / 8);
-        const int64_t p = tile * 32 + rr;
-        if (p < a.n) v = *reinterpret_cast<const half8*>(a.hin + p * in0 + 8 * c8);
-      }
-      r[k] = v;
-    }
-  };
-  auto park_tile = [&](half_t* buf, const half8 (&r)[kTrLoads]) {
+        for (int ks = 0; ks < 2; ++ks) {
+          const half8 af = tp_frag(xtg + (32 * w + col) * T + 16 * ks + 8 * h);
 #pragma unroll
-    for (int k = 0; k < kTrLoads; ++k) {
-      const int i = k * kTpThreads + int(threadIdx.x);
-      if (i < g_chunks) {
-        const int rr = i / (out / 8), c8 = i % (out / 8);
-        *reinterpret_cast<half8*>(buf + rr * OP + 8 * c8) = r[k];
-      } else if (i < g_chunks + h_chunks) {
-        const int kk = i - g_chunks;
-        const int rr = kk / (in0 / 8), c8 = kk % (in0 / 8);
-        *reinterpret_cast<half8*>(buf + 32 * OP + rr * IP + 8 * c8) = r[k];
-      }
-    }
-  };
-  if (t_begin < t_end) {
-    half8 r[kTrLoads];
-    load_tile(t_begin, r);
-    park_tile(stile, r);
-  }
-  __syncthreads();
-
-  for (int64_t tile = t_begin; tile < t_end; ++tile) {
-    const int cur = int((tile - t_begin) & 1);
-    const half_t* tg = stile + cur * tile_halves;
-    const half_t* th = tg + 32 * OP;
-    half8 r[kTrLoads];
-    const bool more = tile + 1 < t_end;
-    if (more) load_tile(tile + 1, r);
-
-    if (w < mtm) {
-      // ---- h_l rows 32w..32w+31 (the forward's MFMA sequence for layer l - 1)
-      f32x16 acc;
+          for (int j = 0; j < 8; ++j) dbl += float(af[j]);
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const f32x4 bv = *reinterpret_cast<const f32x4*>(sbias + 32 * w + 8 * q + 4 * h);
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj) acc[4 * q + jj] = bv[jj];
-      }
-#pragma unroll
-      for (int c = 0; c < kc0; ++c) {
-        half8 bf;
-        if constexpr (NAT0) {
-          bf = *reinterpret_cast<const half8*>(th + col * IP + 16 * c + 8 * h);
-        } else {
-          const half4v lo = *reinterpret_cast<const half4v*>(th + col * IP + 16 * c + 4 * h);
-          const half4v hi = *reinterpret_cast<const half4v*>(th + col * IP + 16 * c + 8 + 4 * h);
-          bf = half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-        }
-        acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(swf[(w * kc0 + c) * 64 + lane], bf, acc, 0, 0, 0);
-      }
-      // D register 4q + jj is row 32w + 8q + 4h + jj: fp16, ReLU; into LDS row-major
-      half4v hv[4];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj) hv[q][jj] = half_t(acc[4 * q + jj]);
-        hv[q] = __builtin_elementwise_max(hv[q], half4v{0, 0, 0, 0});
-        *reinterpret_cast<half4v*>(shl + col * MP + 32 * w + 8 * q + 4 * h) = hv[q];
-      }
-      // ---- g_{l-1} rows 32w.. = W_l^T[32w.., :] g_l^T, masked by h_l > 0
-      f32x16 accg = {};
-#pragma unroll
-      for (int c = 0; c < kco; ++c) {
-        const half8 bf = *reinterpret_cast<const half8*>(tg + col * OP + 16 * c + 8 * h);
-        accg = __builtin_amdgcn_mfma_f32_32x32x16_f16(swl[(w * kco + c) * 64 + lane], bf, accg, 0, 0, 0);
-      }
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        half4v o;
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj) o[jj] = float(hv[q][jj]) > 0.0f ? half_t(accg[4 * q + jj]) : half_t(0.0f);
-        *reinterpret_cast<half4v*>(sg1 + col * MP + 32 * w + 8 * q + 4 * h) = o;
-      }
-    }
-    __syncthreads();  // h_l and g_{l-1} tiles complete
-
-    // ---- dW_l rows 32w.. += g_l^T[32w.., points] h_l[points, :]
-    if (w < mto) {
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        half8 af;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) af[j] = tg[(16 * ks + 8 * h + j) * OP + 32 * w + col];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) dbl += float(af[j]);
-#pragma unroll
-        for (int t = 0; t < kTrMT; ++t) {
-          if (t < mtm) {
-            half8 bf;
-#pragma unroll
-            for (int j = 0; j < 8; ++j) bf[j] = shl[(16 * ks + 8 * h + j) * MP + 32 * t + col];
-            accl[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf, accl[t], 0, 0, 0);
+          for (int t = 0; t < kTrMT; ++t) {
+            if (t < mtm) {
+              const half8 bf = tp_frag(xhl + (32 * t + col) * T + 16 * ks + 8 * h);
+              accl[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf, accl[t], 0, 0, 0);
+            }
           }
         }
       }
-    }
-    if (w < mtm) {
       // ---- dW_{l-1} rows 32w.. += g_{l-1}^T[32w.., points] h_{l-1}[points, :]
+      if (w < mtm) {
+        const half_t* xt1 = tg1(b);
+        const half_t* xth = th(b);
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        half8 af;
+        for (int ks = 0; ks < 2; ++ks) {
+          const half8 af = tp_frag(xt1 + (32 * w + col) * T + 16 * ks + 8 * h);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) af[j] = sg1[(16 * ks + 8 * h + j) * MP + 32 * w + col];
+          for (int j = 0; j < 8; ++j) dbl1 += float(af[j]);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) dbl1 += float(af[j]);
+          for (int t = 0; t < kTrMT; ++t) {
+            if (t < mti) {
+              const half8 bf = tp_frag(xth + (32 * t + col) * T + 16 * ks + 8 * h);
+              accl1[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf, accl1[t], 0, 0, 0);
+            }
+          }
+        }
+      }
+      // ---- g_{l-2} rows 32w.. = W_{l-1}^T[32w.., :] g_{l-1}^T, masked by h_{l-1} > 0
+      if (w < mtg) {
+        const half_t* xg1 = rg1(b);
+        const half_t* xh = rh(b);
+        f32x16 acc = {};
 #pragma unroll
-        for (int t = 0; t < kTrMT; ++t) {
-          if (t < mti) {
-            half8 bf;
+        for (int c = 0; c < kTrKC; ++c) {
+          if (c < kcm) {
+            const half8 bf = *reinterpret_cast<const half8*>(xg1 + col * MP + 16 * c + 8 * h);
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(wl1[c], bf, acc, 0, 0, 0);
+          }
+        }
+        const int64_t p = tile * 32 + col;
+        if (p < a.n) {
 #pragma unroll
-            for (int j = 0; j < 8; ++j) bf[j] = th[(16 * ks + 8 * h + j) * IP + 32 * t + col];
-            accl1[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf, accl1[t], 0, 0, 0);
+          for (int q = 0; q < 4; ++q) {
+            const int i0 = 32 * w + 8 * q + 4 * h;
+            const half4v hv = *reinterpret_cast<const half4v*>(xh + col * IP + i0);
+            half4v o;
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj) o[jj] = float(hv[jj]) > 0.0f ? half_t(acc[4 * q + jj]) : half_t(0.0f);
+            *reinterpret_cast<half4v*>(a.gout + p * in0 + i0) = o;
           }
         }
       }
     }
-    if (w < mtg) {
-      // ---- g_{l-2} rows 32w.. = W_{l-1}^T[32w.., :] g_{l-1}^T, masked by h_{l-1} > 0
-      f32x16 acc = {};
-#pragma unroll
-      for (int c = 0; c < kcm; ++c) {
-        const half8 bf = *reinterpret_cast<const half8*>(sg1 + col * MP + 16 * c + 8 * h);
-        acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(swl1[(w * kcm + c) * 64 + lane], bf, acc, 0, 0, 0);
-      }
-      const int64_t p = tile * 32 + col;
-      if (p < a.n) {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int i0 = 32 * w + 8 * q + 4 * h;
-          const half4v hv = *reinterpret_cast<const half4v*>(th + col * IP + i0);
-          half4v o;
-#pragma unroll
-          for (int jj = 0; jj < 4; ++jj) o[jj] = float(hv[jj]) > 0.0f ? half_t(acc[4 * q + jj]) : half_t(0.0f);
-          *reinterpret_cast<half4v*>(a.gout + p * in0 + i0) = o;
-        }
-      }
-    }
-    if (more) park_tile(stile + (cur ^ 1) * tile_halves, r);  // the other buffer: last read a tile ago
+    __syncthreads();  // tile it's products and tile it-1's reads complete
+    if (more) park_tile((it + 1) & 1, r);
     __syncthreads();
   }
 
@@ -734,11 +813,10 @@ static const void* pair_kernel(const TrainPairArgs& pa) {
 
 // LDS bytes of train_pair_kernel (same carve-up as the kernel).
 static int64_t pair_lds(int in0, int mid, int out, int kc0, bool gout) {
-  const int mtm = mid / 32, mto = (out + 31) / 32, mti = (in0 + 31) / 32;
-  const int kco = (out + 15) / 16, kcm = mid / 16;
-  const int64_t frags = int64_t(mtm) * kc0 + int64_t(mtm) * kco + (gout ? int64_t(in0 / 32) * kcm : 0);
-  const int64_t tiles = 2 * 32 * int64_t((32 * mto + kTrPad) + (32 * mti + kTrPad)) + 64 * int64_t(mid + kTrPad);
-  return frags * 1024 + int64_t(mid) * 4 + tiles * 2;
+  (void)kc0;
+  (void)gout;
+  const PairLds L(in0, mid, out);
+  return int64_t(mid) * 4 + int64_t(L.total_halves()) * 2;
 }
 
 static int64_t group_lds(const MlpLayout& lay, int l0, int l1) {
