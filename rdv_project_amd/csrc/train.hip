@@ -406,7 +406,7 @@ struct TrainPairArgs {
   const float* bias;     // layer l-1 padded bias [mid]
   const half_t* wtl;     // W_l^T fragments [mid / 32][ceil(out / 16)][64][8]
   const half_t* wtl1;    // W_{l-1}^T fragments [in0 / 32][mid / 16][64][8] (gout only)
-  half_t* gout;          // [n, in0] g_{l-2}, or null
+  half_t* gout;          // [n + 1, in0] g_{l-2} (row n: spare, written by lanes past n), or null
   float* dw_l;           // [gridDim.x][out][mid]
   float* db_l;           // [gridDim.x][out]
   float* dw_l1;          // [gridDim.x][mid][in0]
@@ -454,8 +454,9 @@ struct PairLds {
 //
 // IN0 / MID / OUT: the widths as compile-time constants (fully unrolled K loops),
 // or 0 for the generic kernel that reads them from the arguments.  NAT0: the K
-// order of layer l - 1's forward fragments (natural for layer 0, chunk_sigma after).
-template <int IN0, int MID, int OUT, bool NAT0>
+// order of layer l - 1's forward fragments (natural for layer 0, chunk_sigma
+// after).  GOUT: 1 when g_{l-2} is written, 0 when not, -1 to read a.gout.
+template <int IN0, int MID, int OUT, bool NAT0, int GOUT>
 __global__ __launch_bounds__(kTpThreads, 1) void train_pair_kernel(TrainPairArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const int lane = threadIdx.x & 63;
@@ -466,7 +467,8 @@ __global__ __launch_bounds__(kTpThreads, 1) void train_pair_kernel(TrainPairArgs
   const int mtm = mid / 32;              // row blocks of h_l and g_{l-1}
   const int mto = (out + 31) / 32;       // row blocks of dW_l
   const int mti = (in0 + 31) / 32;       // column blocks of dW_{l-1}
-  const int mtg = a.gout != nullptr ? in0 / 32 : 0;  // row blocks of g_{l-2}
+  const bool gout = GOUT < 0 ? a.gout != nullptr : GOUT != 0;
+  const int mtg = gout ? in0 / 32 : 0;   // row blocks of g_{l-2}
   const int kco = (out + 15) / 16;
   const int kcm = mid / 16;
   const int kc0 = IN0 ? (NAT0 ? (IN0 + 15) / 16 : IN0 / 16) : a.kc0;
@@ -502,39 +504,37 @@ __global__ __launch_bounds__(kTpThreads, 1) void train_pair_kernel(TrainPairArgs
   constexpr int kLoads = 2;  // 16-byte chunks per thread: 32 x (128 + 128) halves / 512 threads
   const int g_chunks = 32 * (out / 8);
   const int h_chunks = 32 * (in0 / 8);
+  // Loads are unconditional (rows clamped into range, unused slots re-read a valid
+  // chunk) so that the compiler can count the wave's outstanding memory ops
+  // exactly: a wait for these loads then never waits for the g_{l-2} stores
+  // issued after them.  Rows past n are zeroed when parked.
+  __builtin_assume(threadIdx.x < kTpThreads);
   auto load_tile = [&](int64_t tile, half8 (&r)[kLoads]) {
 #pragma unroll
     for (int k = 0; k < kLoads; ++k) {
       const int i = k * kTpThreads + int(threadIdx.x);
-      half8 v = {};
-      if (i < g_chunks) {
-        const int64_t p = tile * 32 + (i & 31);
-        if (p < a.n) v = *reinterpret_cast<const half8*>(a.g + p * out + 8 * (i >> 5));
-      } else if (i < g_chunks + h_chunks) {
-        const int kk = i - g_chunks;
-        const int64_t p = tile * 32 + (kk & 31);
-        if (p < a.n) v = *reinterpret_cast<const half8*>(a.hin + p * in0 + 8 * (kk >> 5));
-      }
-      r[k] = v;
+      const bool isg = i < g_chunks;
+      const int kk = isg ? i : (i < g_chunks + h_chunks ? i - g_chunks : 0);
+      int64_t p = tile * 32 + (kk & 31);
+      p = p < a.n ? p : a.n - 1;
+      const half_t* src = isg ? a.g + p * out + 8 * (kk >> 5) : a.hin + p * in0 + 8 * (kk >> 5);
+      r[k] = *reinterpret_cast<const half8*>(src);
     }
   };
-  auto park_tile = [&](int b, const half8 (&r)[kLoads]) {
+  auto park_tile = [&](int b, int64_t tile, const half8 (&r)[kLoads]) {
 #pragma unroll
     for (int k = 0; k < kLoads; ++k) {
       const int i = k * kTpThreads + int(threadIdx.x);
-      if (i < g_chunks) {
-        const int pp = i & 31, f0 = 8 * (i >> 5);
-        *reinterpret_cast<half8*>(rg(b) + pp * OP + f0) = r[k];
-        half_t* t = tg(b) + f0 * T + pp;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) t[j * T] = r[k][j];
-      } else if (i < g_chunks + h_chunks) {
-        const int kk = i - g_chunks;
+      if (i < g_chunks + h_chunks) {
+        const bool isg = i < g_chunks;
+        const int kk = isg ? i : i - g_chunks;
         const int pp = kk & 31, f0 = 8 * (kk >> 5);
-        *reinterpret_cast<half8*>(rh(b) + pp * IP + f0) = r[k];
-        half_t* t = th(b) + f0 * T + pp;
+        const half8 v = tile * 32 + pp < a.n ? r[k] : half8{};
+        half_t* rowp = isg ? rg(b) + pp * OP + f0 : rh(b) + pp * IP + f0;
+        half_t* t = (isg ? tg(b) : th(b)) + f0 * T + pp;
+        *reinterpret_cast<half8*>(rowp) = v;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) t[j * T] = r[k][j];
+        for (int j = 0; j < 8; ++j) t[j * T] = v[j];
       }
     }
   };
@@ -542,7 +542,7 @@ __global__ __launch_bounds__(kTpThreads, 1) void train_pair_kernel(TrainPairArgs
   if (count > 0) {
     half8 r[kLoads];
     load_tile(t_begin, r);
-    park_tile(0, r);
+    park_tile(0, t_begin, r);
   }
   __syncthreads();
 
@@ -554,6 +554,9 @@ __global__ __launch_bounds__(kTpThreads, 1) void train_pair_kernel(TrainPairArgs
       wf[c] = (w < mtm && c < kc0) ? reinterpret_cast<const half8*>(a.wf)[(w * kc0 + c) * 64 + lane] : half8{};
       wl[c] = (w < mtm && c < kco) ? reinterpret_cast<const half8*>(a.wtl)[(w * kco + c) * 64 + lane] : half8{};
     }
+    // all of them in registers before the loop, so that no wait inside it has
+    // to cover these loads
+    __builtin_amdgcn_s_waitcnt(0);
     for (int it = 0; it <= count; ++it) {
       half8 r[kLoads];
       const bool more = it + 1 < count;
@@ -614,7 +617,7 @@ __global__ __launch_bounds__(kTpThreads, 1) void train_pair_kernel(TrainPairArgs
         }
       }
       __syncthreads();  // tile it's products and tile it-1's reads complete
-      if (more) park_tile((it + 1) & 1, r);
+      if (more) park_tile((it + 1) & 1, t_begin + it + 1, r);
       __syncthreads();
     }
     return;
@@ -625,6 +628,7 @@ __global__ __launch_bounds__(kTpThreads, 1) void train_pair_kernel(TrainPairArgs
 #pragma unroll
   for (int c = 0; c < kTrKC; ++c)
     wl1[c] = (w < mtg && c < kcm) ? reinterpret_cast<const half8*>(a.wtl1)[(w * kcm + c) * 64 + lane] : half8{};
+  __builtin_amdgcn_s_waitcnt(0);
   f32x16 accl[kTrMT], accl1[kTrMT];
 #pragma unroll
   for (int t = 0; t < kTrMT; ++t) {
@@ -687,22 +691,23 @@ __global__ __launch_bounds__(kTpThreads, 1) void train_pair_kernel(TrainPairArgs
             acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(wl1[c], bf, acc, 0, 0, 0);
           }
         }
-        const int64_t p = tile * 32 + col;
-        if (p < a.n) {
+        // unconditional stores (exact wait counts): points past n go to the
+        // spare row n of gout
+        int64_t p = tile * 32 + col;
+        p = p < a.n ? p : a.n;
 #pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const int i0 = 32 * w + 8 * q + 4 * h;
-            const half4v hv = *reinterpret_cast<const half4v*>(xh + col * IP + i0);
-            half4v o;
+        for (int q = 0; q < 4; ++q) {
+          const int i0 = 32 * w + 8 * q + 4 * h;
+          const half4v hv = *reinterpret_cast<const half4v*>(xh + col * IP + i0);
+          half4v o;
 #pragma unroll
-            for (int jj = 0; jj < 4; ++jj) o[jj] = float(hv[jj]) > 0.0f ? half_t(acc[4 * q + jj]) : half_t(0.0f);
-            *reinterpret_cast<half4v*>(a.gout + p * in0 + i0) = o;
-          }
+          for (int jj = 0; jj < 4; ++jj) o[jj] = float(hv[jj]) > 0.0f ? half_t(acc[4 * q + jj]) : half_t(0.0f);
+          *reinterpret_cast<half4v*>(a.gout + p * in0 + i0) = o;
         }
       }
     }
     __syncthreads();  // tile it's products and tile it-1's reads complete
-    if (more) park_tile((it + 1) & 1, r);
+    if (more) park_tile((it + 1) & 1, t_begin + it + 1, r);
     __syncthreads();
   }
 
@@ -799,15 +804,16 @@ static constexpr int64_t kTrPairLdsCap = 160 * 1024;
 // Specialisations of train_pair_kernel: the layer pairs of the benchmark chain
 // (128-wide hidden layers, a 16-wide head), then the generic kernel.
 static const void* const kPairKernels[] = {
-    reinterpret_cast<const void*>(&train_pair_kernel<128, 128, 128, false>),
-    reinterpret_cast<const void*>(&train_pair_kernel<128, 128, 16, false>),
-    reinterpret_cast<const void*>(&train_pair_kernel<0, 0, 0, false>),
-    reinterpret_cast<const void*>(&train_pair_kernel<0, 0, 0, true>),
+    reinterpret_cast<const void*>(&train_pair_kernel<128, 128, 128, false, 1>),
+    reinterpret_cast<const void*>(&train_pair_kernel<128, 128, 16, false, 1>),
+    reinterpret_cast<const void*>(&train_pair_kernel<0, 0, 0, false, -1>),
+    reinterpret_cast<const void*>(&train_pair_kernel<0, 0, 0, true, -1>),
 };
 
 static const void* pair_kernel(const TrainPairArgs& pa) {
-  if (!pa.natural0 && pa.in0 == 128 && pa.mid == 128 && pa.out == 128) return kPairKernels[0];
-  if (!pa.natural0 && pa.in0 == 128 && pa.mid == 128 && pa.out == 16) return kPairKernels[1];
+  const bool g = pa.gout != nullptr;
+  if (g && !pa.natural0 && pa.in0 == 128 && pa.mid == 128 && pa.out == 128) return kPairKernels[0];
+  if (g && !pa.natural0 && pa.in0 == 128 && pa.mid == 128 && pa.out == 16) return kPairKernels[1];
   return kPairKernels[pa.natural0 ? 3 : 2];
 }
 
@@ -883,8 +889,8 @@ static void train_plan(const rdv_mlp_desc& d, const MlpLayout& lay, int64_t n, i
   }
   for (int i = 0; i < L; ++i) p->h_off[i] = (i >= 1 && p->keep[i]) ? take(n * d.dims[i] * 2) : -1;
   p->g_off = take(n * d.dims[L] * 2);
-  p->dz_off[0] = take(n * maxw * 2);
-  p->dz_off[1] = take(n * maxw * 2);
+  p->dz_off[0] = take((n + 1) * maxw * 2);  // + the pair kernel's spare row
+  p->dz_off[1] = take((n + 1) * maxw * 2);
   const int64_t parts = std::max(p->blocks_bwd, p->blocks_pair);
   for (int k = 0; k < 2; ++k) {
     p->dw_off[k] = take(parts * maxoi * 4);
