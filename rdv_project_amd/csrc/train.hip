@@ -13,21 +13,22 @@
 // Kernels.
 //  - train_fwd_kernel: a group of consecutive layers whose A fragments fit in
 //    LDS, per wave 32-point tiles, the same register layer hand-off as the
-//    fused MLP (mlp_layout.h); every hidden output is also stored (fp16, row
-//    major) for the backward pass; the group that ends the chain computes
-//    g = 2 (y - t) and per-block partial sums of (y - t)^2.
+//    fused MLP (mlp_layout.h); the hidden outputs the backward pass reads are
+//    also stored (fp16, tile-fragment layout, below); the group that ends the
+//    chain computes g = 2 (y - t) and per-block partial sums of (y - t)^2.
+//    train_fwd_pair_kernel is the same with compile-time shapes and two
+//    staggered tiles per wave.
 //  - train_pair_kernel: layers l and l - 1 in one pass (pairs from the head
 //    down): recomputes h_l from the stored h_{l-1}, keeps g_{l-1} in LDS, and
 //    accumulates dW of both layers; only g_{l-2} reaches HBM.  The forward
 //    therefore stores every other activation.
-//  - train_bwd_kernel: one layer (layer 0 when the chain has an odd number of
-//    layers); a block of 4 waves stages 32-point tiles of dz_{l+1} and h_l in
-//    two LDS buffers (the next tile's loads in flight while the current one is
-//    computed), then wave w computes one 32-row tile of
-//    dz_l^T = W^T dz_{l+1}^T (v_mfma_f32_32x32x16_f16 with packed W^T fragments)
-//    and one 32-row tile of dW (K = the tile's points, operands
-//    gathered from the LDS tile); dW stays in registers across the block's whole
-//    point range and is written once as a per-block partial.
+//  - train_bwd_kernel: dW and db of layer 0 alone (when the chain has an odd
+//    number of layers); a block of 4 waves stages 32-point tiles of dz_1 and
+//    the chain input in two LDS buffers (the next tile's loads in flight while
+//    the current one is computed), then wave w computes one 32-row tile of dW
+//    (K = the tile's points, operands gathered from the LDS tile); dW stays in
+//    registers across the block's whole point range and is written once as a
+//    per-block partial.
 //  - train_reduce1/2_kernel: sum the per-block partials in a fixed order.
 #include <algorithm>
 
@@ -45,10 +46,10 @@ struct TrainFwdArgs {
   const uint8_t* packed;
   MlpLayout lay;
   int L, l0, l1;                        // layers [l0, l1) of an L-layer chain
-  const half_t* in;                     // layer l0's input [n, in_w[l0]] fp16
-  half_t* hout[RDV_MLP_MAX_LAYERS];     // hout[l]: output of layer l (l < L - 1) [n, out_w[l]], or null (not kept)
+  const half_t* in;                     // layer l0's input: the chain input [n, in_w[0]] fp16 (l0 == 0), else tile-fragment layout
+  half_t* hout[RDV_MLP_MAX_LAYERS];     // hout[l]: output of layer l (l < L - 1), tile-fragment layout, or null (not kept)
   const float* target;                  // [n, out] fp32 (l1 == L)
-  half_t* g;                            // [n, out] fp16 2 (y - t) (l1 == L)
+  half_t* g;                            // 2 (y - t), tile-fragment layout of width out (l1 == L)
   float* loss_partial;                  // [gridDim.x] (l1 == L)
   int64_t n;
   int has_bias;
@@ -70,6 +71,18 @@ __device__ __forceinline__ float tr_wave_sum(float v) {
 }
 
 typedef half_t half4v __attribute__((ext_vector_type(4)));
+
+// Tile-fragment layout of the step's intermediate fp16 buffers (the kept hidden
+// activations h_i, the head gradient g and the gradients g_i between backward
+// launches), [rows][W] with rows a multiple of 64: 32-point tiles of
+// Wp = 16 ceil(W / 16) features, tile k at k 32 Wp; within a tile, 16-byte chunk
+// c = 64 s + 32 hh + col holds point col, features 16 s + 4 hh + 0..3 and then
+// 16 s + 8 + 4 hh + 0..3 (tfl_feature).  That chunk is lane 32 hh + col's B
+// fragment of K chunk s in the hidden (chunk_sigma) order, and equally the fp16
+// of D registers 8 (s % 2) .. + 7 of 32-row block s / 2, so a wave writes or
+// reads a whole 1 KiB slot s with one 16-byte access per lane.  Features past W
+// are stored as zeros.
+__device__ __forceinline__ int tfl_feature(int s, int hh, int j) { return 16 * s + 4 * hh + (j & 3) + ((j >> 2) << 3); }
 
 __global__ __launch_bounds__(kTrFwdThreads, 1) void train_fwd_kernel(TrainFwdArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -109,20 +122,15 @@ __global__ __launch_bounds__(kTrFwdThreads, 1) void train_fwd_kernel(TrainFwdArg
     half8 b[kTrKC];
     {
       const int w0 = lay.in_w[a.l0];
-      const half_t* row = a.in + pc * w0;
       const int kc0 = lay.kc[a.l0];
+      const half_t* row = a.in + pc * w0;
+      const half8* slots = reinterpret_cast<const half8*>(a.in + tile * 32 * w0);
 #pragma unroll
       for (int c = 0; c < kTrKC; ++c) {
         if (c < kc0) {
-          if (a.l0 == 0) {
-            // natural order: features 16c + 8h + 0..7
-            b[c] = *reinterpret_cast<const half8*>(row + 16 * c + 8 * h);
-          } else {
-            // hidden slot order (chunk_sigma): 16c + 4h + 0..3, then 16c + 8 + 4h + 0..3
-            const half4v lo = *reinterpret_cast<const half4v*>(row + 16 * c + 4 * h);
-            const half4v hi = *reinterpret_cast<const half4v*>(row + 16 * c + 8 + 4 * h);
-            b[c] = half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-          }
+          // natural order (the chain input): features 16c + 8h + 0..7; a hidden
+          // input: slot c of the tile-fragment layout
+          b[c] = a.l0 == 0 ? *reinterpret_cast<const half8*>(row + 16 * c + 8 * h) : slots[c * 64 + lane];
         }
       }
     }
@@ -156,32 +164,43 @@ __global__ __launch_bounds__(kTrFwdThreads, 1) void train_fwd_kernel(TrainFwdArg
         }
       }
       if (l == a.L - 1) {
-        // head: y = acc rows (32t + 8q + 4h + jj) < out; g = 2 (y - t), loss += (y - t)^2
+        // head: y = D rows (32t + 8q + 4h + jj) < out; g = 2 (y - t), loss += (y - t)^2
         const int out = lay.out_w[l];
+        const int wg = 16 * ((out + 15) / 16);
+        half8* gs = reinterpret_cast<half8*>(a.g + tile * 32 * wg);
 #pragma unroll
         for (int t = 0; t < kTrMT; ++t) {
           if (t < mt) {
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              const int r = 32 * t + 8 * q + 4 * h;
-              if (r < out && pv) {
-                const f32x4 tv = *reinterpret_cast<const f32x4*>(a.target + p * out + r);
-                half4v gv;
+            for (int qq = 0; qq < 2; ++qq) {
+              if (32 * t + 16 * qq < out) {
+                half8 gv;
 #pragma unroll
-                for (int jj = 0; jj < 4; ++jj) {
-                  const float d = acc[t][4 * q + jj] - tv[jj];
-                  loss += d * d;
-                  gv[jj] = half_t(d + d);
+                for (int hi = 0; hi < 2; ++hi) {
+                  // registers 8qq + 4hi + jj: rows 32t + 16qq + 8hi + 4h + jj
+                  const int r = 32 * t + 16 * qq + 8 * hi + 4 * h;
+                  if (32 * t + 16 * qq + 8 * hi < out) {
+                    const f32x4 tv = *reinterpret_cast<const f32x4*>(a.target + pc * out + r);
+#pragma unroll
+                    for (int jj = 0; jj < 4; ++jj) {
+                      const float d = acc[t][8 * qq + 4 * hi + jj] - tv[jj];
+                      loss += pv ? d * d : 0.0f;
+                      gv[4 * hi + jj] = half_t(d + d);
+                    }
+                  } else {
+#pragma unroll
+                    for (int jj = 0; jj < 4; ++jj) gv[4 * hi + jj] = half_t(0.0f);
+                  }
                 }
-                *reinterpret_cast<half4v*>(a.g + p * out + r) = gv;
+                gs[(2 * t + qq) * 64 + lane] = gv;
               }
             }
           }
         }
       } else {
-        // ReLU, fp16: store the hidden output and hand it to the next layer
+        // ReLU, fp16: store the hidden output (slot 2t + qq of the tile) and hand it to the next layer
         const int out = lay.out_w[l];
-        half_t* dst = a.hout[l] == nullptr ? nullptr : a.hout[l] + p * out;
+        half8* dst = a.hout[l] == nullptr ? nullptr : reinterpret_cast<half8*>(a.hout[l] + tile * 32 * out);
 #pragma unroll
         for (int t = 0; t < kTrMT; ++t) {
           if (t < mt) {
@@ -192,11 +211,7 @@ __global__ __launch_bounds__(kTrFwdThreads, 1) void train_fwd_kernel(TrainFwdArg
               for (int j = 0; j < 8; ++j) v[j] = half_t(acc[t][8 * qq + j]);
               v = __builtin_elementwise_max(v, half8{0, 0, 0, 0, 0, 0, 0, 0});
               b[2 * t + qq] = v;
-              if (pv && dst != nullptr) {
-                // registers 8qq + 0..3 are rows 32t + 16qq + 4h + 0..3, 8qq + 4..7 rows 32t + 16qq + 8 + 4h + 0..3
-                *reinterpret_cast<half4v*>(dst + 32 * t + 16 * qq + 4 * h) = half4v{v[0], v[1], v[2], v[3]};
-                *reinterpret_cast<half4v*>(dst + 32 * t + 16 * qq + 8 + 4 * h) = half4v{v[4], v[5], v[6], v[7]};
-              }
+              if (dst != nullptr) dst[(2 * t + qq) * 64 + lane] = v;
             }
           }
         }
@@ -215,12 +230,246 @@ __global__ __launch_bounds__(kTrFwdThreads, 1) void train_fwd_kernel(TrainFwdArg
   }
 }
 
+// ------------------------------------------------- forward, tile pairs
+// train_fwd_pair_kernel: the same group evaluation with a compile-time chain
+// shape N (Net<RDV_ENC_NONE, in width, 0, out width, kc of the group's first
+// layer, mt of each layer>).  Each wave evaluates 64 points at a time as two
+// 32-point tiles A and B staggered by half a layer (stage_pair, mlp_core.h):
+// one tile's fp32 -> fp16 hand-off runs between the other tile's MFMAs.  A
+// kept activation is stored from the hand-off registers, one 1 KiB slot per
+// store (tile-fragment layout).
+//   KEEP: bit l set when the output of the group's layer l is stored
+//         (a.hout[a.l0 + l]); NAT0: the group input is the chain input (natural
+//         K order), else a stored hidden activation (chunk_sigma K order);
+//   HEAD: the group ends the chain (g = 2 (y - t) and the loss partials).
+// Buffers hold whole pair tiles (rows rounded up to 64), so every store is
+// unconditional; rows >= n hold values never read as data.
+template <class N, int l>
+__device__ __forceinline__ void tf_store(const half8 (&b)[N::kMaxKC], half_t* tile_base, int lane) {
+  half8* d = reinterpret_cast<half8*>(tile_base);
+#pragma unroll
+  for (int s = 0; s < 2 * N::mt(l); ++s) d[s * 64 + lane] = b[s];
+}
+
+// tA, tB: the two tiles' indices.
+template <class N, int l, int KEEP, bool HEAD>
+__device__ __forceinline__ void tf_layers(const LdsWeights& ws, const float* sb, int h, half8 (&bA)[N::kMaxKC],
+                                          half8 (&bB)[N::kMaxKC], f32x16 (&accA)[N::kMaxMT],
+                                          f32x16 (&accB)[N::kMaxMT], const TrainFwdArgs& a, int64_t tA, int64_t tB) {
+  constexpr int L = N::kL;
+  constexpr int W = 32 * N::mt(l);  // output width of a hidden layer
+  const int lane = ws.lane;
+  // stage boundaries are scheduling barriers: a stage holds the accumulators
+  // of two tiles, never three
+  __builtin_amdgcn_sched_barrier(0);
+  load_bias<N, l>(accA, sb, h);
+  if constexpr (l == 0) {
+    stage_pair<N, 0, -1, true, true>(ws, bA, accA, accB, bB);
+  } else {
+    constexpr int Wp = 32 * N::mt(l - 1);
+    stage_pair<N, l, l - 1, true, true>(ws, bA, accA, accB, bB);
+    if constexpr ((KEEP >> (l - 1)) & 1) tf_store<N, l - 1>(bB, a.hout[a.l0 + l - 1] + tB * 32 * Wp, lane);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  load_bias<N, l>(accB, sb, h);
+  constexpr bool handA = l + 1 < L || !HEAD;
+  stage_pair<N, l, handA ? l : -1, true, true>(ws, bB, accB, accA, bA);
+  if constexpr (handA && ((KEEP >> l) & 1)) tf_store<N, l>(bA, a.hout[a.l0 + l] + tA * 32 * W, lane);
+  if constexpr (l + 1 < L) {
+    tf_layers<N, l + 1, KEEP, HEAD>(ws, sb, h, bA, bB, accA, accB, a, tA, tB);
+  } else if constexpr (!HEAD) {
+#pragma unroll
+    for (int s = 0; s < 2 * N::mt(l); ++s) handoff_slot<N, l, true>(s, accB, bB);
+    if constexpr ((KEEP >> l) & 1) tf_store<N, l>(bB, a.hout[a.l0 + l] + tB * 32 * W, lane);
+  }
+}
+
+constexpr int kTfWaves = 8;  // two per SIMD
+constexpr int kTfThreads = 64 * kTfWaves;
+
+template <class N, int KEEP, bool HEAD, bool NAT0>
+__global__ __launch_bounds__(kTfThreads, 1) void train_fwd_pair_kernel(TrainFwdArgs a) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  __shared__ float s_loss[kTfWaves];
+  constexpr int L = N::kL;
+  constexpr int IN0 = N::kIn;
+  constexpr int KC0 = N::kc(0);
+  constexpr int OUT = N::kOut;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
+  const int h = lane >> 5, col = lane & 31;
+  half8* sw = reinterpret_cast<half8*>(smem);
+  float* sb = reinterpret_cast<float*>(smem + N::kFrags * 1024);
+
+  const int64_t n = a.n;
+  const int64_t npairs = (n + 63) / 64;
+  const int64_t per_block = (npairs + gridDim.x - 1) / gridDim.x;
+  const int64_t p_begin = int64_t(blockIdx.x) * per_block;
+  const int64_t p_end = p_begin + per_block < npairs ? p_begin + per_block : npairs;
+
+  // this lane's input fragments of tile `tile`: the chain input by rows (clamped;
+  // rows >= n compute values that are never used), a hidden input by slots
+  auto load_in = [&](int64_t tile, half8 (&b)[N::kMaxKC]) {
+    int64_t row = tile * 32 + col;
+    row = row < n - 1 ? row : n - 1;
+    const half_t* src = a.in + row * IN0;
+    const half8* slots = reinterpret_cast<const half8*>(a.in + tile * 32 * IN0);
+#pragma unroll
+    for (int c = 0; c < KC0; ++c) {
+      if constexpr (NAT0) b[c] = *reinterpret_cast<const half8*>(src + 16 * c + 8 * h);
+      else b[c] = slots[c * 64 + lane];
+    }
+  };
+  half8 bA[N::kMaxKC], bB[N::kMaxKC];
+  int64_t pt = p_begin + wave;
+  if (pt < p_end) {
+    load_in(2 * pt, bA);
+    load_in(2 * pt + 1, bB);
+  }
+  // stage the group's fragments and biases (biases compacted to Net's bias_base)
+#pragma unroll
+  for (int l = 0; l < L; ++l) {
+    const half8* fsrc = reinterpret_cast<const half8*>(a.packed + a.lay.frag_off[a.l0 + l]);
+    for (int i = threadIdx.x; i < N::kc(l) * N::mt(l) * 64; i += kTfThreads) sw[N::frag_base(l) * 64 + i] = fsrc[i];
+    const float* bsrc = reinterpret_cast<const float*>(a.packed + a.lay.bias_off[a.l0 + l]);
+    for (int i = threadIdx.x; i < 32 * N::mt(l); i += kTfThreads) sb[N::bias_base(l) + i] = bsrc[i];
+  }
+  __syncthreads();
+
+  // narrow inputs (KC0 <= 4) are loaded a whole iteration ahead into spare
+  // registers; wider ones at the end of the previous iteration, into bA / bB
+  constexpr bool kEarly = KC0 <= 4;
+  half8 nA[kEarly ? KC0 : 1], nB[kEarly ? KC0 : 1];
+  float loss = 0.0f;
+  for (; pt < p_end; pt += kTfWaves) {
+    const int64_t pA = pt * 64 + col, pB = pA + 32;
+    const int64_t nxt = pt + kTfWaves;
+    if constexpr (kEarly) {
+      if (nxt < p_end) {
+        half8 fA[N::kMaxKC], fB[N::kMaxKC];
+        load_in(2 * nxt, fA);
+        load_in(2 * nxt + 1, fB);
+#pragma unroll
+        for (int c = 0; c < KC0; ++c) {
+          nA[c] = fA[c];
+          nB[c] = fB[c];
+        }
+      }
+    }
+    f32x16 accA[N::kMaxMT], accB[N::kMaxMT];
+    const LdsWeights ws{sw + opaque_zero(), lane};
+    tf_layers<N, 0, KEEP, HEAD>(ws, sb + opaque_zero(), h, bA, bB, accA, accB, a, 2 * pt, 2 * pt + 1);
+    if constexpr (HEAD) {
+      // y = D rows 32t + 16qq + 8hi + 4h + jj (registers 8qq + 4hi + jj) < OUT;
+      // g = 2 (y - t) as slot 2t + qq of the tile, zero past OUT; loss over rows < n
+      constexpr int WG = 16 * ((OUT + 15) / 16);
+      const int64_t cA = pA < n ? pA : n - 1, cB = pB < n ? pB : n - 1;
+      half8* gA = reinterpret_cast<half8*>(a.g + 2 * pt * 32 * WG);
+      half8* gB = reinterpret_cast<half8*>(a.g + (2 * pt + 1) * 32 * WG);
+#pragma unroll
+      for (int t = 0; t < N::mt(L - 1); ++t) {
+#pragma unroll
+        for (int qq = 0; qq < 2; ++qq) {
+          if (32 * t + 16 * qq < OUT) {
+            half8 vA, vB;
+#pragma unroll
+            for (int hi = 0; hi < 2; ++hi) {
+              const int r = 32 * t + 16 * qq + 8 * hi + 4 * h;
+              if (32 * t + 16 * qq + 8 * hi < OUT) {
+                const f32x4 tA = *reinterpret_cast<const f32x4*>(a.target + cA * OUT + r);
+                const f32x4 tB = *reinterpret_cast<const f32x4*>(a.target + cB * OUT + r);
+#pragma unroll
+                for (int jj = 0; jj < 4; ++jj) {
+                  const float dA = accA[t][8 * qq + 4 * hi + jj] - tA[jj];
+                  const float dB = accB[t][8 * qq + 4 * hi + jj] - tB[jj];
+                  loss += (pA < n ? dA * dA : 0.0f) + (pB < n ? dB * dB : 0.0f);
+                  vA[4 * hi + jj] = half_t(dA + dA);
+                  vB[4 * hi + jj] = half_t(dB + dB);
+                }
+              } else {
+#pragma unroll
+                for (int jj = 0; jj < 4; ++jj) {
+                  vA[4 * hi + jj] = half_t(0.0f);
+                  vB[4 * hi + jj] = half_t(0.0f);
+                }
+              }
+            }
+            gA[(2 * t + qq) * 64 + lane] = vA;
+            gB[(2 * t + qq) * 64 + lane] = vB;
+          }
+        }
+      }
+    }
+    if constexpr (kEarly) {
+#pragma unroll
+      for (int c = 0; c < KC0; ++c) {
+        bA[c] = nA[c];
+        bB[c] = nB[c];
+      }
+    } else if (nxt < p_end) {
+      load_in(2 * nxt, bA);
+      load_in(2 * nxt + 1, bB);
+    }
+  }
+  if constexpr (HEAD) {
+    loss = tr_wave_sum(loss);
+    if (lane == 0) s_loss[wave] = loss;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      float s = 0.0f;
+      for (int w = 0; w < kTfWaves; ++w) s += s_loss[w];
+      a.loss_partial[blockIdx.x] = s;
+    }
+  }
+}
+
+// LDS bytes of train_fwd_pair_kernel<N, ...>.
+template <class N>
+constexpr int64_t tf_lds() {
+  return int64_t(N::kFrags) * 1024 + int64_t(N::kBias) * 4;
+}
+
+// Specialisations: the two forward groups of the benchmark chain
+// 32 -> 128 x 8 -> 16 (layers 0-4 and 5-8 under the 150 KiB LDS cap).
+using TfNetC5a = Net<RDV_ENC_NONE, 32, 0, 128, 2, 4, 4, 4, 4, 4>;  // 32 -> 128 x 5, keeps h1, h3, h5
+using TfNetC5b = Net<RDV_ENC_NONE, 128, 0, 16, 8, 4, 4, 4, 1>;     // 128 -> 128 x 3 -> 16, keeps h7
+
+struct TfEntry {
+  int in0, nat0, head, keep, L, out, kc0;
+  int mt[RDV_MLP_MAX_LAYERS];
+  const void* fn;
+  int64_t lds;
+};
+
+template <class N, int KEEP, bool HEAD, bool NAT0>
+TfEntry tf_entry() {
+  TfEntry e{};
+  e.in0 = N::kIn;
+  e.nat0 = NAT0;
+  e.head = HEAD;
+  e.keep = KEEP;
+  e.L = N::kL;
+  e.out = N::kOut;
+  e.kc0 = N::kc(0);
+  for (int i = 0; i < N::kL; ++i) e.mt[i] = N::mt(i);
+  e.fn = reinterpret_cast<const void*>(&train_fwd_pair_kernel<N, KEEP, HEAD, NAT0>);
+  e.lds = tf_lds<N>();
+  return e;
+}
+
+static const TfEntry* tf_table(int* count) {
+  static const TfEntry table[] = {
+      tf_entry<TfNetC5a, 0x15, false, true>(),
+      tf_entry<TfNetC5b, 0x2, true, false>(),
+  };
+  *count = int(sizeof(table) / sizeof(table[0]));
+  return table;
+}
+
 // --------------------------------------------------------------- backward
 struct TrainBwdArgs {
-  const half_t* dz;   // [n, out] gradient of layer l's output (pre-activation)
-  const half_t* hin;  // [n, in] layer l's input
-  const half_t* wt;   // W^T A fragments [in / 32][ceil(out / 16)][64][8]
-  half_t* dzin;       // [n, in] gradient of the input's pre-activation (masked), or null
+  const half_t* dz;   // gradient of layer 0's output (pre-activation), tile-fragment layout of width out
+  const half_t* hin;  // [n, in] the chain input
   float* dw_part;     // [gridDim.x][out][in]
   float* db_part;     // [gridDim.x][out]
   int in, out;
@@ -237,14 +486,11 @@ __global__ __launch_bounds__(kTrBwdThreads, 2) void train_bwd_kernel(TrainBwdArg
   const int h = lane >> 5, col = lane & 31;
   const int mto = (a.out + 31) / 32;       // dW row tiles (o)
   const int mti = (a.in + 31) / 32;        // dW column tiles (i)
-  const int mtx = a.dzin != nullptr ? a.in / 32 : 0;  // dX row tiles (hidden inputs: multiples of 32)
-  const int kco = (a.out + 15) / 16;       // K chunks of the dX product
+  const int kco = (a.out + 15) / 16;       // 16-feature slots of dz
   const int OP = 32 * mto + kTrPad;        // LDS dz row stride (halves), columns >= out stay 0
   const int IP = 32 * mti + kTrPad;        // LDS h row stride (halves), columns >= in stay 0
-  half8* swt = reinterpret_cast<half8*>(smem);
-  half_t* sdz = reinterpret_cast<half_t*>(smem + int64_t(mtx) * kco * 1024);
-  // W^T fragments -> LDS, zero both tile buffers (their padding columns stay zero)
-  for (int i = threadIdx.x; i < mtx * kco * 64; i += blockDim.x) swt[i] = reinterpret_cast<const half8*>(a.wt)[i];
+  half_t* sdz = reinterpret_cast<half_t*>(smem);
+  // zero both tile buffers (their padding columns stay zero)
   for (int i = threadIdx.x; i < 2 * 32 * (OP + IP); i += blockDim.x) sdz[i] = half_t(0.0f);
   __syncthreads();
 
@@ -254,26 +500,26 @@ __global__ __launch_bounds__(kTrBwdThreads, 2) void train_bwd_kernel(TrainBwdArg
   const int64_t t_end = t_begin + per_block < ntiles ? t_begin + per_block : ntiles;
 
   const int to = __builtin_amdgcn_readfirstlane(wave);  // this wave's dW row tile (if < mto)
-  const int ti = to;              // this wave's dX row tile (if < mti)
   __builtin_assume(to >= 0 && to < kTrBwdThreads / 64);
   f32x16 accw[kTrMT];
 #pragma unroll
   for (int t = 0; t < kTrMT; ++t) accw[t] = f32x16{};
   float dbs = 0.0f;               // db of row 32 to + col, this lane's half of the points
 
-  const int dz_chunks = 32 * a.out / 8;   // 16-byte chunks per tile
+  const int dz_chunks = 64 * kco;         // 16-byte chunks per tile
   const int h_chunks = 32 * a.in / 8;
   const int tile_halves = 32 * (OP + IP);
-  // this thread's share of a tile's chunks (at most kTrLoads: widths <= 128)
+  // this thread's share of a tile's chunks (at most kTrLoads: widths <= 128);
+  // dz chunk i is the tile's i-th 16 bytes (point i % 32, features
+  // tfl_feature(i / 64, (i / 32) % 2, 0..7))
   auto load_tile = [&](int64_t tile, half8 (&r)[kTrLoads]) {
 #pragma unroll
     for (int k = 0; k < kTrLoads; ++k) {
       const int i = k * kTrBwdThreads + int(threadIdx.x);
       half8 v = {};
       if (i < dz_chunks) {
-        const int rr = i / (a.out / 8), c8 = i % (a.out / 8);
-        const int64_t p = tile * 32 + rr;
-        if (p < a.n) v = *reinterpret_cast<const half8*>(a.dz + p * a.out + 8 * c8);
+        const int64_t p = tile * 32 + (i & 31);
+        if (p < a.n) v = *reinterpret_cast<const half8*>(a.dz + tile * 32 * (16 * kco) + 8 * i);
       } else if (i < dz_chunks + h_chunks) {
         const int kk = i - dz_chunks;
         const int rr = kk / (a.in / 8), c8 = kk % (a.in / 8);
@@ -288,8 +534,10 @@ __global__ __launch_bounds__(kTrBwdThreads, 2) void train_bwd_kernel(TrainBwdArg
     for (int k = 0; k < kTrLoads; ++k) {
       const int i = k * kTrBwdThreads + int(threadIdx.x);
       if (i < dz_chunks) {
-        const int rr = i / (a.out / 8), c8 = i % (a.out / 8);
-        *reinterpret_cast<half8*>(buf + rr * OP + 8 * c8) = r[k];
+        const int f0 = tfl_feature(i >> 6, (i >> 5) & 1, 0);
+        half_t* row = buf + (i & 31) * OP + f0;
+        *reinterpret_cast<half4v*>(row) = half4v{r[k][0], r[k][1], r[k][2], r[k][3]};
+        *reinterpret_cast<half4v*>(row + 8) = half4v{r[k][4], r[k][5], r[k][6], r[k][7]};
       } else if (i < dz_chunks + h_chunks) {
         const int kk = i - dz_chunks;
         const int rr = kk / (a.in / 8), c8 = kk % (a.in / 8);
@@ -312,26 +560,6 @@ __global__ __launch_bounds__(kTrBwdThreads, 2) void train_bwd_kernel(TrainBwdArg
     const bool more = tile + 1 < t_end;
     if (more) load_tile(tile + 1, r);
 
-    // ---- dz_in^T tile ti = W^T[32 ti .. +31][:] . dz^T, masked by h > 0
-    if (ti < mtx) {
-      f32x16 acc = {};
-      for (int c = 0; c < kco; ++c) {
-        const half8 bf = *reinterpret_cast<const half8*>(tdz + col * OP + 16 * c + 8 * h);
-        acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(swt[(ti * kco + c) * 64 + lane], bf, acc, 0, 0, 0);
-      }
-      const int64_t p = tile * 32 + col;
-      if (p < a.n) {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int i0 = 32 * ti + 8 * q + 4 * h;
-          const half4v hv = *reinterpret_cast<const half4v*>(th + col * IP + i0);
-          half4v o;
-#pragma unroll
-          for (int jj = 0; jj < 4; ++jj) o[jj] = float(hv[jj]) > 0.0f ? half_t(acc[4 * q + jj]) : half_t(0.0f);
-          *reinterpret_cast<half4v*>(a.dzin + p * a.in + i0) = o;
-        }
-      }
-    }
     // ---- dW rows tile to += dz^T[32 to .. +31][tile points] . h[tile points][:]
     if (to < mto) {
 #pragma unroll
@@ -400,13 +628,13 @@ __global__ __launch_bounds__(kTrBwdThreads, 2) void train_bwd_kernel(TrainBwdArg
 // with 2-byte stores as tiles are parked or produced; their 36-half rows make
 // both the stores and the 8-byte reads bank-conflict free.
 struct TrainPairArgs {
-  const half_t* g;       // [n, out] g_l
-  const half_t* hin;     // [n, in0] h_{l-1} (natural feature order)
+  const half_t* g;       // g_l, tile-fragment layout of width out
+  const half_t* hin;     // h_{l-1}: the chain input [n, in0] when l - 1 == 0, else tile-fragment layout
   const half_t* wf;      // layer l-1 forward A fragments [mid / 32][kc0][64][8] (packed layout)
   const float* bias;     // layer l-1 padded bias [mid]
   const half_t* wtl;     // W_l^T fragments [mid / 32][ceil(out / 16)][64][8]
   const half_t* wtl1;    // W_{l-1}^T fragments [in0 / 32][mid / 16][64][8] (gout only)
-  half_t* gout;          // [n + 1, in0] g_{l-2} (row n: spare, written by lanes past n), or null
+  half_t* gout;          // g_{l-2}, tile-fragment layout of width in0, or null
   float* dw_l;           // [gridDim.x][out][mid]
   float* db_l;           // [gridDim.x][out]
   float* dw_l1;          // [gridDim.x][mid][in0]
@@ -497,17 +725,19 @@ __global__ __launch_bounds__(kTpThreads, 1) void train_pair_kernel(TrainPairArgs
   __builtin_assume(wave >= 0 && wave < kTpThreads / 64);
   const int role = wave >> 2, w = wave & 3;
 
-  // Tile chunks (16 bytes, 8 features of one point): chunk i covers point i % 32
-  // and features 8 (i / 32) ..; g_l's chunks first, then h_{l-1}'s.  Consecutive
-  // lanes take consecutive points, so the feature-major stores of a chunk fill
-  // consecutive halves of a row.
+  // Tile chunks (16 bytes of one point): chunk kk covers point kk % 32.  g_l and
+  // a hidden h_{l-1} come in the tile-fragment layout (chunk kk is the tile's
+  // kk-th 16 bytes: features tfl_feature(kk / 64, (kk / 32) % 2, 0..7)); the
+  // chain input by rows (features 8 (kk / 32) + 0..7).  g_l's chunks first,
+  // then h_{l-1}'s.  Consecutive lanes take consecutive points, so the
+  // feature-major stores of a chunk fill consecutive halves of a row.
   constexpr int kLoads = 2;  // 16-byte chunks per thread: 32 x (128 + 128) halves / 512 threads
-  const int g_chunks = 32 * (out / 8);
+  const int g_chunks = 64 * kco;
   const int h_chunks = 32 * (in0 / 8);
-  // Loads are unconditional (rows clamped into range, unused slots re-read a valid
+  // Loads are unconditional (in-range rows or slots; unused slots re-read a valid
   // chunk) so that the compiler can count the wave's outstanding memory ops
   // exactly: a wait for these loads then never waits for the g_{l-2} stores
-  // issued after them.  Rows past n are zeroed when parked.
+  // issued after them.  Points past n are zeroed when parked.
   __builtin_assume(threadIdx.x < kTpThreads);
   auto load_tile = [&](int64_t tile, half8 (&r)[kLoads]) {
 #pragma unroll
@@ -515,9 +745,16 @@ __global__ __launch_bounds__(kTpThreads, 1) void train_pair_kernel(TrainPairArgs
       const int i = k * kTpThreads + int(threadIdx.x);
       const bool isg = i < g_chunks;
       const int kk = isg ? i : (i < g_chunks + h_chunks ? i - g_chunks : 0);
-      int64_t p = tile * 32 + (kk & 31);
-      p = p < a.n ? p : a.n - 1;
-      const half_t* src = isg ? a.g + p * out + 8 * (kk >> 5) : a.hin + p * in0 + 8 * (kk >> 5);
+      const half_t* src;
+      if (isg) {
+        src = a.g + tile * 32 * (16 * kco) + 8 * kk;
+      } else if (NAT0) {
+        int64_t p = tile * 32 + (kk & 31);
+        p = p < a.n ? p : a.n - 1;
+        src = a.hin + p * in0 + 8 * (kk >> 5);
+      } else {
+        src = a.hin + tile * 32 * in0 + 8 * kk;
+      }
       r[k] = *reinterpret_cast<const half8*>(src);
     }
   };
@@ -528,13 +765,23 @@ __global__ __launch_bounds__(kTpThreads, 1) void train_pair_kernel(TrainPairArgs
       if (i < g_chunks + h_chunks) {
         const bool isg = i < g_chunks;
         const int kk = isg ? i : i - g_chunks;
-        const int pp = kk & 31, f0 = 8 * (kk >> 5);
+        const int pp = kk & 31;
         const half8 v = tile * 32 + pp < a.n ? r[k] : half8{};
-        half_t* rowp = isg ? rg(b) + pp * OP + f0 : rh(b) + pp * IP + f0;
-        half_t* t = (isg ? tg(b) : th(b)) + f0 * T + pp;
-        *reinterpret_cast<half8*>(rowp) = v;
+        half_t* rowp = isg ? rg(b) + pp * OP : rh(b) + pp * IP;
+        half_t* t = (isg ? tg(b) : th(b)) + pp;
+        if (isg || !NAT0) {
+          // tile-fragment chunk: features f0 + 0..3 and f0 + 8 + 0..3
+          const int f0 = tfl_feature(kk >> 6, (kk >> 5) & 1, 0);
+          *reinterpret_cast<half4v*>(rowp + f0) = half4v{v[0], v[1], v[2], v[3]};
+          *reinterpret_cast<half4v*>(rowp + f0 + 8) = half4v{v[4], v[5], v[6], v[7]};
 #pragma unroll
-        for (int j = 0; j < 8; ++j) t[j * T] = v[j];
+          for (int j = 0; j < 8; ++j) t[(f0 + (j & 3) + ((j >> 2) << 3)) * T] = v[j];
+        } else {
+          const int f0 = 8 * (kk >> 5);
+          *reinterpret_cast<half8*>(rowp + f0) = v;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) t[(f0 + j) * T] = v[j];
+        }
       }
     }
   };
@@ -691,18 +938,21 @@ __global__ __launch_bounds__(kTpThreads, 1) void train_pair_kernel(TrainPairArgs
             acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(wl1[c], bf, acc, 0, 0, 0);
           }
         }
-        // unconditional stores (exact wait counts): points past n go to the
-        // spare row n of gout
-        int64_t p = tile * 32 + col;
-        p = p < a.n ? p : a.n;
+        // slots 2w + qq of the tile (registers 8qq + 0..7: features
+        // tfl_feature(2w + qq, h, 0..7)); unconditional stores (exact wait counts)
+        half8* dst = reinterpret_cast<half8*>(a.gout + tile * 32 * in0);
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int i0 = 32 * w + 8 * q + 4 * h;
-          const half4v hv = *reinterpret_cast<const half4v*>(xh + col * IP + i0);
-          half4v o;
+        for (int qq = 0; qq < 2; ++qq) {
+          const int f0 = tfl_feature(2 * w + qq, h, 0);
+          const half4v lo = *reinterpret_cast<const half4v*>(xh + col * IP + f0);
+          const half4v hi = *reinterpret_cast<const half4v*>(xh + col * IP + f0 + 8);
+          half8 o;
 #pragma unroll
-          for (int jj = 0; jj < 4; ++jj) o[jj] = float(hv[jj]) > 0.0f ? half_t(acc[4 * q + jj]) : half_t(0.0f);
-          *reinterpret_cast<half4v*>(a.gout + p * in0 + i0) = o;
+          for (int jj = 0; jj < 4; ++jj) {
+            o[jj] = float(lo[jj]) > 0.0f ? half_t(acc[8 * qq + jj]) : half_t(0.0f);
+            o[4 + jj] = float(hi[jj]) > 0.0f ? half_t(acc[8 * qq + 4 + jj]) : half_t(0.0f);
+          }
+          dst[(2 * w + qq) * 64 + lane] = o;
         }
       }
     }
@@ -825,6 +1075,27 @@ static int64_t pair_lds(int in0, int mid, int out, int kc0, bool gout) {
   return int64_t(mid) * 4 + int64_t(L.total_halves()) * 2;
 }
 
+// train_fwd_pair_kernel instantiation for forward group [fa.l0, fa.l1), or nullptr.
+static const TfEntry* find_tf(const rdv_mlp_desc& d, const MlpLayout& lay, const TrainFwdArgs& fa) {
+  const int L = d.n_layers;
+  int keep = 0;
+  for (int i = fa.l0; i < fa.l1; ++i)
+    if (fa.hout[i] != nullptr) keep |= 1 << (i - fa.l0);
+  int nt = 0;
+  const TfEntry* t = tf_table(&nt);
+  for (int k = 0; k < nt; ++k) {
+    const TfEntry& e = t[k];
+    if (e.L != fa.l1 - fa.l0 || e.in0 != d.dims[fa.l0] || e.nat0 != (fa.l0 == 0) || e.head != (fa.l1 == L) ||
+        e.keep != keep || e.out != d.dims[fa.l1])
+      continue;
+    bool ok = true;
+    for (int i = 0; i < e.L && ok; ++i) ok = e.mt[i] == lay.mt[fa.l0 + i];
+    if (e.kc0 != lay.kc[fa.l0]) ok = false;
+    if (ok) return &e;
+  }
+  return nullptr;
+}
+
 static int64_t group_lds(const MlpLayout& lay, int l0, int l1) {
   int64_t f = 0, b = 0;
   for (int l = l0; l < l1; ++l) {
@@ -887,10 +1158,12 @@ static void train_plan(const rdv_mlp_desc& d, const MlpLayout& lay, int64_t n, i
     maxoi = std::max(maxoi, d.dims[i] * d.dims[i + 1]);
     maxo = std::max(maxo, d.dims[i + 1]);
   }
-  for (int i = 0; i < L; ++i) p->h_off[i] = (i >= 1 && p->keep[i]) ? take(n * d.dims[i] * 2) : -1;
-  p->g_off = take(n * d.dims[L] * 2);
-  p->dz_off[0] = take((n + 1) * maxw * 2);  // + the pair kernel's spare row
-  p->dz_off[1] = take((n + 1) * maxw * 2);
+  // tile-fragment buffers: whole pair tiles (rows rounded up to 64), widths padded to 16
+  const int64_t rows = (n + 63) / 64 * 64;
+  for (int i = 0; i < L; ++i) p->h_off[i] = (i >= 1 && p->keep[i]) ? take(rows * d.dims[i] * 2) : -1;
+  p->g_off = take(rows * ((d.dims[L] + 15) / 16 * 16) * 2);
+  p->dz_off[0] = take(rows * maxw * 2);
+  p->dz_off[1] = take(rows * maxw * 2);
   const int64_t parts = std::max(p->blocks_bwd, p->blocks_pair);
   for (int k = 0; k < 2; ++k) {
     p->dw_off[k] = take(parts * maxoi * 4);
@@ -928,6 +1201,10 @@ int launch_train_step(const rdv_mlp_desc& d, const MlpLayout& lay, const void* p
                                     hipFuncAttributeMaxDynamicSharedMemorySize, 80 * 1024));
     for (const void* fn : kPairKernels)
       RDV_HIP_TRY(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, int(kTrPairLdsCap)));
+    int nt = 0;
+    const TfEntry* tt = tf_table(&nt);
+    for (int k = 0; k < nt; ++k)
+      RDV_HIP_TRY(hipFuncSetAttribute(tt[k].fn, hipFuncAttributeMaxDynamicSharedMemorySize, int(tt[k].lds)));
     attr_set = true;
   }
   TrainFwdArgs fa;
@@ -946,8 +1223,14 @@ int launch_train_step(const rdv_mlp_desc& d, const MlpLayout& lay, const void* p
     fa.l0 = p.g0[k];
     fa.l1 = p.g0[k + 1];
     fa.in = fa.l0 == 0 ? static_cast<const half_t*>(x) : reinterpret_cast<const half_t*>(ws + p.h_off[fa.l0]);
-    const int64_t lds = group_lds(lay, fa.l0, fa.l1);
-    train_fwd_kernel<<<dim3(unsigned(p.blocks_fwd)), dim3(kTrFwdThreads), size_t(lds), stream>>>(fa);
+    const TfEntry* e = find_tf(d, lay, fa);
+    if (e != nullptr) {
+      void* args[] = {&fa};
+      RDV_HIP_TRY(hipLaunchKernel(e->fn, dim3(unsigned(p.blocks_fwd)), dim3(kTfThreads), args, size_t(e->lds), stream));
+    } else {
+      const int64_t lds = group_lds(lay, fa.l0, fa.l1);
+      train_fwd_kernel<<<dim3(unsigned(p.blocks_fwd)), dim3(kTrFwdThreads), size_t(lds), stream>>>(fa);
+    }
     RDV_HIP_TRY(hipGetLastError());
   }
   const float scale = 1.0f / float(double(n) * d.dims[L]);
@@ -1024,8 +1307,6 @@ int launch_train_step(const rdv_mlp_desc& d, const MlpLayout& lay, const void* p
     TrainBwdArgs ba;
     ba.dz = gsrc;
     ba.hin = static_cast<const half_t*>(x);
-    ba.wt = reinterpret_cast<half_t*>(ws + p.wt_off[0]);
-    ba.dzin = nullptr;
     ba.dw_part = reinterpret_cast<float*>(ws + p.dw_off[0]);
     ba.db_part = reinterpret_cast<float*>(ws + p.db_off[0]);
     ba.in = in;

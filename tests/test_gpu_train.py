@@ -5,7 +5,13 @@ Bar: loss within 1e-4 relative; per layer, ||dW - ref||_F <= 1e-2 ||ref||_F and
 likewise for db (the GPU rounds g = 2 (y - t) and every propagated gradient to
 fp16, the oracle keeps float64).  At the full C5 size: the loss equals the mean
 squared error of the forward path, and the gradient of the whole set equals the
-point-weighted mean of the gradients of its two halves."""
+point-weighted mean of the gradients of its two halves.
+
+The forward sums in a different fp32 order than the oracle, so a few
+activations round to a neighbouring fp16 value; where that flips a ReLU mask
+(an activation at zero on one side only) the gradient of that one point
+differs entirely.  The 1e-2 bars hold for about a thousand points or more,
+where one such point weighs little."""
 import numpy as np
 import pytest
 import torch
@@ -39,7 +45,7 @@ def _check(loss, grads, ref_loss, ref_grads, what):
         assert ew <= 1e-2 and eb <= 1e-2, f"{what}: layer {l} relative error dW {ew:.3g}, db {eb:.3g}"
 
 
-@pytest.mark.parametrize("n", [4096, 1000])
+@pytest.mark.parametrize("n", [4096, 1000, 4167])  # 4167: 131 tiles, the last 64-point pair tile half past n
 def test_c5_shape_matches_oracle(n):
     x, t, layers = WL.c5(n)
     layers = [(w, torch.randn(w.shape[0], generator=torch.Generator().manual_seed(i)) * 0.1)
@@ -65,6 +71,24 @@ def test_other_widths_and_tail():
     loss, grads = rdv.mse_backward(_chain(layers), x.cuda(), t.cuda())
     ref_loss, ref_grads = T.mse_grads(x.float().numpy(), [(w.numpy(), b.numpy()) for w, b in layers], t.numpy())
     _check(loss.item(), grads, ref_loss, ref_grads, "16-64-32-8")
+
+
+@pytest.mark.parametrize("dims,n", [
+    ([48, 128, 128, 128, 128, 128, 128, 8], 1500),  # two forward groups (the second on a stored input), odd L, 8-wide head
+    ([32, 96, 64, 128, 24], 333),                   # even L, a 24-wide head (padded to 32 in the gradient buffer)
+])
+def test_generic_chains(dims, n):
+    g = torch.Generator().manual_seed(len(dims) * 1000 + n)
+    layers = []
+    for i in range(len(dims) - 1):
+        lim = (6.0 / dims[i]) ** 0.5
+        layers.append((((torch.rand(dims[i + 1], dims[i], generator=g) * 2 - 1) * lim).half().float(),
+                       torch.randn(dims[i + 1], generator=g) * 0.1))
+    x = torch.randn(n, dims[0], generator=g).half()
+    t = torch.randn(n, dims[-1], generator=g)
+    loss, grads = rdv.mse_backward(_chain(layers), x.cuda(), t.cuda())
+    ref_loss, ref_grads = T.mse_grads(x.float().numpy(), [(w.numpy(), b.numpy()) for w, b in layers], t.numpy())
+    _check(loss.item(), grads, ref_loss, ref_grads, "-".join(map(str, dims)))
 
 
 def test_unsupported_chain_raises():
