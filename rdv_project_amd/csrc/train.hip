@@ -1032,6 +1032,305 @@ __global__ void train_pack_wt_kernel(const float* __restrict__ w32, int in, int 
   wt[e] = half_t(o < out ? w32[int64_t(o) * in + i] : 0.0f);
 }
 
+// W^T fragments in the tile-fragment K order: element
+// ((ti * kc + c) * 64 + lane) * 8 + j = W[tfl_feature(c, lane / 32, j)][32 ti + lane % 32]
+// (zero past `out`), kc = ceil(out / 16).  As an MFMA operand: rows (A) or
+// columns (B) 32 ti .. of W^T, K = W's output features, chunk c.
+__global__ void train_pack_wts_kernel(const float* __restrict__ w32, int in, int out, half_t* __restrict__ wt) {
+  const int kc = (out + 15) / 16;
+  const int64_t total = int64_t(in / 32) * kc * 64 * 8;
+  const int64_t e = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (e >= total) return;
+  const int j = int(e & 7);
+  const int lane = int((e >> 3) & 63);
+  const int64_t r = e >> 9;
+  const int c = int(r % kc), ti = int(r / kc);
+  const int o = tfl_feature(c, lane >> 5, j);
+  const int i = 32 * ti + (lane & 31);
+  wt[e] = half_t(o < out ? w32[int64_t(o) * in + i] : 0.0f);
+}
+
+// ------------------------------------------ backward, layer pairs, point-major
+// train_pair2_kernel: the layer pair of train_pair_kernel for 128-wide hidden
+// layers l and l - 1 >= 1 (OUT = the width of g_l), with no operand gathered
+// element by element.  The two products that read the tile put the points on
+// the MFMA's M side, so their D registers hold, per lane, one feature over 16
+// points: the layout of a K = points operand.
+//   h_l     [points x m] = h_{l-1} W_{l-1}^T + b  (A: h_{l-1} slots, B: the forward's fragments)
+//   g_{l-1} [points x m] = (g_l W_l) * [h_l > 0]   (A: g_l slots,     B: W_l^T, train_pack_wts)
+//   dW_l    [o x m]      += g_l^T h_l               (A: g_l^T,         B: h_l)
+//   dW_{l-1}[m x i]      += g_{l-1}^T h_{l-1}       (A: g_{l-1},       B: h_{l-1}^T)
+//   g_{l-2}^T [i x points] = W_{l-1}^T g_{l-1}^T, masked by h_{l-1} > 0, stored as slots
+// Three operands change orientation: g_l and h_{l-1} (slots -> K = points) and
+// g_{l-1} (K = points -> slots).  Each is an MFMA against a 0/1 selection
+// fragment (tp2_select): every output is one fp16 value times 1 plus zeros,
+// exact in fp32.  Wave w owns the 32-feature block w of every product and
+// shares its block of the three through LDS as 1 KiB fragments.
+//   Per tile: park (double-buffered slots of g_l, h_{l-1}), phase 1 (h_l, g_{l-1},
+//   the three re-orientations, db), barrier, phase 2 (dW_l, dW_{l-1}, g_{l-2}),
+//   the next tile's park, barrier.
+// Points past n are parked as zeros: g_l = 0 there, so they add nothing.
+struct TrainPair2Args {
+  const half_t* g;     // g_l, tile-fragment layout of width OUT
+  const half_t* hin;   // h_{l-1}, tile-fragment layout of width 128
+  const half_t* wf;    // layer l-1 forward A fragments (packed layout)
+  const float* bias;   // layer l-1 padded bias [128]
+  const half_t* wls;   // W_l^T, train_pack_wts(W_l, 128, OUT)
+  const half_t* wl1s;  // W_{l-1}^T, train_pack_wts(W_{l-1}, 128, 128)
+  half_t* gout;        // g_{l-2}, tile-fragment layout of width 128
+  float* dw_l;         // [gridDim.x][OUT][128]
+  float* db_l;         // [gridDim.x][OUT]
+  float* dw_l1;        // [gridDim.x][128][128]
+  float* db_l1;        // [gridDim.x][128]
+  int64_t n;
+};
+
+constexpr int kT2Threads = 512;  // 8 waves: two roles of 4
+
+// 0/1 fragment par: lane (n = lane % 32, hh = lane / 32), element j is 1 where
+// tfl_feature(par, hh, j) == n.  A x select(0) + A' x select(1) turns the K
+// slots of two consecutive 16-feature chunks (or of the two 16-point halves of
+// a K = points fragment pair) into the 32 columns of D.
+__device__ __forceinline__ half8 tp2_select(int par, int lane) {
+  half8 v;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) v[j] = tfl_feature(par, lane >> 5, j) == (lane & 31) ? half_t(1.0f) : half_t(0.0f);
+  return v;
+}
+
+// D registers 8 ks .. 8 ks + 7 as fp16 (points tfl_feature(ks, h, 0..7) of a
+// point-major product; features 32 block + tfl_feature(ks, h, 0..7) of a
+// feature-major one).
+__device__ __forceinline__ half8 tp2_half(const f32x16& d, int ks) {
+  half8 v;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) v[j] = half_t(d[8 * ks + j]);
+  return v;
+}
+
+// Sum of 8 fp16 values into an fp32 accumulator.
+__device__ __forceinline__ float tp2_sum(const half8& v, float acc) {
+#pragma unroll
+  for (int j = 0; j < 8; j += 2) acc = __builtin_amdgcn_fdot2(half2v{v[j], v[j + 1]}, half2v{1, 1}, acc, false);
+  return acc;
+}
+
+// LDS carve-up of train_pair2_kernel (half8 units): three input buffers
+// (g_l slots, then h_{l-1} slots) and two exchange buffers (g_l and h_{l-1} as
+// K = points fragments [block][ks][lane], g_{l-1} slots, h_l and g_{l-1} as
+// K = points fragments).
+template <int OUT>
+struct Pair2Lds {
+  static constexpr int KCO = (OUT + 15) / 16, MTO = (OUT + 31) / 32;
+  static constexpr int kIn = 64 * (KCO + 8);
+  static constexpr int kGT = 0, kHT = kGT + 2 * MTO * 64, kGP = kHT + 8 * 64, kHF = kGP + 8 * 64,
+                       kGF = kHF + 8 * 64, kEx = kGF + 8 * 64;
+  static constexpr int kBytes = (3 * kIn + 2 * kEx) * 16;
+};
+
+template <int OUT>
+__global__ __launch_bounds__(kT2Threads, 1) void train_pair2_kernel(TrainPair2Args a) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  using LD = Pair2Lds<OUT>;
+  constexpr int KC = 8;                  // 16-feature chunks of a 128-wide layer
+  constexpr int KCO = LD::KCO;           // chunks of g_l
+  constexpr int MTO = LD::MTO;           // 32-row blocks of dW_l
+  constexpr int kChunks = LD::kIn;       // 16-byte chunks per tile (g_l, then h_{l-1})
+  constexpr int kLd = (kChunks + kT2Threads - 1) / kT2Threads;
+  half8* const sIn = reinterpret_cast<half8*>(smem);
+  half8* const sEx = sIn + 3 * LD::kIn;
+  const int tid = int(threadIdx.x);
+  const int lane = tid & 63;
+  const int h = lane >> 5, col = lane & 31;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  __builtin_assume(wave >= 0 && wave < 8);
+  __builtin_assume(tid < kT2Threads);
+  const int role = wave >> 2, w = wave & 3;
+
+  const int64_t ntiles = (a.n + 31) / 32;
+  const int64_t per_block = (ntiles + gridDim.x - 1) / gridDim.x;
+  const int64_t t_begin = int64_t(blockIdx.x) * per_block;
+  const int64_t t_end = t_begin + per_block < ntiles ? t_begin + per_block : ntiles;
+  const int count = int(t_end > t_begin ? t_end - t_begin : 0);
+
+  // chunk i of a tile: g_l slot i / 64 (i < 64 KCO), else h_{l-1} slot (i - 64 KCO) / 64;
+  // the chunk counts are multiples of 64, so a wave is all g_l or all h_{l-1}
+  auto load = [&](int64_t tile, half8 (&r)[kLd]) {
+#pragma unroll
+    for (int k = 0; k < kLd; ++k) {
+      const int i0 = k * kT2Threads + tid;
+      const int i = i0 < kChunks ? i0 : 0;
+      const half_t* src = i < 64 * KCO ? a.g + tile * 32 * (16 * KCO) + 8 * i
+                                       : a.hin + tile * 32 * 128 + 8 * (i - 64 * KCO);
+      r[k] = *reinterpret_cast<const half8*>(src);
+    }
+  };
+  auto park = [&](int buf, int64_t tile, const half8 (&r)[kLd]) {
+#pragma unroll
+    for (int k = 0; k < kLd; ++k) {
+      const int i = k * kT2Threads + tid;
+      if (i < kChunks) sIn[buf * LD::kIn + i] = tile * 32 + (i & 31) < a.n ? r[k] : half8{};
+    }
+  };
+  if (count > 0) {
+    half8 r[kLd];
+    load(t_begin, r);
+    park(0, t_begin, r);
+  }
+
+  if (role == 0) {
+    // ============ phase 1 of tile it: h_l, g_{l-1} of feature block w (point-major),
+    // g_l and h_{l-1} block w to K = points fragments, g_{l-1} block w to slots
+    half8 wf[KC], wl[KCO];
+#pragma unroll
+    for (int c = 0; c < KC; ++c) wf[c] = reinterpret_cast<const half8*>(a.wf)[(w * KC + c) * 64 + lane];
+#pragma unroll
+    for (int c = 0; c < KCO; ++c) wl[c] = reinterpret_cast<const half8*>(a.wls)[(w * KCO + c) * 64 + lane];
+    f32x16 bias;  // D column 32w + col: the same bias in every register
+    {
+      const float bm = a.bias[32 * w + col];
+#pragma unroll
+      for (int q = 0; q < 16; ++q) bias[q] = bm;
+    }
+    const half8 sel0 = tp2_select(0, lane), sel1 = tp2_select(1, lane);
+    float dbl = 0.0f, dbl1 = 0.0f;
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    for (int it = 0; it <= count; ++it) {
+      half8 r[kLd];
+      const bool more = it + 1 < count;
+      if (more) load(t_begin + it + 1, r);
+      if (it < count) {
+        const half8* G = sIn + (it % 3) * LD::kIn;
+        const half8* H = G + 64 * KCO;
+        half8* E = sEx + (it & 1) * LD::kEx;
+        const half8 h0 = H[(2 * w) * 64 + lane], h1 = H[(2 * w + 1) * 64 + lane];
+        f32x16 accR = __builtin_amdgcn_mfma_f32_32x32x16_f16(H[lane], wf[0], bias, 0, 0, 0);
+#pragma unroll
+        for (int c = 1; c < KC; ++c) accR = __builtin_amdgcn_mfma_f32_32x32x16_f16(H[c * 64 + lane], wf[c], accR, 0, 0, 0);
+        f32x16 accG = {};
+#pragma unroll
+        for (int c = 0; c < KCO; ++c) accG = __builtin_amdgcn_mfma_f32_32x32x16_f16(G[c * 64 + lane], wl[c], accG, 0, 0, 0);
+        f32x16 tH = {};
+        tH = __builtin_amdgcn_mfma_f32_32x32x16_f16(h0, sel0, tH, 0, 0, 0);
+        tH = __builtin_amdgcn_mfma_f32_32x32x16_f16(h1, sel1, tH, 0, 0, 0);
+        E[LD::kHT + (2 * w) * 64 + lane] = tp2_half(tH, 0);
+        E[LD::kHT + (2 * w + 1) * 64 + lane] = tp2_half(tH, 1);
+        if (w < MTO) {
+          f32x16 tG = {};
+          tG = __builtin_amdgcn_mfma_f32_32x32x16_f16(G[(2 * w) * 64 + lane], sel0, tG, 0, 0, 0);
+          if (2 * w + 1 < KCO)
+            tG = __builtin_amdgcn_mfma_f32_32x32x16_f16(G[(2 * w + 1) * 64 + lane], sel1, tG, 0, 0, 0);
+          const half8 g0 = tp2_half(tG, 0), g1 = tp2_half(tG, 1);
+          E[LD::kGT + (2 * w) * 64 + lane] = g0;
+          E[LD::kGT + (2 * w + 1) * 64 + lane] = g1;
+          dbl = tp2_sum(g1, tp2_sum(g0, dbl));
+        }
+        // h_l = relu(fp16); g_{l-1} = fp16 where h_l > 0, i.e. where the
+        // pre-activation exceeds 2^-25 (the largest value that rounds to 0)
+        half8 gF[2];
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+          half8 hv = tp2_half(accR, ks);
+          hv = __builtin_elementwise_max(hv, half8{0, 0, 0, 0, 0, 0, 0, 0});
+          f32x16 gm;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) gm[j] = accR[8 * ks + j] > 0x1p-25f ? accG[8 * ks + j] : 0.0f;
+          half8 gv;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) gv[j] = half_t(gm[j]);
+          gF[ks] = gv;
+          E[LD::kHF + (2 * w + ks) * 64 + lane] = hv;
+          E[LD::kGF + (2 * w + ks) * 64 + lane] = gv;
+          dbl1 = tp2_sum(gv, dbl1);
+        }
+        f32x16 tP = {};
+        tP = __builtin_amdgcn_mfma_f32_32x32x16_f16(gF[0], sel0, tP, 0, 0, 0);
+        tP = __builtin_amdgcn_mfma_f32_32x32x16_f16(gF[1], sel1, tP, 0, 0, 0);
+        E[LD::kGP + (2 * w) * 64 + lane] = tp2_half(tP, 0);
+        E[LD::kGP + (2 * w + 1) * 64 + lane] = tp2_half(tP, 1);
+      }
+      if (more) park((it + 1) % 3, t_begin + it + 1, r);
+      __syncthreads();
+    }
+    // db partials: this lane's half of the points, feature 32w + col
+    const float o0 = __shfl_xor(dbl, 32, 64);
+    if (w < MTO && h == 0 && 32 * w + col < OUT) a.db_l[int64_t(blockIdx.x) * OUT + 32 * w + col] = dbl + o0;
+    const float o1 = __shfl_xor(dbl1, 32, 64);
+    if (h == 0) a.db_l1[int64_t(blockIdx.x) * 128 + 32 * w + col] = dbl1 + o1;
+    return;
+  }
+
+  // ============ phase 2 of tile it - 1: dW_l[:, block w], dW_{l-1}[block w, :], g_{l-2} block w
+  half8 wl1[KC];
+#pragma unroll
+  for (int c = 0; c < KC; ++c) wl1[c] = reinterpret_cast<const half8*>(a.wl1s)[(w * KC + c) * 64 + lane];
+  f32x16 accL[MTO], accL1[4];
+#pragma unroll
+  for (int t = 0; t < MTO; ++t) accL[t] = f32x16{};
+#pragma unroll
+  for (int t = 0; t < 4; ++t) accL1[t] = f32x16{};
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  for (int it = 0; it <= count; ++it) {
+    half8 r[kLd];
+    const bool more = it + 1 < count;
+    if (more) load(t_begin + it + 1, r);
+    if (it > 0) {
+      const int64_t tile = t_begin + it - 1;
+      const half8* H = sIn + ((it - 1) % 3) * LD::kIn + 64 * KCO;
+      const half8* E = sEx + ((it - 1) & 1) * LD::kEx;
+      const half8 hf0 = E[LD::kHF + (2 * w) * 64 + lane], hf1 = E[LD::kHF + (2 * w + 1) * 64 + lane];
+      const half8 gf0 = E[LD::kGF + (2 * w) * 64 + lane], gf1 = E[LD::kGF + (2 * w + 1) * 64 + lane];
+#pragma unroll
+      for (int ob = 0; ob < MTO; ++ob) {
+        accL[ob] = __builtin_amdgcn_mfma_f32_32x32x16_f16(E[LD::kGT + (2 * ob) * 64 + lane], hf0, accL[ob], 0, 0, 0);
+        accL[ob] = __builtin_amdgcn_mfma_f32_32x32x16_f16(E[LD::kGT + (2 * ob + 1) * 64 + lane], hf1, accL[ob], 0, 0, 0);
+      }
+#pragma unroll
+      for (int ib = 0; ib < 4; ++ib) {
+        accL1[ib] = __builtin_amdgcn_mfma_f32_32x32x16_f16(gf0, E[LD::kHT + (2 * ib) * 64 + lane], accL1[ib], 0, 0, 0);
+        accL1[ib] = __builtin_amdgcn_mfma_f32_32x32x16_f16(gf1, E[LD::kHT + (2 * ib + 1) * 64 + lane], accL1[ib], 0, 0, 0);
+      }
+      f32x16 acc2 = {};
+#pragma unroll
+      for (int c = 0; c < KC; ++c)
+        acc2 = __builtin_amdgcn_mfma_f32_32x32x16_f16(wl1[c], E[LD::kGP + c * 64 + lane], acc2, 0, 0, 0);
+      half8* dst = reinterpret_cast<half8*>(a.gout + tile * 32 * 128);
+#pragma unroll
+      for (int qq = 0; qq < 2; ++qq) {
+        const half8 hm = H[(2 * w + qq) * 64 + lane];  // h_{l-1}: the same features and point
+        half8 o;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) o[j] = float(hm[j]) > 0.0f ? half_t(acc2[8 * qq + j]) : half_t(0.0f);
+        dst[(2 * w + qq) * 64 + lane] = o;
+      }
+    }
+    if (more) park((it + 1) % 3, t_begin + it + 1, r);
+    __syncthreads();
+  }
+  {
+    float* dst = a.dw_l + int64_t(blockIdx.x) * OUT * 128;
+#pragma unroll
+    for (int ob = 0; ob < MTO; ++ob)
+#pragma unroll
+      for (int q = 0; q < 16; ++q) {
+        const int o = 32 * ob + 8 * (q >> 2) + 4 * h + (q & 3);  // D row of accL[ob]; column m = 32w + col
+        if (o < OUT) dst[int64_t(o) * 128 + 32 * w + col] = accL[ob][q];
+      }
+  }
+  {
+    float* dst = a.dw_l1 + int64_t(blockIdx.x) * 128 * 128;
+#pragma unroll
+    for (int ib = 0; ib < 4; ++ib)
+#pragma unroll
+      for (int q = 0; q < 16; ++q) {
+        const int m = 32 * w + 8 * (q >> 2) + 4 * h + (q & 3);  // D row of accL1[ib]; column i = 32ib + col
+        dst[int64_t(m) * 128 + 32 * ib + col] = accL1[ib][q];
+      }
+  }
+}
+
 // ------------------------------------------------------------------- host
 // Backward schedule: layer pairs (L-1, L-2), (L-3, L-4), ... through
 // train_pair_kernel, then layer 0 alone (train_bwd_kernel, dW only) when L is
@@ -1201,6 +1500,10 @@ int launch_train_step(const rdv_mlp_desc& d, const MlpLayout& lay, const void* p
                                     hipFuncAttributeMaxDynamicSharedMemorySize, 80 * 1024));
     for (const void* fn : kPairKernels)
       RDV_HIP_TRY(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, int(kTrPairLdsCap)));
+    RDV_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&train_pair2_kernel<128>),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, Pair2Lds<128>::kBytes));
+    RDV_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&train_pair2_kernel<16>),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, Pair2Lds<16>::kBytes));
     int nt = 0;
     const TfEntry* tt = tf_table(&nt);
     for (int k = 0; k < nt; ++k)
@@ -1257,10 +1560,53 @@ int launch_train_step(const rdv_mlp_desc& d, const MlpLayout& lay, const void* p
     }
     return wt;
   };
+  auto pack_wts = [&](int l, half_t* wt) {
+    const int in = d.dims[l], out = d.dims[l + 1];
+    const int64_t total = int64_t(in / 32) * ((out + 15) / 16) * 64 * 8;
+    train_pack_wts_kernel<<<dim3(unsigned((total + 255) / 256)), dim3(256), 0, stream>>>(
+        reinterpret_cast<const float*>(pk + lay.w32_off[l]), in, out, wt);
+    return wt;
+  };
   const half_t* gsrc = reinterpret_cast<const half_t*>(ws + p.g_off);
   int dst = 0;
   int l = L - 1;
   for (; l >= 1; l -= 2) {
+    if (l - 1 >= 1 && d.dims[l - 1] == 128 && d.dims[l] == 128 && (d.dims[l + 1] == 128 || d.dims[l + 1] == 16)) {
+      // point-major pair kernel
+      TrainPair2Args pa;
+      pa.g = gsrc;
+      pa.hin = reinterpret_cast<const half_t*>(ws + p.h_off[l - 1]);
+      pa.wf = reinterpret_cast<const half_t*>(pk + lay.frag_off[l - 1]);
+      pa.bias = reinterpret_cast<const float*>(pk + lay.bias_off[l - 1]);
+      pa.wls = pack_wts(l, reinterpret_cast<half_t*>(ws + p.wt_off[l]));
+      RDV_HIP_TRY(hipGetLastError());
+      pa.wl1s = pack_wts(l - 1, reinterpret_cast<half_t*>(ws + p.wt_off[l - 1]));
+      RDV_HIP_TRY(hipGetLastError());
+      pa.gout = reinterpret_cast<half_t*>(ws + p.dz_off[dst]);
+      pa.dw_l = reinterpret_cast<float*>(ws + p.dw_off[0]);
+      pa.db_l = reinterpret_cast<float*>(ws + p.db_off[0]);
+      pa.dw_l1 = reinterpret_cast<float*>(ws + p.dw_off[1]);
+      pa.db_l1 = reinterpret_cast<float*>(ws + p.db_off[1]);
+      pa.n = n;
+      const dim3 grid(unsigned(p.blocks_pair)), block(kT2Threads);
+      if (d.dims[l + 1] == 128)
+        train_pair2_kernel<128><<<grid, block, size_t(Pair2Lds<128>::kBytes), stream>>>(pa);
+      else
+        train_pair2_kernel<16><<<grid, block, size_t(Pair2Lds<16>::kBytes), stream>>>(pa);
+      RDV_HIP_TRY(hipGetLastError());
+      const int out = d.dims[l + 1];
+      rc = reduce(pa.dw_l, p.blocks_pair, int64_t(out) * 128, dW[l]);
+      if (rc != RDV_OK) return rc;
+      rc = reduce(pa.db_l, p.blocks_pair, out, db[l]);
+      if (rc != RDV_OK) return rc;
+      rc = reduce(pa.dw_l1, p.blocks_pair, int64_t(128) * 128, dW[l - 1]);
+      if (rc != RDV_OK) return rc;
+      rc = reduce(pa.db_l1, p.blocks_pair, 128, db[l - 1]);
+      if (rc != RDV_OK) return rc;
+      gsrc = pa.gout;
+      dst ^= 1;
+      continue;
+    }
     TrainPairArgs pa;
     pa.in0 = d.dims[l - 1];
     pa.mid = d.dims[l];
