@@ -1331,6 +1331,79 @@ __global__ __launch_bounds__(kT2Threads, 1) void train_pair2_kernel(TrainPair2Ar
   }
 }
 
+// ------------------------------------------------ backward, layer 0, point-major
+// train_bwd0_kernel: dW_0 and db_0 for a 32-wide chain input and a 128-wide
+// first layer.  dW_0[m][i] = sum_p g_0[p][m] x[p][i] with K = the points: wave
+// w re-orients its 32-feature block of g_0 (slots 2w, 2w + 1) and the tile of
+// x (two natural 16-feature chunks) with 0/1-fragment MFMAs, then accumulates
+// its 32 x 32 block of dW_0.  No LDS: the four waves of a block walk the same
+// tiles, each reading the tile's x (2 KiB) from L2.
+constexpr int kB0Threads = 256;
+
+// 0/1 fragment for the natural feature order of chunk par: lane (n, hh),
+// element j is 1 where 16 par + 8 hh + j == n.
+__device__ __forceinline__ half8 tp2_select_nat(int par, int lane) {
+  half8 v;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) v[j] = 16 * par + 8 * (lane >> 5) + j == (lane & 31) ? half_t(1.0f) : half_t(0.0f);
+  return v;
+}
+
+__global__ __launch_bounds__(kB0Threads, 2) void train_bwd0_kernel(TrainBwdArgs a) {
+  const int tid = int(threadIdx.x);
+  const int lane = tid & 63;
+  const int h = lane >> 5, col = lane & 31;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  __builtin_assume(w >= 0 && w < 4);
+  const int64_t ntiles = (a.n + 31) / 32;
+  const int64_t per_block = (ntiles + gridDim.x - 1) / gridDim.x;
+  const int64_t t_begin = int64_t(blockIdx.x) * per_block;
+  const int64_t t_end = t_begin + per_block < ntiles ? t_begin + per_block : ntiles;
+  const half8 sel0 = tp2_select(0, lane), sel1 = tp2_select(1, lane);
+  const half8 nat0 = tp2_select_nat(0, lane), nat1 = tp2_select_nat(1, lane);
+  // this lane's chunks of tile t: g_0 slots 2w, 2w + 1 and x row col, features 8h .. and 16 + 8h ..
+  auto load = [&](int64_t t, half8 (&r)[4]) {
+    const half8* gs = reinterpret_cast<const half8*>(a.dz + t * 32 * 128);
+    r[0] = gs[(2 * w) * 64 + lane];
+    r[1] = gs[(2 * w + 1) * 64 + lane];
+    int64_t p = t * 32 + col;
+    p = p < a.n ? p : a.n - 1;
+    const half_t* xr = a.hin + p * 32;
+    r[2] = *reinterpret_cast<const half8*>(xr + 8 * h);
+    r[3] = *reinterpret_cast<const half8*>(xr + 16 + 8 * h);
+  };
+  f32x16 acc = {};
+  float dbs = 0.0f;
+  half8 cur[4];
+  if (t_begin < t_end) load(t_begin, cur);
+  for (int64_t t = t_begin; t < t_end; ++t) {
+    half8 nxt[4];
+    if (t + 1 < t_end) load(t + 1, nxt);
+    // points past n: g_0 = 0 there (x is clamped, so finite)
+    const bool valid = t * 32 + col < a.n;
+    const half8 g0 = valid ? cur[0] : half8{}, g1 = valid ? cur[1] : half8{};
+    f32x16 tg = {}, tx = {};
+    tg = __builtin_amdgcn_mfma_f32_32x32x16_f16(g0, sel0, tg, 0, 0, 0);
+    tg = __builtin_amdgcn_mfma_f32_32x32x16_f16(g1, sel1, tg, 0, 0, 0);
+    tx = __builtin_amdgcn_mfma_f32_32x32x16_f16(cur[2], nat0, tx, 0, 0, 0);
+    tx = __builtin_amdgcn_mfma_f32_32x32x16_f16(cur[3], nat1, tx, 0, 0, 0);
+    // K = points fragments: lane = feature (m for g_0, i for x), registers = points
+    const half8 ga = tp2_half(tg, 0), gb = tp2_half(tg, 1);
+    const half8 xa = tp2_half(tx, 0), xb = tp2_half(tx, 1);
+    acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(ga, xa, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(gb, xb, acc, 0, 0, 0);
+    dbs = tp2_sum(gb, tp2_sum(ga, dbs));
+#pragma unroll
+    for (int k = 0; k < 4; ++k) cur[k] = nxt[k];
+  }
+  // partials: D row m = 32w + 8(q/4) + 4h + q%4, column i = col
+  float* dst = a.dw_part + int64_t(blockIdx.x) * 128 * 32;
+#pragma unroll
+  for (int q = 0; q < 16; ++q) dst[int64_t(32 * w + 8 * (q >> 2) + 4 * h + (q & 3)) * 32 + col] = acc[q];
+  const float other = __shfl_xor(dbs, 32, 64);
+  if (h == 0) a.db_part[int64_t(blockIdx.x) * 128 + 32 * w + col] = dbs + other;
+}
+
 // ------------------------------------------------------------------- host
 // Backward schedule: layer pairs (L-1, L-2), (L-3, L-4), ... through
 // train_pair_kernel, then layer 0 alone (train_bwd_kernel, dW only) when L is
@@ -1658,9 +1731,13 @@ int launch_train_step(const rdv_mlp_desc& d, const MlpLayout& lay, const void* p
     ba.in = in;
     ba.out = out;
     ba.n = n;
-    const size_t lds = 2 * (size_t(32) * (32 * mto + kTrPad) * 2 + size_t(32) * (32 * mti + kTrPad) * 2);
+    if (in == 32 && out == 128) {
+      train_bwd0_kernel<<<dim3(unsigned(p.blocks_bwd)), dim3(kB0Threads), 0, stream>>>(ba);
+    } else {
+      const size_t lds = 2 * (size_t(32) * (32 * mto + kTrPad) * 2 + size_t(32) * (32 * mti + kTrPad) * 2);
+      train_bwd_kernel<<<dim3(unsigned(p.blocks_bwd)), dim3(kTrBwdThreads), lds, stream>>>(ba);
+    }
     (void)kco;
-    train_bwd_kernel<<<dim3(unsigned(p.blocks_bwd)), dim3(kTrBwdThreads), lds, stream>>>(ba);
     RDV_HIP_TRY(hipGetLastError());
     rc = reduce(ba.dw_part, p.blocks_bwd, int64_t(out) * in, dW[0]);
     if (rc != RDV_OK) return rc;
