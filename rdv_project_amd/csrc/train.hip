@@ -995,25 +995,52 @@ __global__ __launch_bounds__(kTpThreads, 1) void train_pair_kernel(TrainPairArgs
   }
 }
 
-// Deterministic two-stage sum over nb partials part[b][count]:
-//  stage 1: mid[s][i] = sum of part[b][i] for b = s, s + S, s + 2S, ... (in order)
-//  stage 2: out[i] = scale * sum over s < S of mid[s][i] (in order)
+// All of a step's reductions in two launches, in a fixed order (so dW is the
+// same run to run).  Job j sums its partials part_j[b][i] over b < nb_j into
+// out_j[i] = scale * sum, i < count_j; the jobs' elements are concatenated
+// (job j at start[j]) and so are their blocks (job j's first block bstart[j],
+// 256 elements per block), so a block's job is wave-uniform.
+//  stage 1: mid[s][e] = sum of part[b][i] for b = s, s + S, s + 2S, ... (in order)
+//  stage 2: out[i] = scale * sum over s < S of mid[s][e] (in order)
 constexpr int kTrSplit = 32;
-__global__ void train_reduce1_kernel(const float* __restrict__ part, int nb, int64_t count, float* __restrict__ mid) {
-  const int s = blockIdx.y;
-  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < count; i += int64_t(gridDim.x) * blockDim.x) {
-    float acc = 0.0f;
-    for (int b = s; b < nb; b += kTrSplit) acc += part[int64_t(b) * count + i];
-    mid[int64_t(s) * count + i] = acc;
-  }
+constexpr int kTrMaxJobs = 2 * RDV_MLP_MAX_LAYERS + 1;
+struct ReduceJobs {
+  int n;
+  const float* part[kTrMaxJobs];
+  float* out[kTrMaxJobs];
+  int nb[kTrMaxJobs];
+  int64_t start[kTrMaxJobs + 1];
+  int bstart[kTrMaxJobs + 1];
+};
+
+__device__ __forceinline__ int reduce_job(const ReduceJobs& J) {
+  int j = 0;
+  while (j + 1 < J.n && int(blockIdx.x) >= J.bstart[j + 1]) ++j;
+  return j;
 }
-__global__ void train_reduce2_kernel(const float* __restrict__ mid, int64_t count, float scale, float* __restrict__ out) {
-  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < count; i += int64_t(gridDim.x) * blockDim.x) {
-    float acc = 0.0f;
+
+__global__ void train_reduce1_kernel(ReduceJobs J, float* __restrict__ mid) {
+  const int j = reduce_job(J);
+  const int64_t count = J.start[j + 1] - J.start[j];
+  const int64_t i = int64_t(int(blockIdx.x) - J.bstart[j]) * 256 + threadIdx.x;
+  if (i >= count) return;
+  const int s = blockIdx.y;
+  const float* part = J.part[j];
+  float acc = 0.0f;
+  for (int b = s; b < J.nb[j]; b += kTrSplit) acc += part[int64_t(b) * count + i];
+  mid[int64_t(s) * J.start[J.n] + J.start[j] + i] = acc;
+}
+
+__global__ void train_reduce2_kernel(ReduceJobs J, const float* __restrict__ mid, float scale) {
+  const int j = reduce_job(J);
+  const int64_t count = J.start[j + 1] - J.start[j];
+  const int64_t i = int64_t(int(blockIdx.x) - J.bstart[j]) * 256 + threadIdx.x;
+  if (i >= count) return;
+  const int64_t total = J.start[J.n];
+  float acc = 0.0f;
 #pragma unroll 8
-    for (int s = 0; s < kTrSplit; ++s) acc += mid[int64_t(s) * count + i];
-    out[i] = acc * scale;
-  }
+  for (int s = 0; s < kTrSplit; ++s) acc += mid[int64_t(s) * total + J.start[j] + i];
+  J.out[j][i] = acc * scale;
 }
 
 // W^T A fragments of layer li from the fp32 copy: element
@@ -1415,8 +1442,8 @@ struct TrainPlan {
   int g0[RDV_MLP_MAX_LAYERS + 1];  // group k = layers [g0[k], g0[k + 1])
   int blocks_fwd, blocks_bwd, blocks_pair;
   bool keep[RDV_MLP_MAX_LAYERS];   // h_i stored by the forward
-  int64_t wt_off[RDV_MLP_MAX_LAYERS], h_off[RDV_MLP_MAX_LAYERS], g_off, dz_off[2], dw_off[2], db_off[2], loss_off,
-      mid_off;
+  int64_t wt_off[RDV_MLP_MAX_LAYERS], h_off[RDV_MLP_MAX_LAYERS], g_off, dz_off[2], dw_off[RDV_MLP_MAX_LAYERS],
+      db_off[RDV_MLP_MAX_LAYERS], loss_off, mid_off;
   int64_t total;
 };
 
@@ -1523,12 +1550,10 @@ static void train_plan(const rdv_mlp_desc& d, const MlpLayout& lay, int64_t n, i
     off = align256(off + bytes);
     return o;
   };
-  int maxw = 0, maxoi = 0, maxo = 0;
+  int maxw = 0;
   for (int i = 0; i < L; ++i) {
     p->wt_off[i] = take(int64_t(d.dims[i] / 32 > 0 ? d.dims[i] / 32 : 1) * ((d.dims[i + 1] + 15) / 16) * 1024);
     maxw = std::max(maxw, d.dims[i]);
-    maxoi = std::max(maxoi, d.dims[i] * d.dims[i + 1]);
-    maxo = std::max(maxo, d.dims[i + 1]);
   }
   // tile-fragment buffers: whole pair tiles (rows rounded up to 64), widths padded to 16
   const int64_t rows = (n + 63) / 64 * 64;
@@ -1536,13 +1561,16 @@ static void train_plan(const rdv_mlp_desc& d, const MlpLayout& lay, int64_t n, i
   p->g_off = take(rows * ((d.dims[L] + 15) / 16 * 16) * 2);
   p->dz_off[0] = take(rows * maxw * 2);
   p->dz_off[1] = take(rows * maxw * 2);
+  // per-layer partials, all reduced together at the end of the step
   const int64_t parts = std::max(p->blocks_bwd, p->blocks_pair);
-  for (int k = 0; k < 2; ++k) {
-    p->dw_off[k] = take(parts * maxoi * 4);
-    p->db_off[k] = take(parts * maxo * 4);
+  int64_t all = 1;  // the loss
+  for (int i = 0; i < L; ++i) {
+    p->dw_off[i] = take(parts * d.dims[i + 1] * d.dims[i] * 4);
+    p->db_off[i] = take(parts * d.dims[i + 1] * 4);
+    all += int64_t(d.dims[i + 1]) * (d.dims[i] + 1);
   }
   p->loss_off = take(int64_t(p->blocks_fwd) * 4);
-  p->mid_off = take(int64_t(kTrSplit) * std::max(maxoi, p->blocks_fwd) * 4);
+  p->mid_off = take(int64_t(kTrSplit) * all * 4);
   p->total = off;
 }
 
@@ -1610,13 +1638,18 @@ int launch_train_step(const rdv_mlp_desc& d, const MlpLayout& lay, const void* p
     RDV_HIP_TRY(hipGetLastError());
   }
   const float scale = 1.0f / float(double(n) * d.dims[L]);
-  float* mid = reinterpret_cast<float*>(ws + p.mid_off);
+  ReduceJobs jobs;
+  jobs.n = 0;
+  jobs.start[0] = 0;
+  jobs.bstart[0] = 0;
+  // queues the reduction of part[nb][count] into out (run after the backward)
   auto reduce = [&](const float* part, int nb, int64_t count, float* out) -> int {
-    const unsigned gx = unsigned(std::min<int64_t>((count + 255) / 256, 1024));
-    train_reduce1_kernel<<<dim3(gx, kTrSplit), dim3(256), 0, stream>>>(part, nb, count, mid);
-    RDV_HIP_TRY(hipGetLastError());
-    train_reduce2_kernel<<<dim3(gx), dim3(256), 0, stream>>>(mid, count, scale, out);
-    RDV_HIP_TRY(hipGetLastError());
+    const int j = jobs.n++;
+    jobs.part[j] = part;
+    jobs.out[j] = out;
+    jobs.nb[j] = nb;
+    jobs.start[j + 1] = jobs.start[j] + count;
+    jobs.bstart[j + 1] = jobs.bstart[j] + int((count + 255) / 256);
     return RDV_OK;
   };
   rc = reduce(reinterpret_cast<float*>(ws + p.loss_off), p.blocks_fwd, 1, loss);
@@ -1656,10 +1689,10 @@ int launch_train_step(const rdv_mlp_desc& d, const MlpLayout& lay, const void* p
       pa.wl1s = pack_wts(l - 1, reinterpret_cast<half_t*>(ws + p.wt_off[l - 1]));
       RDV_HIP_TRY(hipGetLastError());
       pa.gout = reinterpret_cast<half_t*>(ws + p.dz_off[dst]);
-      pa.dw_l = reinterpret_cast<float*>(ws + p.dw_off[0]);
-      pa.db_l = reinterpret_cast<float*>(ws + p.db_off[0]);
-      pa.dw_l1 = reinterpret_cast<float*>(ws + p.dw_off[1]);
-      pa.db_l1 = reinterpret_cast<float*>(ws + p.db_off[1]);
+      pa.dw_l = reinterpret_cast<float*>(ws + p.dw_off[l]);
+      pa.db_l = reinterpret_cast<float*>(ws + p.db_off[l]);
+      pa.dw_l1 = reinterpret_cast<float*>(ws + p.dw_off[l - 1]);
+      pa.db_l1 = reinterpret_cast<float*>(ws + p.db_off[l - 1]);
       pa.n = n;
       const dim3 grid(unsigned(p.blocks_pair)), block(kT2Threads);
       if (d.dims[l + 1] == 128)
@@ -1696,10 +1729,10 @@ int launch_train_step(const rdv_mlp_desc& d, const MlpLayout& lay, const void* p
     pa.wtl1 = l - 1 > 0 ? pack_wt(l - 1) : nullptr;
     RDV_HIP_TRY(hipGetLastError());
     pa.gout = l - 1 > 0 ? reinterpret_cast<half_t*>(ws + p.dz_off[dst]) : nullptr;
-    pa.dw_l = reinterpret_cast<float*>(ws + p.dw_off[0]);
-    pa.db_l = reinterpret_cast<float*>(ws + p.db_off[0]);
-    pa.dw_l1 = reinterpret_cast<float*>(ws + p.dw_off[1]);
-    pa.db_l1 = reinterpret_cast<float*>(ws + p.db_off[1]);
+    pa.dw_l = reinterpret_cast<float*>(ws + p.dw_off[l]);
+    pa.db_l = reinterpret_cast<float*>(ws + p.db_off[l]);
+    pa.dw_l1 = reinterpret_cast<float*>(ws + p.dw_off[l - 1]);
+    pa.db_l1 = reinterpret_cast<float*>(ws + p.db_off[l - 1]);
     const size_t lds = size_t(pair_lds(pa.in0, pa.mid, pa.out, pa.kc0, pa.gout != nullptr));
     const void* fn = pair_kernel(pa);
     void* args[] = {&pa};
@@ -1744,6 +1777,12 @@ int launch_train_step(const rdv_mlp_desc& d, const MlpLayout& lay, const void* p
     rc = reduce(ba.db_part, p.blocks_bwd, out, db[0]);
     if (rc != RDV_OK) return rc;
   }
+  float* mid = reinterpret_cast<float*>(ws + p.mid_off);
+  const unsigned gx = unsigned(jobs.bstart[jobs.n]);
+  train_reduce1_kernel<<<dim3(gx, kTrSplit), dim3(256), 0, stream>>>(jobs, mid);
+  RDV_HIP_TRY(hipGetLastError());
+  train_reduce2_kernel<<<dim3(gx), dim3(256), 0, stream>>>(jobs, mid, scale);
+  RDV_HIP_TRY(hipGetLastError());
   return RDV_OK;
 }
 
