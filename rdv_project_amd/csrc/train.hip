@@ -1309,20 +1309,33 @@ __global__ __launch_bounds__(kT2Threads, 1) void train_pair2_kernel(TrainPair2Ar
       const half8* E = sEx + ((it - 1) & 1) * LD::kEx;
       const half8 hf0 = E[LD::kHF + (2 * w) * 64 + lane], hf1 = E[LD::kHF + (2 * w + 1) * 64 + lane];
       const half8 gf0 = E[LD::kGF + (2 * w) * 64 + lane], gf1 = E[LD::kGF + (2 * w + 1) * 64 + lane];
-#pragma unroll
-      for (int ob = 0; ob < MTO; ++ob) {
-        accL[ob] = __builtin_amdgcn_mfma_f32_32x32x16_f16(E[LD::kGT + (2 * ob) * 64 + lane], hf0, accL[ob], 0, 0, 0);
-        accL[ob] = __builtin_amdgcn_mfma_f32_32x32x16_f16(E[LD::kGT + (2 * ob + 1) * 64 + lane], hf1, accL[ob], 0, 0, 0);
-      }
-#pragma unroll
-      for (int ib = 0; ib < 4; ++ib) {
-        accL1[ib] = __builtin_amdgcn_mfma_f32_32x32x16_f16(gf0, E[LD::kHT + (2 * ib) * 64 + lane], accL1[ib], 0, 0, 0);
-        accL1[ib] = __builtin_amdgcn_mfma_f32_32x32x16_f16(gf1, E[LD::kHT + (2 * ib + 1) * 64 + lane], accL1[ib], 0, 0, 0);
-      }
       f32x16 acc2 = {};
+      if constexpr (MTO < 4) {
+        // few dW_l products: each link of the g_{l-2} chain alternates with the
+        // independent dW products (measured faster for the 16-wide head only)
 #pragma unroll
-      for (int c = 0; c < KC; ++c)
-        acc2 = __builtin_amdgcn_mfma_f32_32x32x16_f16(wl1[c], E[LD::kGP + c * 64 + lane], acc2, 0, 0, 0);
+        for (int c = 0; c < KC; ++c) {
+          acc2 = __builtin_amdgcn_mfma_f32_32x32x16_f16(wl1[c], E[LD::kGP + c * 64 + lane], acc2, 0, 0, 0);
+          const int ks = c & 1, blk = c >> 1;
+          accL1[blk] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ks ? gf1 : gf0, E[LD::kHT + c * 64 + lane], accL1[blk], 0, 0, 0);
+          if (blk < MTO)
+            accL[blk] = __builtin_amdgcn_mfma_f32_32x32x16_f16(E[LD::kGT + c * 64 + lane], ks ? hf1 : hf0, accL[blk], 0, 0, 0);
+        }
+      } else {
+#pragma unroll
+        for (int ob = 0; ob < MTO; ++ob) {
+          accL[ob] = __builtin_amdgcn_mfma_f32_32x32x16_f16(E[LD::kGT + (2 * ob) * 64 + lane], hf0, accL[ob], 0, 0, 0);
+          accL[ob] = __builtin_amdgcn_mfma_f32_32x32x16_f16(E[LD::kGT + (2 * ob + 1) * 64 + lane], hf1, accL[ob], 0, 0, 0);
+        }
+#pragma unroll
+        for (int ib = 0; ib < 4; ++ib) {
+          accL1[ib] = __builtin_amdgcn_mfma_f32_32x32x16_f16(gf0, E[LD::kHT + (2 * ib) * 64 + lane], accL1[ib], 0, 0, 0);
+          accL1[ib] = __builtin_amdgcn_mfma_f32_32x32x16_f16(gf1, E[LD::kHT + (2 * ib + 1) * 64 + lane], accL1[ib], 0, 0, 0);
+        }
+#pragma unroll
+        for (int c = 0; c < KC; ++c)
+          acc2 = __builtin_amdgcn_mfma_f32_32x32x16_f16(wl1[c], E[LD::kGP + c * 64 + lane], acc2, 0, 0, 0);
+      }
       half8* dst = reinterpret_cast<half8*>(a.gout + tile * 32 * 128);
 #pragma unroll
       for (int qq = 0; qq < 2; ++qq) {
