@@ -274,8 +274,8 @@ def bench_train(steps, warmup):
         "workload": "C5 MLP training step: 4,194,304 points x ~ N(0,1) fp16 (seed 5), 32 -> 128 x 8 -> 16, ReLU, "
                     "MSE against N(0,1) targets (seed 6), Kaiming-uniform fp16 weights (seed 7); forward, loss, "
                     "backward with fp32 dW / db reduced over all points",
-        "kernels": "train_fwd_pair_kernel x2 (layers 0-4, 5-8) + train_pair_kernel x4 (layer pairs 8-7 .. 2-1) + "
-                   "train_bwd_kernel (layer 0) + reductions",
+        "kernels": "train_fwd_pair_kernel x2 (layers 0-4, 5-8) + train_pair2_kernel x4 (layer pairs 8-7 .. 2-1) + "
+                   "train_bwd0_kernel (layer 0) + one reduction",
     }
 
 
