@@ -18,11 +18,12 @@
 //
 // MLP-in-the-loop mapping: one wave owns one ray at a time; a 32-sample chunk
 // of the ray is one MFMA N block (lane l evaluates sample l % 32, both feature
-// halves), so the layer chain is exactly the fused MLP kernel's.  The samples'
-// positions are generated in registers and the head values never leave the
-// wave: transmittance along the chunk is an inclusive wavefront scan of
-// sigma * dt (T_i = T_in exp(-sum_{j<i} sigma_j dt)), the colour a per-lane
-// partial sum reduced once per ray.
+// halves), and two consecutive chunks go through the layer chain together as
+// the fused MLP kernel's staggered tile pair (run_pair, mlp_core.h).  The
+// samples' positions are generated in registers and the head values never
+// leave the wave: transmittance along a chunk is an inclusive wavefront scan of
+// sigma * dt (T_i = T_in exp(-sum_{j<i} sigma_j dt)), the chunks composited in
+// ray order, the colour a per-lane partial sum reduced once per ray.
 #include "mlp_core.h"
 
 namespace rdv {
@@ -148,8 +149,12 @@ __device__ __forceinline__ void eval_chunk(const half8* sw, const float* sb, boo
   for (int t = 0; t < N::kMaxMT; ++t) fin[t] = (LL % 2 == 0) ? accA[t] : accB[t];
 }
 
-constexpr int kRenderWaves = 16;
+constexpr int kRenderWaves = 16;  // transmittance kernel
 constexpr int kRenderThreads = 64 * kRenderWaves;
+// emission-absorption renderer: 12 waves (3 per SIMD; the tile-pair chain needs
+// ~168 registers), measured faster than 8 or 16
+constexpr int kEaWaves = 12;
+constexpr int kEaThreads = 64 * kEaWaves;
 
 // Weights and biases of the packed MLP into LDS (block-wide), counter reset.
 template <class N>
@@ -176,7 +181,7 @@ struct RenderArgs {
 };
 
 template <class N>
-__global__ __launch_bounds__(kRenderThreads, 1) void render_ea_kernel(RenderArgs a) {
+__global__ __launch_bounds__(kEaThreads, 1) void render_ea_kernel(RenderArgs a) {
   static_assert(N::kIn == 3 && N::kOut == 4, "the renderer evaluates a 3 -> 4 (density, RGB) field");
   __shared__ float sb[N::kBias];
   __shared__ half8 sw[N::kFrags * 64];
@@ -212,21 +217,38 @@ __global__ __launch_bounds__(kRenderThreads, 1) void render_ea_kernel(RenderArgs
       t0 = fmaxf(t0, 0.0f);
       const float dt = (t1 - t0) / float(a.samples);
       float Tin = 1.0f;
-      for (int c = 0; c < chunks; ++c) {
-        const float ts = t0 + (float(32 * c + col) + 0.5f) * dt;
-        const float p[3] = {o[0] + ts * w[0], o[1] + ts * w[1], o[2] + ts * w[2]};
-        f32x16 fin[N::kMaxMT];
-        eval_chunk<N, true>(sw, sb, has_bias, lane, h, p, fin);
-        // lanes 0..31 hold rows 0..3 = (density, r, g, b) of sample col
-        const float sigma = fast_softplus(fin[0][0]);
+      auto composite = [&](const f32x16& f) {
+        const float sigma = fast_softplus(f[0]);
         const float ad = h == 0 ? sigma * dt : 0.0f;
         const float incl = wave_scan_incl(ad, lane);
         const float total = lane_value(incl, 31);
         const float wgt = h == 0 ? Tin * __expf(-(incl - ad)) * (1.0f - __expf(-ad)) : 0.0f;
-        cr += wgt * fast_sigmoid(fin[0][1]);
-        cg += wgt * fast_sigmoid(fin[0][2]);
-        cb += wgt * fast_sigmoid(fin[0][3]);
+        cr += wgt * fast_sigmoid(f[1]);
+        cg += wgt * fast_sigmoid(f[2]);
+        cb += wgt * fast_sigmoid(f[3]);
         Tin *= __expf(-total);
+      };
+      for (int c = 0; c + 1 < chunks; c += 2) {
+        const float ta = t0 + (float(32 * c + col) + 0.5f) * dt;
+        const float tb = t0 + (float(32 * c + 32 + col) + 0.5f) * dt;
+        const float pa[3] = {o[0] + ta * w[0], o[1] + ta * w[1], o[2] + ta * w[2]};
+        const float pb[3] = {o[0] + tb * w[0], o[1] + tb * w[1], o[2] + tb * w[2]};
+        f32x16 accA[N::kMaxMT], accB[N::kMaxMT];
+        half8 bA[N::kMaxKC], bB[N::kMaxKC];
+        const LdsWeights ws{sw + opaque_zero(), lane};
+        build_input<N>(pa, h, bA);
+        if (has_bias) run_pair<N, 0, true, true>(ws, pb, h, bA, bB, accA, accB, sb + opaque_zero());
+        else run_pair<N, 0, true, false>(ws, pb, h, bA, bB, accA, accB, sb);
+        composite(accA[0]);
+        composite(accB[0]);
+      }
+      if (chunks & 1) {
+        const int c = chunks - 1;
+        const float ts = t0 + (float(32 * c + col) + 0.5f) * dt;
+        const float p[3] = {o[0] + ts * w[0], o[1] + ts * w[1], o[2] + ts * w[2]};
+        f32x16 fin[N::kMaxMT];
+        eval_chunk<N, true>(sw, sb, has_bias, lane, h, p, fin);
+        composite(fin[0]);
       }
       cr = wave_sum(cr);
       cg = wave_sum(cg);
@@ -530,9 +552,9 @@ int launch_render_ea(const rdv_camera_desc& c, const float* poses, const rdv_mlp
   a.samples = samples;
   const int64_t nrays = int64_t(c.n_cams) * c.height * c.width;
   int64_t blocks = di.cu_count;
-  const int64_t need = (nrays + kRenderWaves - 1) / kRenderWaves;
+  const int64_t need = (nrays + kEaWaves - 1) / kEaWaves;
   if (need < blocks) blocks = need;
-  render_ea_kernel<RenderNet64x3><<<dim3(unsigned(blocks)), dim3(kRenderThreads), 0, stream>>>(a);
+  render_ea_kernel<RenderNet64x3><<<dim3(unsigned(blocks)), dim3(kEaThreads), 0, stream>>>(a);
   RDV_HIP_TRY(hipGetLastError());
   return RDV_OK;
 }
