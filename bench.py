@@ -167,7 +167,7 @@ def bench_winograd(steps, warmup):
         "hbm_frac": round(C3_BYTES / (ev * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
         "workload": "C3 Winograd F(2x2,3x3): NCHW fp16 1x64x256x256 U[0,1] (seed 3), 64 -> 64, "
                     "w ~ N(0, sqrt(2/576)) fp16 (seed 4), zero bias, ReLU, fp16 out",
-        "kernel": "winograd3x3_strip_kernel<2>",
+        "kernel": "winograd3x3_pipe_kernel<2>",
     }
 
 

@@ -20,11 +20,14 @@
 //   from global memory for every (position, channel block) pair, .h:113-137) is
 //   replaced by one staging of the haloed input in LDS per tile group.
 //
-// Work decomposition: a tile group is 16 consecutive tiles of one tile row (2
-// output rows x 32 output columns).  Each block owns a contiguous range of
-// groups; per group it stages the 4 x 34 x CIN input region in LDS (fp32),
-// transforms it to V in B-fragment order (fp16), then every wave evaluates its
-// 16 output channels for the 16 tiles.
+// Work decomposition (generic kernel, any layout and dtype): a tile group is 16
+// consecutive tiles of one tile row (2 output rows x 32 output columns).  Each
+// block owns a contiguous range of groups; per group it stages the 4 x 34 x CIN
+// input region in LDS (fp32), transforms it to V in B-fragment order (fp16),
+// then every wave evaluates its 16 output channels for the 16 tiles.  NCHW fp16
+// input takes winograd3x3_pipe_kernel (below): the same transforms and GEMMs,
+// input rows by DMA, and the input transform of one tile row overlapped with
+// the GEMMs of the previous one.
 #include <algorithm>
 #include <type_traits>
 
@@ -94,9 +97,9 @@ struct WinogradArgs {
   int relu;
   int th, seg;        // tile rows per image, 16-tile segments per tile row
   int64_t ngroups;    // batch * th * seg
-  int rows_per_item;  // strip kernel: tile rows per work item
-  int chunks;         // strip kernel: work items per strip (ceil(th / rows_per_item))
-  int64_t items;      // strip kernel: batch * seg * chunks
+  int rows_per_item;  // pipelined kernel: tile rows per work item
+  int chunks;         // pipelined kernel: work items per strip (ceil(th / rows_per_item))
+  int64_t items;      // pipelined kernel: batch * seg * chunks
 };
 
 // The 16 channel-reduction GEMMs of one 16-tile group for this wave's 16
@@ -363,29 +366,16 @@ __global__ __launch_bounds__(256, 2) void winograd3x3_kernel(WinogradArgs a) {
 }
 
 
-// ------------------------------------------------------------ strip kernel
-// Fast path for NCHW fp16 input with W % 8 == 0 (the benchmark layout).
-//
-// Each block (4 waves, two per CU) walks a vertical strip of one image: 32 output
-// columns (16 tiles) by `rows_per_item` tile rows, top to bottom.  Input rows
-// arrive in LDS by direct global->LDS DMA (global_load_lds_dwordx4: lane l of
-// an instruction writes its 16 bytes at M0 + 16 l) into a ring of 4 row-pair
-// slots (pair k = input rows 2k-1 and 2k, fp16, 48 columns [32 s - 8, 32 s + 40)
-// per channel row); tile row tr reads pairs tr and tr+1, so every input row of
-// the strip is fetched from HBM once, and pairs are requested 3 tile rows
-// ahead without occupying registers.  Chunks outside the image are fetched
-// from a 16-byte zero block.
-//
-// The DMA and the output stores are issued from inline assembly, so the wave's
-// vector-memory stream inside the loop is exactly: the DMAs of one pair (Ld
-// instructions) and the stores of one step (St instructions) per step; the
-// wait for a pair is then an exact s_waitcnt vmcnt(N) for the number of
-// operations issued after it (loads and stores retire in order on gfx9).
-//
-// The V transform is one (tile, 4-channel) unit per thread: 4 x 4 patch reads
-// from the ring (fp16 -> fp32), the reference's fp32 operation order, fp16
-// rounding, and 16 8-byte writes in B-fragment order.
-constexpr int kStripSlots = 3;                 // row-pair ring = prefetch distance
+// ------------------------------------------------------- NCHW fp16 fast path
+// For NCHW fp16 input with W % 8 == 0 (the benchmark layout).  Input rows arrive
+// in LDS by direct global->LDS DMA (global_load_lds_dwordx4: lane l of an
+// instruction writes its 16 bytes at M0 + 16 l) as row pairs (pair k = input
+// rows 2k-1 and 2k, fp16, 48 columns [32 s - 8, 32 s + 40) per channel row); tile
+// row tr reads pairs tr and tr+1, so every input row of a strip is fetched from
+// HBM once.  Chunks outside the image are fetched from a 16-byte zero block.
+// The DMA and the output stores are issued from inline assembly, so each wave's
+// vector-memory stream is exactly the operations its waits count (loads and
+// stores retire in order on gfx9).
 constexpr int kRowBytes = 96;                  // 48 fp16 columns per staged channel row
 
 __device__ __attribute__((aligned(16))) uint32_t g_wg_zero16[4] = {0u, 0u, 0u, 0u};
@@ -475,50 +465,46 @@ __device__ __forceinline__ void wg_store_asm(const f32x4 (&yv)[2][2], const Wino
   }
 }
 
+// ------------------------------------------------------- pipelined kernel
+// winograd3x3_pipe_kernel: each 8-wave block (one per CU) walks a vertical strip
+// of one image, 32 output columns (16 tiles) by rows_per_item tile rows, top to
+// bottom, in two roles of 4 waves, so that a tile row's input transform runs
+// while the previous row's GEMMs and stores run:
+//   waves 4-7 (input role): row pairs into a 4-slot ring by DMA (3 pairs
+//     ahead), then V of tile row s into sv buffer s % 2;
+//   waves 0-3 (GEMM role): U resident in registers; the GEMMs, inverse
+//     transform and stores of tile row s - 1 from sv buffer (s - 1) % 2.
+// Step s = 0 .. R ends with one barrier.  Each role's vector-memory stream is
+// its own (DMAs only; U's loads then stores only), so the input role's waits
+// count its DMA instructions alone.  The V transform is one (tile, 4-channel)
+// unit per input-role thread: 4 x 4 patch reads from the ring (fp16 -> fp32),
+// the reference's fp32 operation order, fp16 rounding, and 16 8-byte writes in
+// B-fragment order.
+constexpr int kPipeSlots = 4;
 template <int KC>
-__global__ __launch_bounds__(256, 2) void winograd3x3_strip_kernel(WinogradArgs a) {
+struct WgPipeLds {
+  static constexpr int kSlotBytes = 2 * 32 * KC * kRowBytes;
+  static constexpr int kSvHalf8 = 16 * KC * 64;
+  static constexpr int kBytes = kPipeSlots * kSlotBytes + 2 * kSvHalf8 * 16;
+};
+
+template <int KC>
+__global__ __launch_bounds__(512, 1) void winograd3x3_pipe_kernel(WinogradArgs a) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  using LD = WgPipeLds<KC>;
   constexpr int CH = 32 * KC;                          // staged channels
   constexpr int kPairChunks = 2 * CH * 6;              // 16-byte chunks per row pair (multiple of 64)
   constexpr int kLoads = (kPairChunks + 255) / 256;    // DMA rounds per pair
-  constexpr int kSlotBytes = 2 * CH * kRowBytes;
-  constexpr int D = kStripSlots;
-  __shared__ __attribute__((aligned(16))) uint32_t ring[kStripSlots * kSlotBytes / 4];
-  __shared__ half8 sv[16 * KC * 64];
+  constexpr int kSlotBytes = LD::kSlotBytes;
+  uint32_t* const ring = reinterpret_cast<uint32_t*>(smem);
+  half8* const svb = reinterpret_cast<half8*>(smem + kPipeSlots * kSlotBytes);
   const int tid = int(threadIdx.x);
   const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int g = blockIdx.y * 4 + wave;
-  const bool active = 16 * g < a.cout;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  __builtin_assume(wave >= 0 && wave < 8);
+  const int role = wave >> 2, w = wave & 3;
   const int hw = a.H * a.W;
   const half_t* __restrict__ x = static_cast<const half_t*>(a.x);
-  const uint32_t ring_lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(ring));
-
-  // this wave's vector-memory operations per pair (DMA) and per step (stores)
-  int Ld = 0;
-#pragma unroll
-  for (int i = 0; i < kLoads; ++i) Ld += (i * 256 + wave * 64 < kPairChunks) ? 1 : 0;
-  const int St = active ? (a.out_layout == RDV_LAYOUT_CHW ? 8 : 4) : 0;
-
-  // DMA of row pair k of strip (img, seg) into ring slot `slot`
-  auto dma_pair = [&](int img, int seg, int k, int slot) {
-    const half_t* base = x + int64_t(img) * a.cin * hw;
-#pragma unroll
-    for (int i = 0; i < kLoads; ++i) {
-      const int first = i * 256 + wave * 64;  // wave-uniform
-      if (first < kPairChunks) {
-        const int lin = first + lane;
-        const int cc = lin % 6;
-        const int rest = lin / 6;
-        const int ci = rest % CH;
-        const int row = 2 * k - 1 + rest / CH;
-        const int col = 32 * seg - 8 + 8 * cc;
-        const bool ok = (ci < a.cin) & (row >= 0) & (row < a.H) & (col >= 0) & (col < a.W);
-        const void* src = ok ? static_cast<const void*>(base + (ci * a.H + row) * a.W + col)
-                             : static_cast<const void*>(g_wg_zero16);
-        wg_dma16(src, ring_lds + uint32_t(slot * kSlotBytes + first * 16));
-      }
-    }
-  };
 
   auto decode = [&](int64_t item, int& img, int& seg, int& tr0) {
     const int chunk = int(item % a.chunks);
@@ -528,9 +514,108 @@ __global__ __launch_bounds__(256, 2) void winograd3x3_strip_kernel(WinogradArgs 
     tr0 = chunk * a.rows_per_item;
   };
 
-  // U and the bias, resident for the whole block, and the first item's first
-  // row pairs; all waited for before the loop so that no compiler-generated
-  // vector-memory wait is left inside it
+  if (role == 1) {
+    // ================= input role
+    const uint32_t ring_lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(ring));
+    int Ld = 0;  // this wave's DMA instructions per pair
+#pragma unroll
+    for (int i = 0; i < kLoads; ++i) Ld += (i * 256 + w * 64 < kPairChunks) ? 1 : 0;
+    auto dma_pair = [&](int img, int seg, int k, int slot) {
+      const half_t* base = x + int64_t(img) * a.cin * hw;
+#pragma unroll
+      for (int i = 0; i < kLoads; ++i) {
+        const int first = i * 256 + w * 64;  // wave-uniform
+        if (first < kPairChunks) {
+          const int lin = first + lane;
+          const int cc = lin % 6;
+          const int rest = lin / 6;
+          const int ci = rest % CH;
+          const int row = 2 * k - 1 + rest / CH;
+          const int col = 32 * seg - 8 + 8 * cc;
+          const bool ok = (ci < a.cin) & (row >= 0) & (row < a.H) & (col >= 0) & (col < a.W);
+          const void* src = ok ? static_cast<const void*>(base + (ci * a.H + row) * a.W + col)
+                               : static_cast<const void*>(g_wg_zero16);
+          wg_dma16(src, ring_lds + uint32_t(slot * kSlotBytes + first * 16));
+        }
+      }
+    };
+    const int vt = tid - 256;  // this thread's (tile, 4-channel) unit
+    const int n = vt & 15, qd = vt >> 4;
+    for (int64_t item = blockIdx.x; item < a.items; item += gridDim.x) {
+      int img, seg, tr0;
+      decode(item, img, seg, tr0);
+      const int R = min(a.rows_per_item, a.th - tr0);  // tile rows (>= 1); pairs 0..R
+      for (int q = 0; q < min(3, R + 1); ++q) dma_pair(img, seg, tr0 + q, q);
+      wg_wait_vmcnt(2 <= R ? Ld : 0);  // pairs 0 and 1 landed (pair 2 may be in flight)
+      __syncthreads();
+      for (int s = 0; s <= R; ++s) {
+        if (s < R) {
+          // ---- V = B^T d B of tile row s (pairs s, s + 1) per (tile, 4 channels)
+          if (qd < CH / 4) {
+            const int sa = s % kPipeSlots, sb = (s + 1) % kPipeSlots;
+            half4 hv[16];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+              const int ci = 4 * qd + c;
+              float d[4][4];
+#pragma unroll
+              for (int dr = 0; dr < 4; ++dr) {
+                const uint32_t* row = ring + ((dr < 2 ? sa : sb) * kSlotBytes + ((dr & 1) * CH + ci) * kRowBytes) / 4;
+                // columns 2n-1 .. 2n+2 of the tile = halves 2n+7 .. 2n+10 of the staged row
+                const uint32_t w0 = row[n + 3], w1 = row[n + 4], w2 = row[n + 5];
+                const half2v h0 = __builtin_bit_cast(half2v, w0);
+                const half2v h1 = __builtin_bit_cast(half2v, w1);
+                const half2v h2 = __builtin_bit_cast(half2v, w2);
+                d[dr][0] = float(h0[1]);
+                d[dr][1] = float(h1[0]);
+                d[dr][2] = float(h1[1]);
+                d[dr][3] = float(h2[0]);
+              }
+              float m[4][4];
+#pragma unroll
+              for (int cj = 0; cj < 4; ++cj) {
+                m[0][cj] = d[0][cj] - d[2][cj];
+                m[1][cj] = d[1][cj] + d[2][cj];
+                m[2][cj] = d[2][cj] - d[1][cj];
+                m[3][cj] = d[1][cj] - d[3][cj];
+              }
+#pragma unroll
+              for (int r = 0; r < 4; ++r) {
+                float vv[4];
+                vv[0] = m[r][0] - m[r][2];
+                vv[1] = m[r][1] + m[r][2];
+                vv[2] = m[r][2] - m[r][1];
+                vv[3] = m[r][1] - m[r][3];
+#pragma unroll
+                for (int b = 0; b < 4; ++b) {
+                  float v = vv[b];
+                  asm volatile("" : "+v"(v));  // fp32 result first, then fp16 (no fused fma_mix rounding)
+                  hv[4 * r + b][c] = half_t(v);
+                }
+              }
+            }
+            half8* sv = svb + (s & 1) * LD::kSvHalf8;
+            const int ci0 = 4 * qd;
+            const int kc = ci0 / 32, k = ci0 % 32;
+            const int flane = (k / 8) * 16 + n, j0 = k % 8;
+#pragma unroll
+            for (int p = 0; p < 16; ++p)
+              *reinterpret_cast<half4*>(reinterpret_cast<half_t*>(&sv[(p * KC + kc) * 64 + flane]) + j0) = hv[p];
+          }
+          // pair s + 3 into the slot pair s - 1 used (read by step s - 1, before its barrier)
+          if (s + 3 <= R) dma_pair(img, seg, tr0 + s + 3, (s + 3) % kPipeSlots);
+          // pair s + 2 landed for the next step (only pair s + 3 may still be in flight)
+          if (s + 2 <= R) wg_wait_vmcnt(s + 3 <= R ? Ld : 0);
+        }
+        __syncthreads();
+      }
+    }
+    return;
+  }
+
+  // ================= GEMM role: wave w owns output channels 16 (4 blockIdx.y + w) + 0..15
+  const int g = blockIdx.y * 4 + w;
+  const bool active = 16 * g < a.cout;
   half8 u[16][KC];
   const int g_n = (a.cout + 15) / 16;
   const int gu = active ? g : 0;
@@ -540,108 +625,22 @@ __global__ __launch_bounds__(256, 2) void winograd3x3_strip_kernel(WinogradArgs 
     for (int kc = 0; kc < KC; ++kc)
       u[p][kc] = reinterpret_cast<const half8*>(a.U)[((int64_t(p) * KC + kc) * g_n + gu) * 64 + lane];
   const f32x4 bias = wg_lane_bias(a, gu, lane);
-  if (int64_t(blockIdx.x) < a.items) {
-    int img, seg, tr0;
-    decode(blockIdx.x, img, seg, tr0);
-    const int R = min(a.rows_per_item, a.th - tr0);
-    for (int q = 0; q < min(D, R + 1); ++q) dma_pair(img, seg, tr0 + q, q);
-  }
 #pragma unroll
   for (int p = 0; p < 16; ++p)
 #pragma unroll
     for (int kc = 0; kc < KC; ++kc) asm volatile("" ::"v"(u[p][kc]));
   asm volatile("" ::"v"(bias));
-  wg_wait_vmcnt(0);
-  __syncthreads();
-
+  wg_wait_vmcnt(0);  // U and the bias resident: no compiler-generated wait inside the loop
   for (int64_t item = blockIdx.x; item < a.items; item += gridDim.x) {
     int img, seg, tr0;
     decode(item, img, seg, tr0);
-    const int R = min(a.rows_per_item, a.th - tr0);  // tile rows of this item (>= 1); pairs 0..R
-    const int P = min(D, R + 1);                     // pairs requested up front
-    if (item != int64_t(blockIdx.x))
-      for (int q = 0; q < P; ++q) dma_pair(img, seg, tr0 + q, q);
-
-    for (int j = 0; j < R; ++j) {
-      const int tr = tr0 + j;
-      // ---- wait until pairs j and j+1 are in LDS (this wave's DMAs), then for every wave
-      {
-        int after;
-        if (j + 1 < P) {
-          const int hi = min(j - 1, R - D);
-          after = Ld * (P - j - 2) + St * j + Ld * (hi >= 0 ? hi + 1 : 0);
-        } else {
-          const int lo = j + 2 - D, hi = min(j - 1, R - D);
-          after = St * (D - 1) + Ld * (hi >= lo ? hi - lo + 1 : 0);
-        }
-        wg_wait_vmcnt(after);
-      }
-      __syncthreads();
-
-      // ---- V = B^T d B per (tile, 4 channels)
-      {
-        const int n = tid & 15;
-        const int qd = tid >> 4;
-        if (qd < CH / 4) {
-          const int sa = j % D, sb = (j + 1) % D;
-          half4 hv[16];
-#pragma unroll
-          for (int c = 0; c < 4; ++c) {
-            const int ci = 4 * qd + c;
-            float d[4][4];
-#pragma unroll
-            for (int dr = 0; dr < 4; ++dr) {
-              const uint32_t* row = ring + ((dr < 2 ? sa : sb) * kSlotBytes + ((dr & 1) * CH + ci) * kRowBytes) / 4;
-              // columns 2n-1 .. 2n+2 of the tile = halves 2n+7 .. 2n+10 of the staged row
-              const uint32_t w0 = row[n + 3], w1 = row[n + 4], w2 = row[n + 5];
-              const half2v h0 = __builtin_bit_cast(half2v, w0);
-              const half2v h1 = __builtin_bit_cast(half2v, w1);
-              const half2v h2 = __builtin_bit_cast(half2v, w2);
-              d[dr][0] = float(h0[1]);
-              d[dr][1] = float(h1[0]);
-              d[dr][2] = float(h1[1]);
-              d[dr][3] = float(h2[0]);
-            }
-            float m[4][4];
-#pragma unroll
-            for (int cj = 0; cj < 4; ++cj) {
-              m[0][cj] = d[0][cj] - d[2][cj];
-              m[1][cj] = d[1][cj] + d[2][cj];
-              m[2][cj] = d[2][cj] - d[1][cj];
-              m[3][cj] = d[1][cj] - d[3][cj];
-            }
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              float vv[4];
-              vv[0] = m[r][0] - m[r][2];
-              vv[1] = m[r][1] + m[r][2];
-              vv[2] = m[r][2] - m[r][1];
-              vv[3] = m[r][1] - m[r][3];
-#pragma unroll
-              for (int b = 0; b < 4; ++b) {
-                float v = vv[b];
-                asm volatile("" : "+v"(v));  // fp32 result first, then fp16 (no fused fma_mix rounding)
-                hv[4 * r + b][c] = half_t(v);
-              }
-            }
-          }
-          const int ci0 = 4 * qd;
-          const int kc = ci0 / 32, k = ci0 % 32;
-          const int flane = (k / 8) * 16 + n, j0 = k % 8;
-#pragma unroll
-          for (int p = 0; p < 16; ++p)
-            *reinterpret_cast<half4*>(reinterpret_cast<half_t*>(&sv[(p * KC + kc) * 64 + flane]) + j0) = hv[p];
-        }
-      }
-      __syncthreads();  // sv complete; every wave is done with the slot of pair j
-
-      // ---- request pair j + D into the slot pair j used
-      if (j + D <= R) dma_pair(img, seg, tr0 + j + D, j % D);
-
-      // ---- GEMMs, inverse transform, bias / ReLU, stores
-      if (active) {
+    const int R = min(a.rows_per_item, a.th - tr0);
+    __syncthreads();  // the input role's first two pairs
+    for (int s = 0; s <= R; ++s) {
+      if (s >= 1 && active) {
+        const int tr = tr0 + s - 1;
         f32x4 yv[2][2];
-        wg_gemm(u, sv, lane, yv);
+        wg_gemm(u, svb + ((s - 1) & 1) * LD::kSvHalf8, lane, yv);
         const int n = lane & 15;
         const int tc = seg * kWgTiles + n;
         const int co0 = 16 * g + 4 * (lane >> 4);
@@ -657,11 +656,8 @@ __global__ __launch_bounds__(256, 2) void winograd3x3_strip_kernel(WinogradArgs 
             }
         if (tc < a.W / 2) wg_store_asm(yv, a, img, co0, 2 * tr, 2 * tc);
       }
+      __syncthreads();
     }
-    // all of this item's DMAs have landed (the last step waited for pair R)
-    // and every wave is past its last read of the ring before the next item's
-    // DMAs overwrite it
-    __syncthreads();
   }
 }
 
@@ -708,17 +704,25 @@ int launch_winograd3x3(const rdv_conv_desc& d, const void* x, const void* U, con
   const int slices = (groups16 + 3) / 4;  // 64-channel slices (grid y)
   const bool f16 = d.in_dtype == RDV_DTYPE_F16, chw = d.in_layout == RDV_LAYOUT_CHW;
   if (f16 && chw && d.W % 8 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0) {
-    // strip kernel: one block per CU, each walking rows_per_item tile rows of a strip
+    // pipelined kernel: one 8-wave block per CU, each walking rows_per_item tile rows of a strip
+    static bool attr = false;
+    if (!attr) {
+      RDV_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&winograd3x3_pipe_kernel<1>),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, WgPipeLds<1>::kBytes));
+      RDV_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&winograd3x3_pipe_kernel<2>),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, WgPipeLds<2>::kBytes));
+      attr = true;
+    }
     const int64_t strips = int64_t(d.batch) * a.seg;
-    const int64_t target = std::max<int64_t>(1, 2 * di.cu_count / slices);  // two blocks per CU
+    const int64_t target = std::max<int64_t>(1, di.cu_count / slices);
     const int64_t per_strip = std::max<int64_t>(1, target / strips);
     a.rows_per_item = int((a.th + per_strip - 1) / per_strip);
     a.chunks = (a.th + a.rows_per_item - 1) / a.rows_per_item;
     a.items = strips * a.chunks;
-    const int64_t blocks = std::min<int64_t>(a.items, std::max<int64_t>(target, 1));
-    const dim3 grid(static_cast<unsigned>(blocks), static_cast<unsigned>(slices)), block(256);
-    if (d.cin <= 32) winograd3x3_strip_kernel<1><<<grid, block, 0, stream>>>(a);
-    else winograd3x3_strip_kernel<2><<<grid, block, 0, stream>>>(a);
+    const int64_t blocks = std::min<int64_t>(a.items, target);
+    const dim3 grid(static_cast<unsigned>(blocks), static_cast<unsigned>(slices)), block(512);
+    if (d.cin <= 32) winograd3x3_pipe_kernel<1><<<grid, block, WgPipeLds<1>::kBytes, stream>>>(a);
+    else winograd3x3_pipe_kernel<2><<<grid, block, WgPipeLds<2>::kBytes, stream>>>(a);
     RDV_HIP_TRY(hipGetLastError());
     return RDV_OK;
   }
