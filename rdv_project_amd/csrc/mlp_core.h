@@ -126,6 +126,40 @@ __device__ __forceinline__ void load_bias(f32x16 (&acc)[N::kMaxMT], const float*
   }
 }
 
+// Copies the chain's A fragments and biases into LDS (fragment f at sw[64 f ..],
+// bias b at sb[b], the compact order of Net::frag_base / bias_base).  The
+// fragments are one contiguous region from frag_off[0] (every layer's block is
+// a multiple of 1 KiB, so the 256-byte alignment adds no gaps).  Every global
+// load is issued before the first LDS write, so the copy costs one memory
+// latency rather than one per layer and array.
+template <class N, int THREADS>
+__device__ __forceinline__ void stage_net_weights(const uint8_t* packed, const MlpLayout& lay, float* sb, half8* sw) {
+  static_assert(N::kBias <= THREADS, "one bias per thread");
+  constexpr int kF = N::kFrags * 64;
+  constexpr int kFPer = (kF + THREADS - 1) / THREADS;
+  const int tid = int(threadIdx.x);
+  const half8* fsrc = reinterpret_cast<const half8*>(packed + lay.frag_off[0]);
+  half8 f[kFPer];
+#pragma unroll
+  for (int k = 0; k < kFPer; ++k) {
+    const int i = k * THREADS + tid;
+    f[k] = fsrc[i < kF ? i : kF - 1];
+  }
+  // bias element tid of layer l lives at bias_off[l] + 4 (tid - bias_base(l))
+  int64_t boff = lay.bias_off[0];
+#pragma unroll
+  for (int q = 1; q < N::kL; ++q)
+    if (tid >= N::bias_base(q)) boff = lay.bias_off[q] - 4 * int64_t(N::bias_base(q));
+  const int bi = tid < N::kBias ? tid : 0;
+  const float b = *reinterpret_cast<const float*>(packed + (tid < N::kBias ? boff : lay.bias_off[0]) + 4 * int64_t(bi));
+#pragma unroll
+  for (int k = 0; k < kFPer; ++k) {
+    const int i = k * THREADS + tid;
+    if (i < kF) sw[i] = f[k];
+  }
+  if (tid < N::kBias) sb[tid] = b;
+}
+
 // A wave's view of the block's LDS copy of the A fragments: fragment f is a
 // conflict-free 1 KiB line, one ds_read_b128 per lane, read right before its MFMA.
 struct LdsWeights {

@@ -91,13 +91,7 @@ __global__ __launch_bounds__(kThreads2, 1) void mlp_fused_f16_kernel(FusedArgs a
   float r0[2][D];
   load_tile(cur, r0);
 
-#pragma unroll
-  for (int l = 0; l < N::kL; ++l) {
-    const float* src = reinterpret_cast<const float*>(a.packed + a.lay.bias_off[l]);
-    for (int i = threadIdx.x; i < 32 * N::mt(l); i += kThreads2) sb[N::bias_base(l) + i] = src[i];
-    const half8* fsrc = reinterpret_cast<const half8*>(a.packed + a.lay.frag_off[l]);
-    for (int i = threadIdx.x; i < N::kc(l) * N::mt(l) * 64; i += kThreads2) sw[N::frag_base(l) * 64 + i] = fsrc[i];
-  }
+  stage_net_weights<N, kThreads2>(a.packed, a.lay, sb, sw);
   if (threadIdx.x == 0) s_next = kWaves2;
   __syncthreads();
 

@@ -156,17 +156,11 @@ constexpr int kRenderThreads = 64 * kRenderWaves;
 constexpr int kEaWaves = 12;
 constexpr int kEaThreads = 64 * kEaWaves;
 
-// Weights and biases of the packed MLP into LDS (block-wide), counter reset.
-template <class N>
+// Weights and biases of the packed MLP into LDS (block of THREADS threads), counter reset.
+template <class N, int THREADS>
 __device__ __forceinline__ void stage_weights(const uint8_t* packed, const MlpLayout& lay, float* sb, half8* sw,
                                               int* s_next) {
-#pragma unroll
-  for (int l = 0; l < N::kL; ++l) {
-    const float* src = reinterpret_cast<const float*>(packed + lay.bias_off[l]);
-    for (int i = threadIdx.x; i < 32 * N::mt(l); i += blockDim.x) sb[N::bias_base(l) + i] = src[i];
-    const half8* fsrc = reinterpret_cast<const half8*>(packed + lay.frag_off[l]);
-    for (int i = threadIdx.x; i < N::kc(l) * N::mt(l) * 64; i += blockDim.x) sw[N::frag_base(l) * 64 + i] = fsrc[i];
-  }
+  stage_net_weights<N, THREADS>(packed, lay, sb, sw);
   if (threadIdx.x == 0) *s_next = 0;
   __syncthreads();
 }
@@ -194,7 +188,7 @@ __global__ __launch_bounds__(kEaThreads, 1) void render_ea_kernel(RenderArgs a) 
   const int64_t r_end = r_begin + per_block < nrays ? r_begin + per_block : nrays;
   const int nr = int(r_end > r_begin ? r_end - r_begin : 0);
   const bool has_bias = (reinterpret_cast<const MlpPackHeader*>(a.packed)->flags & kMlpHasBias) != 0;
-  stage_weights<N>(a.packed, a.lay, sb, sw, &s_next);
+  stage_weights<N, kEaThreads>(a.packed, a.lay, sb, sw, &s_next);
 
   auto claim = [&]() {
     int t = 0;
@@ -414,7 +408,7 @@ __global__ __launch_bounds__(kRenderThreads, 1) void raymarch_transmittance_kern
   const int64_t r_end = r_begin + per_block < a.nrays ? r_begin + per_block : a.nrays;
   const int nr = int(r_end > r_begin ? r_end - r_begin : 0);
   const bool has_bias = (reinterpret_cast<const MlpPackHeader*>(a.packed)->flags & kMlpHasBias) != 0;
-  stage_weights<N>(a.packed, a.lay, sb, sw, &s_next);
+  stage_weights<N, kRenderThreads>(a.packed, a.lay, sb, sw, &s_next);
   float L[9];
   inverse3(a.M, L);
 
