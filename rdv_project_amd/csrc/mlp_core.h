@@ -126,38 +126,52 @@ __device__ __forceinline__ void load_bias(f32x16 (&acc)[N::kMaxMT], const float*
   }
 }
 
-// Copies the chain's A fragments and biases into LDS (fragment f at sw[64 f ..],
-// bias b at sb[b], the compact order of Net::frag_base / bias_base).  The
-// fragments are one contiguous region from frag_off[0] (every layer's block is
-// a multiple of 1 KiB, so the 256-byte alignment adds no gaps).  Every global
-// load is issued before the first LDS write, so the copy costs one memory
-// latency rather than one per layer and array.
-template <class N, int THREADS>
-__device__ __forceinline__ void stage_net_weights(const uint8_t* packed, const MlpLayout& lay, float* sb, half8* sw) {
-  static_assert(N::kBias <= THREADS, "one bias per thread");
+// Copies the A fragments and biases of layers l0 .. l0 + N::kL - 1 into LDS
+// (fragment f at sw[64 f ..], bias b at sb[b], the compact order of
+// Net::frag_base / bias_base).  The fragments are one contiguous region from
+// frag_off[l0] (every layer's block is a multiple of 1 KiB, so the 256-byte
+// alignment adds no gaps).  Global loads go out BATCH per thread before their
+// LDS writes (all of them by default), so the copy costs a memory latency per
+// batch rather than one per layer and array.
+template <class N, int THREADS, int BATCH = (N::kFrags * 64 + THREADS - 1) / THREADS>
+__device__ __forceinline__ void stage_net_weights(const uint8_t* packed, const MlpLayout& lay, float* sb, half8* sw,
+                                                  int l0 = 0) {
   constexpr int kF = N::kFrags * 64;
   constexpr int kFPer = (kF + THREADS - 1) / THREADS;
+  constexpr int kBPer = (N::kBias + THREADS - 1) / THREADS;
   const int tid = int(threadIdx.x);
-  const half8* fsrc = reinterpret_cast<const half8*>(packed + lay.frag_off[0]);
-  half8 f[kFPer];
+  // biases: element i of layer q lives at bias_off[l0 + q] + 4 (i - bias_base(q))
+  float b[kBPer];
 #pragma unroll
-  for (int k = 0; k < kFPer; ++k) {
-    const int i = k * THREADS + tid;
-    f[k] = fsrc[i < kF ? i : kF - 1];
+  for (int k = 0; k < kBPer; ++k) {
+    const int i0 = k * THREADS + tid;
+    const int i = i0 < N::kBias ? i0 : N::kBias - 1;
+    int64_t off = lay.bias_off[l0];
+#pragma unroll
+    for (int q = 1; q < N::kL; ++q)
+      if (i >= N::bias_base(q)) off = lay.bias_off[l0 + q] - 4 * int64_t(N::bias_base(q));
+    b[k] = *reinterpret_cast<const float*>(packed + off + 4 * int64_t(i));
   }
-  // bias element tid of layer l lives at bias_off[l] + 4 (tid - bias_base(l))
-  int64_t boff = lay.bias_off[0];
+  const half8* fsrc = reinterpret_cast<const half8*>(packed + lay.frag_off[l0]);
 #pragma unroll
-  for (int q = 1; q < N::kL; ++q)
-    if (tid >= N::bias_base(q)) boff = lay.bias_off[q] - 4 * int64_t(N::bias_base(q));
-  const int bi = tid < N::kBias ? tid : 0;
-  const float b = *reinterpret_cast<const float*>(packed + (tid < N::kBias ? boff : lay.bias_off[0]) + 4 * int64_t(bi));
+  for (int k0 = 0; k0 < kFPer; k0 += BATCH) {
+    half8 f[BATCH];
 #pragma unroll
-  for (int k = 0; k < kFPer; ++k) {
-    const int i = k * THREADS + tid;
-    if (i < kF) sw[i] = f[k];
+    for (int k = 0; k < BATCH; ++k) {
+      const int i = (k0 + k) * THREADS + tid;
+      if (k0 + k < kFPer) f[k] = fsrc[i < kF ? i : kF - 1];
+    }
+#pragma unroll
+    for (int k = 0; k < BATCH; ++k) {
+      const int i = (k0 + k) * THREADS + tid;
+      if (k0 + k < kFPer && i < kF) sw[i] = f[k];
+    }
   }
-  if (tid < N::kBias) sb[tid] = b;
+#pragma unroll
+  for (int k = 0; k < kBPer; ++k) {
+    const int i = k * THREADS + tid;
+    if (i < N::kBias) sb[i] = b[k];
+  }
 }
 
 // A wave's view of the block's LDS copy of the A fragments: fragment f is a

@@ -326,14 +326,9 @@ __global__ __launch_bounds__(kTfThreads, 1) void train_fwd_pair_kernel(TrainFwdA
     load_in(2 * pt, bA);
     load_in(2 * pt + 1, bB);
   }
-  // stage the group's fragments and biases (biases compacted to Net's bias_base)
-#pragma unroll
-  for (int l = 0; l < L; ++l) {
-    const half8* fsrc = reinterpret_cast<const half8*>(a.packed + a.lay.frag_off[a.l0 + l]);
-    for (int i = threadIdx.x; i < N::kc(l) * N::mt(l) * 64; i += kTfThreads) sw[N::frag_base(l) * 64 + i] = fsrc[i];
-    const float* bsrc = reinterpret_cast<const float*>(a.packed + a.lay.bias_off[a.l0 + l]);
-    for (int i = threadIdx.x; i < 32 * N::mt(l); i += kTfThreads) sb[N::bias_base(l) + i] = bsrc[i];
-  }
+  // stage the group's fragments and biases (biases compacted to Net's bias_base),
+  // eight 16-byte loads per thread in flight at a time
+  stage_net_weights<N, kTfThreads, 8>(a.packed, a.lay, sb, sw, a.l0);
   __syncthreads();
 
   // narrow inputs (KC0 <= 4) are loaded a whole iteration ahead into spare
