@@ -206,11 +206,24 @@ __device__ __forceinline__ void wg_gemm_store(const half8 (&u)[16][KC], const ha
   }
 }
 
-// The four biases of this lane's output channels 16 g + 4 (lane / 16) + 0..3.
+// 16 zero bytes: the source of every load that falls outside the operands.
+__device__ __attribute__((aligned(16))) uint32_t g_wg_zero16[4] = {0u, 0u, 0u, 0u};
+
+// The four biases of this lane's output channels 16 g + 4 (lane / 16) + 0..3
+// (zero past cout or without a bias).  The loads are unconditional (clamped
+// index, the zero block for a null bias), so no wait is forced on loads issued
+// before them.
 __device__ __forceinline__ f32x4 wg_lane_bias(const WinogradArgs& a, int g, int lane) {
   const int co0 = 16 * g + 4 * (lane >> 4);
-  f32x4 b = {0.0f, 0.0f, 0.0f, 0.0f};
-  if (a.bias && co0 < a.cout) b = *reinterpret_cast<const f32x4*>(a.bias + co0);
+  const float* src = a.bias ? a.bias : reinterpret_cast<const float*>(g_wg_zero16);
+  const int last = a.bias ? a.cout - 1 : 0;
+  f32x4 b;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int c = co0 + j;
+    const float v = src[c < last ? c : last];
+    b[j] = c < a.cout ? v : 0.0f;
+  }
   return b;
 }
 
@@ -378,7 +391,6 @@ __global__ __launch_bounds__(256, 2) void winograd3x3_kernel(WinogradArgs a) {
 // stores retire in order on gfx9).
 constexpr int kRowBytes = 96;                  // 48 fp16 columns per staged channel row
 
-__device__ __attribute__((aligned(16))) uint32_t g_wg_zero16[4] = {0u, 0u, 0u, 0u};
 
 // 16-byte global -> LDS DMA for this lane; lds_wave is the wave's LDS base
 // (lane l lands at lds_wave + 16 l).  M0 is saved and restored around it.
@@ -428,6 +440,109 @@ __device__ __forceinline__ void wg_wait_vmcnt(int n) {
       asm volatile("s_waitcnt vmcnt(63)" ::: "memory");
       break;
   }
+}
+
+// f(integral_constant<int, I>) for I = 0 .. N-1, in order, at compile time.
+template <class F, int... I>
+__device__ __forceinline__ void wg_static_for(std::integer_sequence<int, I...>, F&& f) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+
+// LDS reads issued from inline assembly, so the compiler neither sinks them to
+// their use nor waits for them itself: the role that issues them waits with
+// s_waitcnt lgkmcnt and names the registers it completes (no use of them can
+// be scheduled above the wait).  That role issues no other LDS read, and keeps
+// at most 15 in flight (the counter's range).
+template <int OFF>
+__device__ __forceinline__ uint32_t wg_lds_u32(uint32_t addr) {
+  uint32_t v;
+  asm volatile("ds_read_b32 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF));
+  return v;
+}
+template <int OFF>
+__device__ __forceinline__ half8 wg_lds_frag(uint32_t addr) {
+  half8 v;
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF));
+  return v;
+}
+template <int N>
+__device__ __forceinline__ void wg_lds_wait(uint32_t (&w)[4][3]) {
+  asm volatile("s_waitcnt lgkmcnt(%12)"
+               : "+v"(w[0][0]), "+v"(w[0][1]), "+v"(w[0][2]), "+v"(w[1][0]), "+v"(w[1][1]), "+v"(w[1][2]),
+                 "+v"(w[2][0]), "+v"(w[2][1]), "+v"(w[2][2]), "+v"(w[3][0]), "+v"(w[3][1]), "+v"(w[3][2])
+               : "i"(N)
+               : "memory");
+}
+template <int N, int KC>
+__device__ __forceinline__ void wg_lds_wait(half8 (&f)[2][KC]) {
+  if constexpr (KC == 2)
+    asm volatile("s_waitcnt lgkmcnt(%4)" : "+v"(f[0][0]), "+v"(f[0][1]), "+v"(f[1][0]), "+v"(f[1][1]) : "i"(N) : "memory");
+  else
+    asm volatile("s_waitcnt lgkmcnt(%2)" : "+v"(f[0][0]), "+v"(f[1][0]) : "i"(N) : "memory");
+}
+
+// wg_gemm for the pipelined kernel: the same products and inverse transform in
+// the same order, with the V fragments read two groups ahead of their use (a
+// group: column b = G / 2 of the 4 x 4 domain, rows 2 (G % 2) + 0..1, every kc).
+template <int KC>
+__device__ __forceinline__ void wg_gemm_pipe(const half8 (&u)[16][KC], const half8* sv, int lane, f32x4 (&yv)[2][2]) {
+  const uint32_t addr = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(sv + lane));
+  half8 fr[3][2][KC];
+  f32x4 y00, y01, y10, y11, ma[4];
+  auto issue = [&](auto gc) {
+    constexpr int G = decltype(gc)::value, b = G / 2, ra0 = 2 * (G % 2);
+    half8(&f)[2][KC] = fr[G % 3];
+    wg_static_for(std::make_integer_sequence<int, 2 * KC>{}, [&](auto ic) {
+      constexpr int r = decltype(ic)::value / KC, kc = decltype(ic)::value % KC;
+      f[r][kc] = wg_lds_frag<((4 * (ra0 + r) + b) * KC + kc) * 1024>(addr);
+    });
+  };
+  issue(std::integral_constant<int, 0>{});
+  issue(std::integral_constant<int, 1>{});
+  wg_static_for(std::make_integer_sequence<int, 8>{}, [&](auto gc) {
+    constexpr int G = decltype(gc)::value, b = G / 2, ra0 = 2 * (G % 2);
+    if constexpr (G + 2 < 8) {
+      issue(std::integral_constant<int, G + 2>{});
+      wg_lds_wait<4 * KC, KC>(fr[G % 3]);
+    } else if constexpr (G + 1 < 8) {
+      wg_lds_wait<2 * KC, KC>(fr[G % 3]);
+    } else {
+      wg_lds_wait<0, KC>(fr[G % 3]);
+    }
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      f32x4 acc = {};
+#pragma unroll
+      for (int kc = 0; kc < KC; ++kc)
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(u[4 * (ra0 + r) + b][kc], fr[G % 3][r][kc], acc, 0, 0, 0);
+      ma[ra0 + r] = acc;
+    }
+    if constexpr (G % 2 == 1) {
+      const f32x4 t0 = ma[0] + ma[1] + ma[2];
+      const f32x4 t1 = ma[1] - ma[2] - ma[3];
+      if constexpr (b == 0) {
+        y00 = t0;
+        y10 = t1;
+      } else if constexpr (b == 1) {
+        y00 += t0;
+        y01 = t0;
+        y10 += t1;
+        y11 = t1;
+      } else if constexpr (b == 2) {
+        y00 += t0;
+        y01 -= t0;
+        y10 += t1;
+        y11 -= t1;
+      } else {
+        y01 -= t0;
+        y11 -= t1;
+      }
+    }
+  });
+  yv[0][0] = y00;
+  yv[0][1] = y01;
+  yv[1][0] = y10;
+  yv[1][1] = y11;
 }
 
 // Stores of one tile's 2x2 outputs for this lane's 4 channels (after bias /
@@ -553,19 +668,34 @@ __global__ __launch_bounds__(512, 1) void winograd3x3_pipe_kernel(WinogradArgs a
           // ---- V = B^T d B of tile row s (pairs s, s + 1) per (tile, 4 channels)
           if (qd < CH / 4) {
             const int sa = s % kPipeSlots, sb = (s + 1) % kPipeSlots;
+            // columns 2n-1 .. 2n+2 of the tile = halves 2n+7 .. 2n+10 of a staged
+            // row = dwords n+3 .. n+5; input rows 0, 1 in slot sa, rows 2, 3 in sb.
+            // Read i (0..47) is dword i % 3 of row (i % 12) / 3 of channel i / 12.
+            // 15 go out first; once channel c's 12 have landed, the reads up to
+            // 15 past them are issued, and channel c is transformed under them.
+            const uint32_t at = ring_lds + uint32_t(4 * qd * kRowBytes + 4 * (n + 3));
+            const uint32_t base0 = at + uint32_t(sa * kSlotBytes), base1 = at + uint32_t(sb * kSlotBytes);
+            uint32_t wv[4][4][3];
+            auto reads = [&](auto lo, auto hi) {
+              constexpr int L = decltype(lo)::value, H = decltype(hi)::value;
+              wg_static_for(std::make_integer_sequence<int, H - L>{}, [&](auto ii) {
+                constexpr int i = L + decltype(ii)::value, c = i / 12, dr = (i % 12) / 3, k = i % 3;
+                wv[c][dr][k] = wg_lds_u32<((dr & 1) * CH + c) * kRowBytes + 4 * k>(dr < 2 ? base0 : base1);
+              });
+            };
+            reads(std::integral_constant<int, 0>{}, std::integral_constant<int, 15>{});
             half4 hv[16];
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-              const int ci = 4 * qd + c;
+            wg_static_for(std::make_integer_sequence<int, 4>{}, [&](auto cc) {
+              constexpr int c = decltype(cc)::value;
+              wg_lds_wait<c < 3 ? 3 : 0>(wv[c]);
+              if constexpr (c < 3)
+                reads(std::integral_constant<int, 15 + 12 * c>{}, std::integral_constant<int, (27 + 12 * c < 48 ? 27 + 12 * c : 48)>{});
               float d[4][4];
 #pragma unroll
               for (int dr = 0; dr < 4; ++dr) {
-                const uint32_t* row = ring + ((dr < 2 ? sa : sb) * kSlotBytes + ((dr & 1) * CH + ci) * kRowBytes) / 4;
-                // columns 2n-1 .. 2n+2 of the tile = halves 2n+7 .. 2n+10 of the staged row
-                const uint32_t w0 = row[n + 3], w1 = row[n + 4], w2 = row[n + 5];
-                const half2v h0 = __builtin_bit_cast(half2v, w0);
-                const half2v h1 = __builtin_bit_cast(half2v, w1);
-                const half2v h2 = __builtin_bit_cast(half2v, w2);
+                const half2v h0 = __builtin_bit_cast(half2v, wv[c][dr][0]);
+                const half2v h1 = __builtin_bit_cast(half2v, wv[c][dr][1]);
+                const half2v h2 = __builtin_bit_cast(half2v, wv[c][dr][2]);
                 d[dr][0] = float(h0[1]);
                 d[dr][1] = float(h1[0]);
                 d[dr][2] = float(h1[1]);
@@ -593,7 +723,7 @@ __global__ __launch_bounds__(512, 1) void winograd3x3_pipe_kernel(WinogradArgs a
                   hv[4 * r + b][c] = half_t(v);
                 }
               }
-            }
+            });
             half8* sv = svb + (s & 1) * LD::kSvHalf8;
             const int ci0 = 4 * qd;
             const int kc = ci0 / 32, k = ci0 % 32;
@@ -616,6 +746,11 @@ __global__ __launch_bounds__(512, 1) void winograd3x3_pipe_kernel(WinogradArgs a
   // ================= GEMM role: wave w owns output channels 16 (4 blockIdx.y + w) + 0..15
   const int g = blockIdx.y * 4 + w;
   const bool active = 16 * g < a.cout;
+  // U's loads are issued after the first item's first barrier (its first pairs
+  // landed), so the input role's DMAs go first, and they run under the input
+  // role's V of tile row 0, which needs no U; the wait for them follows step 0
+  const bool any = int64_t(blockIdx.x) < a.items;
+  if (any) __syncthreads();
   half8 u[16][KC];
   const int g_n = (a.cout + 15) / 16;
   const int gu = active ? g : 0;
@@ -625,6 +760,7 @@ __global__ __launch_bounds__(512, 1) void winograd3x3_pipe_kernel(WinogradArgs a
     for (int kc = 0; kc < KC; ++kc)
       u[p][kc] = reinterpret_cast<const half8*>(a.U)[((int64_t(p) * KC + kc) * g_n + gu) * 64 + lane];
   const f32x4 bias = wg_lane_bias(a, gu, lane);
+  if (any) __syncthreads();  // end of the first item's step 0
 #pragma unroll
   for (int p = 0; p < 16; ++p)
 #pragma unroll
@@ -635,12 +771,13 @@ __global__ __launch_bounds__(512, 1) void winograd3x3_pipe_kernel(WinogradArgs a
     int img, seg, tr0;
     decode(item, img, seg, tr0);
     const int R = min(a.rows_per_item, a.th - tr0);
-    __syncthreads();  // the input role's first two pairs
-    for (int s = 0; s <= R; ++s) {
+    const int s0 = item == blockIdx.x ? 1 : 0;  // the first item's step 0 barriers are above
+    if (s0 == 0) __syncthreads();               // the input role's first two pairs
+    for (int s = s0; s <= R; ++s) {
       if (s >= 1 && active) {
         const int tr = tr0 + s - 1;
         f32x4 yv[2][2];
-        wg_gemm(u, svb + ((s - 1) & 1) * LD::kSvHalf8, lane, yv);
+        wg_gemm_pipe(u, svb + ((s - 1) & 1) * LD::kSvHalf8, lane, yv);
         const int n = lane & 15;
         const int tc = seg * kWgTiles + n;
         const int co0 = 16 * g + 4 * (lane >> 4);
