@@ -545,6 +545,23 @@ __device__ __forceinline__ void wg_gemm_pipe(const half8 (&u)[16][KC], const hal
   yv[1][1] = y11;
 }
 
+// 4 x 4 transpose of 32-bit elements within each quad of lanes: lane k (lane %
+// 4) ends with element k of quad lanes 0..3, in that order.  Two exchange stages
+// through DPP quad permutes (partner lane k ^ 1, then k ^ 2).
+__device__ __forceinline__ void wg_quad_transpose(uint32_t (&e)[4], int k) {
+  uint32_t t[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const uint32_t x = __builtin_amdgcn_update_dpp(0u, e[c ^ 1], 0xB1, 0xF, 0xF, true);  // quad_perm 1,0,3,2
+    t[c] = ((c ^ k) & 1) ? x : e[c];
+  }
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const uint32_t x = __builtin_amdgcn_update_dpp(0u, t[c ^ 2], 0x4E, 0xF, 0xF, true);  // quad_perm 2,3,0,1
+    e[c] = ((c ^ k) & 2) ? x : t[c];
+  }
+}
+
 // Stores of one tile's 2x2 outputs for this lane's 4 channels (after bias /
 // ReLU) through wg_st*: CHW issues 8 instructions, HWC 4.
 __device__ __forceinline__ void wg_store_asm(const f32x4 (&yv)[2][2], const WinogradArgs& a, int img, int co0,
@@ -791,7 +808,30 @@ __global__ __launch_bounds__(512, 1) void winograd3x3_pipe_kernel(WinogradArgs a
               if (a.relu) val = fmaxf(val, 0.0f);
               yv[i][jx][jj] = val;
             }
-        if (tc < a.W / 2) wg_store_asm(yv, a, img, co0, 2 * tr, 2 * tc);
+        if (a.out_layout == RDV_LAYOUT_CHW && a.out_dtype == RDV_DTYPE_F16) {
+          // lane 4q + k of the 16 tile lanes takes channel co0 + k of tiles 4q .. 4q+3
+          // (8 consecutive fp16 columns of each output row): two 16-byte stores
+          // instead of eight 4-byte ones.  W % 8 == 0, so a quad's tiles are all
+          // inside the image or all outside.
+          uint32_t r0[4], r1[4];
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj) {
+            r0[jj] = __builtin_bit_cast(uint32_t, half2v{half_t(yv[0][0][jj]), half_t(yv[0][1][jj])});
+            r1[jj] = __builtin_bit_cast(uint32_t, half2v{half_t(yv[1][0][jj]), half_t(yv[1][1][jj])});
+          }
+          const int k = lane & 3;
+          wg_quad_transpose(r0, k);
+          wg_quad_transpose(r1, k);
+          const int tq = tc - k;  // the quad's first tile
+          if (tq < a.W / 2) {
+            half_t* dst = static_cast<half_t*>(a.y) + (int64_t(img) * a.cout + co0 + k) * (int64_t(a.H) * a.W) +
+                          int64_t(2 * tr) * a.W + 2 * tq;
+            wg_st128(dst, __builtin_bit_cast(f32x4, r0));
+            wg_st128(dst + a.W, __builtin_bit_cast(f32x4, r1));
+          }
+        } else if (tc < a.W / 2) {
+          wg_store_asm(yv, a, img, co0, 2 * tr, 2 * tc);
+        }
       }
       __syncthreads();
     }
