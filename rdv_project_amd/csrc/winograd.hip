@@ -545,6 +545,24 @@ __device__ __forceinline__ void wg_gemm_pipe(const half8 (&u)[16][KC], const hal
   yv[1][1] = y11;
 }
 
+// x +/- y for two fp16 operands, each the high (HI) or low half of its dword, in
+// one v_fma_mix_f32 (x * 1.0 +/- y, the operands widened exactly, one fp32
+// rounding): the value of converting both to fp32 and adding, without the two
+// conversions.
+template <int HI, bool SUB>
+__device__ __forceinline__ float wg_mix(uint32_t x, uint32_t y) {
+  float r;
+  if constexpr (HI && SUB)
+    asm("v_fma_mix_f32 %0, %1, 1.0, -%2 op_sel:[1,0,1] op_sel_hi:[1,0,1]" : "=v"(r) : "v"(x), "v"(y));
+  else if constexpr (HI)
+    asm("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel:[1,0,1] op_sel_hi:[1,0,1]" : "=v"(r) : "v"(x), "v"(y));
+  else if constexpr (SUB)
+    asm("v_fma_mix_f32 %0, %1, 1.0, -%2 op_sel_hi:[1,0,1]" : "=v"(r) : "v"(x), "v"(y));
+  else
+    asm("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel_hi:[1,0,1]" : "=v"(r) : "v"(x), "v"(y));
+  return r;
+}
+
 // 4 x 4 transpose of 32-bit elements within each quad of lanes: lane k (lane %
 // 4) ends with element k of quad lanes 0..3, in that order.  Two exchange stages
 // through DPP quad permutes (partner lane k ^ 1, then k ^ 2).
@@ -707,25 +725,17 @@ __global__ __launch_bounds__(512, 1) void winograd3x3_pipe_kernel(WinogradArgs a
               wg_lds_wait<c < 3 ? 3 : 0>(wv[c]);
               if constexpr (c < 3)
                 reads(std::integral_constant<int, 15 + 12 * c>{}, std::integral_constant<int, (27 + 12 * c < 48 ? 27 + 12 * c : 48)>{});
-              float d[4][4];
-#pragma unroll
-              for (int dr = 0; dr < 4; ++dr) {
-                const half2v h0 = __builtin_bit_cast(half2v, wv[c][dr][0]);
-                const half2v h1 = __builtin_bit_cast(half2v, wv[c][dr][1]);
-                const half2v h2 = __builtin_bit_cast(half2v, wv[c][dr][2]);
-                d[dr][0] = float(h0[1]);
-                d[dr][1] = float(h1[0]);
-                d[dr][2] = float(h1[1]);
-                d[dr][3] = float(h2[0]);
-              }
+              // m = B^T d, in fp32 from the fp16 inputs: d[dr][cj] is the high half
+              // of dword 0 (cj = 0), the low / high half of dword 1 (cj = 1, 2) or
+              // the low half of dword 2 (cj = 3) of row dr
               float m[4][4];
-#pragma unroll
-              for (int cj = 0; cj < 4; ++cj) {
-                m[0][cj] = d[0][cj] - d[2][cj];
-                m[1][cj] = d[1][cj] + d[2][cj];
-                m[2][cj] = d[2][cj] - d[1][cj];
-                m[3][cj] = d[1][cj] - d[3][cj];
-              }
+              wg_static_for(std::make_integer_sequence<int, 4>{}, [&](auto jc) {
+                constexpr int cj = decltype(jc)::value, wd = (cj + 1) / 2, hi = (cj + 1) % 2;
+                m[0][cj] = wg_mix<hi, true>(wv[c][0][wd], wv[c][2][wd]);   // d0 - d2
+                m[1][cj] = wg_mix<hi, false>(wv[c][1][wd], wv[c][2][wd]);  // d1 + d2
+                m[2][cj] = wg_mix<hi, true>(wv[c][2][wd], wv[c][1][wd]);   // d2 - d1
+                m[3][cj] = wg_mix<hi, true>(wv[c][1][wd], wv[c][3][wd]);   // d1 - d3
+              });
 #pragma unroll
               for (int r = 0; r < 4; ++r) {
                 float vv[4];
