@@ -170,12 +170,14 @@ def test_shapes_layouts_and_types(N, H, W, C, K, inl, ind, outl, outd, relu, bia
     (3, 6, 72, 40, 112, _lib.LAYOUT_HWC, _lib.DTYPE_F16, True),
     (1, 34, 24, 64, 80, _lib.LAYOUT_HWC, _lib.DTYPE_F32, False),
     (1, 130, 16, 32, 64, _lib.LAYOUT_CHW, _lib.DTYPE_F16, False),
+    (20, 4, 512, 64, 64, _lib.LAYOUT_CHW, _lib.DTYPE_F16, True),
 ])
 def test_pipelined_path_nchw_f16(N, H, W, C, K, outl, outd, relu):
     """NCHW fp16 input with W % 8 == 0 (winograd3x3_pipe_kernel, the path of the
     benchmark configuration): partial strips, several images, one-row items,
     channel padding (CIN <= 32 and <= 64), several 64-channel output slices,
-    every output form."""
+    every output form, and more strips than CUs (320 for 20 images of width
+    512), so blocks walk a second work item."""
     rng = np.random.default_rng(N * 131 + H * 17 + W + C + K)
     x = O.f16(rng.uniform(-1, 1, (N, H, W, C)).astype(np.float32))
     w = rng.normal(0, 0.1, (3, 3, C, K)).astype(np.float32)
