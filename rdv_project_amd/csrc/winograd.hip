@@ -666,6 +666,9 @@ __global__ __launch_bounds__(512, 1) void winograd3x3_pipe_kernel(WinogradArgs a
 
   if (role == 1) {
     // ================= input role
+    // the input role issues first where both roles are ready (measured 2-4% faster
+    // than equal priority, and than the GEMM role first)
+    __builtin_amdgcn_s_setprio(3);
     const uint32_t ring_lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(ring));
     int Ld = 0;  // this wave's DMA instructions per pair
 #pragma unroll
