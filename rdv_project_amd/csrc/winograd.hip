@@ -622,14 +622,16 @@ __device__ __forceinline__ void wg_store_asm(const f32x4 (&yv)[2][2], const Wino
 // while the previous row's GEMMs and stores run:
 //   waves 4-7 (input role): row pairs into a 4-slot ring by DMA (3 pairs
 //     ahead), then V of tile row s into sv buffer s % 2;
-//   waves 0-3 (GEMM role): U resident in registers; the GEMMs, inverse
-//     transform and stores of tile row s - 1 from sv buffer (s - 1) % 2.
+//   waves 0-3 (GEMM role): U in registers (its loads run under the first V
+//     transform); the GEMMs, inverse transform and stores of tile row s - 1
+//     from sv buffer (s - 1) % 2.
 // Step s = 0 .. R ends with one barrier.  Each role's vector-memory stream is
 // its own (DMAs only; U's loads then stores only), so the input role's waits
 // count its DMA instructions alone.  The V transform is one (tile, 4-channel)
-// unit per input-role thread: 4 x 4 patch reads from the ring (fp16 -> fp32),
-// the reference's fp32 operation order, fp16 rounding, and 16 8-byte writes in
-// B-fragment order.
+// unit per input-role thread: 4 x 4 fp16 patch reads from the ring, the
+// reference's fp32 operation order (the first stage widens the fp16 inputs
+// inside v_fma_mix_f32), fp16 rounding, and 16 8-byte writes in B-fragment
+// order.
 constexpr int kPipeSlots = 4;
 template <int KC>
 struct WgPipeLds {
