@@ -1,7 +1,7 @@
 """Oracle for the MLP training step (forward, MSE, backward) — TEST
 INFRASTRUCTURE ONLY (see oracle/__init__.py).
 
-Build-defined (the reference has no backward pass).  The forward
+Build-defined (the reference has no backward pass for this path).  The forward
 is the LinearFast chain of oracle.mlp (fp16 layer inputs and weights, fp32
 accumulation, fp32 bias, ReLU hidden layers, linear head).  The loss is the mean
 over n x out of (y - t)^2.  The gradients are those of that forward function
