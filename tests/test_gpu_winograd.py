@@ -149,6 +149,7 @@ def test_tensor_op_rejects_reference_invalid_shapes():
     (3, 10, 66, 64, 32, _lib.LAYOUT_HWC, _lib.DTYPE_F16, _lib.LAYOUT_CHW, _lib.DTYPE_F16, True, False),
     (2, 18, 40, 17, 48, _lib.LAYOUT_HWC, _lib.DTYPE_F32, _lib.LAYOUT_HWC, _lib.DTYPE_F16, False, True),
     (1, 64, 32, 32, 272, _lib.LAYOUT_CHW, _lib.DTYPE_F16, _lib.LAYOUT_CHW, _lib.DTYPE_F32, True, True),
+    (1, 8, 48, 64, 64, _lib.LAYOUT_CHW, _lib.DTYPE_F16, _lib.LAYOUT_CHW, _lib.DTYPE_F16, True, False),
 ])
 def test_shapes_layouts_and_types(N, H, W, C, K, inl, ind, outl, outd, relu, bias):
     rng = np.random.default_rng(N * 7919 + H * 31 + W + C + K)
