@@ -202,3 +202,18 @@ def test_c3_full_config():
     _check_close(y, O.winograd_conv(x_hwc, w_rsck, relu=True), "C3 vs oracle", f16_out=True)
     direct = torch.nn.functional.conv2d(x.float(), w.float(), padding=1).clamp_min(0)[0].permute(1, 2, 0).numpy()
     _check_direct(y, direct.astype(np.float64), "C3 vs direct fp32 conv")
+
+
+def test_c3_repeats_are_identical():
+    """Fifty back-to-back calls of the benchmark configuration give the same bits.
+    The pipelined kernel issues its LDS reads and global stores from inline
+    assembly with hand-counted waits; a miscounted wait would read data that is
+    still landing and show here as calls that differ."""
+    x, w, b = WL.c3()
+    conv = rdv.Winograd3x3Conv2d(w.cuda(), b.cuda())
+    xd = x.cuda()
+    ref = conv(xd, relu=True).clone()
+    outs = [conv(xd, relu=True) for _ in range(50)]
+    torch.cuda.synchronize()
+    differ = sum(0 if torch.equal(y, ref) else 1 for y in outs)
+    assert differ == 0, f"{differ} of 50 repeated calls differ from the first"
