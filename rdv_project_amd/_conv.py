@@ -93,6 +93,8 @@ class Winograd3x3Conv2d:
         if out is None:
             out = torch.empty((n, self.out_channels, H, W), dtype=odt, device=x.device)
         else:
+            if not isinstance(out, torch.Tensor) or out.device.type != "cuda" or out.device != x.device:
+                raise TypeError(f"out must be a GPU tensor on {x.device}")
             assert out.is_contiguous() and tuple(out.shape) == (n, self.out_channels, H, W) and out.dtype == odt
         d = conv_desc(n, H, W, cin, self.out_channels, _lib.LAYOUT_CHW, _dtype_code(x, "x"), _lib.LAYOUT_CHW,
                       _dtype_code(out, "out"), relu)

@@ -109,7 +109,13 @@ def composite(sigma_rgb: torch.Tensor, dt: torch.Tensor, out: torch.Tensor | Non
     s = sigma_rgb.to(device=device(), dtype=torch.float32).contiguous()
     d = dt.to(device=device(), dtype=torch.float32).contiguous()
     assert tuple(d.shape) == (n,), "dt must be [n_rays]"
-    out = out if out is not None else torch.empty((n, 3), dtype=torch.float32, device=device())
+    if out is None:
+        out = torch.empty((n, 3), dtype=torch.float32, device=device())
+    else:
+        if not isinstance(out, torch.Tensor) or out.device.type != "cuda":
+            raise TypeError("out must be a GPU tensor")
+        assert out.dtype == torch.float32 and tuple(out.shape) == (n, 3) and out.is_contiguous(), \
+            "out must be a contiguous float32 [n_rays, 3] tensor"
     with launch_scope():
         _lib.check(_lib.load().rdv_composite(C.c_void_p(s.data_ptr()), C.c_void_p(d.data_ptr()), C.c_int64(n),
                                              C.c_int32(S), C.c_void_p(out.data_ptr()),

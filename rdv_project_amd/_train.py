@@ -26,17 +26,44 @@ def _workspace(key, nbytes: int) -> torch.Tensor:
     return buf
 
 
+def _check_grads(grads, layers) -> None:
+    """Caller-supplied gradient buffers must be exactly what the kernels write:
+    one (dW, db) pair per layer, contiguous fp32 GPU tensors of shape [OUT, IN]
+    and [OUT].  Checked before anything is launched."""
+    if not isinstance(grads, (list, tuple)) or len(grads) != len(layers):
+        raise TypeError(f"grads must be a list of {len(layers)} (dW, db) pairs, one per layer")
+    for i, (pair, lay) in enumerate(zip(grads, layers)):
+        if not isinstance(pair, (list, tuple)) or len(pair) != 2:
+            raise TypeError(f"grads[{i}] must be a (dW, db) pair")
+        for t, shape, what in ((pair[0], (lay.OUT, lay.IN), "dW"), (pair[1], (lay.OUT,), "db")):
+            if not isinstance(t, torch.Tensor):
+                raise TypeError(f"grads[{i}] {what} must be a torch tensor")
+            if t.dtype != torch.float32:
+                raise TypeError(f"grads[{i}] {what} must be float32, got {t.dtype}")
+            if tuple(t.shape) != shape:
+                raise TypeError(f"grads[{i}] {what} must have shape {list(shape)}, got {list(t.shape)}")
+            if not t.is_contiguous():
+                raise TypeError(f"grads[{i}] {what} must be contiguous")
+            if t.device.type != "cuda":
+                raise TypeError(f"grads[{i}] {what} must be a GPU tensor, got device {t.device}")
+
+
 def mse_backward(m: Map, x, target, grads=None):
     """Loss and gradients of mean((m(x) - target)^2) with respect to every
     layer's weight and bias.  x: [n, in] (fp16, or fp32 rounded to fp16 as
     LinearFast does), target: [n, out] fp32.  Returns (loss, [(dW, db), ...])
     with fp32 dW [out, in] and db [out] per layer, in chain order; `grads`
-    may supply those output tensors."""
+    may supply those output tensors (contiguous fp32 GPU tensors of exactly
+    those shapes, else TypeError).  The loss tensor is allocated on the first
+    call for a chain and device and reused after that."""
     xt = torch.as_tensor(x)
     tt = torch.as_tensor(target)
     assert xt.dim() == 2 and tt.dim() == 2 and xt.shape[0] == tt.shape[0], "x [n, in] and target [n, out]"
     n = int(xt.shape[0])
     p = _chain.plan_chain(m, int(xt.shape[1]))
+    assert tt.shape[1] == p.out_features, f"target has {tt.shape[1]} columns, the chain outputs {p.out_features}"
+    if grads is not None:
+        _check_grads(grads, p.layers)
     packed = _chain.packed_params(m, p)
     xh = xt.to(device=device(), dtype=torch.float16).contiguous()
     th = tt.to(device=device(), dtype=torch.float32).contiguous()
@@ -48,7 +75,7 @@ def mse_backward(m: Map, x, target, grads=None):
     if grads is None:
         grads = [(torch.empty(l.OUT, l.IN, dtype=torch.float32, device=device()),
                   torch.empty(l.OUT, dtype=torch.float32, device=device())) for l in p.layers]
-    loss = torch.empty((), dtype=torch.float32, device=device())
+    loss = _loss_buffer(m, xh.device)
     dws = _lib.void_ptr_array([g[0].data_ptr() for g in grads])
     dbs = _lib.void_ptr_array([g[1].data_ptr() for g in grads])
     with launch_scope():
@@ -57,3 +84,13 @@ def mse_backward(m: Map, x, target, grads=None):
                                           C.c_int64(ws.numel()), C.c_void_p(loss.data_ptr()), dws, dbs,
                                           C.c_void_p(current_stream_handle())), "mse_backward")
     return loss, grads
+
+
+def _loss_buffer(m: Map, dev) -> torch.Tensor:
+    """The chain's loss scalar, reused across calls (each call overwrites it, as
+    the reference's evaluators reuse their output buffers)."""
+    cached = getattr(m, "_rdv_loss", None)
+    if cached is None or cached.device != dev:
+        cached = torch.empty((), dtype=torch.float32, device=dev)
+        m._rdv_loss = cached
+    return cached

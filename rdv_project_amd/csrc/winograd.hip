@@ -895,7 +895,9 @@ int launch_winograd3x3(const rdv_conv_desc& d, const void* x, const void* U, con
   const int groups16 = (d.cout + 15) / 16;
   const int slices = (groups16 + 3) / 4;  // 64-channel slices (grid y)
   const bool f16 = d.in_dtype == RDV_DTYPE_F16, chw = d.in_layout == RDV_LAYOUT_CHW;
-  if (f16 && chw && d.W % 8 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0) {
+  // the pipelined kernel reads x and writes y with 16-byte vector accesses; other buffers take the strip kernel
+  if (f16 && chw && d.W % 8 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
+      reinterpret_cast<uintptr_t>(y) % 16 == 0) {
     // pipelined kernel: one 8-wave block per CU, each walking rows_per_item tile rows of a strip
     static bool attr = false;
     if (!attr) {

@@ -205,6 +205,27 @@ def test_inplace_weight_update_is_seen():
     _assert_fp16_parity(y2.cpu().numpy(), ref, "updated weights")
 
 
+def test_weight_update_without_version_bump_is_seen():
+    """A write through `.data` (or any alias that torch's version counter does
+    not track) is seen by the next call: the packed block is rebuilt from the
+    weight buffers at every call, as the reference reads its weights through
+    pointers at every dispatch."""
+    x, layers = WL.c1(64)
+    w0 = layers[0][0].cuda()
+    m = rdv.linear(w0, layers[0][1].cuda(), f16=True)
+    for w, b in layers[1:]:
+        m = m >> rdv.relu >> rdv.linear(w.cuda(), b.cuda(), f16=True)
+    y1 = m(x.cuda()).as_tensor("torch").clone()
+    v = w0._version
+    w0.data.mul_(0.25)
+    assert w0._version == v  # the counter did not move
+    y2 = m(x.cuda()).as_tensor("torch").clone()
+    assert not torch.equal(y1, y2)
+    ref = O.mlp_forward(x.numpy(), [(w0.cpu().numpy(), layers[0][1].numpy())] + _np_layers(layers[1:]),
+                        ["relu"] * 4 + ["none"], ["f16"] * 5)
+    _assert_fp16_parity(y2.cpu().numpy(), ref, "weights updated through .data")
+
+
 def test_shape_errors_raise_before_launch():
     x, layers = WL.c1(64)
     m = _chain(layers, ["relu"] * 4 + ["none"])

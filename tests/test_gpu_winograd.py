@@ -189,7 +189,16 @@ def test_pipelined_path_nchw_f16(N, H, W, C, K, outl, outd, relu):
         _check_close(y[i], ref, f"image {i}", f16_out=outd == _lib.DTYPE_F16)
 
 
-def test_c3_full_config():
+@pytest.fixture(scope="module")
+def c3_oracle():
+    """The oracle's C3 output, [H, W, COUT] (computed once for the module)."""
+    x, w, b = WL.c3()
+    x_hwc = x.float().numpy()[0].transpose(1, 2, 0)
+    w_rsck = w.float().numpy().transpose(2, 3, 1, 0)
+    return O.winograd_conv(x_hwc, w_rsck, relu=True)
+
+
+def test_c3_full_config(c3_oracle):
     """The benchmark configuration: NCHW fp16 1x64x256x256, 64 -> 64, zero bias, ReLU, fp16 out."""
     x, w, b = WL.c3()
     conv = rdv.Winograd3x3Conv2d(w.cuda(), b.cuda())
@@ -197,18 +206,17 @@ def test_c3_full_config():
     torch.cuda.synchronize()
     assert y.dtype == torch.float16 and tuple(y.shape) == (1, 64, 256, 256)
     y = y.float().cpu().numpy()[0].transpose(1, 2, 0)
-    x_hwc = x.float().numpy()[0].transpose(1, 2, 0)
-    w_rsck = w.float().numpy().transpose(2, 3, 1, 0)
-    _check_close(y, O.winograd_conv(x_hwc, w_rsck, relu=True), "C3 vs oracle", f16_out=True)
+    _check_close(y, c3_oracle, "C3 vs oracle", f16_out=True)
     direct = torch.nn.functional.conv2d(x.float(), w.float(), padding=1).clamp_min(0)[0].permute(1, 2, 0).numpy()
     _check_direct(y, direct.astype(np.float64), "C3 vs direct fp32 conv")
 
 
-def test_c3_repeats_are_identical():
-    """Fifty back-to-back calls of the benchmark configuration give the same bits.
-    The pipelined kernel issues its LDS reads and global stores from inline
-    assembly with hand-counted waits; a miscounted wait would read data that is
-    still landing and show here as calls that differ."""
+def test_c3_repeats_are_identical(c3_oracle):
+    """Fifty back-to-back calls of the benchmark configuration give the same
+    bits, and those bits pass the oracle check.  The repeats catch run-to-run
+    races (data read while still landing, in some calls and not others); a wait
+    miscounted the same way in every call would give the same wrong bits each
+    time, which the oracle comparison catches instead."""
     x, w, b = WL.c3()
     conv = rdv.Winograd3x3Conv2d(w.cuda(), b.cuda())
     xd = x.cuda()
@@ -217,3 +225,19 @@ def test_c3_repeats_are_identical():
     torch.cuda.synchronize()
     differ = sum(0 if torch.equal(y, ref) else 1 for y in outs)
     assert differ == 0, f"{differ} of 50 repeated calls differ from the first"
+    _check_close(ref.float().cpu().numpy()[0].transpose(1, 2, 0), c3_oracle, "C3 repeat vs oracle", f16_out=True)
+
+
+def test_c3_unaligned_out_view(c3_oracle):
+    """An fp16 `out` view 8 bytes past a 16-byte boundary is a valid buffer (the
+    C ABI asks 8-byte alignment for fp16 output); the call takes the kernel
+    without 16-byte stores and still matches the oracle."""
+    x, w, b = WL.c3()
+    conv = rdv.Winograd3x3Conv2d(w.cuda(), b.cuda())
+    n_out = 64 * 256 * 256
+    base = torch.empty(n_out + 8, dtype=torch.float16, device="cuda")
+    view = base[4: 4 + n_out].view(1, 64, 256, 256)
+    assert view.data_ptr() % 16 == 8
+    y = conv(x.cuda(), relu=True, out=view)
+    torch.cuda.synchronize()
+    _check_close(y.float().cpu().numpy()[0].transpose(1, 2, 0), c3_oracle, "C3 unaligned out vs oracle", f16_out=True)

@@ -1,0 +1,46 @@
+"""Host-side argument checks of mse_backward: caller-supplied gradient buffers
+that the kernels could not write correctly are rejected with TypeError before
+anything is packed or launched (these run without a GPU)."""
+import pytest
+import torch
+
+import rdv_project_amd as rdv
+
+
+def _chain():
+    g = torch.Generator().manual_seed(3)
+    dims = [16, 32, 8]
+    m = None
+    for i in range(2):
+        lin = rdv.linear(torch.randn(dims[i + 1], dims[i], generator=g), torch.zeros(dims[i + 1]), f16=True)
+        m = lin if m is None else m >> rdv.relu >> lin
+    return m
+
+
+def _good():
+    return [(torch.zeros(32, 16), torch.zeros(32)), (torch.zeros(8, 32), torch.zeros(8))]
+
+
+@pytest.mark.parametrize("case", ["short", "not_pairs", "fp16", "shape", "bias_shape", "strided", "host"])
+def test_bad_grads_rejected_before_launch(case):
+    grads = _good()
+    if case == "short":
+        grads = grads[:1]
+    elif case == "not_pairs":
+        grads = [grads[0][0], grads[1][0]]
+    elif case == "fp16":
+        grads[0] = (grads[0][0].half(), grads[0][1])
+    elif case == "shape":
+        grads[1] = (torch.zeros(32, 8), grads[1][1])
+    elif case == "bias_shape":
+        grads[1] = (grads[1][0], torch.zeros(9))
+    elif case == "strided":
+        grads[0] = (torch.zeros(16, 32).t(), grads[0][1])
+    # "host": correct shapes and types, but CPU tensors: the kernels need device pointers
+    with pytest.raises(TypeError):
+        rdv.mse_backward(_chain(), torch.zeros(64, 16), torch.zeros(64, 8), grads)
+
+
+def test_target_width_checked():
+    with pytest.raises(AssertionError):
+        rdv.mse_backward(_chain(), torch.zeros(64, 16), torch.zeros(64, 7))
