@@ -221,6 +221,22 @@ int rdv_mlp_train_step(const rdv_mlp_desc* desc, const void* packed, const void*
                        void* workspace, int64_t workspace_bytes, float* loss, float* const* dW, float* const* db,
                        void* stream);
 
+/* Size of the static device scratch behind rdv_mlp_train_step_static. */
+#define RDV_TRAIN_STATIC_SCRATCH_BYTES (64LL << 20)
+
+/* rdv_mlp_train_step without a workspace argument and without any device
+ * allocation: the workspace is a file-scope device array of
+ * RDV_TRAIN_STATIC_SCRATCH_BYTES bytes, one per GPU, held until the process
+ * ends.  No counterpart in the reference (which has no backward pass); it is
+ * for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  Same
+ * arguments, kernels and results as rdv_mlp_train_step.  Returns
+ * RDV_ERR_WORKSPACE when rdv_mlp_train_workspace_bytes(desc, n) exceeds the
+ * scratch size.  Every call on one GPU shares that GPU's scratch: calls that
+ * overlap on one GPU (two streams, two threads) race. */
+int rdv_mlp_train_step_static(const rdv_mlp_desc* desc, const void* packed, const void* x, const float* target,
+                              int64_t n, float* loss, float* const* dW, float* const* db, void* stream);
+
 /* ------------------------------------------------ cameras and volume rendering */
 typedef struct rdv_camera_desc {
   int32_t n_cams;       /* poses rows                                             */

@@ -21,6 +21,7 @@ RDV_ERR_WORKSPACE = -4
 
 MLP_MAX_LAYERS = 16
 MLP_MAX_WIDTH = 256
+TRAIN_STATIC_SCRATCH_BYTES = 64 << 20  # RDV_TRAIN_STATIC_SCRATCH_BYTES
 
 ACT_NONE, ACT_RELU, ACT_SOFTPLUS, ACT_SIGMOID, ACT_DENSITY_RGB = 0, 1, 2, 3, 4
 PREC_F32, PREC_F16 = 0, 1
@@ -104,6 +105,8 @@ _SIGNATURES = {
     "rdv_mlp_train_step": (C.c_int, [C.POINTER(MlpDesc), C.c_void_p, C.c_void_p, C.c_void_p, C.c_int64, C.c_void_p,
                                      C.c_int64, C.c_void_p, C.POINTER(C.c_void_p), C.POINTER(C.c_void_p),
                                      C.c_void_p]),
+    "rdv_mlp_train_step_static": (C.c_int, [C.POINTER(MlpDesc), C.c_void_p, C.c_void_p, C.c_void_p, C.c_int64,
+                                            C.c_void_p, C.POINTER(C.c_void_p), C.POINTER(C.c_void_p), C.c_void_p]),
     "rdv_cameras_rays": (C.c_int, [C.POINTER(CameraDesc), C.c_void_p, C.c_void_p, C.c_void_p]),
     "rdv_render_emission_absorption": (C.c_int, [C.POINTER(CameraDesc), C.c_void_p, C.POINTER(MlpDesc), C.c_void_p,
                                                  C.c_int32, C.c_void_p, C.c_void_p]),

@@ -61,6 +61,9 @@ int64_t train_workspace_bytes(const rdv_mlp_desc& d, const MlpLayout& lay, int64
 int launch_train_step(const rdv_mlp_desc& d, const MlpLayout& lay, const void* packed, const void* x,
                       const float* target, int64_t n, void* workspace, int64_t ws_bytes, float* loss,
                       float* const* dW, float* const* db, hipStream_t stream);
+int launch_train_step_static(const rdv_mlp_desc& d, const MlpLayout& lay, const void* packed, const void* x,
+                             const float* target, int64_t n, float* loss, float* const* dW, float* const* db,
+                             hipStream_t stream);
 int launch_camera_rays(const rdv_camera_desc& c, const float* poses, float* rays, hipStream_t stream);
 int launch_render_ea(const rdv_camera_desc& c, const float* poses, const rdv_mlp_desc& d, const MlpLayout& lay,
                      const void* packed, int samples, float* image, hipStream_t stream);
@@ -308,6 +311,23 @@ int rdv_mlp_train_step(const rdv_mlp_desc* desc, const void* packed, const void*
     return fail(RDV_ERR_INVALID, "x and target must be 16-byte aligned, the workspace 256-byte aligned");
   return launch_train_step(*desc, lay, packed, x, target, n, workspace, workspace_bytes, loss, dW, db,
                            static_cast<hipStream_t>(stream));
+}
+
+int rdv_mlp_train_step_static(const rdv_mlp_desc* desc, const void* packed, const void* x, const float* target,
+                              int64_t n, float* loss, float* const* dW, float* const* db, void* stream) {
+  MlpLayout lay;
+  int rc = check_mlp(desc, &lay);
+  if (rc != RDV_OK) return rc;
+  rc = train_check(*desc, lay);
+  if (rc != RDV_OK) return rc;
+  if (n < 1) return fail(RDV_ERR_INVALID, "n must be >= 1");
+  if (!packed || !x || !target || !loss || !dW || !db)
+    return fail(RDV_ERR_INVALID, "rdv_mlp_train_step_static: NULL pointer argument");
+  for (int i = 0; i < desc->n_layers; ++i)
+    if (!dW[i] || !db[i]) return fail(RDV_ERR_INVALID, "rdv_mlp_train_step_static: NULL gradient pointer");
+  if (reinterpret_cast<uintptr_t>(x) % 16 || reinterpret_cast<uintptr_t>(target) % 16)
+    return fail(RDV_ERR_INVALID, "x and target must be 16-byte aligned");
+  return launch_train_step_static(*desc, lay, packed, x, target, n, loss, dW, db, static_cast<hipStream_t>(stream));
 }
 
 static int check_camera(const rdv_camera_desc* c) {

@@ -31,6 +31,8 @@
 //    per-block partial.
 //  - train_reduce1/2_kernel: sum the per-block partials in a fixed order.
 #include <algorithm>
+#include <mutex>
+#include <string>
 
 #include "mlp_core.h"
 
@@ -1792,6 +1794,60 @@ int launch_train_step(const rdv_mlp_desc& d, const MlpLayout& lay, const void* p
   train_reduce2_kernel<<<dim3(gx), dim3(256), 0, stream>>>(jobs, mid, scale);
   RDV_HIP_TRY(hipGetLastError());
   return RDV_OK;
+}
+
+}  // namespace rdv
+
+// ------------------------------------------------ no-allocation variant
+// rdv_mlp_train_step_static: the training step with its workspace in a
+// file-scope device array instead of a caller buffer, for callers that cannot
+// allocate device memory (code under HIP graph capture, serving loops).  Each
+// GPU the library runs on holds its own copy of the array until the process
+// ends; every call on that GPU shares it, so calls that overlap on one GPU
+// race.  Nothing in it has to start at zero: every launch of the step writes
+// each partial it later reads (blocks without tiles write zero partials).
+namespace rdv {
+
+constexpr int64_t kTrainScratchBytes = RDV_TRAIN_STATIC_SCRATCH_BYTES;
+static __device__ __align__(256) uint8_t scratch[kTrainScratchBytes];
+
+// Device address of this GPU's copy of `scratch`, resolved once per device with
+// that device current.  The array's name is only a host-side stand-in: kernels
+// get this address, never the name.
+static int scratch_address(void** out) {
+  static std::mutex mu;
+  static void* addr[64] = {};
+  int dev = 0;
+  RDV_HIP_TRY(hipGetDevice(&dev));
+  if (dev < 0 || dev >= 64) return fail(RDV_ERR_UNSUPPORTED, "device index out of range");
+  std::lock_guard<std::mutex> lock(mu);
+  if (addr[dev] == nullptr) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+    if (p == nullptr) return fail(RDV_ERR_HIP, "hipGetSymbolAddress(scratch) returned NULL");
+    addr[dev] = p;
+  }
+  *out = addr[dev];
+  return RDV_OK;
+}
+
+int launch_train_step_static(const rdv_mlp_desc& d, const MlpLayout& lay, const void* packed, const void* x,
+                             const float* target, int64_t n, float* loss, float* const* dW, float* const* db,
+                             hipStream_t stream) {
+  DeviceInfo di;
+  int rc = device_info(&di);
+  if (rc != RDV_OK) return rc;
+  TrainPlan p;
+  train_plan(d, lay, n, di.cu_count, &p);
+  if (p.total > kTrainScratchBytes)
+    return fail(RDV_ERR_WORKSPACE, "rdv_mlp_train_step_static: this chain and n need " + std::to_string(p.total) +
+                                       " bytes of workspace, more than the " + std::to_string(kTrainScratchBytes) +
+                                       "-byte static scratch (use rdv_mlp_train_step with a caller workspace)");
+  void* ws = nullptr;
+  rc = scratch_address(&ws);
+  if (rc != RDV_OK) return rc;
+  return launch_train_step(d, lay, packed, x, target, n, ws, kTrainScratchBytes, loss, dW, db, stream);
 }
 
 }  // namespace rdv
