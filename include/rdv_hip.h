@@ -100,7 +100,10 @@ int64_t rdv_mlp_packed_bytes(const rdv_mlp_desc* desc);
 int rdv_mlp_pack(const rdv_mlp_desc* desc, const float* const* weights,
                  const float* const* biases, void* packed, void* stream);
 
-/* y[n, dims[L]] = chain(x[n, in_features]) for fp32 row-major x and y.
+/* y[n, dims[L]] = chain(x[n, in_features]) for fp32 row-major x and y.  Every
+ * all-LinearFast chain runs on the fp16 matrix cores (a compile-time kernel for
+ * the benchmark shapes, a runtime-shaped one for the rest); chains with an
+ * exact fp32 Linear layer run on the vector ALUs.
  * Replaces Map.__call__ -> dispatch(MapEvaluator) over a chain of
  * LinearFast / Linear / ReLU maps (src/rdv/maths/__init__.py:1451-1487,
  * src/rdv/shaders/maps/map_evaluator.h:1-5, composite.h:8-12).
@@ -254,8 +257,8 @@ int rdv_cameras_rays(const rdv_camera_desc* cam, const float* poses, float* rays
 /* Emission-absorption render of a density / RGB field (build-defined; no
  * reference counterpart): for every pixel ray of `cam` that meets [-1,1]^3 on
  * [t0, t1] (t0 >= 0), `samples` points t_i = t0 + (i + 1/2) dt, dt = (t1 - t0) /
- * samples, are evaluated by `field` (3 -> 64 -> 64 -> 64 -> 4 LinearFast chain,
- * ReLU hidden, raw head; sigma = softplus(o0), c = sigmoid(o1..3)) and composited
+ * samples, are evaluated by `field` (a LinearFast chain from 3 inputs to 4 raw
+ * outputs; sigma = softplus(o0), c = sigmoid(o1..3)) and composited
  * front to back: alpha_i = 1 - exp(-sigma_i dt), T_i = prod_{j<i} (1 - alpha_j),
  * image = sum_i T_i alpha_i c_i (0 for rays that miss).  image: device
  * [n, H, W, 3] fp32.  samples: a positive multiple of 32. */
@@ -272,8 +275,9 @@ int rdv_composite(const float* sigma_rgb, const float* dt, int64_t n_rays, int32
  * [-1,1]^3 in the object space of transform (mat4x3, column-major: three linear
  * columns then the translation, 12 floats on the host), marched with fixed
  * steps of step_size: tau += extinction(x) * density_scale * step_size, 0 once
- * tau > 16, exp(-tau) at the end (1 for rays that miss).  extinction: a
- * 3 -> 64 -> 64 -> 64 -> 1 LinearFast chain with ReLU hidden activations.
+ * tau > 16, exp(-tau) at the end (1 for rays that miss).  extinction: any
+ * LinearFast chain from 3 inputs to 1 output (the reference marches any
+ * extinction Map[3, 1]).
  * Replaces RaymarchingTransmittance (src/rdv/domain/volumes.py:124-141,
  * src/rdv/shaders/volumes/raymarching_transmittance.h:1-22,
  * raymarching_transmittance_trait.h:1-14, libraries/math_library.h:48-57). */

@@ -25,6 +25,7 @@ SOURCES = [
     "mlp_pack.hip",
     "mlp_f32.hip",
     "mlp_fused.hip",
+    "mlp_generic.hip",
     "winograd.hip",
     "render.hip",
     "train.hip",

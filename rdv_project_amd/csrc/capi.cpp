@@ -48,6 +48,10 @@ const FusedEntry* find_fused(const rdv_mlp_desc& d, const MlpLayout& lay);
 const char* fused_name(const FusedEntry* e);
 int launch_fused_entry(const FusedEntry* e, const rdv_mlp_desc& d, const MlpLayout& lay, const void* packed,
                        const float* x, float* y, int64_t nrows, hipStream_t stream);
+bool generic_f16_supported(const rdv_mlp_desc& d);
+const char* generic_f16_name(const rdv_mlp_desc& d, const MlpLayout& lay);
+int launch_mlp_generic_f16(const rdv_mlp_desc& d, const MlpLayout& lay, const void* packed, const float* x, float* y,
+                           int64_t nrows, hipStream_t stream);
 int launch_mlp_chain_f32(const rdv_mlp_desc& d, const MlpLayout& lay, const void* packed, const float* x,
                          float* y, int64_t row0, int64_t nrows, bool force_f32, hipStream_t stream);
 int launch_mlp_pack(const rdv_mlp_desc& d, const MlpLayout& lay, const float* const* W, const float* const* b,
@@ -205,6 +209,8 @@ static int mlp_forward_impl(const rdv_mlp_desc* desc, const void* packed, const 
   const FusedEntry* e = find_fused(*desc, lay);
   if (e) {
     rc = launch_fused_entry(e, *desc, lay, packed, x, y, n_full, s);
+  } else if (generic_f16_supported(*desc)) {
+    rc = launch_mlp_generic_f16(*desc, lay, packed, x, y, n_full, s);
   } else {
     rc = prepare_chain_f32(*desc);
     if (rc == RDV_OK) rc = launch_mlp_chain_f32(*desc, lay, packed, x, y, 0, n_full, false, s);
@@ -388,7 +394,8 @@ const char* rdv_mlp_kernel_name(const rdv_mlp_desc* desc) {
   MlpLayout lay;
   if (check_mlp(desc, &lay) != RDV_OK) return "";
   const FusedEntry* e = find_fused(*desc, lay);
-  return e ? fused_name(e) : "mlp_chain_f32_kernel";
+  if (e) return fused_name(e);
+  return generic_f16_supported(*desc) ? generic_f16_name(*desc, lay) : "mlp_chain_f32_kernel";
 }
 
 }  // extern "C"

@@ -25,6 +25,7 @@
 // sigma * dt (T_i = T_in exp(-sum_{j<i} sigma_j dt)), the chunks composited in
 // ray order, the colour a per-lane partial sum reduced once per ray.
 #include "mlp_core.h"
+#include "mlp_generic.h"
 
 namespace rdv {
 
@@ -395,26 +396,22 @@ __device__ __forceinline__ void inverse3(const float (&M)[12], float (&L)[9]) {
 // reference's, bit for bit), the 32 extinctions are evaluated together, and tau
 // is an inclusive wavefront scan of the increments (the order of that fp32 sum
 // is the only difference from the reference).
-template <class N, int HEAD_ACT>
-__global__ __launch_bounds__(kRenderThreads, 1) void raymarch_transmittance_kernel(TransmittanceArgs a) {
-  static_assert(N::kIn == 3 && N::kOut == 1, "the extinction is a Map[3, 1]");
-  __shared__ float sb[N::kBias];
-  __shared__ half8 sw[N::kFrags * 64];
-  __shared__ int s_next;
+// The march of every ray of this block: sigma_of(x) returns this lane's
+// extinction at its sample position x (lanes l and l + 32 hold the same sample;
+// the value of lanes 0..31 is used).
+template <class Sigma>
+__device__ __forceinline__ void raymarch_rays(const TransmittanceArgs& a, int* s_next, Sigma&& sigma_of) {
   const int lane = threadIdx.x & 63;
   const int h = lane >> 5, col = lane & 31;
   const int64_t per_block = (a.nrays + gridDim.x - 1) / gridDim.x;
   const int64_t r_begin = int64_t(blockIdx.x) * per_block;
   const int64_t r_end = r_begin + per_block < a.nrays ? r_begin + per_block : a.nrays;
   const int nr = int(r_end > r_begin ? r_end - r_begin : 0);
-  const bool has_bias = (reinterpret_cast<const MlpPackHeader*>(a.packed)->flags & kMlpHasBias) != 0;
-  stage_weights<N, kRenderThreads>(a.packed, a.lay, sb, sw, &s_next);
   float L[9];
   inverse3(a.M, L);
-
   auto claim = [&]() {
     int t = 0;
-    if (lane == 0) t = atomicAdd(&s_next, 1);
+    if (lane == 0) t = atomicAdd(s_next, 1);
     return __builtin_amdgcn_readfirstlane(t);
   };
   for (int r = claim(); r < nr; r = claim()) {
@@ -456,9 +453,7 @@ __global__ __launch_bounds__(kRenderThreads, 1) void raymarch_transmittance_kern
         }
         const bool valid = dc > 0.0f && k0 + col < 4096;
         // every lane in [0, c) was valid when lane c is (d only decreases)
-        f32x16 fin[N::kMaxMT];
-        eval_chunk<N, true>(sw, sb, has_bias, lane, h, xc, fin);
-        const float sigma = head_act<HEAD_ACT>(0, fin[0][0]);
+        const float sigma = sigma_of(xc);
         const float ce = sigma * a.density_scale;
         float inc = ce * a.step;
         asm volatile("" : "+v"(inc));
@@ -486,6 +481,214 @@ __global__ __launch_bounds__(kRenderThreads, 1) void raymarch_transmittance_kern
     }
     if (lane == 0) a.out[ray] = T;
   }
+}
+
+template <class N, int HEAD_ACT>
+__global__ __launch_bounds__(kRenderThreads, 1) void raymarch_transmittance_kernel(TransmittanceArgs a) {
+  static_assert(N::kIn == 3 && N::kOut == 1, "the extinction is a Map[3, 1]");
+  __shared__ float sb[N::kBias];
+  __shared__ half8 sw[N::kFrags * 64];
+  __shared__ int s_next;
+  const int lane = threadIdx.x & 63;
+  const int h = lane >> 5;
+  const bool has_bias = (reinterpret_cast<const MlpPackHeader*>(a.packed)->flags & kMlpHasBias) != 0;
+  stage_weights<N, kRenderThreads>(a.packed, a.lay, sb, sw, &s_next);
+  raymarch_rays(a, &s_next, [&](const float (&xc)[3]) {
+    f32x16 fin[N::kMaxMT];
+    eval_chunk<N, true>(sw, sb, has_bias, lane, h, xc, fin);
+    return head_act<HEAD_ACT>(0, fin[0][0]);
+  });
+}
+
+// ------------------------------------------- runtime-shaped fields (mlp_generic.h)
+// Any LinearFast field or extinction chain without a compile-time instance:
+// the same per-ray work, with each 32-sample chunk evaluated by gen_chain.
+constexpr int64_t kGenFieldLdsCap = 152 * 1024;
+
+// A-fragment and bias sources of a block: the LDS copy (staged here) or the
+// packed block in global memory.
+template <bool LDSW>
+__device__ __forceinline__ void gen_sources(const uint8_t* packed, const GenNet& g, uint8_t* smem, const half8** w,
+                                            const float** b) {
+  if constexpr (LDSW) {
+    gen_stage(packed, g, smem);
+    *w = reinterpret_cast<const half8*>(smem);
+    *b = reinterpret_cast<const float*>(smem + int64_t(g.n_frag) * 1024);
+  } else {
+    *w = reinterpret_cast<const half8*>(packed + g.frag_off0);
+    *b = reinterpret_cast<const float*>(packed + g.bias_off0);
+  }
+}
+
+// The chain's head value of row 0 at this lane's sample p (3 coordinates).
+template <int MT>
+__device__ __forceinline__ float gen_field_row0(const GenNet& g, const half8* w0, const float* b0, bool has_bias,
+                                                int lane, int h, const float (&p)[3], int act) {
+  const int z = opaque_zero();
+  const half8* wsrc = w0 + z;
+  auto wf = [&](int f) { return wsrc[f * 64 + lane]; };
+  auto get = [&](int d) { return d == 0 ? p[0] : (d == 1 ? p[1] : p[2]); };
+  auto l0 = [&](int c) { return gen_l0_chunk(g, c, h, get); };
+  float v = 0.0f;
+  auto sink = [&](const auto& acc) { v = gen_head_act(act, 0, acc[0][0]); };
+  gen_chain<MT>(g, GenCtx{b0 + z, has_bias, h}, wf, l0, sink);
+  return v;
+}
+
+struct TransmittanceGenArgs {
+  TransmittanceArgs t;
+  GenNet net;
+};
+
+template <int MT, bool LDSW>
+__global__ __launch_bounds__(64 * gen_waves<MT>(), 1) void raymarch_generic_kernel(TransmittanceGenArgs ga) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  __shared__ int s_next;
+  const TransmittanceArgs& a = ga.t;
+  const GenNet& g = ga.net;
+  const int lane = threadIdx.x & 63;
+  const int h = lane >> 5;
+  const bool has_bias = (reinterpret_cast<const MlpPackHeader*>(a.packed)->flags & kMlpHasBias) != 0;
+  const half8* w0;
+  const float* b0;
+  gen_sources<LDSW>(a.packed, g, smem, &w0, &b0);
+  if (threadIdx.x == 0) s_next = 0;
+  __syncthreads();
+  const int act = g.act[g.L - 1];
+  raymarch_rays(a, &s_next, [&](const float (&xc)[3]) {
+    return gen_field_row0<MT>(g, w0, b0, has_bias, lane, h, xc, act);
+  });
+}
+
+struct RenderGenArgs {
+  RenderArgs r;
+  GenNet net;
+};
+
+// Emission-absorption render with a runtime-shaped field (raw 4-wide head):
+// one ray per wave at a time, one 32-sample chunk per chain evaluation.
+template <int MT, bool LDSW>
+__global__ __launch_bounds__(64 * gen_waves<MT>(), 1) void render_ea_generic_kernel(RenderGenArgs ga) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  __shared__ int s_next;
+  const RenderArgs& a = ga.r;
+  const GenNet& g = ga.net;
+  const int lane = threadIdx.x & 63;
+  const int h = lane >> 5, col = lane & 31;
+  const int64_t nrays = int64_t(a.cam.n) * a.cam.H * a.cam.W;
+  const int64_t per_block = (nrays + gridDim.x - 1) / gridDim.x;
+  const int64_t r_begin = int64_t(blockIdx.x) * per_block;
+  const int64_t r_end = r_begin + per_block < nrays ? r_begin + per_block : nrays;
+  const int nr = int(r_end > r_begin ? r_end - r_begin : 0);
+  const bool has_bias = (reinterpret_cast<const MlpPackHeader*>(a.packed)->flags & kMlpHasBias) != 0;
+  const half8* w0;
+  const float* b0;
+  gen_sources<LDSW>(a.packed, g, smem, &w0, &b0);
+  if (threadIdx.x == 0) s_next = 0;
+  __syncthreads();
+  auto claim = [&]() {
+    int t = 0;
+    if (lane == 0) t = atomicAdd(&s_next, 1);
+    return __builtin_amdgcn_readfirstlane(t);
+  };
+  const int chunks = a.samples / 32;
+  for (int r = claim(); r < nr; r = claim()) {
+    const int64_t ray = r_begin + r;
+    const int x = int(ray % a.cam.W);
+    const int64_t rest = ray / a.cam.W;
+    const int y = int(rest % a.cam.H);
+    const int cam = int(rest / a.cam.H);
+    float o[3], w[3];
+    camera_ray(a.cam, cam, y, x, o, w);
+    float t0, t1;
+    ray_box(o, w, t0, t1);
+    float cr = 0.0f, cg = 0.0f, cb = 0.0f;
+    if (!(t1 <= 0.0f || t0 > t1)) {
+      t0 = fmaxf(t0, 0.0f);
+      const float dt = (t1 - t0) / float(a.samples);
+      float Tin = 1.0f;
+      for (int c = 0; c < chunks; ++c) {
+        const float ts = t0 + (float(32 * c + col) + 0.5f) * dt;
+        const float p[3] = {o[0] + ts * w[0], o[1] + ts * w[1], o[2] + ts * w[2]};
+        const int z = opaque_zero();
+        const half8* wsrc = w0 + z;
+        auto wf = [&](int f) { return wsrc[f * 64 + lane]; };
+        auto get = [&](int d) { return d == 0 ? p[0] : (d == 1 ? p[1] : p[2]); };
+        auto l0 = [&](int cc) { return gen_l0_chunk(g, cc, h, get); };
+        f32x4 o4 = {0.0f, 0.0f, 0.0f, 0.0f};
+        auto sink = [&](const auto& acc) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) o4[j] = acc[0][j];
+        };
+        gen_chain<MT>(g, GenCtx{b0 + z, has_bias, h}, wf, l0, sink);
+        // rows 0..3 (density, RGB logits) sit in registers 0..3 of lanes 0..31
+        const float sigma = fast_softplus(o4[0]);
+        const float ad = h == 0 ? sigma * dt : 0.0f;
+        const float incl = wave_scan_incl(ad, lane);
+        const float total = lane_value(incl, 31);
+        const float wgt = h == 0 ? Tin * __expf(-(incl - ad)) * (1.0f - __expf(-ad)) : 0.0f;
+        cr += wgt * fast_sigmoid(o4[1]);
+        cg += wgt * fast_sigmoid(o4[2]);
+        cb += wgt * fast_sigmoid(o4[3]);
+        Tin *= __expf(-total);
+      }
+      cr = wave_sum(cr);
+      cg = wave_sum(cg);
+      cb = wave_sum(cb);
+    }
+    if (lane == 0) {
+      float* dst = a.image + ray * 3;
+      dst[0] = cr;
+      dst[1] = cg;
+      dst[2] = cb;
+    }
+  }
+}
+
+template <class Args, int MT, bool LDSW>
+static int launch_gen_field(void (*kernel)(Args), const Args& a, int64_t work_items, int cu, size_t lds,
+                            hipStream_t stream) {
+  static bool attr = false;
+  if (LDSW && !attr) {
+    RDV_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    int(kGenFieldLdsCap)));
+    attr = true;
+  }
+  constexpr int waves = gen_waves<MT>();
+  int64_t blocks = cu;
+  const int64_t need = (work_items + waves - 1) / waves;
+  if (need < blocks) blocks = need;
+  kernel<<<dim3(unsigned(blocks)), dim3(64 * waves), lds, stream>>>(a);
+  RDV_HIP_TRY(hipGetLastError());
+  return RDV_OK;
+}
+
+#define RDV_GEN_FIELD_DISPATCH(KERNEL, ARGS, ITEMS, CU, NET, STREAM)                                          \
+  do {                                                                                                       \
+    const int64_t lds_ = gen_lds_bytes(NET);                                                                 \
+    const bool in_lds_ = lds_ <= kGenFieldLdsCap;                                                            \
+    switch (gen_mt_bound(NET)) {                                                                             \
+      case 1:                                                                                                \
+        return in_lds_ ? launch_gen_field<decltype(ARGS), 1, true>(&KERNEL<1, true>, ARGS, ITEMS, CU, lds_, STREAM) \
+                       : launch_gen_field<decltype(ARGS), 1, false>(&KERNEL<1, false>, ARGS, ITEMS, CU, 0, STREAM); \
+      case 2:                                                                                                \
+        return in_lds_ ? launch_gen_field<decltype(ARGS), 2, true>(&KERNEL<2, true>, ARGS, ITEMS, CU, lds_, STREAM) \
+                       : launch_gen_field<decltype(ARGS), 2, false>(&KERNEL<2, false>, ARGS, ITEMS, CU, 0, STREAM); \
+      case 4:                                                                                                \
+        return in_lds_ ? launch_gen_field<decltype(ARGS), 4, true>(&KERNEL<4, true>, ARGS, ITEMS, CU, lds_, STREAM) \
+                       : launch_gen_field<decltype(ARGS), 4, false>(&KERNEL<4, false>, ARGS, ITEMS, CU, 0, STREAM); \
+      default:                                                                                               \
+        return in_lds_ ? launch_gen_field<decltype(ARGS), 8, true>(&KERNEL<8, true>, ARGS, ITEMS, CU, lds_, STREAM) \
+                       : launch_gen_field<decltype(ARGS), 8, false>(&KERNEL<8, false>, ARGS, ITEMS, CU, 0, STREAM); \
+    }                                                                                                        \
+  } while (0)
+
+// A LinearFast chain from 3 inputs (raw or FREQ-encoded) to `out` outputs?
+static bool is_f16_field(const rdv_mlp_desc& d, int out) {
+  if (d.in_features != 3 || d.dims[d.n_layers] != out) return false;
+  for (int i = 0; i < d.n_layers; ++i)
+    if (d.prec[i] != RDV_PREC_F16) return false;
+  return true;
 }
 
 // ---------------------------------------------------------- instantiations
@@ -531,10 +734,11 @@ int launch_camera_rays(const rdv_camera_desc& c, const float* poses, float* rays
 
 int launch_render_ea(const rdv_camera_desc& c, const float* poses, const rdv_mlp_desc& d, const MlpLayout& lay,
                      const void* packed, int samples, float* image, hipStream_t stream) {
-  if (!is_render_field(d, lay))
+  const bool fixed = is_render_field(d, lay);
+  if (!fixed && !(is_f16_field(d, 4) && d.act[d.n_layers - 1] == RDV_ACT_NONE))
     return fail(RDV_ERR_UNSUPPORTED,
-                "the renderer's field must be a 3 -> 64 -> 64 -> 64 -> 4 LinearFast chain with ReLU hidden "
-                "activations and no head activation");
+                "the renderer's field must be a LinearFast chain from 3 inputs to 4 raw outputs (density and RGB "
+                "logits; the renderer applies softplus and sigmoid)");
   DeviceInfo di;
   int rc = device_info(&di);
   if (rc != RDV_OK) return rc;
@@ -545,6 +749,12 @@ int launch_render_ea(const rdv_camera_desc& c, const float* poses, const rdv_mlp
   a.image = image;
   a.samples = samples;
   const int64_t nrays = int64_t(c.n_cams) * c.height * c.width;
+  if (!fixed) {
+    RenderGenArgs ga;
+    ga.r = a;
+    gen_net(d, lay, &ga.net);
+    RDV_GEN_FIELD_DISPATCH(render_ea_generic_kernel, ga, nrays, di.cu_count, ga.net, stream);
+  }
   int64_t blocks = di.cu_count;
   const int64_t need = (nrays + kEaWaves - 1) / kEaWaves;
   if (need < blocks) blocks = need;
@@ -574,10 +784,9 @@ int launch_composite(const float* sigma_rgb, const float* dts, int64_t nrays, in
 int launch_raymarch_transmittance(const rdv_mlp_desc& d, const MlpLayout& lay, const void* packed, const float* rays,
                                   int64_t nrays, const float* transform12, float step, float density_scale,
                                   float* out, hipStream_t stream) {
-  if (!is_extinction_field(d, lay))
-    return fail(RDV_ERR_UNSUPPORTED,
-                "the extinction field must be a 3 -> 64 -> 64 -> 64 -> 1 LinearFast chain with ReLU hidden "
-                "activations (head: none, relu or softplus)");
+  const bool fixed = is_extinction_field(d, lay);
+  if (!fixed && !is_f16_field(d, 1))
+    return fail(RDV_ERR_UNSUPPORTED, "the extinction must be a LinearFast chain from 3 inputs to 1 output");
   DeviceInfo di;
   int rc = device_info(&di);
   if (rc != RDV_OK) return rc;
@@ -590,6 +799,12 @@ int launch_raymarch_transmittance(const rdv_mlp_desc& d, const MlpLayout& lay, c
   a.step = step;
   a.density_scale = density_scale;
   a.out = out;
+  if (!fixed) {
+    TransmittanceGenArgs ga;
+    ga.t = a;
+    gen_net(d, lay, &ga.net);
+    RDV_GEN_FIELD_DISPATCH(raymarch_generic_kernel, ga, nrays, di.cu_count, ga.net, stream);
+  }
   int64_t blocks = di.cu_count;
   const int64_t need = (nrays + kRenderWaves - 1) / kRenderWaves;
   if (need < blocks) blocks = need;

@@ -56,7 +56,9 @@ class RaymarchingTransmittance(Map):
     marched with fixed steps: tau += extinction(x) * density_scale * step_size,
     0 once tau > 16, exp(-tau) at the end; 1 when the ray misses
     (reference: volumes.py:124-141, shaders/volumes/raymarching_transmittance.h).
-    extinction: a Map[3, 1] (here a 3 -> 64 -> 64 -> 64 -> 1 LinearFast chain)."""
+    extinction: a Map[3, 1]: any LinearFast chain from 3 inputs (raw or
+    frequency-encoded) to 1 output, evaluated on the matrix cores 32 march
+    steps at a time."""
 
     IN = 6
     OUT = 1
@@ -79,7 +81,8 @@ class RaymarchingTransmittance(Map):
 class EmissionAbsorption(Map):
     """Build-defined volume renderer (no reference counterpart): along each ray
     (origin, direction) through [-1,1]^3, `samples` points t_i = t0 + (i + 1/2) dt
-    are fed through `field` (Map[3, 4]: density logit, RGB logits), with
+    are fed through `field` (Map[3, 4]: density logit, RGB logits; any
+    LinearFast chain with a raw head), with
     sigma = softplus, c = sigmoid, and composited front to back:
     alpha_i = 1 - exp(-sigma_i dt), T_i = prod_{j<i} (1 - alpha_j),
     C = sum_i T_i alpha_i c_i (0 for rays that miss)."""

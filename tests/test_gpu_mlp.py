@@ -29,6 +29,10 @@ def _chain(layers, acts, f16=True, enc=None):
             m = m >> rdv.density_rgb
         elif a == "softplus":
             m = m >> rdv.softplus
+        elif a == "sigmoid":
+            m = m >> rdv.sigmoid
+        else:
+            assert a == "none", a
     return m
 
 
@@ -125,23 +129,67 @@ def test_golden_vectors(path):
         _assert_fp16_parity(y, z["y"], os.path.basename(path))
 
 
-@pytest.mark.parametrize("dims,f16", [
-    ([5, 37, 19, 7], True),     # no matrix-core instantiation -> generic kernel (fp16 emulated)
-    ([3, 64, 64, 4], False),    # exact fp32 Linear chain
-    ([64, 128, 128, 16], True),
+@pytest.mark.parametrize("dims,f16,n,kernel", [
+    ([5, 37, 19, 7], True, 1000, "mlp_generic_f16<2,lds>"),          # odd widths, partial tiles and chunks
+    ([3, 64, 64, 4], False, 1000, "mlp_chain_f32_kernel"),            # exact fp32 Linear chain
+    ([64, 128, 128, 16], True, 1000, "mlp_generic_f16<4,lds>"),
+    ([64, 128, 128, 16], True, 40_000, "mlp_generic_f16<4,lds>"),     # several tiles per wave
+    ([17, 96, 200, 33], True, 777, "mlp_generic_f16<8,lds>"),         # 3, 7 and 2 M tiles
+    ([3, 256, 256, 4], True, 3000, "mlp_generic_f16<8,global>"),      # fragments beyond the LDS cap
+    ([256, 32, 1], True, 500, "mlp_generic_f16<1,lds>"),              # 16 K chunks in layer 0
+    ([8] + [32] * 15 + [2], True, 2048, "mlp_generic_f16<1,lds>"),    # 16 layers
 ])
-def test_generic_chains(dims, f16):
+def test_generic_chains(dims, f16, n, kernel):
     g = WL.gen(5)
-    layers = [((torch.rand(dims[i + 1], dims[i], generator=g) * 2 - 1) / dims[i] ** 0.5,
+    layers = [((torch.rand(dims[i + 1], dims[i], generator=g) * 2 - 1) / dims[i] ** 0.5 * 1.7,
                torch.rand(dims[i + 1], generator=g) * 0.2 - 0.1) for i in range(len(dims) - 1)]
     acts = ["relu"] * (len(dims) - 2) + ["none"]
-    x = torch.rand(1000, dims[0], generator=g) * 2 - 1
-    y = _chain(layers, acts, f16=f16)(x.cuda()).as_tensor("torch").cpu().numpy()
+    x = torch.rand(n, dims[0], generator=g) * 2 - 1
+    m = _chain(layers, acts, f16=f16)
+    y = m(x.cuda()).as_tensor("torch").cpu().numpy()
     ref = O.mlp_forward(x.numpy(), _np_layers(layers), acts, ["f16" if f16 else "f32"] * len(layers))
     if f16:
         _assert_fp16_parity(y, ref, str(dims))
+        assert np.abs(ref).max() > 0.05  # the chain did not collapse to ~0
     else:
         np.testing.assert_allclose(y, ref, rtol=1e-5, atol=1e-6)
+    from rdv_project_amd import _chain as CH, _lib
+    p = CH.plan_chain(m, dims[0])
+    assert _lib.load().rdv_mlp_kernel_name(p.desc).decode() == kernel
+
+
+@pytest.mark.parametrize("acts", [
+    ["softplus", "relu", "none"],       # a transcendental hidden activation
+    ["relu", "none", "sigmoid"],        # a linear hidden layer, sigmoid head
+    ["relu", "relu", "density_rgb"],
+])
+def test_generic_hidden_and_head_activations(acts):
+    g = WL.gen(9)
+    dims = [6, 48, 40, 4]
+    layers = [((torch.rand(dims[i + 1], dims[i], generator=g) * 2 - 1) / dims[i] ** 0.5 * 1.7,
+               torch.rand(dims[i + 1], generator=g) * 0.2 - 0.1) for i in range(3)]
+    x = torch.rand(2048, dims[0], generator=g) * 2 - 1
+    y = _chain(layers, acts)(x.cuda()).as_tensor("torch").cpu().numpy()
+    ref = O.mlp_forward(x.numpy(), _np_layers(layers), acts, ["f16"] * 3)
+    _assert_fp16_parity(y, ref, "-".join(acts))
+
+
+def test_generic_unaligned_rows_take_scalar_loads():
+    """x viewed 4 bytes past a 16-byte boundary: layer 0 reads its row with
+    scalar loads instead of 16-byte ones; the result is the same."""
+    g = WL.gen(10)
+    dims = [16, 64, 8]
+    layers = [((torch.rand(dims[i + 1], dims[i], generator=g) * 2 - 1) / dims[i] ** 0.5,
+               torch.zeros(dims[i + 1])) for i in range(2)]
+    acts = ["relu", "none"]
+    base = torch.empty(512 * 16 + 1, device="cuda")
+    x = base[1:].view(512, 16)
+    x.copy_((torch.rand(512, 16, generator=g) * 2 - 1).cuda())
+    assert x.data_ptr() % 16 == 4
+    m = _chain(layers, acts)
+    y = m(rdv.wrap(x)).as_tensor("torch").cpu().numpy()
+    ref = O.mlp_forward(x.cpu().numpy(), _np_layers(layers), acts, ["f16"] * 2)
+    _assert_fp16_parity(y, ref, "unaligned x")
 
 
 def test_freq_encoding_odd_octaves_generic_path():

@@ -148,3 +148,42 @@ def test_raymarching_transmittance_transform_scale_and_cutoff():
                                    transform=np.array(M).reshape(4, 3), step=0.01, density_scale=12.0)
     assert (ref == 0).any() and (ref == 1).any()
     _close(T, ref, 1e-3, 1e-6, "transformed transmittance")
+
+
+def _rand_field(dims, seed, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    layers = []
+    for i in range(len(dims) - 1):
+        lim = (6.0 / dims[i]) ** 0.5 * scale
+        layers.append((((torch.rand(dims[i + 1], dims[i], generator=g) * 2 - 1) * lim).half().float(),
+                       torch.rand(dims[i + 1], generator=g) * 0.2 - 0.1))
+    return layers
+
+
+@pytest.mark.parametrize("dims", [[3, 32, 32, 4], [3, 128, 128, 4], [3, 200, 4]])
+def test_emission_absorption_runtime_shaped_fields(dims):
+    """Fields without a compile-time instance run on the runtime-shaped kernel."""
+    layers = _rand_field(dims, seed=len(dims) * 100 + dims[1])
+    cam = rdv.Cameras(20, 14, WL.c4_pose().cuda())
+    img = (cam >> rdv.EmissionAbsorption(_field(layers), samples=64))().as_tensor("torch").cpu().numpy()
+    rays = R.camera_rays(20, 14, WL.c4_pose().numpy()).reshape(-1, 6)
+    ref = R.render_ea(rays, _np(layers), 64)
+    _close(img.reshape(-1, 3), ref, 1e-3, 1e-5, f"EA field {dims}")
+    assert (ref > 0.01).any()
+
+
+@pytest.mark.parametrize("dims,head", [([3, 32, 32, 1], "softplus"), ([3, 128, 128, 1], "relu"),
+                                       ([3, 64, 96, 64, 1], "softplus")])
+def test_raymarching_transmittance_runtime_shaped_extinction(dims, head):
+    """Any LinearFast Map[3, 1] as the extinction, as the reference marches any
+    extinction map it is given."""
+    layers = _rand_field(dims, seed=dims[1] + 7)
+    ext = _field(layers, head=head if head == "softplus" else None)
+    if head == "relu":
+        ext = ext >> rdv.relu
+    cam = rdv.Cameras(9, 7, WL.c4_pose().cuda())
+    T = (cam >> rdv.RaymarchingTransmittance(ext, step_size=0.004, density_scale=4.0))().as_tensor("torch")
+    rays = cam().as_tensor("torch").reshape(-1, 6).cpu().numpy()
+    ref = R.raymarch_transmittance(rays, _np(layers), head=head, step=0.004, density_scale=4.0)
+    _close(T.reshape(-1).cpu().numpy(), ref, 1e-4, 1e-6, f"transmittance {dims}")
+    assert (ref < 0.99).any() and (ref == 1).any()
