@@ -9,9 +9,12 @@ A step is one call over the 2^20 points with inputs already resident in HBM
 
     python bench.py [--steps K] [--warmup W] [--gpus 1]
 
-Prints ONE JSON line.  `roofline` is computed live from HIP events recorded on
-the stream the kernels run on; `cpu_baseline` times this repo's numpy
-restatement (oracle/) on a bounded sample on the host cores.
+Prints ONE JSON line.  One clock throughout: `value`, `ms_per_step` and
+`roofline` all come from HIP events recorded on the stream the kernels run on,
+around exactly the K timed steps (the wall-clock time of the same region, with
+its synchronisations, is reported beside them as `wall_ms_per_step`).
+`cpu_baseline` times this repo's torch-CPU restatement (oracle/torch_cpu.py) on
+the host cores, C1 in full and bounded samples of C2-C5.
 """
 from __future__ import annotations
 
@@ -46,13 +49,16 @@ C4_FLOP_PER_SAMPLE = 2 * (3 * 64 + 64 * 64 + 64 * 64 + 64 * 4)   # 17,280
 C4_COMPOSITE_BYTES_PER_RAY = 128 * 16 + 4 + 12
 # C5: forward 2 (32 128 + 7 128^2 + 128 16), dW the same, dX of layers 2..9
 C5_FLOP_PER_POINT = 241664 + 241664 + 233472                        # 716,800
+# Runtime-shaped matrix-core MLP (no compile-time instance): 2^20 points, 64 -> 128 -> 128 -> 128 -> 16
+GEN_DIMS = [64, 128, 128, 128, 16]
+GEN_FLOP_PER_POINT = 2 * sum(GEN_DIMS[i] * GEN_DIMS[i + 1] for i in range(len(GEN_DIMS) - 1))  # 86,016
 
 
 def _log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def _mlp_setup(x_cpu, layers, acts, enc=None):
+def _mlp_setup(x_cpu, layers, acts, enc=None, rotate=ROTATE):
     """Builds the rdv chain, packs it, and returns (desc, packed, rotating x/y sets)."""
     import torch
     import rdv_project_amd as rdv
@@ -67,8 +73,8 @@ def _mlp_setup(x_cpu, layers, acts, enc=None):
     p = _chain.plan_chain(m, x_cpu.shape[1])
     packed = _chain.packed_params(m, p)
     xd = x_cpu.cuda()
-    xs = [xd] + [xd.clone() for _ in range(ROTATE - 1)]
-    ys = [torch.empty(x_cpu.shape[0], p.out_features, device="cuda") for _ in range(ROTATE)]
+    xs = [xd] + [xd.clone() for _ in range(rotate - 1)]
+    ys = [torch.empty(x_cpu.shape[0], p.out_features, device="cuda") for _ in range(rotate)]
     return m, p, packed, xs, ys
 
 
@@ -105,11 +111,11 @@ def _time_launches(launch, steps: int, warmup: int, prewarm_s: float | None = No
     return wall, ev
 
 
-def bench_mlp(x_cpu, layers, acts, enc, steps, warmup):
+def bench_mlp(x_cpu, layers, acts, enc, steps, warmup, rotate=ROTATE):
     import torch
     from rdv_project_amd import _lib
     lib = _lib.load()
-    m, p, packed, xs, ys = _mlp_setup(x_cpu, layers, acts, enc)
+    m, p, packed, xs, ys = _mlp_setup(x_cpu, layers, acts, enc, rotate)
     n = x_cpu.shape[0]
     stream = C.c_void_p(torch.cuda.current_stream().cuda_stream)
     dptr = C.byref(p.desc)
@@ -120,7 +126,7 @@ def bench_mlp(x_cpu, layers, acts, enc, steps, warmup):
     fwd = lib.rdv_mlp_forward
 
     def launch(i):
-        k = i % ROTATE
+        k = i % rotate
         rc = fwd(dptr, pk, xp[k], yp[k], nn, stream)
         if rc != 0:
             _lib.check(rc, "mlp forward")
@@ -317,33 +323,107 @@ def bench_tensor_ops(steps, warmup):
     }
 
 
-def cpu_baseline_c2(sample: int = 1 << 16):
-    """The oracle's C2 forward on `sample` points: 3 warm-ups, median of 5."""
-    import numpy as np
-    from oracle import mlp as O
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+    return platform.processor() or "unknown"
+
+
+def _median_time(fn, warm: int = 3, runs: int = 5) -> float:
+    for _ in range(warm):
+        fn()
+    ts = []
+    for _ in range(runs):
+        t = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t)
+    return statistics.median(ts)
+
+
+def cpu_baseline():
+    """The torch-CPU restatement (oracle/torch_cpu.py) on the host cores: C1 in
+    full, bounded samples of C2 (2^18 points), C3 (the whole 256x256 image), C4
+    (4,096 rays x 128 samples) and C5 (2^16 points, forward + backward); each a
+    median of 5 after 3 warm-ups, data generation excluded."""
+    import torch
+    from oracle import torch_cpu as TC
     from rdv_project_amd import workloads as WL
     cores = len(os.sched_getaffinity(0))
+    prev_threads = torch.get_num_threads()
+    torch.set_num_threads(cores)
     try:
-        from threadpoolctl import threadpool_limits
-        limiter = threadpool_limits(limits=cores)
-    except Exception:  # noqa: BLE001 - threadpoolctl is optional
-        limiter = None
-    x, layers = WL.c2(sample)
-    L = [(w.numpy(), b.numpy()) for w, b in layers]
-    xn = x.numpy()
-    acts = ["relu"] * 3 + ["none"]
-    times = []
-    for i in range(8):
-        t = time.perf_counter()
-        O.mlp_forward(xn, L, acts, ["f16"] * 4, encoding=(WL.C2_OCTAVES, WL.C2_PAD))
-        if i >= 3:
-            times.append(time.perf_counter() - t)
-    if limiter is not None:
-        limiter.unregister() if hasattr(limiter, "unregister") else None
-    med = statistics.median(times)
-    return {"value": round(sample / med / 1e6, 4), "unit": "Mpoints/s", "cores": cores, "kind": "port",
-            "sample": f"C2 forward on {sample} of the 2^20 points (numpy oracle: fp16-rounded operands, "
-                      f"float64 sums), median of 5 after 3 warm-ups; BLAS threads = {cores}"}
+        with torch.no_grad():
+            n2 = 1 << 18
+            x2, l2 = WL.c2(n2)
+            p2 = TC.pack_layers(l2)
+            t2 = _median_time(lambda: TC.mlp_forward(x2, p2, ["relu"] * 3 + ["none"], (WL.C2_OCTAVES, WL.C2_PAD)))
+            x1, l1 = WL.c1()
+            p1 = TC.pack_layers(l1)
+            t1 = _median_time(lambda: TC.mlp_forward(x1, p1, ["relu"] * 4 + ["none"]))
+            x3, w3, _ = WL.c3()
+            x3f, w3f = x3.float(), w3.float()
+            t3 = _median_time(lambda: TC.conv3x3(x3f, w3f, relu=True), warm=1, runs=3)
+            p4 = TC.pack_layers(WL.c4_mlp())
+            g = torch.Generator().manual_seed(0)
+            rays = torch.cat([torch.tensor([[0.0, 0.0, -3.5]]).expand(4096, 3),
+                              torch.nn.functional.normalize(torch.randn(4096, 3, generator=g) * 0.15 +
+                                                            torch.tensor([0.0, 0.0, 1.0]), dim=1)], dim=1)
+            t4 = _median_time(lambda: TC.render_ea(rays, p4, WL.C4_SAMPLES), warm=1, runs=3)
+        n5 = 1 << 16
+        x5, tg5, l5 = WL.c5(n5)
+        x5f = x5.float()
+        params = [(w.clone().requires_grad_(True), b.clone().requires_grad_(True)) for w, b in l5]
+        t5 = _median_time(lambda: TC.train_step(x5f, tg5, params), warm=1, runs=3)
+    finally:
+        torch.set_num_threads(prev_threads)
+    return {
+        "value": round(n2 / t2 / 1e6, 3),
+        "unit": "Mpoints/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": f"C2 forward on {n2} of the 2^20 points: torch-CPU fp32 GEMMs on fp16-rounded operands "
+                  f"(oracle/torch_cpu.py), torch threads = {cores}, median of 5 after 3 warm-ups",
+        "cpu_model": _cpu_model(),
+        "per_config": {
+            "C1_full_Mpoints_per_s": round(x1.shape[0] / t1 / 1e6, 3),
+            "C2_sample_Mpoints_per_s": round(n2 / t2 / 1e6, 3),
+            "C3_full_TFLOP_s_direct_equiv": round(C3_DIRECT_FLOP / t3 / 1e12, 4),
+            "C4_sample_Msamples_per_s": round(4096 * WL.C4_SAMPLES / t4 / 1e6, 3),
+            "C5_sample_Mpoints_per_s": round(n5 / t5 / 1e6, 4),
+            "C5_sample_TFLOP_s": round(C5_FLOP_PER_POINT * n5 / t5 / 1e12, 4),
+        },
+    }
+
+
+def bench_generic_mlp(steps, warmup):
+    """The runtime-shaped matrix-core MLP (a chain without a compile-time
+    instance): 2^20 points U[-1,1]^64 (seed 13), 64 -> 128 -> 128 -> 128 -> 16,
+    ReLU, Kaiming-uniform fp16 weights (seed 14)."""
+    import torch
+    from rdv_project_amd import workloads as WL
+    n = 1 << 20
+    x = torch.rand(n, GEN_DIMS[0], generator=WL.gen(13)) * 2.0 - 1.0
+    layers = WL.kaiming_uniform_f16([(GEN_DIMS[i + 1], GEN_DIMS[i]) for i in range(len(GEN_DIMS) - 1)], seed=14)
+    acts = ["relu"] * (len(layers) - 1) + ["none"]
+    wall, ev, name = bench_mlp(x, layers, acts, None, steps, warmup, rotate=4)
+    tflops = GEN_FLOP_PER_POINT * n / (ev * 1e-3) / 1e12
+    return {
+        "workload": "runtime-shaped LinearFast chain: 2^20 points U[-1,1]^64 (seed 13), 64 -> 128 -> 128 -> 128 -> 16, "
+                    "ReLU, Kaiming-uniform fp16 weights (seed 14), fp32 accumulate, one kernel",
+        "kernel": name,
+        "us_per_call": round(ev * 1e3, 2),
+        "wall_us_per_call": round(wall * 1e3, 2),
+        "Mpoints_per_s": round(n / (ev * 1e-3) / 1e6, 1),
+        "TFLOP_s": round(tflops, 1),
+        "mfma_peak_pct": round(100 * tflops / PEAK_FP16_TFLOPS, 2),
+        "flop_per_point": GEN_FLOP_PER_POINT,
+    }
 
 
 def main() -> int:
@@ -394,9 +474,9 @@ def main() -> int:
     acts = ["relu"] * 3 + ["none"]
     wall, ev, kname = bench_mlp(x, layers, acts, enc, args.steps, args.warmup)
     n = x.shape[0]
-    mpts = n / (wall * 1e-3) / 1e6
+    mpts = n / (ev * 1e-3) / 1e6
     achieved = C2_FLOP_PER_POINT * n / (ev * 1e-3) / 1e12
-    _log(f"C2 {kname}: wall {wall * 1e3:.2f} us/step, events {ev * 1e3:.2f} us/launch, "
+    _log(f"C2 {kname}: events {ev * 1e3:.2f} us/step, wall {wall * 1e3:.2f} us/step, "
          f"{mpts:.0f} Mpts/s, {achieved:.1f} TFLOP/s")
 
     extras = {}
@@ -424,11 +504,15 @@ def main() -> int:
         _log("tensor ops")
         extras["tensor_ops"] = bench_tensor_ops(20, 3)
         _log(f"tensor ops {extras['tensor_ops']}")
+        _log("generic MLP")
+        extras["generic_mlp"] = bench_generic_mlp(max(args.steps // 5, 10), args.warmup)
+        _log(f"generic MLP {extras['generic_mlp']}")
 
     cpu = None
     if not args.no_cpu_baseline:
-        _log("CPU baseline (oracle, bounded sample)")
-        cpu = cpu_baseline_c2()
+        _log("CPU baseline (torch-CPU restatement, bounded samples)")
+        cpu = cpu_baseline()
+        _log(f"CPU baseline {cpu}")
 
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "mlp_fused_c2_traffic.json")
@@ -443,7 +527,9 @@ def main() -> int:
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(wall, 6),
+        "ms_per_step": round(ev, 6),
+        "wall_ms_per_step": round(wall, 6),
+        "clock": "hip_events on the launch stream around the K timed steps (value, ms_per_step, roofline)",
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -463,6 +549,8 @@ def main() -> int:
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_FP16_TFLOPS, 4),
             "traffic": traffic,
+            "traffic_source": "profiles/mlp_fused_c2_traffic.json: two rocprofv3 --pmc runs of this command "
+                              "(FETCH_SIZE, WRITE_SIZE) scaled by a copy kernel of known size",
         },
         "mfma_peak_pct": round(100.0 * achieved / PEAK_FP16_TFLOPS, 2),
         "cpu_baseline": cpu,
