@@ -206,6 +206,60 @@ int rdv_linear_op(const rdv_linear_op_desc* desc, const float* x, const void* we
  * src/rdv/shaders/tensors/relu_tensor_op.h:3-22). */
 int rdv_relu_op(const float* x, float* y, int64_t n, void* stream);
 
+/* Direct 2-D convolution of a KH x KW kernel, stride 1, 'same' zero padding
+ * (KH / 2 rows above, KW / 2 columns to the left, the rest below / right),
+ * over a channels-last fp32 image x[H*W, cin] -> y[H*W, cout] fp32. */
+typedef struct rdv_conv2d_desc {
+  int32_t H, W;       /* image size (>= 0)                                         */
+  int32_t cin;        /* multiple of 8 (RDV_PREC_F16) or 4 (RDV_PREC_F32)           */
+  int32_t cout;       /* multiple of 4                                              */
+  int32_t kh, kw;     /* kernel size, 1..31                                         */
+  int32_t precision;  /* RDV_PREC_F16: x and w rounded to fp16, fp32 accumulation;
+                         RDV_PREC_F32: fp32 throughout                              */
+  int32_t w_layout;   /* RDV_WLAYOUT_RSCK [kh][kw][cin][cout] (the tensor ops') or
+                         RDV_WLAYOUT_KCRS [cout][cin][kh][kw] (PyTorch, Conv2dGrid) */
+  int32_t relu;       /* 1: y = max(y, 0) after the bias (build-defined fusion)     */
+  int32_t reserved;   /* 0                                                          */
+} rdv_conv2d_desc;
+
+/* Host-only shape check; launches nothing. */
+int rdv_conv2d_validate(const rdv_conv2d_desc* desc);
+
+/* y = conv(x, w) + bias: y[p][o] = bias[o] + sum over taps (kh, kw) inside the
+ * image and channels c of x[tap pixel][c] * w[kh][kw][c][o], the taps in (kh,
+ * kw) order and channels ascending (fp32 association order otherwise
+ * unspecified).  x, y: 16-byte aligned fp32 device pointers; w: fp32 device
+ * pointer in desc->w_layout, read at every call; bias: fp32 [cout] or NULL.
+ * Replaces the dispatches of Conv2DTensorOp (src/rdv/domain/nn.py:414-470,
+ * src/rdv/shaders/tensors/conv2d_tensor_op.h:20-80; RDV_PREC_F32) and of
+ * Conv2DTensorOpFast, Conv2DTensorOpSimple, Conv2DTensorOpSimple3x3 and
+ * Conv2DTensorOpWindow3x3 (nn.py:608-1000, shaders/tensors/conv2d_tensor_op_
+ * {fast,simple,simple3x3,window3x3}.h; RDV_PREC_F16), and of the grid
+ * convolutions Conv2dGrid / Conv2D (nn.py:122-266, shaders/grids/conv2d.h,
+ * conv2d_per_output.h) over a materialised input grid. */
+int rdv_conv2d(const rdv_conv2d_desc* desc, const float* x, const float* w, const float* bias, float* y,
+               void* stream);
+
+/* Data movement over channels-last fp32 images x[H*W, C] (C a multiple of 4;
+ * x and y 16-byte aligned device pointers; the reference asks C % 8 == 0 and
+ * row counts that are multiples of 4, which the Python classes keep).
+ * y[(H/2)*(W/2), C] = 2x2 average pool, stride 2: ((x00 + x01) + x10) + x11
+ * summed left to right in fp32, times 0.25 (H, W even).
+ * Replaces Downsample2xTensorOp (src/rdv/domain/nn.py:1090-1107,
+ * src/rdv/shaders/tensors/downsample2x_tensor_op.h:1-37). */
+int rdv_downsample2x(const float* x, int64_t H, int64_t W, int32_t C, float* y, void* stream);
+
+/* y[(2H)*(2W), C]: nearest-neighbour 2x upsample of x[H*W, C].
+ * Replaces Upsample2xTensorOp (src/rdv/domain/nn.py:1110-1125,
+ * src/rdv/shaders/tensors/upsample2x_tensor_op.h:1-29). */
+int rdv_upsample2x(const float* x, int64_t H, int64_t W, int32_t C, float* y, void* stream);
+
+/* y[rows, C1 + C2] = [x1[rows, C1] | x2[rows, C2]] (C1, C2 multiples of 4).
+ * Replaces ConcatTensorOp (src/rdv/domain/nn.py:1128-1150,
+ * src/rdv/shaders/tensors/concat_tensor_op.h:1-25). */
+int rdv_concat_channels(const float* x1, int32_t C1, const float* x2, int32_t C2, int64_t rows, float* y,
+                        void* stream);
+
 /* ------------------------------------------------- MLP training step (C5) */
 /* Bytes of workspace rdv_mlp_train_step needs for `desc` and n points (< 0 if
  * the chain is not supported by the training kernels). */

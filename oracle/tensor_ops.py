@@ -73,3 +73,79 @@ def max_subgroups(fixed_bytes, per_subgroup_bytes, divides, budget=49152, cap=32
     while spt * 2 <= cap and fixed_bytes + spt * 2 * per_subgroup_bytes <= budget and divides(spt * 2):
         spt *= 2
     return spt
+
+
+# ----------------------------------------------------------- data movement
+# Channels-last fp32 images x [H*W, C], row r = h * W + w.  Bit-exact restatements.
+
+def downsample2x(x, H: int, W: int) -> np.ndarray:
+    """Downsample2xTensorOp (domain/nn.py:1090-1107, shaders/tensors/downsample2x_tensor_op.h:22-34):
+    v = x00 + x01 + x10 + x11 summed left to right in fp32, result v * 0.25."""
+    x = np.asarray(x, np.float32).reshape(H, W, -1)
+    a, b = x[0::2, 0::2], x[0::2, 1::2]
+    c, d = x[1::2, 0::2], x[1::2, 1::2]
+    v = ((a + b) + c) + d                      # float32 adds, in the shader's order
+    return (v * np.float32(0.25)).reshape((H // 2) * (W // 2), -1)
+
+
+def upsample2x(x, H: int, W: int) -> np.ndarray:
+    """Upsample2xTensorOp (domain/nn.py:1110-1125, shaders/tensors/upsample2x_tensor_op.h:19-27):
+    output pixel (oh, ow) copies input pixel (oh // 2, ow // 2)."""
+    x = np.asarray(x, np.float32).reshape(H, W, -1)
+    return np.repeat(np.repeat(x, 2, axis=0), 2, axis=1).reshape(4 * H * W, -1)
+
+
+def concat(x1, x2) -> np.ndarray:
+    """ConcatTensorOp (domain/nn.py:1128-1150, shaders/tensors/concat_tensor_op.h:19-23):
+    columns < C1 from x1, the rest from x2."""
+    return np.concatenate([np.asarray(x1, np.float32), np.asarray(x2, np.float32)], axis=1)
+
+
+# ------------------------------------------------------------ direct conv
+def _im2col(x, H: int, W: int, KH: int, KW: int) -> np.ndarray:
+    """[H*W, KH*KW*C] patches in the shaders' K order (kh, kw, channel): tap
+    (kh, kw) of output pixel (h, w) reads input (h + kh - KH//2, w + kw - KW//2),
+    zero outside the image (conv2d_tensor_op.h:27-28, 45-53)."""
+    x = np.asarray(x, np.float64).reshape(H, W, -1)
+    C = x.shape[2]
+    ph, pw = KH // 2, KW // 2
+    xp = np.zeros((H + KH - 1, W + KW - 1, C))
+    xp[ph:ph + H, pw:pw + W] = x
+    cols = [xp[kh:kh + H, kw:kw + W] for kh in range(KH) for kw in range(KW)]
+    return np.concatenate(cols, axis=2).reshape(H * W, KH * KW * C)
+
+
+def conv2d_op_f32(x, w, b, H: int, W: int) -> np.ndarray:
+    """Conv2DTensorOp (domain/nn.py:414-470, shaders/tensors/conv2d_tensor_op.h:20-80):
+    acc = bias[o]; acc += x[tap pixel][k] * w[kh][kw][k][o] over the valid taps in
+    (kh, kw) order and k ascending, fp32.  w is [KH, KW, CIN, COUT]."""
+    w = np.asarray(w, np.float32)
+    KH, KW, C, K = w.shape
+    acc = _im2col(x, H, W, KH, KW) @ w.astype(np.float64).reshape(KH * KW * C, K)
+    return (acc + np.asarray(b, np.float64)).astype(np.float32)
+
+
+def conv2d_op_f16(x, w, b, H: int, W: int) -> np.ndarray:
+    """Conv2DTensorOp{Fast,Simple,Simple3x3,Window3x3} (domain/nn.py:608-1000,
+    shaders/tensors/conv2d_tensor_op_{fast,simple,simple3x3,window3x3}.h): x and w
+    staged as float16 (e.g. conv2d_tensor_op_fast.h:77-86), products summed in
+    fp32 over every tap and channel, fp32 bias (seeded by Simple/Simple3x3/
+    Window3x3, added after by Fast: the same value up to the fp32 sum order)."""
+    w = M.f16(w)
+    KH, KW, C, K = w.shape
+    acc = _im2col(M.f16(x), H, W, KH, KW) @ w.astype(np.float64).reshape(KH * KW * C, K)
+    return (acc + np.asarray(b, np.float64)).astype(np.float32)
+
+
+def conv2d_error_bound(x, w, b, H: int, W: int, f16: bool) -> np.ndarray:
+    """gamma_n (sum |x w| + |b|) per output, n = KH KW CIN + 2: the bound on
+    any fp32 summation order of the products (the same argument as
+    gemm_error_bound)."""
+    w = np.asarray(w, np.float32)
+    KH, KW, C, K = w.shape
+    xs = M.f16(x) if f16 else np.asarray(x, np.float32)
+    ws = M.f16(w) if f16 else w
+    mag = np.abs(_im2col(xs, H, W, KH, KW)) @ np.abs(ws.astype(np.float64)).reshape(KH * KW * C, K)
+    n = KH * KW * C + 2
+    u = 2.0 ** -24
+    return (n * u / (1 - n * u)) * (mag + np.abs(np.asarray(b, np.float64)))

@@ -25,7 +25,15 @@ from ._render import composite
 from ._train import mse_backward
 from .rendering import Cameras, EmissionAbsorption, RaymarchingTransmittance
 from .nn import (
+    ConcatTensorOp,
+    Conv2DTensorOp,
+    Conv2DTensorOpFast,
+    Conv2DTensorOpSimple,
+    Conv2DTensorOpSimple3x3,
+    Conv2DTensorOpWindow3x3,
     Conv2DTensorOpWinograd3x3,
+    Downsample2xTensorOp,
+    Upsample2xTensorOp,
     DensityRGB,
     LinearTensorOp,
     LinearTensorOpFast,

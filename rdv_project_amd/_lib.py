@@ -85,6 +85,22 @@ class LinearOpDesc(C.Structure):
     ]
 
 
+class Conv2dDesc(C.Structure):
+    """Mirror of rdv_conv2d_desc."""
+    _fields_ = [
+        ("H", C.c_int32),
+        ("W", C.c_int32),
+        ("cin", C.c_int32),
+        ("cout", C.c_int32),
+        ("kh", C.c_int32),
+        ("kw", C.c_int32),
+        ("precision", C.c_int32),
+        ("w_layout", C.c_int32),
+        ("relu", C.c_int32),
+        ("reserved", C.c_int32),
+    ]
+
+
 class RDVError(RuntimeError):
     """A HIP runtime failure reported by the library."""
 
@@ -117,6 +133,12 @@ _SIGNATURES = {
     "rdv_linear_op": (C.c_int, [C.POINTER(LinearOpDesc), C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
                                 C.c_void_p]),
     "rdv_relu_op": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int64, C.c_void_p]),
+    "rdv_conv2d_validate": (C.c_int, [C.POINTER(Conv2dDesc)]),
+    "rdv_conv2d": (C.c_int, [C.POINTER(Conv2dDesc), C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p]),
+    "rdv_downsample2x": (C.c_int, [C.c_void_p, C.c_int64, C.c_int64, C.c_int32, C.c_void_p, C.c_void_p]),
+    "rdv_upsample2x": (C.c_int, [C.c_void_p, C.c_int64, C.c_int64, C.c_int32, C.c_void_p, C.c_void_p]),
+    "rdv_concat_channels": (C.c_int, [C.c_void_p, C.c_int32, C.c_void_p, C.c_int32, C.c_int64, C.c_void_p,
+                                      C.c_void_p]),
     "rdv_winograd3x3_validate": (C.c_int, [C.POINTER(ConvDesc)]),
     "rdv_winograd3x3_weight_bytes": (C.c_int64, [C.c_int32, C.c_int32]),
     "rdv_winograd3x3_transform_weight": (C.c_int, [C.c_void_p, C.c_int32, C.c_int32, C.c_int32, C.c_int32,

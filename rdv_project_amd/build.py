@@ -30,6 +30,8 @@ SOURCES = [
     "render.hip",
     "train.hip",
     "linear_op.hip",
+    "tensor_data.hip",
+    "conv_op.hip",
 ]
 
 ARCH = os.environ.get("RDV_OFFLOAD_ARCH", "gfx950")

@@ -84,6 +84,13 @@ int launch_linear_op(const rdv_linear_op_desc& d, const float* x, const void* w,
                      hipStream_t stream);
 int launch_relu_op(const float* x, float* y, int64_t n, hipStream_t stream);
 
+int conv2d_check(const rdv_conv2d_desc& d, std::string* why);
+int launch_conv2d(const rdv_conv2d_desc& d, const float* x, const float* w, const float* bias, float* y,
+                  hipStream_t stream);
+int launch_downsample2x(const float* x, int64_t H, int64_t W, int C, float* y, hipStream_t stream);
+int launch_upsample2x(const float* x, int64_t H, int64_t W, int C, float* y, hipStream_t stream);
+int launch_concat(const float* x1, int C1, const float* x2, int C2, int64_t rows, float* y, hipStream_t stream);
+
 static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 static int check_linear_op(const rdv_linear_op_desc* d) {
@@ -284,6 +291,64 @@ int rdv_relu_op(const float* x, float* y, int64_t n, void* stream) {
   if (!x || !y) return fail(RDV_ERR_INVALID, "relu op: NULL pointer");
   if (!aligned16(x) || !aligned16(y)) return fail(RDV_ERR_INVALID, "relu op: x and y must be 16-byte aligned");
   return launch_relu_op(x, y, n, static_cast<hipStream_t>(stream));
+}
+
+static int check_conv2d(const rdv_conv2d_desc* d) {
+  if (!d) return fail(RDV_ERR_INVALID, "conv2d descriptor is NULL");
+  std::string why;
+  if (conv2d_check(*d, &why) != RDV_OK) return fail(RDV_ERR_INVALID, "conv2d: " + why);
+  return RDV_OK;
+}
+
+int rdv_conv2d_validate(const rdv_conv2d_desc* desc) { return check_conv2d(desc); }
+
+int rdv_conv2d(const rdv_conv2d_desc* desc, const float* x, const float* w, const float* bias, float* y,
+               void* stream) {
+  if (int rc = check_conv2d(desc)) return rc;
+  if (int64_t(desc->H) * desc->W == 0) return RDV_OK;
+  if (!x || !w || !y) return fail(RDV_ERR_INVALID, "conv2d: NULL pointer argument");
+  if (!aligned16(x) || !aligned16(y)) return fail(RDV_ERR_INVALID, "conv2d: x and y must be 16-byte aligned");
+  if (reinterpret_cast<uintptr_t>(w) % 4 || reinterpret_cast<uintptr_t>(bias) % 4)
+    return fail(RDV_ERR_INVALID, "conv2d: w and bias must be 4-byte aligned");
+  return launch_conv2d(*desc, x, w, bias, y, static_cast<hipStream_t>(stream));
+}
+
+static int check_image(const char* what, int64_t H, int64_t W, int32_t C) {
+  if (H < 0 || W < 0) return fail(RDV_ERR_INVALID, std::string(what) + ": H and W must be >= 0");
+  if (C < 4 || C % 4) return fail(RDV_ERR_INVALID, std::string(what) + ": channels (" + std::to_string(C) +
+                                                       ") must be a positive multiple of 4");
+  if (H > (int64_t(1) << 24) || W > (int64_t(1) << 24) || H * W > (int64_t(1) << 40) / C)
+    return fail(RDV_ERR_INVALID, std::string(what) + ": image too large");
+  return RDV_OK;
+}
+
+int rdv_downsample2x(const float* x, int64_t H, int64_t W, int32_t C, float* y, void* stream) {
+  if (int rc = check_image("downsample2x", H, W, C)) return rc;
+  if (H % 2 || W % 2) return fail(RDV_ERR_INVALID, "downsample2x: H and W must be even");
+  if (H == 0 || W == 0) return RDV_OK;
+  if (!x || !y) return fail(RDV_ERR_INVALID, "downsample2x: NULL pointer argument");
+  if (!aligned16(x) || !aligned16(y)) return fail(RDV_ERR_INVALID, "downsample2x: x and y must be 16-byte aligned");
+  return launch_downsample2x(x, H, W, C, y, static_cast<hipStream_t>(stream));
+}
+
+int rdv_upsample2x(const float* x, int64_t H, int64_t W, int32_t C, float* y, void* stream) {
+  if (int rc = check_image("upsample2x", H, W, C)) return rc;
+  if (H == 0 || W == 0) return RDV_OK;
+  if (!x || !y) return fail(RDV_ERR_INVALID, "upsample2x: NULL pointer argument");
+  if (!aligned16(x) || !aligned16(y)) return fail(RDV_ERR_INVALID, "upsample2x: x and y must be 16-byte aligned");
+  return launch_upsample2x(x, H, W, C, y, static_cast<hipStream_t>(stream));
+}
+
+int rdv_concat_channels(const float* x1, int32_t C1, const float* x2, int32_t C2, int64_t rows, float* y,
+                        void* stream) {
+  if (C1 < 4 || C1 % 4 || C2 < 4 || C2 % 4)
+    return fail(RDV_ERR_INVALID, "concat: channel counts must be positive multiples of 4");
+  if (rows < 0 || rows > (int64_t(1) << 40) / (int64_t(C1) + C2)) return fail(RDV_ERR_INVALID, "concat: bad row count");
+  if (rows == 0) return RDV_OK;
+  if (!x1 || !x2 || !y) return fail(RDV_ERR_INVALID, "concat: NULL pointer argument");
+  if (!aligned16(x1) || !aligned16(x2) || !aligned16(y))
+    return fail(RDV_ERR_INVALID, "concat: x1, x2 and y must be 16-byte aligned");
+  return launch_concat(x1, C1, x2, C2, rows, y, static_cast<hipStream_t>(stream));
 }
 
 int64_t rdv_mlp_train_workspace_bytes(const rdv_mlp_desc* desc, int64_t n) {

@@ -1,0 +1,366 @@
+// Direct 2-D convolution of any KH x KW kernel, stride 1, 'same' zero padding
+// (pad = K / 2 on the top and left, as the reference's kernels index it), over
+// channels-last fp32 images: y[H*W, COUT] = conv(x[H*W, CIN], w) + bias.
+//
+// Replaces the dispatches of Conv2DTensorOp (fp32, src/rdv/domain/nn.py:414-470,
+// src/rdv/shaders/tensors/conv2d_tensor_op.h:20-80), and of the fp16-operand
+// variants Conv2DTensorOpFast (nn.py:608-668, conv2d_tensor_op_fast.h),
+// Conv2DTensorOpSimple (nn.py:669-756, conv2d_tensor_op_simple.h),
+// Conv2DTensorOpSimple3x3 (nn.py:757-850, conv2d_tensor_op_simple3x3.h) and
+// Conv2DTensorOpWindow3x3 (nn.py:851-1000, conv2d_tensor_op_window3x3.h).  The
+// four fp16 variants compute one function -- x and w rounded to fp16, products
+// summed in fp32 over K = KH KW CIN, fp32 bias -- and differ only in tiling,
+// so one kernel serves them; the fp32 op is the same kernel on fp32 matrix
+// cores.  The reference's sum order (taps in (kh, kw) order, channels
+// ascending) is the order of the K index here; only the fp32 association
+// inside the matrix cores differs.
+//
+// MI355X mapping: implicit GEMM.  M = the H W output pixels, N = COUT, K = the
+// KH KW CIN taps-and-channels.  A block of 4 waves owns one block of <= 128
+// output channels for the whole launch and stages that block of w into LDS
+// once, converted to fp16 (or kept fp32) in MFMA-fragment order; its waves
+// then walk 32-pixel tiles with a grid stride.  Per K chunk a lane gathers 8
+// (fp16) or 4 (fp32) consecutive channels of one tap of one pixel straight
+// from x -- the im2col matrix is never formed -- and the next chunk's loads are
+// issued before the current chunk's MFMAs.  Taps outside the image and K past
+// KH KW CIN read a clamped address and are zeroed on conversion, so every load
+// is in bounds and unconditional.  Neighbouring taps re-read neighbouring
+// pixels, which the L2 serves (a tile's receptive field is a few image rows).
+//   fp16: v_mfma_f32_16x16x32_f16, A = w[16 out][32 k], B = x^T[32 k][16 px]
+//   fp32: v_mfma_f32_16x16x4f32 over 16-k chunks (a lane's float4 feeds 4 MFMAs)
+// When a block of w exceeds the LDS budget it is restaged per K pass per tile.
+#include <algorithm>
+
+#include "rdv_common.h"
+
+namespace rdv {
+
+namespace {
+
+constexpr int kCvThreads = 256;
+constexpr int kCvWaves = kCvThreads / 64;
+constexpr int kCvRT = 2;            // 16-pixel subtiles per wave
+constexpr int kCvMaxOb = 128;       // output channels per block
+constexpr int64_t kCvLdsCap = 144 * 1024;
+
+struct ConvArgs {
+  const float* x;     // [H W, cin]
+  const float* w;     // RSCK [kh][kw][cin][cout] or KCRS [cout][cin][kh][kw], fp32
+  const float* bias;  // [cout] or null
+  float* y;           // [H W, cout]
+  int64_t rows;       // H W
+  int64_t tasks;      // pixel tiles of kCvWaves * 16 * kCvRT
+  int H, W, cin, cout, kh, kw, ph, pw;
+  int K;              // kh kw cin
+  int wlayout, relu;
+  int kp;             // K per LDS pass (multiple of the chunk width)
+  int passes;
+  int ob, n_ob;
+};
+
+template <bool F16>
+struct CvStep;
+template <>
+struct CvStep<true> {
+  static constexpr int kK = 32;   // K per chunk
+  static constexpr int kLane = 8; // consecutive channels per lane
+};
+template <>
+struct CvStep<false> {
+  static constexpr int kK = 16;
+  static constexpr int kLane = 4;
+};
+
+__device__ __forceinline__ float w_at(const ConvArgs& a, int o, int k) {
+  // k = tap * cin + ci, tap = kh * KW + kw
+  if (a.wlayout == RDV_WLAYOUT_RSCK) return a.w[int64_t(k) * a.cout + o];
+  const int tap = k / a.cin, ci = k - tap * a.cin;
+  return a.w[(int64_t(o) * a.cin + ci) * (a.kh * a.kw) + tap];
+}
+
+// w block [o0, o0 + ob) x K [k0, k0 + kp) into LDS, fragment order: slot
+// ((t * nkc + c) * 64 + lane) = 16 bytes, out o0 + 16 t + lane % 16, K
+// k0 + c kK + (lane / 16) kLane + 0 .. kLane-1 (fp16 halves or fp32 floats);
+// outputs past cout and K past KH KW CIN are zero.  Also the bias block.
+template <bool F16>
+__device__ void cv_stage(const ConvArgs& a, int o0, int k0, int nkc, f32x4* sw, float* sb) {
+  using S = CvStep<F16>;
+  const int nt = a.ob / 16;
+  const int slots = nt * nkc * 64;
+  for (int s = threadIdx.x; s < slots; s += kCvThreads) {
+    const int t = s / (nkc * 64);
+    const int rem = s - t * (nkc * 64);
+    const int c = rem >> 6, ln = rem & 63;
+    const int o = o0 + 16 * t + (ln & 15);
+    const int k = k0 + c * S::kK + (ln >> 4) * S::kLane;
+    f32x4 v = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (o < a.cout && k < a.K) {
+      if constexpr (F16) {
+        half8 h;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) h[i] = half_t(w_at(a, o, k + i));
+        v = __builtin_bit_cast(f32x4, h);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = w_at(a, o, k + i);
+      }
+    }
+    sw[s] = v;
+  }
+  for (int i = threadIdx.x; i < a.ob; i += kCvThreads)
+    sb[i] = (a.bias != nullptr && o0 + i < a.cout) ? a.bias[o0 + i] : 0.0f;
+}
+
+// One lane's view of its kCvRT pixels: image coordinates and validity.
+struct CvPix {
+  int h[kCvRT], w[kCvRT];
+  bool live[kCvRT];
+};
+
+// Gathers K chunk kk0 (this lane's kLane channels of one tap) for each pixel.
+template <bool F16>
+__device__ __forceinline__ void cv_load(const ConvArgs& a, const CvPix& px, int kk0, int q,
+                                        f32x4 (&raw)[kCvRT][CvStep<F16>::kLane / 4], bool (&ok)[kCvRT]) {
+  using S = CvStep<F16>;
+  const int kk = kk0 + q * S::kLane;
+  const int tap = kk / a.cin;
+  const int ci = kk - tap * a.cin;
+  const int th = tap / a.kw;
+  const int tw = tap - th * a.kw;
+  const bool kin = kk < a.K;
+#pragma unroll
+  for (int rr = 0; rr < kCvRT; ++rr) {
+    const int ih = px.h[rr] + th - a.ph, iw = px.w[rr] + tw - a.pw;
+    const bool v = kin && px.live[rr] && ih >= 0 && ih < a.H && iw >= 0 && iw < a.W;
+    const int64_t off = v ? (int64_t(ih) * a.W + iw) * a.cin + ci : 0;
+    const f32x4* src = reinterpret_cast<const f32x4*>(a.x + off);
+#pragma unroll
+    for (int j = 0; j < S::kLane / 4; ++j) raw[rr][j] = src[j];
+    ok[rr] = v;
+  }
+}
+
+template <bool F16, int NT>
+__device__ __forceinline__ void cv_mma(const f32x4* sw, int nt, int nkc, int c, int lane,
+                                       const f32x4 (&raw)[kCvRT][CvStep<F16>::kLane / 4], const bool (&ok)[kCvRT],
+                                       f32x4 (&acc)[kCvRT][NT]) {
+  if constexpr (F16) {
+    half8 xb[kCvRT];
+#pragma unroll
+    for (int rr = 0; rr < kCvRT; ++rr) {
+      half8 hv;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        hv[j] = half_t(raw[rr][0][j]);
+        hv[4 + j] = half_t(raw[rr][1][j]);
+      }
+      xb[rr] = ok[rr] ? hv : half8{};
+    }
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      if (t < nt) {
+        const half8 wh = __builtin_bit_cast(half8, sw[(t * nkc + c) * 64 + lane]);
+#pragma unroll
+        for (int rr = 0; rr < kCvRT; ++rr)
+          acc[rr][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wh, xb[rr], acc[rr][t], 0, 0, 0);
+      }
+    }
+  } else {
+    f32x4 xv[kCvRT];
+#pragma unroll
+    for (int rr = 0; rr < kCvRT; ++rr) xv[rr] = ok[rr] ? raw[rr][0] : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      if (t < nt) {
+        const f32x4 wv = sw[(t * nkc + c) * 64 + lane];
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+          for (int rr = 0; rr < kCvRT; ++rr)
+            acc[rr][t] = __builtin_amdgcn_mfma_f32_16x16x4f32(wv[s], xv[rr][s], acc[rr][t], 0, 0, 0);
+      }
+    }
+  }
+}
+
+template <bool F16, int NT>
+__global__ __launch_bounds__(kCvThreads) void conv_op_kernel(ConvArgs a) {
+  using S = CvStep<F16>;
+  extern __shared__ f32x4 cv_smem[];
+  const int nt = a.ob / 16;
+  const int nkc = a.kp / S::kK;
+  f32x4* sw = cv_smem;
+  float* sb = reinterpret_cast<float*>(cv_smem + nt * nkc * 64);
+  const int lane = threadIdx.x & 63;
+  const int q = lane >> 4;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  // blockIdx.x = pixel workgroup * n_ob + output block: the blocks sharing
+  // pixels are dispatched back to back, so their x re-reads hit the cache.
+  const int ob_idx = blockIdx.x % a.n_ob;
+  const int64_t rwg = blockIdx.x / a.n_ob;
+  const int64_t rstride = gridDim.x / a.n_ob;
+  const int o0 = ob_idx * a.ob;
+
+  if (a.passes == 1) {
+    cv_stage<F16>(a, o0, 0, nkc, sw, sb);
+    __syncthreads();
+  }
+  for (int64_t task = rwg; task < a.tasks; task += rstride) {
+    CvPix px;
+#pragma unroll
+    for (int rr = 0; rr < kCvRT; ++rr) {
+      const int64_t p = (task * kCvWaves + wave) * (16 * kCvRT) + rr * 16 + (lane & 15);
+      px.live[rr] = p < a.rows;
+      const int64_t pc = px.live[rr] ? p : 0;
+      px.h[rr] = int(pc / a.W);
+      px.w[rr] = int(pc - int64_t(px.h[rr]) * a.W);
+    }
+    f32x4 acc[kCvRT][NT];
+    for (int pass = 0; pass < a.passes; ++pass) {
+      const int k0 = pass * a.kp;
+      if (a.passes > 1) {
+        __syncthreads();
+        cv_stage<F16>(a, o0, k0, nkc, sw, sb);
+        __syncthreads();
+      }
+      if (pass == 0) {
+        const f32x4* sb4 = reinterpret_cast<const f32x4*>(sb);
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+          const f32x4 b = t < nt ? sb4[t * 4 + q] : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+          for (int rr = 0; rr < kCvRT; ++rr) acc[rr][t] = b;
+        }
+      }
+      // chunks in pairs on two register sets: chunk c + 1's gathers are in
+      // flight while chunk c is converted and multiplied
+      f32x4 ra[kCvRT][S::kLane / 4], rb[kCvRT][S::kLane / 4];
+      bool oka[kCvRT], okb[kCvRT];
+      cv_load<F16>(a, px, k0, q, ra, oka);
+      for (int c = 0; c < nkc; c += 2) {
+        const bool more = c + 1 < nkc;
+        if (more) cv_load<F16>(a, px, k0 + (c + 1) * S::kK, q, rb, okb);
+        cv_mma<F16, NT>(sw, nt, nkc, c, lane, ra, oka, acc);
+        if (c + 2 < nkc) cv_load<F16>(a, px, k0 + (c + 2) * S::kK, q, ra, oka);
+        if (more) cv_mma<F16, NT>(sw, nt, nkc, c + 1, lane, rb, okb, acc);
+      }
+    }
+#pragma unroll
+    for (int rr = 0; rr < kCvRT; ++rr) {
+      if (px.live[rr]) {
+        const int64_t p = (task * kCvWaves + wave) * (16 * kCvRT) + rr * 16 + (lane & 15);
+        float* yr = a.y + p * a.cout;
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+          const int col = o0 + 16 * t + 4 * q;
+          if (t < nt && col < a.cout) {
+            f32x4 v = acc[rr][t];
+            if (a.relu) {
+#pragma unroll
+              for (int j = 0; j < 4; ++j) v[j] = fmaxf(v[j], 0.0f);
+            }
+            *reinterpret_cast<f32x4*>(yr + col) = v;
+          }
+        }
+      }
+    }
+  }
+}
+
+template <bool F16, int NT>
+const void* cv_fn() {
+  return reinterpret_cast<const void*>(&conv_op_kernel<F16, NT>);
+}
+
+}  // namespace
+
+int conv2d_check(const rdv_conv2d_desc& d, std::string* why) {
+  auto bad = [&](const std::string& m) {
+    *why = m;
+    return RDV_ERR_INVALID;
+  };
+  if (d.H < 0 || d.W < 0) return bad("H and W must be >= 0");
+  if (d.kh < 1 || d.kw < 1 || d.kh > 31 || d.kw > 31) return bad("kernel size must be in [1, 31]");
+  if (d.precision != RDV_PREC_F16 && d.precision != RDV_PREC_F32) return bad("unknown precision code");
+  if (d.w_layout != RDV_WLAYOUT_RSCK && d.w_layout != RDV_WLAYOUT_KCRS) return bad("unknown filter layout");
+  const int cstep = d.precision == RDV_PREC_F16 ? 8 : 4;
+  if (d.cin < cstep || d.cin % cstep)
+    return bad("in_channels (" + std::to_string(d.cin) + ") must be a positive multiple of " + std::to_string(cstep));
+  if (d.cout < 4 || d.cout % 4)
+    return bad("out_channels (" + std::to_string(d.cout) + ") must be a positive multiple of 4");
+  if (int64_t(d.kh) * d.kw * d.cin > (int64_t(1) << 20)) return bad("kernel too large");
+  if (int64_t(d.H) * d.W * std::max(d.cin, d.cout) >= (int64_t(1) << 40)) return bad("image too large");
+  if (d.H > (1 << 24) || d.W > (1 << 24)) return bad("image too large");
+  return RDV_OK;
+}
+
+int launch_conv2d(const rdv_conv2d_desc& d, const float* x, const float* w, const float* bias, float* y,
+                  hipStream_t stream) {
+  const int64_t rows = int64_t(d.H) * d.W;
+  if (rows == 0) return RDV_OK;
+  DeviceInfo dev;
+  if (int rc = device_info(&dev)) return rc;
+  const bool f16 = d.precision == RDV_PREC_F16;
+  const int step = f16 ? 32 : 16;
+  const int esize = f16 ? 2 : 4;
+  const int K = d.kh * d.kw * d.cin;
+  const int Kp = (K + step - 1) / step * step;
+  const int cout16 = (d.cout + 15) / 16 * 16;
+  // the largest output block whose whole K fits in LDS, else 16 outputs and K passes
+  int ob = std::min(kCvMaxOb, cout16);
+  while (ob > 16 && int64_t(ob) * Kp * esize > kCvLdsCap) ob /= 2;
+  ob = std::max(16, ob / 16 * 16);
+  int kp = Kp, passes = 1;
+  if (int64_t(ob) * Kp * esize > kCvLdsCap) {
+    const int kmax = int(kCvLdsCap / (int64_t(ob) * esize)) / step * step;
+    passes = (Kp + kmax - 1) / kmax;
+    kp = ((Kp + passes - 1) / passes + step - 1) / step * step;
+  }
+  ConvArgs a;
+  a.x = x;
+  a.w = w;
+  a.bias = bias;
+  a.y = y;
+  a.rows = rows;
+  a.H = d.H;
+  a.W = d.W;
+  a.cin = d.cin;
+  a.cout = d.cout;
+  a.kh = d.kh;
+  a.kw = d.kw;
+  a.ph = d.kh / 2;
+  a.pw = d.kw / 2;
+  a.K = K;
+  a.wlayout = d.w_layout;
+  a.relu = d.relu ? 1 : 0;
+  a.kp = kp;
+  a.passes = passes;
+  a.ob = ob;
+  a.n_ob = (d.cout + ob - 1) / ob;
+  const int64_t rows_per_task = int64_t(kCvWaves) * 16 * kCvRT;
+  a.tasks = (rows + rows_per_task - 1) / rows_per_task;
+  const int nt = ob / 16;
+  const void* fn = nullptr;
+  if (f16) fn = nt <= 2 ? cv_fn<true, 2>() : nt <= 4 ? cv_fn<true, 4>() : cv_fn<true, 8>();
+  else fn = nt <= 2 ? cv_fn<false, 2>() : nt <= 4 ? cv_fn<false, 4>() : cv_fn<false, 8>();
+  const size_t lds = size_t(nt) * (kp / step) * 64 * sizeof(f32x4) + size_t(ob) * sizeof(float);
+  static bool attr_set[2][3] = {};
+  bool& set = attr_set[f16][nt <= 2 ? 0 : nt <= 4 ? 1 : 2];
+  if (!set) {
+    RDV_HIP_TRY(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    int(kCvLdsCap + kCvMaxOb * sizeof(float))));
+    set = true;
+  }
+  int occ = 0;
+  RDV_HIP_TRY(hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, fn, kCvThreads, lds));
+  occ = std::max(occ, 1);
+  const int64_t slots = int64_t(dev.cu_count) * occ;
+  const int64_t rwgs = std::max<int64_t>(1, std::min<int64_t>(a.tasks, (slots + a.n_ob - 1) / a.n_ob));
+  const int64_t grid = rwgs * a.n_ob;
+  if (grid > 0x7fffffff) return fail(RDV_ERR_UNSUPPORTED, "grid too large");
+  void* params[] = {&a};
+  RDV_HIP_TRY(hipLaunchKernel(fn, dim3(static_cast<unsigned>(grid)), dim3(kCvThreads), params, lds, stream));
+  return RDV_OK;
+}
+
+}  // namespace rdv

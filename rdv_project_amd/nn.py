@@ -10,7 +10,15 @@ TensorOperation nodes dispatch eagerly, one kernel per op:
   LinearTensorOpMine             nn.py:1153-1201
   LinearTensorOpSimple           nn.py:1204-1300
   LinearTensorOpSmall            nn.py:1303-1411
+  Conv2DTensorOp                 nn.py:414-470
+  Conv2DTensorOpFast             nn.py:608-668
+  Conv2DTensorOpSimple           nn.py:669-756
+  Conv2DTensorOpSimple3x3        nn.py:757-850
+  Conv2DTensorOpWindow3x3        nn.py:851-1000
   Conv2DTensorOpWinograd3x3      nn.py:1002-1087
+  Downsample2xTensorOp           nn.py:1090-1107
+  Upsample2xTensorOp             nn.py:1110-1125
+  ConcatTensorOp                 nn.py:1128-1150
 Build-defined additions (no reference counterpart, needed by the benchmark
 configurations): FrequencyEncoding, Softplus, Sigmoid, DensityRGB.
 """
@@ -366,3 +374,208 @@ class Conv2DTensorOpWinograd3x3(TensorOperation):
     def _forward(self) -> None:
         _conv.forward(self._desc, self.x_buf.as_tensor("torch"), self.weight_u, self.bias.as_tensor("torch"),
                       self._result_t)
+
+
+class Downsample2xTensorOp(TensorOperation):
+    """2x2 average pool, stride 2, over a flattened channels-last [H*W, C]
+    input (H, W even); channels unchanged (reference: nn.py:1090-1107,
+    shaders/tensors/downsample2x_tensor_op.h).  result [(H/2)(W/2), C] fp32;
+    the four taps are summed left to right in fp32, then scaled by 0.25."""
+
+    def __init__(self, x, H: int, W: int) -> None:
+        data, shape, upstream = _as_op_input(x)
+        assert len(shape) == 2, "Downsample2xTensorOp requires a 2D (H*W, C) input"
+        hw, channels = shape
+        assert hw == H * W, f"H*W ({H * W}) must match x's own row count ({hw})"
+        assert H % 2 == 0 and W % 2 == 0, "Downsample2xTensorOp requires even H and W"
+        self.x_buf = _op_float32(data, "x")
+        self.W = W // 2  # output width (the reference's field)
+        self._in_hw = (int(H), int(W))
+        self._upstream = upstream
+        super().__init__([(H // 2) * (W // 2), channels])
+
+    def _forward(self) -> None:
+        _tensor_ops.downsample2x(self.x_buf.as_tensor("torch"), *self._in_hw, self._result_t)
+
+
+class Upsample2xTensorOp(TensorOperation):
+    """Nearest-neighbour 2x upsample over a flattened channels-last [H*W, C]
+    input; channels unchanged (reference: nn.py:1110-1125,
+    shaders/tensors/upsample2x_tensor_op.h).  result [(2H)(2W), C] fp32."""
+
+    def __init__(self, x, H: int, W: int) -> None:
+        data, shape, upstream = _as_op_input(x)
+        assert len(shape) == 2, "Upsample2xTensorOp requires a 2D (H*W, C) input"
+        hw, channels = shape
+        assert hw == H * W, f"H*W ({H * W}) must match x's own row count ({hw})"
+        self.x_buf = _op_float32(data, "x")
+        self.W = W * 2  # output width (the reference's field)
+        self._in_hw = (int(H), int(W))
+        self._upstream = upstream
+        super().__init__([(H * 2) * (W * 2), channels])
+
+    def _forward(self) -> None:
+        _tensor_ops.upsample2x(self.x_buf.as_tensor("torch"), *self._in_hw, self._result_t)
+
+
+class ConcatTensorOp(TensorOperation):
+    """Channel concat of two ops or tensors with the same row count
+    (reference: nn.py:1128-1150, shaders/tensors/concat_tensor_op.h); both
+    channel counts must be multiples of 8.  result [rows, C1 + C2] fp32."""
+
+    def __init__(self, g1, g2) -> None:
+        data1, shape1, up1 = _as_op_input(g1)
+        data2, shape2, up2 = _as_op_input(g2)
+        assert len(shape1) == 2 and len(shape2) == 2, "ConcatTensorOp requires 2D (H*W, C) inputs"
+        assert shape1[0] == shape2[0], "g1/g2 must share the same H*W leading dim"
+        assert shape1[1] % 8 == 0, f"g1's own channels ({shape1[1]}) must be a multiple of 8"
+        assert shape2[1] % 8 == 0, f"g2's own channels ({shape2[1]}) must be a multiple of 8"
+        self.x1_buf = _op_float32(data1, "g1")
+        self.x2_buf = _op_float32(data2, "g2")
+        self.C1 = int(shape1[1])
+        self._upstream = up1
+        self._extra_upstreams = (up2,) if up2 is not None else ()
+        super().__init__([shape1[0], shape1[1] + shape2[1]])
+
+    def _forward(self) -> None:
+        _tensor_ops.concat(self.x1_buf.as_tensor("torch"), self.x2_buf.as_tensor("torch"), self._result_t)
+
+
+# ------------------------------------------------------- direct convolutions
+class _Conv2DTensorOpBase(TensorOperation):
+    """'same'-padded (zero border), stride-1 2-D convolution over a flattened
+    channels-last x [H*W, in_channels] (a buffer or an upstream
+    TensorOperation), weight [KH, KW, in_channels, out_channels], bias
+    [out_channels]; result [H*W, out_channels] fp32.  The weight is read (and,
+    for the fp16 variants, rounded) at every dispatch, so in-place updates of
+    it are seen by evaluate().  One implicit-GEMM matrix-core kernel serves
+    every variant (rdv_conv2d)."""
+
+    _precision = _lib.PREC_F16
+
+    def _bind(self, x, weight, bias, H: int, W: int, fixed_3x3: bool = False):
+        name = type(self).__name__
+        data, shape, upstream = _as_op_input(x)
+        assert len(shape) == 2, f"{name} requires a 2D (H*W, in_channels) input"
+        hw, in_channels = shape
+        assert hw == H * W, f"H*W ({H * W}) must match x's own row count ({hw})"
+        weight = weight if isinstance(weight, RDVObject) else wrap(weight)
+        bias = bias if isinstance(bias, RDVObject) else wrap(bias)
+        if fixed_3x3:
+            assert tuple(weight.shape[:2]) == (3, 3), "weight must be [3, 3, in_channels, out_channels]"
+        else:
+            assert len(weight.shape) == 4, "weight must be [KH, KW, in_channels, out_channels]"
+        kh, kw, weight_in_channels, out_channels = weight.shape
+        assert weight_in_channels == in_channels, "weight's own in_channels must match x's own trailing dim"
+        assert tuple(bias.shape) == (out_channels,), "bias must be [out_channels]"
+        self.x_buf = _op_float32(data, "x")
+        self.weight = _op_float32(weight, "weight")
+        self.bias = _op_float32(bias, "bias")
+        self._upstream = upstream
+        self.KH, self.KW = int(kh), int(kw)
+        self.CIN, self.COUT, self.H, self.W = int(in_channels), int(out_channels), int(H), int(W)
+        return int(hw), int(in_channels), int(out_channels)
+
+    def _finish(self) -> None:
+        self._desc = _tensor_ops.conv2d_desc(self.H, self.W, self.CIN, self.COUT, self.KH, self.KW, self._precision,
+                                             _lib.WLAYOUT_RSCK)
+        _tensor_ops.conv2d_validate(self._desc, type(self).__name__)
+        super().__init__([self.H * self.W, self.COUT])
+
+    def _forward(self) -> None:
+        _tensor_ops.conv2d(self._desc, self.x_buf.as_tensor("torch"), self.weight.as_tensor("torch"),
+                           self.bias.as_tensor("torch"), self._result_t, type(self).__name__)
+
+
+class Conv2DTensorOp(_Conv2DTensorOpBase):
+    """fp32 throughout (reference: nn.py:414-470, shaders/tensors/conv2d_tensor_op.h):
+    acc = bias; acc += x * w over the valid taps in (kh, kw) order and channels
+    ascending.  H*W must be a multiple of 4, in_channels and out_channels
+    multiples of 8."""
+
+    _precision = _lib.PREC_F32
+
+    def __init__(self, x, weight, bias, H: int, W: int) -> None:
+        _, in_channels, out_channels = self._bind(x, weight, bias, H, W)
+        assert in_channels % 8 == 0, f"in_channels ({in_channels}) must be a multiple of 8"
+        assert out_channels % 8 == 0, f"out_channels ({out_channels}) must be a multiple of 8"
+        self._finish()
+
+
+class Conv2DTensorOpFast(_Conv2DTensorOpBase):
+    """x and weight rounded to fp16, fp32 accumulation, fp32 bias added after
+    (reference: nn.py:608-668, shaders/tensors/conv2d_tensor_op_fast.h).  H*W
+    must be a multiple of 32, in_channels and out_channels multiples of 16."""
+
+    _TILE_ROWS = 32
+    _TILE_COLS = 16
+
+    def __init__(self, x, weight, bias, H: int, W: int) -> None:
+        _, in_channels, out_channels = self._bind(x, weight, bias, H, W)
+        assert in_channels % 16 == 0, f"in_channels ({in_channels}) must be a multiple of 16"
+        assert out_channels % 16 == 0, f"out_channels ({out_channels}) must be a multiple of 16"
+        self._finish()
+
+
+class Conv2DTensorOpSimple(_Conv2DTensorOpBase):
+    """x and weight rounded to fp16, fp32 accumulation seeded with the bias
+    (reference: nn.py:669-756, shaders/tensors/conv2d_tensor_op_simple.h).  H*W
+    must be a multiple of 32, in_channels and out_channels multiples of 16."""
+
+    _TILE_ROWS = 32
+    _TILE_COLS = 16
+
+    def __init__(self, x, weight, bias, H: int, W: int) -> None:
+        hw, in_channels, out_channels = self._bind(x, weight, bias, H, W)
+        assert hw % 32 == 0, f"H*W ({hw}) must be a multiple of 32"
+        assert in_channels % 16 == 0, f"in_channels ({in_channels}) must be a multiple of 16"
+        assert out_channels % 16 == 0, f"out_channels ({out_channels}) must be a multiple of 16"
+        self._finish()
+
+
+class Conv2DTensorOpSimple3x3(_Conv2DTensorOpBase):
+    """3x3 kernel, padding 1; x and weight rounded to fp16, fp32 accumulation
+    seeded with the bias (reference: nn.py:757-850,
+    shaders/tensors/conv2d_tensor_op_simple3x3.h).  H*W must be a multiple of
+    32, in_channels and out_channels multiples of 16.  SPT is the reference's
+    subgroups-per-tile choice (_max_subgroups under its 48 KB budget); the HIP
+    kernel's tiling does not depend on it."""
+
+    _TILE_ROWS = 32
+    _TILE_COLS = 16
+
+    def __init__(self, x, weight, bias, H: int, W: int) -> None:
+        hw, in_channels, out_channels = self._bind(x, weight, bias, H, W, fixed_3x3=True)
+        assert hw % 32 == 0, f"H*W ({hw}) must be a multiple of 32"
+        assert in_channels % 16 == 0, f"in_channels ({in_channels}) must be a multiple of 16"
+        assert out_channels % 16 == 0, f"out_channels ({out_channels}) must be a multiple of 16"
+        tap_k = 9 * in_channels
+        self.SPT = _tensor_ops.max_subgroups(fixed_bytes=32 * tap_k * 2, per_subgroup_bytes=16 * tap_k * 2,
+                                             divides=lambda s: out_channels % (16 * s) == 0)
+        self._finish()
+
+
+class Conv2DTensorOpWindow3x3(_Conv2DTensorOpBase):
+    """3x3 kernel, padding 1; x and weight rounded to fp16, fp32 accumulation
+    seeded with the bias (reference: nn.py:851-1000,
+    shaders/tensors/conv2d_tensor_op_window3x3.h).  H and W must be multiples
+    of 8, in_channels and out_channels multiples of 16, in_channels at most 64
+    (the reference's shared-memory budget).  The reference pads x into a
+    scratch buffer in a first dispatch; here the kernel zero-fills the border
+    taps itself, so there is one dispatch and no scratch."""
+
+    _WIN = 8
+    _TILE_ROWS = 1
+    _TILE_COLS = 16
+
+    def __init__(self, x, weight, bias, H: int, W: int) -> None:
+        _, in_channels, out_channels = self._bind(x, weight, bias, H, W, fixed_3x3=True)
+        assert H % self._WIN == 0, f"H ({H}) must be a multiple of {self._WIN}"
+        assert W % self._WIN == 0, f"W ({W}) must be a multiple of {self._WIN}"
+        assert in_channels % 16 == 0, f"in_channels ({in_channels}) must be a multiple of 16"
+        assert out_channels % 16 == 0, f"out_channels ({out_channels}) must be a multiple of 16"
+        assert in_channels <= 64, f"in_channels ({in_channels}) must be at most 64 (see this op's own docstring)"
+        fetch = self._WIN + 2
+        shared_bytes = (fetch * fetch * in_channels + 16 * 9 * in_channels) * 2 + 64 * 16 * 2 + 64 * 16 * 4
+        assert shared_bytes <= 49152, f"in_channels ({in_channels}) needs {shared_bytes} bytes of shared memory (48KB budget)"
+        self._finish()

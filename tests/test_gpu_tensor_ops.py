@@ -170,3 +170,181 @@ def test_c5_layer_size_sampled_and_position_independent():
     # the same rows computed at other positions give the same bits
     sub = rdv.LinearTensorOpSmall(x[idx].contiguous(), W, b)
     np.testing.assert_array_equal(sub.as_type("numpy"), ys)
+
+
+# ----------------------------------------------------------- data movement
+@pytest.mark.parametrize("H,W,C", [(4, 4, 8), (8, 12, 16), (64, 48, 40), (256, 256, 64)])
+def test_downsample2x_bit_exact(H, W, C):
+    g = torch.Generator().manual_seed(H * W + C)
+    x = torch.randn(H * W, C, generator=g)
+    op = rdv.Downsample2xTensorOp(x.cuda(), H, W)
+    got = op.as_type("torch").cpu().numpy()
+    np.testing.assert_array_equal(got, T.downsample2x(x.numpy(), H, W))
+    assert op.W == W // 2 and op.shape == [(H // 2) * (W // 2), C]
+
+
+@pytest.mark.parametrize("H,W,C", [(1, 1, 8), (3, 5, 16), (40, 30, 24), (128, 128, 64)])
+def test_upsample2x_bit_exact(H, W, C):
+    g = torch.Generator().manual_seed(H * W + C + 1)
+    x = torch.randn(H * W, C, generator=g)
+    op = rdv.Upsample2xTensorOp(x.cuda(), H, W)
+    np.testing.assert_array_equal(op.as_type("torch").cpu().numpy(), T.upsample2x(x.numpy(), H, W))
+    assert op.W == 2 * W
+
+
+@pytest.mark.parametrize("rows,C1,C2", [(4, 8, 8), (100, 16, 40), (65536, 64, 32)])
+def test_concat_bit_exact(rows, C1, C2):
+    g = torch.Generator().manual_seed(rows + C1)
+    a, b = torch.randn(rows, C1, generator=g), torch.randn(rows, C2, generator=g)
+    op = rdv.ConcatTensorOp(a.cuda(), b.cuda())
+    np.testing.assert_array_equal(op.as_type("torch").cpu().numpy(), T.concat(a.numpy(), b.numpy()))
+    assert op.C1 == C1
+
+
+def test_data_movement_c_abi_ragged_sizes():
+    """The C ABI takes any even H, W and channel counts that are multiples of 4
+    (the Python classes add the reference's 4-row / 8-channel tile rules)."""
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(6 * 10, 12, generator=g)
+    y = torch.empty(15, 12, device="cuda")
+    _tensor_ops.downsample2x(x.cuda(), 6, 10, y)
+    up = torch.empty(4 * 15, 12, device="cuda")
+    _tensor_ops.upsample2x(y, 3, 5, up)
+    a, b = torch.randn(7, 4, generator=g), torch.randn(7, 20, generator=g)
+    cat = torch.empty(7, 24, device="cuda")
+    _tensor_ops.concat(a.cuda(), b.cuda(), cat)
+    torch.cuda.synchronize()
+    d = T.downsample2x(x.numpy(), 6, 10)
+    np.testing.assert_array_equal(y.cpu().numpy(), d)
+    np.testing.assert_array_equal(up.cpu().numpy(), T.upsample2x(d, 3, 5))
+    np.testing.assert_array_equal(cat.cpu().numpy(), T.concat(a.numpy(), b.numpy()))
+
+
+def test_data_movement_shape_errors():
+    with pytest.raises(AssertionError):
+        rdv.Downsample2xTensorOp(torch.zeros(15, 8).cuda(), 3, 5)       # odd H and W
+    with pytest.raises(AssertionError):
+        rdv.ConcatTensorOp(torch.zeros(8, 8).cuda(), torch.zeros(8, 12).cuda())  # 12 channels
+    with pytest.raises(AssertionError):
+        rdv.Upsample2xTensorOp(torch.zeros(16, 8).cuda(), 4, 5)        # H*W != rows
+
+
+def test_mixed_chain_evaluate_chain():
+    """conv -> downsample -> concat(linear(...), relu(...)) -> upsample; an
+    in-place update of the input followed by evaluate_chain() re-runs every
+    op in dependency order and matches a fresh oracle pass."""
+    from oracle import winograd as WG
+    H, W, CIN, COUT = 16, 16, 16, 32
+    g = torch.Generator().manual_seed(99)
+    x = torch.rand(H * W, CIN, generator=g).cuda()
+    wc = torch.randn(3, 3, CIN, COUT, generator=g) * 0.1
+    bc = torch.randn(COUT, generator=g) * 0.1
+    Wl = torch.randn(16, COUT, generator=g) / COUT ** 0.5
+    bl = torch.randn(16, generator=g)
+    conv = rdv.Conv2DTensorOpWinograd3x3(x, wc.cuda(), bc.cuda(), H, W)
+    down = rdv.Downsample2xTensorOp(conv, H, W)
+    lin = rdv.LinearTensorOp(down, Wl.cuda(), bl.cuda())
+    act = rdv.ReLUTensorOp(down)
+    cat = rdv.ConcatTensorOp(lin, act)
+    up = rdv.Upsample2xTensorOp(cat, H // 2, W // 2)
+
+    def oracle(xn):
+        c = WG.winograd_conv(xn.reshape(H, W, CIN), wc.numpy(), bc.numpy()).reshape(H * W, COUT)
+        c = c.astype(np.float32)
+        d = T.downsample2x(c, H, W)
+        return T.upsample2x(T.concat(T.linear_op_f32(d, Wl.numpy(), bl.numpy()), T.relu_op(d)), H // 2, W // 2)
+
+    def check(what):
+        ref = oracle(x.cpu().numpy())
+        got = up.as_type("torch").cpu().numpy()
+        np.testing.assert_allclose(got, ref, rtol=2e-4, atol=2e-4, err_msg=what)
+
+    check("first dispatch")
+    x.mul_(-1.5).add_(0.25)   # in place: same buffer, new values
+    up.evaluate_chain()
+    check("after evaluate_chain")
+
+
+# ------------------------------------------------------------ direct conv
+def _conv_case(H, W, C, K, KH, KW, seed):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.rand(H * W, C, generator=g) * 2 - 1
+    w = torch.randn(KH, KW, C, K, generator=g) * (2.0 / (C * KH * KW)) ** 0.5
+    b = torch.randn(K, generator=g) * 0.1
+    return x, w, b
+
+
+def _check_conv(got, x, w, b, H, W, f16, what):
+    got = np.asarray(got, np.float64)
+    fn = T.conv2d_op_f16 if f16 else T.conv2d_op_f32
+    ref = fn(x.numpy(), w.numpy(), b.numpy(), H, W).astype(np.float64)
+    bound = 2 * T.conv2d_error_bound(x.numpy(), w.numpy(), b.numpy(), H, W, f16) + 1e-30
+    err = np.abs(got - ref)
+    assert np.isfinite(got).all(), what
+    worst = np.unravel_index(np.argmax(err - bound), err.shape)
+    assert (err <= bound).all(), f"{what}: |err| {err[worst]:.3g} > bound {bound[worst]:.3g} at {worst}"
+
+
+@pytest.mark.parametrize("cls,f16,shape", [
+    (rdv.Conv2DTensorOp, False, (8, 12, 8, 8, 3, 3)),
+    (rdv.Conv2DTensorOp, False, (16, 16, 32, 24, 5, 5)),
+    (rdv.Conv2DTensorOp, False, (12, 10, 16, 40, 1, 1)),
+    (rdv.Conv2DTensorOp, False, (10, 14, 24, 16, 2, 4)),          # even kernel: asymmetric padding
+    (rdv.Conv2DTensorOp, False, (16, 8, 128, 16, 7, 7)),          # K = 6272: restaged in K passes
+    (rdv.Conv2DTensorOpFast, True, (16, 16, 16, 32, 3, 3)),
+    (rdv.Conv2DTensorOpFast, True, (32, 32, 48, 48, 3, 3)),       # the reference's Winograd shape class
+    (rdv.Conv2DTensorOpFast, True, (16, 12, 32, 16, 7, 7)),
+    (rdv.Conv2DTensorOpSimple, True, (16, 16, 64, 64, 3, 3)),
+    (rdv.Conv2DTensorOpSimple, True, (8, 8, 16, 160, 3, 1)),      # two output blocks
+    (rdv.Conv2DTensorOpSimple3x3, True, (32, 16, 32, 64, 3, 3)),
+    (rdv.Conv2DTensorOpWindow3x3, True, (24, 16, 64, 32, 3, 3)),
+])
+def test_direct_conv_variants_match_oracle(cls, f16, shape):
+    H, W, C, K, KH, KW = shape
+    x, w, b = _conv_case(H, W, C, K, KH, KW, seed=sum(shape))
+    op = cls(x.cuda(), w.cuda(), b.cuda(), H, W)
+    assert op.shape == [H * W, K]
+    _check_conv(op.as_type("torch").cpu().numpy(), x, w, b, H, W, f16, f"{cls.__name__}{shape}")
+
+
+def test_direct_conv_against_torch_full_size():
+    """64 -> 64 3x3 on a 256 x 256 image (the Winograd benchmark's shape) on
+    the fp16 path against torch's fp32 conv of the fp16-rounded operands."""
+    H = W = 256
+    x, w, b = _conv_case(H, W, 64, 64, 3, 3, seed=5)
+    op = rdv.Conv2DTensorOpSimple3x3(x.cuda(), w.cuda(), b.cuda(), H, W)
+    got = op.as_type("torch").cpu()
+    # reference on the CPU in float64 (the GPU's fp32 conv may take a reduced-precision path)
+    xt = x.half().double().reshape(1, H, W, 64).permute(0, 3, 1, 2)
+    wt = w.half().double().permute(3, 2, 0, 1).contiguous()
+    ref = torch.nn.functional.conv2d(xt, wt, b.double(), padding=1).permute(0, 2, 3, 1).reshape(H * W, 64).float()
+    err = (got - ref).abs().max().item()
+    assert err <= 2e-4 * max(1.0, ref.abs().max().item()), f"max |err| {err}"
+
+
+def test_direct_conv_weight_update_seen_and_kcrs_layout():
+    """The fp32 weight is read at every dispatch; the C ABI's PyTorch OIHW
+    layout gives the same result as the channels-last one."""
+    H, W, C, K = 8, 8, 16, 16
+    x, w, b = _conv_case(H, W, C, K, 3, 3, seed=3)
+    wd = w.cuda()
+    op = rdv.Conv2DTensorOpFast(x.cuda(), wd, b.cuda(), H, W)
+    wd.mul_(-2.0)
+    op.evaluate()
+    _check_conv(op.as_type("torch").cpu().numpy(), x, w * -2.0, b, H, W, True, "updated weight")
+    d = _tensor_ops.conv2d_desc(H, W, C, K, 3, 3, _lib.PREC_F16, _lib.WLAYOUT_KCRS)
+    y = torch.empty(H * W, K, device="cuda")
+    _tensor_ops.conv2d(d, x.cuda(), wd.permute(3, 2, 0, 1).contiguous(), b.cuda(), y, "kcrs")
+    torch.cuda.synchronize()
+    assert torch.equal(y, op.as_type("torch"))
+
+
+def test_direct_conv_shape_errors():
+    x = torch.zeros(64, 16).cuda()
+    with pytest.raises(AssertionError):
+        rdv.Conv2DTensorOp(x, torch.zeros(3, 3, 12, 8).cuda(), torch.zeros(8).cuda(), 8, 8)   # CIN mismatch
+    with pytest.raises(AssertionError):
+        rdv.Conv2DTensorOpWindow3x3(torch.zeros(16 * 6, 16).cuda(), torch.zeros(3, 3, 16, 16).cuda(),
+                                    torch.zeros(16).cuda(), 16, 6)                          # W % 8
+    with pytest.raises(AssertionError):
+        rdv.Conv2DTensorOpSimple3x3(x, torch.zeros(5, 5, 16, 16).cuda(), torch.zeros(16).cuda(), 8, 8)  # not 3x3
