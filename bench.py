@@ -346,6 +346,55 @@ def _median_time(fn, warm: int = 3, runs: int = 5) -> float:
     return statistics.median(ts)
 
 
+def bench_conv_and_data_ops(steps, warmup):
+    """The direct-convolution kernel (rdv_conv2d, fp16 operands) at the C3
+    shape in the tensor-op layout (channels-last fp32 x and y, 256 x 256,
+    64 -> 64, 3x3), and the data-movement ops at C3-sized images."""
+    import torch
+    from rdv_project_amd import _lib, _tensor_ops
+    from rdv_project_amd import workloads as WL
+    H = W = 256
+    C = K = 64
+    g = WL.gen(15)
+    x = (torch.rand(H * W, C, generator=g) * 2 - 1).cuda()
+    w = (torch.randn(3, 3, C, K, generator=g) * (2.0 / (9 * C)) ** 0.5).cuda()
+    b = torch.zeros(K).cuda()
+    ys = [torch.empty(H * W, K, device="cuda") for _ in range(4)]
+    xs = [x] + [x.clone() for _ in range(3)]
+    d = _tensor_ops.conv2d_desc(H, W, C, K, 3, 3, _lib.PREC_F16, _lib.WLAYOUT_RSCK)
+    wall, ev = _time_launches(lambda i: _tensor_ops.conv2d(d, xs[i % 4], w, b, ys[i % 4], "conv"), steps, warmup)
+    flop = 2 * H * W * C * K * 9
+    nbytes = H * W * (C + K) * 4
+    out = {"direct_conv": {
+        "workload": "implicit-GEMM direct conv, fp16 operands: channels-last fp32 x [256*256, 64] (seed 15), "
+                    "3x3 64 -> 64, 'same' padding, fp32 y (Conv2DTensorOp{Fast,Simple,Simple3x3,Window3x3})",
+        "kernel": "conv_op_kernel<true, 4>",
+        "us_per_call": round(ev * 1e3, 2),
+        "TFLOP_s": round(flop / (ev * 1e-3) / 1e12, 1),
+        "mfma_peak_pct": round(100 * flop / (ev * 1e-3) / 1e12 / PEAK_FP16_TFLOPS, 2),
+        "hbm_GB_s": round(nbytes / (ev * 1e-3) / 1e9, 1),
+        "hbm_peak_pct": round(100 * nbytes / (ev * 1e-3) / 1e9 / PEAK_HBM_GBS, 2),
+        "bytes_per_call": nbytes,
+    }}
+    big = [(torch.rand(H * W, C, generator=g)).cuda() for _ in range(4)]
+    small = [torch.empty(H * W // 4, C, device="cuda") for _ in range(4)]
+    up_out = [torch.empty(H * W, C, device="cuda") for _ in range(4)]
+    cat_out = [torch.empty(H * W, 2 * C, device="cuda") for _ in range(2)]
+    _, ev_d = _time_launches(lambda i: _tensor_ops.downsample2x(big[i % 4], H, W, small[i % 4]), steps, warmup)
+    _, ev_u = _time_launches(lambda i: _tensor_ops.upsample2x(small[i % 4], H // 2, W // 2, up_out[i % 4]),
+                             steps, warmup)
+    _, ev_c = _time_launches(lambda i: _tensor_ops.concat(big[i % 4], big[(i + 1) % 4], cat_out[i % 2]), steps, warmup)
+    img = H * W * C * 4
+    for name, evx, nb, kern in (("downsample2x", ev_d, img + img // 4, "downsample2x_kernel<uint32_t>"),
+                                ("upsample2x", ev_u, img // 4 + img, "upsample2x_kernel<uint32_t>"),
+                                ("concat", ev_c, 4 * img, "concat_kernel<uint32_t>")):
+        gbs = nb / (evx * 1e-3) / 1e9
+        out[name] = {"us_per_call": round(evx * 1e3, 2), "hbm_GB_s": round(gbs, 1),
+                     "hbm_peak_pct": round(100 * gbs / PEAK_HBM_GBS, 2), "bytes_per_call": nb, "kernel": kern,
+                     "workload": "256 x 256 x 64 fp32 channels-last image (seed 15)"}
+    return out
+
+
 def cpu_baseline():
     """The torch-CPU restatement (oracle/torch_cpu.py) on the host cores: C1 in
     full, bounded samples of C2 (2^18 points), C3 (the whole 256x256 image), C4
@@ -504,6 +553,9 @@ def main() -> int:
         _log("tensor ops")
         extras["tensor_ops"] = bench_tensor_ops(20, 3)
         _log(f"tensor ops {extras['tensor_ops']}")
+        _log("conv and data ops")
+        extras.update(bench_conv_and_data_ops(max(args.steps // 5, 10), args.warmup))
+        _log(f"conv {extras['direct_conv']}")
         _log("generic MLP")
         extras["generic_mlp"] = bench_generic_mlp(max(args.steps // 5, 10), args.warmup)
         _log(f"generic MLP {extras['generic_mlp']}")
