@@ -5,8 +5,11 @@ hot path, behind rdv's own Python API.
     m = rdv.linear(W0, b0, f16=True) >> rdv.relu >> rdv.linear(W1, b1, f16=True)
     y = m(rdv.wrap(x)).as_tensor('torch')
 
-Public names follow the reference's curated surface (src/rdv/__init__.py) for
-the parts this build implements.  Compute runs only through the HIP library
+Public names follow the reference's curated surface (src/rdv/__init__.py:9-157)
+for the parts this build implements: the node and generics machinery
+(Node, Component, Struct, Main, Library, Generic, Generics, dispatch), the
+value and pointer types (vec*/mat*, Type, Pointer, Buffer, FixArray, Deferred,
+deferreds), the Map / Grid / TensorOperation families and their evaluators.  Compute runs only through the HIP library
 (librdv_hip.so); there is no CPU fallback.
 """
 from .core import (
@@ -19,7 +22,62 @@ from .core import (
     set_synchronous,
     wrap,
 )
-from .maths import Composite, Grid, Identity, Map, Sensor, TensorOperation, X, e, pi
+from .maths import (
+    Composite,
+    Grid,
+    GridEvaluator,
+    Identity,
+    Map,
+    MapEvaluator,
+    Sensor,
+    TensorOperation,
+    TensorOpEvaluator,
+    X,
+    e,
+    pi,
+)
+from .types import (
+    Array,
+    Buffer,
+    Code,
+    Component,
+    CooperativeLibrary,
+    Deferred,
+    DeferredLibrary,
+    FixArray,
+    Generic,
+    GenericParam,
+    Generics,
+    GridLibrary,
+    Library,
+    Main,
+    MathLibrary,
+    Node,
+    Pointer,
+    RandomLibrary,
+    Single,
+    Struct,
+    Type,
+    bvec2,
+    bvec3,
+    bvec4,
+    deferreds,
+    dispatch,
+    ivec2,
+    ivec3,
+    ivec4,
+    mat2,
+    mat3,
+    mat3x4,
+    mat4,
+    mat4x3,
+    uvec2,
+    uvec3,
+    uvec4,
+    vec2,
+    vec3,
+    vec4,
+)
 from ._conv import Winograd3x3Conv2d, winograd3x3_conv2d
 from ._render import composite
 from ._train import mse_backward

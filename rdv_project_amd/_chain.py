@@ -131,12 +131,26 @@ def evaluate_map(m: Map, x) -> RDVObject:
     if len(x.shape) < 1:
         raise AssertionError("Map input needs a trailing feature dimension")
     p = plan_chain(m, int(x.shape[-1]))
-    packed = packed_params(m, p)
-    rows = math.prod(x.shape[:-1])
     out = _cached_output(p.signature, (*x.shape[:-1], p.out_features))
-    lib = _lib.load()
     with launch_scope():
-        _lib.check(lib.rdv_mlp_forward(C.byref(p.desc), C.c_void_p(packed.data_ptr()), C.c_void_p(x.device_ptr),
-                                       C.c_void_p(out.device_ptr), C.c_int64(rows),
-                                       C.c_void_p(current_stream_handle())), "mlp forward")
+        _launch(m, p, x.device_ptr, out.device_ptr, math.prod(x.shape[:-1]))
     return out
+
+
+def _launch(m: Map, p: ChainPlan, x_ptr: int, y_ptr: int, rows: int) -> None:
+    packed = packed_params(m, p)
+    _lib.check(_lib.load().rdv_mlp_forward(C.byref(p.desc), C.c_void_p(packed.data_ptr()), C.c_void_p(x_ptr),
+                                           C.c_void_p(y_ptr), C.c_int64(rows),
+                                           C.c_void_p(current_stream_handle())), "mlp forward")
+
+
+def launch_map_rows(m: Map, x_ptr: int, y_ptr: int, rows: int) -> None:
+    """m over `rows` rows of fp32 x at x_ptr into fp32 y at y_ptr (device
+    pointers; m's input width must be known).  What MapEvaluator runs."""
+    rows_fn = getattr(m, "_launch_rows", None)
+    if rows_fn is not None:
+        rows_fn(x_ptr, y_ptr, rows)
+        return
+    if m.IN is None:
+        raise RuntimeError("Generic arguments could not be deduced from input data. You must explicitly cast.")
+    _launch(m, plan_chain(m, int(m.IN)), x_ptr, y_ptr, rows)

@@ -74,9 +74,19 @@ def render_ea(cam: Cameras, ea: EmissionAbsorption, out: RDVObject | None = None
 
 def _transform_array(rt: RaymarchingTransmittance):
     arr = (C.c_float * 12)()
-    for i, v in enumerate(rt.transform):
+    for i, v in enumerate(rt.transform.tolist_flat()):
         arr[i] = v
     return arr
+
+
+def raymarch_ptrs(rt: RaymarchingTransmittance, x_ptr: int, y_ptr: int, rows: int) -> None:
+    """RaymarchingTransmittance over `rows` rays (fp32 [rows, 6] at x_ptr) into
+    fp32 [rows] at y_ptr."""
+    p, packed = _field_plan(rt.extinction, 3)
+    _lib.check(_lib.load().rdv_raymarch_transmittance(
+        C.byref(p.desc), C.c_void_p(packed.data_ptr()), C.c_void_p(x_ptr), C.c_int64(rows), _transform_array(rt),
+        C.c_float(rt.step_size), C.c_float(rt.density_scale), C.c_void_p(y_ptr),
+        C.c_void_p(current_stream_handle())), "RaymarchingTransmittance")
 
 
 def raymarch_rows(rt: RaymarchingTransmittance, x, out: RDVObject | None = None) -> RDVObject:
@@ -123,15 +133,19 @@ def composite(sigma_rgb: torch.Tensor, dt: torch.Tensor, out: torch.Tensor | Non
     return out
 
 
-def evaluate_grid(g: Grid) -> RDVObject:
+def evaluate_grid(g: Grid, out: RDVObject | None = None) -> RDVObject:
     if isinstance(g, Cameras):
-        return camera_rays(g)
+        return camera_rays(g, out)
     if isinstance(g, Sensor) and isinstance(g.grid, Cameras):
         cam, m = g.grid, g.map
         if isinstance(m, EmissionAbsorption):
-            return render_ea(cam, m)
+            return render_ea(cam, m, out)
         rays = camera_rays(cam, _cached(("sensor-rays",), (*cam.shape, 6)))
         if isinstance(m, RaymarchingTransmittance):
-            return raymarch_rows(m, rays, _cached(("sensor-rt",), (*cam.shape, 1)))
-        return m(rays)
+            return raymarch_rows(m, rays, out if out is not None else _cached(("sensor-rt",), (*cam.shape, 1)))
+        y = m(rays)
+        if out is not None:
+            out.as_tensor("torch").copy_(y.as_tensor("torch").reshape(out.shape))
+            return out
+        return y
     raise NotImplementedError(f"grid evaluation of {type(g).__name__} is outside this build")

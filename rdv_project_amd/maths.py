@@ -12,13 +12,31 @@ from __future__ import annotations
 import math as _math
 
 from .core import RDVObject, wrap
+from .types import IN as _IN, OUT as _OUT
+from .types import Component, DeferredLibrary, Generic, Generics, Main, generic_value
 
 
-class Map:
-    """Base of every per-row map.  IN / OUT are None while generic."""
+class Map(Component, Generic[_IN, _OUT]):
+    """Base of every per-row map (reference: maths:1436).  IN / OUT are None
+    while generic; Map[IN, OUT] is the specialisation, and isinstance(m,
+    Map[3, 1]) holds for any map of those widths."""
 
     IN: int | None = None
     OUT: int | None = None
+
+    def cast(self, target):
+        """This map as a `target` (e.g. Map[3, 1]): its known widths must
+        agree (reference: Node.cast, _core.py:1778-1814, as Map.__rshift__
+        and ExtinctionTrait use it).  Maps here carry their widths per
+        instance, so a compatible map is returned as it is."""
+        origin = target.__dict__.get("__rdv_origin__", target) if isinstance(target, type) else None
+        if origin is None or not isinstance(self, origin):
+            raise TypeError(f"cannot cast {type(self).__name__} to {getattr(target, '__name__', target)}")
+        for k, v in getattr(target, "__generics__", {}).items():
+            cur = generic_value(self, k)
+            if v is not None and cur is not None and cur != v:
+                raise TypeError(f"cannot cast {type(self).__name__}: {k} is {cur}, {target.__name__} needs {v}")
+        return self
 
     # ---------------------------------------------------------- composition
     def __rshift__(self, m: "Map") -> "Map":
@@ -45,14 +63,20 @@ class Map:
     def __call__(self, x, **kwargs):
         """Evaluates the map over every row of x; returns a cached output object
         (same buffer when the same structure is called with the same row shape,
-        as the reference's per-class evaluator cache does, maths:1466-1476)."""
+        as the reference's per-class evaluator cache does, maths:1466-1476).
+        Keyword arguments bind deferred names for the duration of the call
+        (reference: DeferredLibrary.bind around the dispatch, maths:1481-1486)."""
         if kwargs:
-            raise NotImplementedError("deferred bindings (Map.__call__(**kwargs)) are outside this build")
-        ev = getattr(self, "_evaluate_rows", None)
-        if ev is not None:  # maps with a kernel of their own (rendering nodes)
-            return ev(x)
-        from . import _chain
-        return _chain.evaluate_map(self, x)
+            DeferredLibrary.bind(**kwargs)
+        try:
+            ev = getattr(self, "_evaluate_rows", None)
+            if ev is not None:  # maps with a kernel of their own (rendering nodes)
+                return ev(x)
+            from . import _chain
+            return _chain.evaluate_map(self, x)
+        finally:
+            if kwargs:
+                DeferredLibrary.unbind(**kwargs)
 
 
 def _check_link(g: Map, f: Map) -> None:
@@ -105,7 +129,7 @@ def _infer_out(stages: list[Map]) -> int | None:
 # ================================================================= GRIDS
 
 
-class Grid:
+class Grid(Component, Generic[_IN, _OUT]):
     """Index space [0..shape[i]) -> float vectors of width OUT (reference: maths:42-225).
 
     Calling a grid with no arguments evaluates every cell in row-major order
@@ -126,10 +150,18 @@ class Grid:
         return NotImplemented
 
     def __call__(self, *args, **kwargs):
-        if args or kwargs:
-            raise NotImplementedError("batched grid evaluation is outside this build")
-        from . import _render
-        return _render.evaluate_grid(self)
+        """Every cell in row-major order into a cached [*shape, OUT] buffer;
+        keyword arguments bind deferred names for the call (maths:77-103)."""
+        if args:
+            raise NotImplementedError("batched grid evaluation (Grid.__call__(indices)) is outside this build")
+        if kwargs:
+            DeferredLibrary.bind(**kwargs)
+        try:
+            from . import _render
+            return _render.evaluate_grid(self)
+        finally:
+            if kwargs:
+                DeferredLibrary.unbind(**kwargs)
 
 
 class Sensor(Grid):
@@ -148,7 +180,7 @@ class Sensor(Grid):
 # ======================================================== TENSOR OPERATIONS
 
 
-class TensorOperation:
+class TensorOperation(Component):
     """Self-materialising 2-D op, dispatched eagerly at construction
     (reference: maths:1251-1380).  Subclasses set up their inputs and call
     super().__init__(shape); `result` then holds the [rows, cols] fp32 output.
@@ -217,3 +249,65 @@ def _collect_tensor_ops(node, seen_ids, out) -> None:
 
 pi = _math.pi
 e = _math.e
+
+
+# ============================================================== EVALUATORS
+
+
+def _pointer_of(v) -> int:
+    if isinstance(v, RDVObject):
+        return v.device_ptr
+    if hasattr(v, "data_ptr"):
+        return int(v.data_ptr())
+    return int(v)
+
+
+class MapEvaluator(Main):
+    """Evaluates `map` over rows: input [rows, IN] fp32 at `input`, output
+    [rows, OUT] fp32 at `output` (RDVObjects or raw device pointers);
+    dispatch(evaluator, rows) runs it (reference: maths:1569-1610)."""
+
+    def __init__(self, map, input, output) -> None:
+        self.map = map
+        self.input_ptr = _pointer_of(input)
+        self.output_ptr = _pointer_of(output)
+
+    def set_direct(self, map, input_ptr: int, output_ptr: int) -> None:
+        self.map, self.input_ptr, self.output_ptr = map, int(input_ptr), int(output_ptr)
+
+    def _dispatch(self, threads: int) -> None:
+        from . import _chain
+        _chain.launch_map_rows(self.map, self.input_ptr, self.output_ptr, threads)
+
+
+class GridEvaluator(Main):
+    """Evaluates every cell of `grid` into `output` ([*shape, OUT] fp32, an
+    RDVObject or a torch tensor); dispatch(evaluator, cells) runs it
+    (reference: maths:785-812)."""
+
+    def __init__(self, grid, output) -> None:
+        self.g = grid
+        self.output = output
+
+    def set_direct(self, g, output) -> None:
+        self.g, self.output = g, output
+
+    def _dispatch(self, threads: int) -> None:
+        from . import _render
+        import math as _m
+        want = _m.prod(self.g.shape)
+        if threads != want:
+            raise AssertionError(f"GridEvaluator dispatches one thread per cell ({want}), got {threads}")
+        out = self.output if isinstance(self.output, RDVObject) else wrap(self.output)
+        _render.evaluate_grid(self.g, out=out)
+
+
+class TensorOpEvaluator(Main):
+    """Re-runs a TensorOperation's kernel over its own result buffer
+    (reference: maths:1382-1399)."""
+
+    def __init__(self, op) -> None:
+        self.op = op
+
+    def _dispatch(self, threads: int) -> None:
+        self.op._forward()

@@ -15,9 +15,10 @@ import torch
 
 from .core import RDVObject, wrap
 from .maths import Grid, Map
+from .types import _MatBase, mat4x3
 
 
-class Cameras(Grid):
+class Cameras(Grid[3, 6]):
     """Pinhole cameras: cell (c, y, x) -> (origin, unit direction) of the ray
     through pixel (x, y) of camera c (reference: rendering.py:10-42,
     shaders/rendering/cameras.h).  poses: [num_cameras, 9] = origin | target | up.
@@ -46,11 +47,18 @@ class Cameras(Grid):
         self.pixel_jitter = 0
 
 
-def _identity_transform() -> list[float]:
-    return [1.0, 0.0, 0.0, 0.0, 1.0, 0.0, 0.0, 0.0, 1.0, 0.0, 0.0, 0.0]
+def _as_mat4x3(t) -> mat4x3:
+    """A transform given as a mat4x3, a 4x3 nested list / tensor (rows are the
+    columns: three linear columns, then the translation) or 12 floats in that
+    column-major order."""
+    if isinstance(t, _MatBase):
+        return mat4x3(t)
+    vals = [float(v) for v in torch.as_tensor(t, dtype=torch.float64).reshape(-1)]
+    assert len(vals) == 12, "transform must be a mat4x3 (12 values)"
+    return mat4x3(*vals)
 
 
-class RaymarchingTransmittance(Map):
+class RaymarchingTransmittance(Map[6, 1]):
     """T(x, w) along a ray through the box [-1,1]^3 of the object space given by
     `transform` (mat4x3, column-major: three linear columns, then the translation),
     marched with fixed steps: tau += extinction(x) * density_scale * step_size,
@@ -64,12 +72,9 @@ class RaymarchingTransmittance(Map):
     OUT = 1
 
     def __init__(self, extinction: Map, transform=None, step_size: float = 0.002, density_scale: float = 1.0) -> None:
-        if extinction.IN not in (None, 3) or extinction.OUT not in (None, 1):
-            raise TypeError("extinction must be a Map[3, 1]")
-        self.extinction = extinction
-        self.transform = _identity_transform() if transform is None else [float(v) for v in
-                                                                          torch.as_tensor(transform).reshape(-1)]
-        assert len(self.transform) == 12, "transform must be a mat4x3 (12 values)"
+        self.extinction = extinction.cast(Map[3, 1])  # TypeError for any other width (volumes.py:16)
+        self.transform = mat4x3(1.0, 0.0, 0.0, 0.0, 1.0, 0.0, 0.0, 0.0, 1.0, 0.0, 0.0, 0.0) \
+            if transform is None else _as_mat4x3(transform)
         self.step_size = float(step_size)
         self.density_scale = float(density_scale)
 
@@ -77,8 +82,12 @@ class RaymarchingTransmittance(Map):
         from . import _render
         return _render.raymarch_rows(self, x)
 
+    def _launch_rows(self, x_ptr: int, y_ptr: int, rows: int) -> None:
+        from . import _render
+        _render.raymarch_ptrs(self, x_ptr, y_ptr, rows)
 
-class EmissionAbsorption(Map):
+
+class EmissionAbsorption(Map[6, 3]):
     """Build-defined volume renderer (no reference counterpart): along each ray
     (origin, direction) through [-1,1]^3, `samples` points t_i = t0 + (i + 1/2) dt
     are fed through `field` (Map[3, 4]: density logit, RGB logits; any
@@ -91,8 +100,7 @@ class EmissionAbsorption(Map):
     OUT = 3
 
     def __init__(self, field: Map, samples: int = 128) -> None:
-        if field.IN not in (None, 3) or field.OUT not in (None, 4):
-            raise TypeError("field must be a Map[3, 4]")
+        field = field.cast(Map[3, 4])  # TypeError for any other width
         assert samples >= 32 and samples % 32 == 0, "samples must be a positive multiple of 32"
         self.field = field
         self.samples = int(samples)

@@ -294,3 +294,18 @@ def test_profiling_counter():
     t = rdv.profiling_submit_times()
     rdv.profiling(False)
     assert t > 0.0
+
+
+def test_dispatch_map_evaluator_and_deferred_kwargs():
+    """rdv.dispatch(MapEvaluator(map, input, output), rows) runs the same
+    kernels as map(x); keyword arguments to a call bind deferred names for
+    that call only."""
+    x, layers = WL.c1(1000)
+    m = _chain(layers, ["relu"] * 4 + ["none"])
+    xd = x.cuda()
+    want = m(rdv.wrap(xd), scale=torch.ones(1, device="cuda")).as_tensor("torch").clone()
+    y = torch.full((1000, 4), float("nan"), device="cuda")
+    rdv.dispatch(rdv.MapEvaluator(m, rdv.wrap(xd), y), 1000)
+    assert torch.equal(y, want)
+    with pytest.raises(RuntimeError):
+        rdv.Deferred("scale").resolve()  # unbound again after the call

@@ -187,3 +187,14 @@ def test_raymarching_transmittance_runtime_shaped_extinction(dims, head):
     ref = R.raymarch_transmittance(rays, _np(layers), head=head, step=0.004, density_scale=4.0)
     _close(T.reshape(-1).cpu().numpy(), ref, 1e-4, 1e-6, f"transmittance {dims}")
     assert (ref < 0.99).any() and (ref == 1).any()
+
+
+def test_grid_evaluator_dispatch_matches_call():
+    layers = WL.kaiming_uniform_f16([(64, 3), (64, 64), (64, 64), (1, 64)], seed=11)
+    ext = _field(layers, head="softplus")
+    cam = rdv.Cameras(8, 6, WL.c4_pose().cuda())
+    sensor = cam >> rdv.RaymarchingTransmittance(ext, transform=rdv.mat4x3(1, 0, 0, 0, 1, 0, 0, 0, 1, 0, 0, 0))
+    want = sensor().as_tensor("torch").clone()
+    out = torch.full((1, 6, 8, 1), float("nan"), device="cuda")
+    rdv.dispatch(rdv.GridEvaluator(sensor, out), 48)
+    assert torch.equal(out, want)
