@@ -211,8 +211,9 @@ int rdv_relu_op(const float* x, float* y, int64_t n, void* stream);
  * over a channels-last fp32 image x[H*W, cin] -> y[H*W, cout] fp32. */
 typedef struct rdv_conv2d_desc {
   int32_t H, W;       /* image size (>= 0)                                         */
-  int32_t cin;        /* multiple of 8 (RDV_PREC_F16) or 4 (RDV_PREC_F32)           */
-  int32_t cout;       /* multiple of 4                                              */
+  int32_t cin;        /* >= 1 (multiples of 8 for fp16, 4 for fp32, take 16-byte
+                         gathers; others a per-element gather)                     */
+  int32_t cout;       /* >= 1 (multiples of 4 take 16-byte stores)                  */
   int32_t kh, kw;     /* kernel size, 1..31                                         */
   int32_t precision;  /* RDV_PREC_F16: x and w rounded to fp16, fp32 accumulation;
                          RDV_PREC_F32: fp32 throughout                              */
@@ -228,7 +229,8 @@ int rdv_conv2d_validate(const rdv_conv2d_desc* desc);
 /* y = conv(x, w) + bias: y[p][o] = bias[o] + sum over taps (kh, kw) inside the
  * image and channels c of x[tap pixel][c] * w[kh][kw][c][o], the taps in (kh,
  * kw) order and channels ascending (fp32 association order otherwise
- * unspecified).  x, y: 16-byte aligned fp32 device pointers; w: fp32 device
+ * unspecified).  x, y: fp32 device pointers (16-byte aligned for the vector
+ * path, 4-byte otherwise); w: fp32 device
  * pointer in desc->w_layout, read at every call; bias: fp32 [cout] or NULL.
  * Replaces the dispatches of Conv2DTensorOp (src/rdv/domain/nn.py:414-470,
  * src/rdv/shaders/tensors/conv2d_tensor_op.h:20-80; RDV_PREC_F32) and of
@@ -240,9 +242,10 @@ int rdv_conv2d_validate(const rdv_conv2d_desc* desc);
 int rdv_conv2d(const rdv_conv2d_desc* desc, const float* x, const float* w, const float* bias, float* y,
                void* stream);
 
-/* Data movement over channels-last fp32 images x[H*W, C] (C a multiple of 4;
- * x and y 16-byte aligned device pointers; the reference asks C % 8 == 0 and
- * row counts that are multiples of 4, which the Python classes keep).
+/* Data movement over channels-last fp32 images x[H*W, C] (any C >= 1; C a
+ * multiple of 4 with 16-byte aligned x and y takes 16-byte accesses; the
+ * reference's tensor ops ask C % 8 == 0 and row counts that are multiples of
+ * 4, which the Python classes keep; its grid versions take any C).
  * y[(H/2)*(W/2), C] = 2x2 average pool, stride 2: ((x00 + x01) + x10) + x11
  * summed left to right in fp32, times 0.25 (H, W even).
  * Replaces Downsample2xTensorOp (src/rdv/domain/nn.py:1090-1107,
@@ -318,6 +321,12 @@ int rdv_cameras_rays(const rdv_camera_desc* cam, const float* poses, float* rays
  * [n, H, W, 3] fp32.  samples: a positive multiple of 32. */
 int rdv_render_emission_absorption(const rdv_camera_desc* cam, const float* poses, const rdv_mlp_desc* field,
                                    const void* packed, int32_t samples, float* image, void* stream);
+
+/* rdv_render_emission_absorption over rays given in memory: rays[n_rays, 6] =
+ * (origin, direction) fp32, out[n_rays, 3] (EmissionAbsorption as a Map[6, 3]
+ * over any grid of rays; build-defined). */
+int rdv_render_emission_absorption_rays(const rdv_mlp_desc* field, const void* packed, const float* rays,
+                                        int64_t n_rays, int32_t samples, float* out, void* stream);
 
 /* The same compositing over precomputed samples (build-defined):
  * sigma_rgb[n_rays, samples, 4] = (sigma, r, g, b), dt[n_rays] the sample

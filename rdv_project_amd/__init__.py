@@ -80,6 +80,17 @@ from .types import (
 )
 from ._conv import Winograd3x3Conv2d, winograd3x3_conv2d
 from ._render import composite
+from .grids import (
+    Conv2D,
+    Conv2dGrid,
+    Downsample2x,
+    TensorGrid,
+    TensorGridBarrier,
+    Upsample2x,
+    barrier,
+    conv2d,
+    conv2d_o,
+)
 from ._train import mse_backward
 from .rendering import Cameras, EmissionAbsorption, RaymarchingTransmittance
 from .nn import (

@@ -126,6 +126,8 @@ _SIGNATURES = {
     "rdv_cameras_rays": (C.c_int, [C.POINTER(CameraDesc), C.c_void_p, C.c_void_p, C.c_void_p]),
     "rdv_render_emission_absorption": (C.c_int, [C.POINTER(CameraDesc), C.c_void_p, C.POINTER(MlpDesc), C.c_void_p,
                                                  C.c_int32, C.c_void_p, C.c_void_p]),
+    "rdv_render_emission_absorption_rays": (C.c_int, [C.POINTER(MlpDesc), C.c_void_p, C.c_void_p, C.c_int64,
+                                                      C.c_int32, C.c_void_p, C.c_void_p]),
     "rdv_composite": (C.c_int, [C.c_void_p, C.c_void_p, C.c_int64, C.c_int32, C.c_void_p, C.c_void_p]),
     "rdv_raymarch_transmittance": (C.c_int, [C.POINTER(MlpDesc), C.c_void_p, C.c_void_p, C.c_int64,
                                              C.POINTER(C.c_float), C.c_float, C.c_float, C.c_void_p, C.c_void_p]),

@@ -72,6 +72,15 @@ def render_ea(cam: Cameras, ea: EmissionAbsorption, out: RDVObject | None = None
     return out
 
 
+def render_ea_rays(ea: EmissionAbsorption, rays_ptr: int, out_ptr: int, n_rays: int) -> None:
+    """EmissionAbsorption over n_rays rays (fp32 [n, 6] at rays_ptr) into fp32
+    [n, 3] at out_ptr: the renderer with rays read from memory."""
+    p, packed = _field_plan(ea.field, 3)
+    _lib.check(_lib.load().rdv_render_emission_absorption_rays(
+        C.byref(p.desc), C.c_void_p(packed.data_ptr()), C.c_void_p(rays_ptr), C.c_int64(n_rays),
+        C.c_int32(ea.samples), C.c_void_p(out_ptr), C.c_void_p(current_stream_handle())), "EmissionAbsorption")
+
+
 def _transform_array(rt: RaymarchingTransmittance):
     arr = (C.c_float * 12)()
     for i, v in enumerate(rt.transform.tolist_flat()):
@@ -148,4 +157,11 @@ def evaluate_grid(g: Grid, out: RDVObject | None = None) -> RDVObject:
             out.as_tensor("torch").copy_(y.as_tensor("torch").reshape(out.shape))
             return out
         return y
-    raise NotImplementedError(f"grid evaluation of {type(g).__name__} is outside this build")
+    # any other grid graph: node by node (grids.py)
+    from .grids import grid_values
+    with launch_scope():
+        v = grid_values(g, {})
+    if out is not None:
+        out.as_tensor("torch").copy_(v.as_tensor("torch").reshape(out.shape))
+        return out
+    return v

@@ -69,8 +69,9 @@ int launch_train_step_static(const rdv_mlp_desc& d, const MlpLayout& lay, const 
                              const float* target, int64_t n, float* loss, float* const* dW, float* const* db,
                              hipStream_t stream);
 int launch_camera_rays(const rdv_camera_desc& c, const float* poses, float* rays, hipStream_t stream);
-int launch_render_ea(const rdv_camera_desc& c, const float* poses, const rdv_mlp_desc& d, const MlpLayout& lay,
-                     const void* packed, int samples, float* image, hipStream_t stream);
+int launch_render_ea(const rdv_camera_desc& c, const float* poses, const float* rays, int64_t n_rays,
+                     const rdv_mlp_desc& d, const MlpLayout& lay, const void* packed, int samples, float* image,
+                     hipStream_t stream);
 int launch_composite(const float* sigma_rgb, const float* dts, int64_t nrays, int samples, float* out,
                      hipStream_t stream);
 int launch_raymarch_transmittance(const rdv_mlp_desc& d, const MlpLayout& lay, const void* packed, const float* rays,
@@ -307,7 +308,8 @@ int rdv_conv2d(const rdv_conv2d_desc* desc, const float* x, const float* w, cons
   if (int rc = check_conv2d(desc)) return rc;
   if (int64_t(desc->H) * desc->W == 0) return RDV_OK;
   if (!x || !w || !y) return fail(RDV_ERR_INVALID, "conv2d: NULL pointer argument");
-  if (!aligned16(x) || !aligned16(y)) return fail(RDV_ERR_INVALID, "conv2d: x and y must be 16-byte aligned");
+  if (reinterpret_cast<uintptr_t>(x) % 4 || reinterpret_cast<uintptr_t>(y) % 4)
+    return fail(RDV_ERR_INVALID, "conv2d: x and y must be 4-byte aligned");
   if (reinterpret_cast<uintptr_t>(w) % 4 || reinterpret_cast<uintptr_t>(bias) % 4)
     return fail(RDV_ERR_INVALID, "conv2d: w and bias must be 4-byte aligned");
   return launch_conv2d(*desc, x, w, bias, y, static_cast<hipStream_t>(stream));
@@ -315,8 +317,7 @@ int rdv_conv2d(const rdv_conv2d_desc* desc, const float* x, const float* w, cons
 
 static int check_image(const char* what, int64_t H, int64_t W, int32_t C) {
   if (H < 0 || W < 0) return fail(RDV_ERR_INVALID, std::string(what) + ": H and W must be >= 0");
-  if (C < 4 || C % 4) return fail(RDV_ERR_INVALID, std::string(what) + ": channels (" + std::to_string(C) +
-                                                       ") must be a positive multiple of 4");
+  if (C < 1) return fail(RDV_ERR_INVALID, std::string(what) + ": channels (" + std::to_string(C) + ") must be >= 1");
   if (H > (int64_t(1) << 24) || W > (int64_t(1) << 24) || H * W > (int64_t(1) << 40) / C)
     return fail(RDV_ERR_INVALID, std::string(what) + ": image too large");
   return RDV_OK;
@@ -327,7 +328,8 @@ int rdv_downsample2x(const float* x, int64_t H, int64_t W, int32_t C, float* y, 
   if (H % 2 || W % 2) return fail(RDV_ERR_INVALID, "downsample2x: H and W must be even");
   if (H == 0 || W == 0) return RDV_OK;
   if (!x || !y) return fail(RDV_ERR_INVALID, "downsample2x: NULL pointer argument");
-  if (!aligned16(x) || !aligned16(y)) return fail(RDV_ERR_INVALID, "downsample2x: x and y must be 16-byte aligned");
+  if (reinterpret_cast<uintptr_t>(x) % 4 || reinterpret_cast<uintptr_t>(y) % 4)
+    return fail(RDV_ERR_INVALID, "downsample2x: x and y must be 4-byte aligned");
   return launch_downsample2x(x, H, W, C, y, static_cast<hipStream_t>(stream));
 }
 
@@ -335,7 +337,8 @@ int rdv_upsample2x(const float* x, int64_t H, int64_t W, int32_t C, float* y, vo
   if (int rc = check_image("upsample2x", H, W, C)) return rc;
   if (H == 0 || W == 0) return RDV_OK;
   if (!x || !y) return fail(RDV_ERR_INVALID, "upsample2x: NULL pointer argument");
-  if (!aligned16(x) || !aligned16(y)) return fail(RDV_ERR_INVALID, "upsample2x: x and y must be 16-byte aligned");
+  if (reinterpret_cast<uintptr_t>(x) % 4 || reinterpret_cast<uintptr_t>(y) % 4)
+    return fail(RDV_ERR_INVALID, "upsample2x: x and y must be 4-byte aligned");
   return launch_upsample2x(x, H, W, C, y, static_cast<hipStream_t>(stream));
 }
 
@@ -428,7 +431,23 @@ int rdv_render_emission_absorption(const rdv_camera_desc* cam, const float* pose
   if (samples < 32 || samples % 32 || samples > (1 << 20))
     return fail(RDV_ERR_INVALID, "samples must be a positive multiple of 32 (at most 2^20)");
   if (!poses || !packed || !image) return fail(RDV_ERR_INVALID, "rdv_render_emission_absorption: NULL pointer argument");
-  return launch_render_ea(*cam, poses, *field, lay, packed, samples, image, static_cast<hipStream_t>(stream));
+  return launch_render_ea(*cam, poses, nullptr, 0, *field, lay, packed, samples, image,
+                          static_cast<hipStream_t>(stream));
+}
+
+int rdv_render_emission_absorption_rays(const rdv_mlp_desc* field, const void* packed, const float* rays,
+                                        int64_t n_rays, int32_t samples, float* out, void* stream) {
+  MlpLayout lay;
+  int rc = check_mlp(field, &lay);
+  if (rc != RDV_OK) return rc;
+  if (samples < 32 || samples % 32 || samples > (1 << 20))
+    return fail(RDV_ERR_INVALID, "samples must be a positive multiple of 32 (at most 2^20)");
+  if (n_rays < 0 || n_rays > (int64_t(1) << 40)) return fail(RDV_ERR_INVALID, "bad ray count");
+  if (n_rays == 0) return RDV_OK;
+  if (!packed || !rays || !out) return fail(RDV_ERR_INVALID, "rdv_render_emission_absorption_rays: NULL pointer argument");
+  const rdv_camera_desc none{1, 1, 1, 1.0f, 1.0f};
+  return launch_render_ea(none, nullptr, rays, n_rays, *field, lay, packed, samples, out,
+                          static_cast<hipStream_t>(stream));
 }
 
 int rdv_composite(const float* sigma_rgb, const float* dt, int64_t n_rays, int32_t samples, float* out,

@@ -24,8 +24,10 @@
 // from x -- the im2col matrix is never formed -- and the next chunk's loads are
 // issued before the current chunk's MFMAs.  Taps outside the image and K past
 // KH KW CIN read a clamped address and are zeroed on conversion, so every load
-// is in bounds and unconditional.  Neighbouring taps re-read neighbouring
-// pixels, which the L2 serves (a tile's receptive field is a few image rows).
+// is in bounds and unconditional (channel counts that are not a multiple of
+// the lane's group take a per-element gather and scalar stores instead).
+// Neighbouring taps re-read neighbouring pixels, which the L2 serves (a tile's
+// receptive field is a few image rows).
 //   fp16: v_mfma_f32_16x16x32_f16, A = w[16 out][32 k], B = x^T[32 k][16 px]
 //   fp32: v_mfma_f32_16x16x4f32 over 16-k chunks (a lane's float4 feeds 4 MFMAs)
 // When a block of w exceeds the LDS budget it is restaged per K pass per tile.
@@ -95,14 +97,15 @@ __device__ void cv_stage(const ConvArgs& a, int o0, int k0, int nkc, f32x4* sw, 
     const int k = k0 + c * S::kK + (ln >> 4) * S::kLane;
     f32x4 v = {0.0f, 0.0f, 0.0f, 0.0f};
     if (o < a.cout && k < a.K) {
+      // K is a multiple of kLane only when cin is; past K the slots are zero
       if constexpr (F16) {
         half8 h;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) h[i] = half_t(w_at(a, o, k + i));
+        for (int i = 0; i < 8; ++i) h[i] = half_t(k + i < a.K ? w_at(a, o, k + i) : 0.0f);
         v = __builtin_bit_cast(f32x4, h);
       } else {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) v[i] = w_at(a, o, k + i);
+        for (int i = 0; i < 4; ++i) v[i] = k + i < a.K ? w_at(a, o, k + i) : 0.0f;
       }
     }
     sw[s] = v;
@@ -118,11 +121,34 @@ struct CvPix {
 };
 
 // Gathers K chunk kk0 (this lane's kLane channels of one tap) for each pixel.
-template <bool F16>
+// VEC: cin is a multiple of kLane and x 16-byte aligned, so a lane's kLane
+// elements are consecutive channels of one tap (16-byte loads); otherwise
+// each element finds its own tap and channel (scalar loads, zero past K).
+template <bool F16, bool VEC>
 __device__ __forceinline__ void cv_load(const ConvArgs& a, const CvPix& px, int kk0, int q,
                                         f32x4 (&raw)[kCvRT][CvStep<F16>::kLane / 4], bool (&ok)[kCvRT]) {
   using S = CvStep<F16>;
   const int kk = kk0 + q * S::kLane;
+  if constexpr (!VEC) {
+#pragma unroll
+    for (int rr = 0; rr < kCvRT; ++rr) ok[rr] = px.live[rr];
+#pragma unroll
+    for (int i = 0; i < S::kLane; ++i) {
+      const int k = kk + i;
+      const int tap = k / a.cin;
+      const int ci = k - tap * a.cin;
+      const int th = tap / a.kw;
+      const int tw = tap - th * a.kw;
+#pragma unroll
+      for (int rr = 0; rr < kCvRT; ++rr) {
+        const int ih = px.h[rr] + th - a.ph, iw = px.w[rr] + tw - a.pw;
+        const bool v = k < a.K && ih >= 0 && ih < a.H && iw >= 0 && iw < a.W;
+        const float e = a.x[v ? (int64_t(ih) * a.W + iw) * a.cin + ci : 0];
+        raw[rr][i >> 2][i & 3] = v ? e : 0.0f;
+      }
+    }
+    return;
+  }
   const int tap = kk / a.cin;
   const int ci = kk - tap * a.cin;
   const int th = tap / a.kw;
@@ -183,7 +209,7 @@ __device__ __forceinline__ void cv_mma(const f32x4* sw, int nt, int nkc, int c, 
   }
 }
 
-template <bool F16, int NT>
+template <bool F16, int NT, bool VEC>
 __global__ __launch_bounds__(kCvThreads) void conv_op_kernel(ConvArgs a) {
   using S = CvStep<F16>;
   extern __shared__ f32x4 cv_smem[];
@@ -236,12 +262,12 @@ __global__ __launch_bounds__(kCvThreads) void conv_op_kernel(ConvArgs a) {
       // flight while chunk c is converted and multiplied
       f32x4 ra[kCvRT][S::kLane / 4], rb[kCvRT][S::kLane / 4];
       bool oka[kCvRT], okb[kCvRT];
-      cv_load<F16>(a, px, k0, q, ra, oka);
+      cv_load<F16, VEC>(a, px, k0, q, ra, oka);
       for (int c = 0; c < nkc; c += 2) {
         const bool more = c + 1 < nkc;
-        if (more) cv_load<F16>(a, px, k0 + (c + 1) * S::kK, q, rb, okb);
+        if (more) cv_load<F16, VEC>(a, px, k0 + (c + 1) * S::kK, q, rb, okb);
         cv_mma<F16, NT>(sw, nt, nkc, c, lane, ra, oka, acc);
-        if (c + 2 < nkc) cv_load<F16>(a, px, k0 + (c + 2) * S::kK, q, ra, oka);
+        if (c + 2 < nkc) cv_load<F16, VEC>(a, px, k0 + (c + 2) * S::kK, q, ra, oka);
         if (more) cv_mma<F16, NT>(sw, nt, nkc, c + 1, lane, rb, okb, acc);
       }
     }
@@ -259,7 +285,13 @@ __global__ __launch_bounds__(kCvThreads) void conv_op_kernel(ConvArgs a) {
 #pragma unroll
               for (int j = 0; j < 4; ++j) v[j] = fmaxf(v[j], 0.0f);
             }
-            *reinterpret_cast<f32x4*>(yr + col) = v;
+            if constexpr (VEC) {
+              *reinterpret_cast<f32x4*>(yr + col) = v;
+            } else {
+#pragma unroll
+              for (int j = 0; j < 4; ++j)
+                if (col + j < a.cout) yr[col + j] = v[j];
+            }
           }
         }
       }
@@ -267,9 +299,9 @@ __global__ __launch_bounds__(kCvThreads) void conv_op_kernel(ConvArgs a) {
   }
 }
 
-template <bool F16, int NT>
+template <bool F16, int NT, bool VEC>
 const void* cv_fn() {
-  return reinterpret_cast<const void*>(&conv_op_kernel<F16, NT>);
+  return reinterpret_cast<const void*>(&conv_op_kernel<F16, NT, VEC>);
 }
 
 }  // namespace
@@ -283,11 +315,8 @@ int conv2d_check(const rdv_conv2d_desc& d, std::string* why) {
   if (d.kh < 1 || d.kw < 1 || d.kh > 31 || d.kw > 31) return bad("kernel size must be in [1, 31]");
   if (d.precision != RDV_PREC_F16 && d.precision != RDV_PREC_F32) return bad("unknown precision code");
   if (d.w_layout != RDV_WLAYOUT_RSCK && d.w_layout != RDV_WLAYOUT_KCRS) return bad("unknown filter layout");
-  const int cstep = d.precision == RDV_PREC_F16 ? 8 : 4;
-  if (d.cin < cstep || d.cin % cstep)
-    return bad("in_channels (" + std::to_string(d.cin) + ") must be a positive multiple of " + std::to_string(cstep));
-  if (d.cout < 4 || d.cout % 4)
-    return bad("out_channels (" + std::to_string(d.cout) + ") must be a positive multiple of 4");
+  if (d.cin < 1) return bad("in_channels (" + std::to_string(d.cin) + ") must be >= 1");
+  if (d.cout < 1) return bad("out_channels (" + std::to_string(d.cout) + ") must be >= 1");
   if (int64_t(d.kh) * d.kw * d.cin > (int64_t(1) << 20)) return bad("kernel too large");
   if (int64_t(d.H) * d.W * std::max(d.cin, d.cout) >= (int64_t(1) << 40)) return bad("image too large");
   if (d.H > (1 << 24) || d.W > (1 << 24)) return bad("image too large");
@@ -296,6 +325,9 @@ int conv2d_check(const rdv_conv2d_desc& d, std::string* why) {
 
 int launch_conv2d(const rdv_conv2d_desc& d, const float* x, const float* w, const float* bias, float* y,
                   hipStream_t stream) {
+  const int cstep = d.precision == RDV_PREC_F16 ? 8 : 4;
+  const bool vec = d.cin % cstep == 0 && d.cout % 4 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
+                   reinterpret_cast<uintptr_t>(y) % 16 == 0;
   const int64_t rows = int64_t(d.H) * d.W;
   if (rows == 0) return RDV_OK;
   DeviceInfo dev;
@@ -340,12 +372,16 @@ int launch_conv2d(const rdv_conv2d_desc& d, const float* x, const float* w, cons
   const int64_t rows_per_task = int64_t(kCvWaves) * 16 * kCvRT;
   a.tasks = (rows + rows_per_task - 1) / rows_per_task;
   const int nt = ob / 16;
-  const void* fn = nullptr;
-  if (f16) fn = nt <= 2 ? cv_fn<true, 2>() : nt <= 4 ? cv_fn<true, 4>() : cv_fn<true, 8>();
-  else fn = nt <= 2 ? cv_fn<false, 2>() : nt <= 4 ? cv_fn<false, 4>() : cv_fn<false, 8>();
+  const int ti = nt <= 2 ? 0 : nt <= 4 ? 1 : 2;
+  static const void* const fns[2][2][3] = {
+      {{cv_fn<false, 2, false>(), cv_fn<false, 4, false>(), cv_fn<false, 8, false>()},
+       {cv_fn<false, 2, true>(), cv_fn<false, 4, true>(), cv_fn<false, 8, true>()}},
+      {{cv_fn<true, 2, false>(), cv_fn<true, 4, false>(), cv_fn<true, 8, false>()},
+       {cv_fn<true, 2, true>(), cv_fn<true, 4, true>(), cv_fn<true, 8, true>()}}};
+  const void* fn = fns[f16][vec][ti];
   const size_t lds = size_t(nt) * (kp / step) * 64 * sizeof(f32x4) + size_t(ob) * sizeof(float);
-  static bool attr_set[2][3] = {};
-  bool& set = attr_set[f16][nt <= 2 ? 0 : nt <= 4 ? 1 : 2];
+  static bool attr_set[2][2][3] = {};
+  bool& set = attr_set[f16][vec][ti];
   if (!set) {
     RDV_HIP_TRY(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
                                     int(kCvLdsCap + kCvMaxOb * sizeof(float))));

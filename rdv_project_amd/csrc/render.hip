@@ -169,11 +169,35 @@ __device__ __forceinline__ void stage_weights(const uint8_t* packed, const MlpLa
 // ------------------------------------------------------ emission-absorption
 struct RenderArgs {
   CameraParams cam;
+  const float* rays;  // [n_rays, 6] (origin, direction) in memory, or null: the rays of `cam`
+  int64_t n_rays;     // with `rays`
   const uint8_t* packed;
   MlpLayout lay;
-  float* image;  // [n, H, W, 3]
+  float* image;  // [n, H, W, 3] (or [n_rays, 3])
   int samples;   // multiple of 32
 };
+
+__device__ __forceinline__ int64_t ea_ray_count(const RenderArgs& a) {
+  return a.rays != nullptr ? a.n_rays : int64_t(a.cam.n) * a.cam.H * a.cam.W;
+}
+
+// Origin and direction of ray `ray`: read from memory, or the camera's pixel ray.
+__device__ __forceinline__ void ea_ray(const RenderArgs& a, int64_t ray, float (&o)[3], float (&w)[3]) {
+  if (a.rays != nullptr) {
+    const float* r = a.rays + ray * 6;
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+      o[i] = r[i];
+      w[i] = r[3 + i];
+    }
+    return;
+  }
+  const int x = int(ray % a.cam.W);
+  const int64_t rest = ray / a.cam.W;
+  const int y = int(rest % a.cam.H);
+  const int cam = int(rest / a.cam.H);
+  camera_ray(a.cam, cam, y, x, o, w);
+}
 
 template <class N>
 __global__ __launch_bounds__(kEaThreads, 1) void render_ea_kernel(RenderArgs a) {
@@ -183,7 +207,7 @@ __global__ __launch_bounds__(kEaThreads, 1) void render_ea_kernel(RenderArgs a) 
   __shared__ int s_next;
   const int lane = threadIdx.x & 63;
   const int h = lane >> 5, col = lane & 31;
-  const int64_t nrays = int64_t(a.cam.n) * a.cam.H * a.cam.W;
+  const int64_t nrays = ea_ray_count(a);
   const int64_t per_block = (nrays + gridDim.x - 1) / gridDim.x;
   const int64_t r_begin = int64_t(blockIdx.x) * per_block;
   const int64_t r_end = r_begin + per_block < nrays ? r_begin + per_block : nrays;
@@ -199,12 +223,8 @@ __global__ __launch_bounds__(kEaThreads, 1) void render_ea_kernel(RenderArgs a) 
   const int chunks = a.samples / 32;
   for (int r = claim(); r < nr; r = claim()) {
     const int64_t ray = r_begin + r;
-    const int x = int(ray % a.cam.W);
-    const int64_t rest = ray / a.cam.W;
-    const int y = int(rest % a.cam.H);
-    const int cam = int(rest / a.cam.H);
     float o[3], w[3];
-    camera_ray(a.cam, cam, y, x, o, w);
+    ea_ray(a, ray, o, w);
     float t0, t1;
     ray_box(o, w, t0, t1);
     float cr = 0.0f, cg = 0.0f, cb = 0.0f;
@@ -575,7 +595,7 @@ __global__ __launch_bounds__(64 * gen_waves<MT>(), 1) void render_ea_generic_ker
   const GenNet& g = ga.net;
   const int lane = threadIdx.x & 63;
   const int h = lane >> 5, col = lane & 31;
-  const int64_t nrays = int64_t(a.cam.n) * a.cam.H * a.cam.W;
+  const int64_t nrays = ea_ray_count(a);
   const int64_t per_block = (nrays + gridDim.x - 1) / gridDim.x;
   const int64_t r_begin = int64_t(blockIdx.x) * per_block;
   const int64_t r_end = r_begin + per_block < nrays ? r_begin + per_block : nrays;
@@ -594,12 +614,8 @@ __global__ __launch_bounds__(64 * gen_waves<MT>(), 1) void render_ea_generic_ker
   const int chunks = a.samples / 32;
   for (int r = claim(); r < nr; r = claim()) {
     const int64_t ray = r_begin + r;
-    const int x = int(ray % a.cam.W);
-    const int64_t rest = ray / a.cam.W;
-    const int y = int(rest % a.cam.H);
-    const int cam = int(rest / a.cam.H);
     float o[3], w[3];
-    camera_ray(a.cam, cam, y, x, o, w);
+    ea_ray(a, ray, o, w);
     float t0, t1;
     ray_box(o, w, t0, t1);
     float cr = 0.0f, cg = 0.0f, cb = 0.0f;
@@ -732,8 +748,9 @@ int launch_camera_rays(const rdv_camera_desc& c, const float* poses, float* rays
   return RDV_OK;
 }
 
-int launch_render_ea(const rdv_camera_desc& c, const float* poses, const rdv_mlp_desc& d, const MlpLayout& lay,
-                     const void* packed, int samples, float* image, hipStream_t stream) {
+int launch_render_ea(const rdv_camera_desc& c, const float* poses, const float* rays, int64_t n_rays,
+                     const rdv_mlp_desc& d, const MlpLayout& lay, const void* packed, int samples, float* image,
+                     hipStream_t stream) {
   const bool fixed = is_render_field(d, lay);
   if (!fixed && !(is_f16_field(d, 4) && d.act[d.n_layers - 1] == RDV_ACT_NONE))
     return fail(RDV_ERR_UNSUPPORTED,
@@ -744,11 +761,13 @@ int launch_render_ea(const rdv_camera_desc& c, const float* poses, const rdv_mlp
   if (rc != RDV_OK) return rc;
   RenderArgs a;
   a.cam = CameraParams{poses, c.n_cams, c.height, c.width, c.aspect_ratio, c.fov};
+  a.rays = rays;
+  a.n_rays = n_rays;
   a.packed = static_cast<const uint8_t*>(packed);
   a.lay = lay;
   a.image = image;
   a.samples = samples;
-  const int64_t nrays = int64_t(c.n_cams) * c.height * c.width;
+  const int64_t nrays = rays != nullptr ? n_rays : int64_t(c.n_cams) * c.height * c.width;
   if (!fixed) {
     RenderGenArgs ga;
     ga.r = a;

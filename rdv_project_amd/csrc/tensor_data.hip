@@ -60,6 +60,35 @@ __global__ __launch_bounds__(256) void concat_kernel(const f32x4* __restrict__ x
   }
 }
 
+// Per-element versions for channel counts that are not a multiple of 4 (or
+// buffers that are not 16-byte aligned): the same arithmetic, one float per lane.
+__global__ __launch_bounds__(256) void downsample2x_scalar_kernel(const float* __restrict__ x, float* __restrict__ y,
+                                                                  int64_t Wo, int64_t C, int64_t total) {
+  const int64_t stride = int64_t(gridDim.x) * blockDim.x;
+  const int64_t row_in = 2 * Wo * C;
+  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < total; i += stride) {
+    const int64_t c = i % C, pix = i / C;
+    const int64_t oh = pix / Wo, ow = pix % Wo;
+    const int64_t base = (2 * oh) * row_in + (2 * ow) * C + c;
+    y[i] = (((x[base] + x[base + C]) + x[base + row_in]) + x[base + row_in + C]) * 0.25f;
+  }
+}
+
+__global__ __launch_bounds__(256) void upsample2x_scalar_kernel(const float* __restrict__ x, float* __restrict__ y,
+                                                                int64_t Wo, int64_t C, int64_t total) {
+  const int64_t stride = int64_t(gridDim.x) * blockDim.x;
+  const int64_t Wi = Wo / 2;
+  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < total; i += stride) {
+    const int64_t c = i % C, pix = i / C;
+    const int64_t oh = pix / Wo, ow = pix % Wo;
+    y[i] = x[((oh / 2) * Wi + ow / 2) * C + c];
+  }
+}
+
+bool vec_ok(const void* a, const void* b, int C) {
+  return C % 4 == 0 && reinterpret_cast<uintptr_t>(a) % 16 == 0 && reinterpret_cast<uintptr_t>(b) % 16 == 0;
+}
+
 // Every index of a launch (input and output, plus a grid-stride step past the
 // end) below 2^32?
 bool fits32(int64_t in_groups, int64_t out_groups) {
@@ -80,6 +109,15 @@ int grid_for(int64_t total, unsigned* blocks) {
 }  // namespace
 
 int launch_downsample2x(const float* x, int64_t H, int64_t W, int C, float* y, hipStream_t stream) {
+  if (!vec_ok(x, y, C)) {
+    const int64_t n = (H / 2) * (W / 2) * C;
+    if (n == 0) return RDV_OK;
+    unsigned blocks = 0;
+    if (int rc = grid_for(n, &blocks)) return rc;
+    downsample2x_scalar_kernel<<<dim3(blocks), dim3(256), 0, stream>>>(x, y, W / 2, C, n);
+    RDV_HIP_TRY(hipGetLastError());
+    return RDV_OK;
+  }
   const int64_t total = (H / 2) * (W / 2) * (C / 4);
   if (total == 0) return RDV_OK;
   unsigned blocks = 0;
@@ -96,6 +134,15 @@ int launch_downsample2x(const float* x, int64_t H, int64_t W, int C, float* y, h
 }
 
 int launch_upsample2x(const float* x, int64_t H, int64_t W, int C, float* y, hipStream_t stream) {
+  if (!vec_ok(x, y, C)) {
+    const int64_t n = (2 * H) * (2 * W) * C;
+    if (n == 0) return RDV_OK;
+    unsigned blocks = 0;
+    if (int rc = grid_for(n, &blocks)) return rc;
+    upsample2x_scalar_kernel<<<dim3(blocks), dim3(256), 0, stream>>>(x, y, 2 * W, C, n);
+    RDV_HIP_TRY(hipGetLastError());
+    return RDV_OK;
+  }
   const int64_t total = (2 * H) * (2 * W) * (C / 4);
   if (total == 0) return RDV_OK;
   unsigned blocks = 0;

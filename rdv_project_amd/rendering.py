@@ -106,4 +106,19 @@ class EmissionAbsorption(Map[6, 3]):
         self.samples = int(samples)
 
     def _evaluate_rows(self, x) -> RDVObject:
-        raise NotImplementedError("EmissionAbsorption renders camera rays: call (Cameras(...) >> it)()")
+        from . import _render
+        x = wrap(x)
+        if x.scalar_type != torch.float32:
+            raise TypeError(f"Map input must be float32, got {x.scalar_type}")
+        assert x.shape[-1] == 6, "EmissionAbsorption expects rows of 6 values (origin, direction)"
+        xt = x.as_tensor("torch").contiguous()
+        rows = xt.numel() // 6
+        out = _render._cached(("ea-rows", id(type(self))), (*x.shape[:-1], 3))
+        from .core import launch_scope
+        with launch_scope():
+            _render.render_ea_rays(self, xt.data_ptr(), out.device_ptr, rows)
+        return out
+
+    def _launch_rows(self, x_ptr: int, y_ptr: int, rows: int) -> None:
+        from . import _render
+        _render.render_ea_rays(self, x_ptr, y_ptr, rows)
