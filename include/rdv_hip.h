@@ -308,8 +308,24 @@ typedef struct rdv_camera_desc {
 /* rays[n, H, W, 6] = (origin, unit direction) of the pinhole camera ray through
  * each pixel centre; poses is a device [n, 9] fp32 array (origin | target | up).
  * Replaces Cameras' grid dispatch (src/rdv/domain/rendering.py:10-42,
- * src/rdv/shaders/rendering/cameras.h:1-20); pixel jitter is not supported. */
+ * src/rdv/shaders/rendering/cameras.h:1-20) with pixel_jitter == 0. */
 int rdv_cameras_rays(const rdv_camera_desc* cam, const float* poses, float* rays, void* stream);
+
+/* rdv_cameras_rays with pixel jitter (Cameras(jitter=True), cameras.h:7): the
+ * ray of cell i (the row-major cell index) passes through sub-pixel position
+ * (u0, u1) instead of the centre, where u0, u1 are the first two random()
+ * values of thread i of a dispatch with these seeds (rdv_random_uniform).
+ * seeds: 4 host words (RandomLibrary's per-dispatch uvec4). */
+int rdv_cameras_rays_jittered(const rdv_camera_desc* cam, const float* poses, const uint32_t* seeds, float* rays,
+                              void* stream);
+
+/* out[t * per_thread + k] = the k-th random() value of thread t of a dispatch
+ * whose seeds are `seeds` (4 host words): the reference's per-thread generator
+ * (three Tausworthe steps and an LCG, GPU Gems 3 ch. 37), spawned from the
+ * seeds and thread index t and mapped to [0, 1) through the mantissa
+ * (src/rdv/shaders/libraries/random_library.h:1-62, :255-267;
+ * src/rdv/core/_common.py:56-89).  n_threads < 2^31. */
+int rdv_random_uniform(const uint32_t* seeds, int64_t n_threads, int32_t per_thread, float* out, void* stream);
 
 /* Emission-absorption render of a density / RGB field (build-defined; no
  * reference counterpart): for every pixel ray of `cam` that meets [-1,1]^3 on
@@ -347,6 +363,57 @@ int rdv_composite(const float* sigma_rgb, const float* dt, int64_t n_rays, int32
 int rdv_raymarch_transmittance(const rdv_mlp_desc* extinction, const void* packed, const float* rays,
                                int64_t n_rays, const float* transform12, float step_size, float density_scale,
                                float* out, void* stream);
+
+/* ------------------------------------------------ ratio tracking and majorants */
+typedef struct rdv_ratiotracking_desc {
+  float transform[12];   /* mat4x3, column-major, as rdv_raymarch_transmittance      */
+  float density_scale;
+  int32_t maj_width, maj_height, maj_depth;  /* the majorant grid [depth, height, width] */
+  uint32_t seeds[4];     /* the dispatch's random seeds                              */
+  int32_t rng_skip;      /* random() draws each thread took before this map (2 when the
+                            rays come from a jittered camera of the same dispatch)   */
+  int32_t reserved;      /* 0                                                        */
+} rdv_ratiotracking_desc;
+
+/* out[n] = ratio-tracking transmittance along each ray rays[n, 6] = (x, w)
+ * through the box [-1,1]^3 in the object space of the transform, with a voxel
+ * majorant field: free flights of -log(1 - random()) / (majorant * density_scale)
+ * capped at the voxel exit, T *= 1 - extinction(x) / majorant at each
+ * collision, Russian roulette below T = 0.05, at most 1024 steps (1 for rays
+ * that miss).  Thread i (ray i) draws from the generator of rdv_random_uniform
+ * with rt->seeds, after skipping rt->rng_skip values.  majorant: device
+ * [depth, height, width] fp32, every value an upper bound of the extinction over
+ * its voxel (else the estimate is biased).  extinction: any LinearFast chain from
+ * 3 inputs to 1 output.
+ * Replaces RatiotrackingTransmittance with VoxelMajorantField
+ * (src/rdv/domain/volumes.py:144-211, shaders/volumes/ratiotracking_transmittance.h,
+ * ratiotracking_transmittance_trait.h:1-31, voxel_majorant_field.h:1-33). */
+int rdv_ratiotracking_transmittance(const rdv_mlp_desc* extinction, const void* packed,
+                                    const rdv_ratiotracking_desc* rt, const float* majorant, const float* rays,
+                                    int64_t n_rays, float* out, void* stream);
+
+/* VoxelMajorantField as a Map[6, 2] over rows: out[i] = (the value of the grid
+ * voxel holding x_i, the distance along w_i to that voxel's exit), rays[n, 6] in
+ * the grid's [-1,1]^3 box; grid: device [depth, height, width] fp32
+ * (src/rdv/domain/volumes.py:191-211, shaders/volumes/voxel_majorant_field.h:1-33). */
+int rdv_voxel_majorant(const float* grid, int32_t width, int32_t height, int32_t depth, const float* rays,
+                       int64_t n_rays, float* out, void* stream);
+
+typedef struct rdv_majorant_grid_desc {
+  int32_t rank;           /* grid dimensions, 1..4                                  */
+  int32_t channels;       /* values per cell (the grid's OUT)                       */
+  int32_t fine_shape[4];  /* the wrapped grid's shape (first `rank` entries)        */
+  int32_t shape[4];       /* the majorant grid's shape                              */
+  int32_t aligned;        /* the sampler convention: 1 ties -1/+1 to the outer voxel centres */
+  int32_t linear;         /* 1: interpolating sampler (reaches one more voxel)      */
+} rdv_majorant_grid_desc;
+
+/* out[shape..., channels] = per coarse cell, the channel-wise maximum over every
+ * fine cell that a sampler with the given aligned / linear convention could read
+ * from inside that coarse cell; fine: device [fine_shape..., channels] fp32.
+ * Replaces MajorantGrid (src/rdv/maths/__init__.py:534-569,
+ * shaders/grids/majorant_grid.h). */
+int rdv_majorant_grid(const rdv_majorant_grid_desc* desc, const float* fine, float* out, void* stream);
 
 #ifdef __cplusplus
 }

@@ -45,16 +45,23 @@ def _normalize(v):
     return v / np.sqrt(np.sum(v * v, axis=-1, keepdims=True))
 
 
-def camera_rays(width: int, height: int, poses, aspect: float | None = None, fov: float | None = None) -> np.ndarray:
-    """[n, H, W, 6] rays (float64) of cameras.h for poses [n, 9]."""
+def camera_rays(width: int, height: int, poses, aspect: float | None = None, fov: float | None = None,
+                jitter: np.ndarray | None = None) -> np.ndarray:
+    """[n, H, W, 6] rays (float64) of cameras.h for poses [n, 9].  jitter:
+    [n, H, W, 2] sub-pixel positions (x, y) in [0, 1) replacing the centre
+    (cameras.h:7: two random() draws per cell when pixel_jitter is set)."""
     poses = np.asarray(poses, np.float64).reshape(-1, 9)
+    n = poses.shape[0]
     aspect = width / height if aspect is None else aspect
     fov = math.pi / 4 if fov is None else fov
     o, t, up = poses[:, 0:3], poses[:, 3:6], poses[:, 6:9]
-    xs = (np.arange(width) + 0.5) / width * 2 - 1
-    ys = (np.arange(height) + 0.5) / height * 2 - 1
-    sx = xs[None, None, :] * aspect
-    sy = ys[None, :, None] * np.ones((1, 1, width))
+    if jitter is None:
+        jitter = np.full((n, height, width, 2), 0.5)
+    jitter = np.asarray(jitter, np.float64).reshape(n, height, width, 2)
+    xs = (np.arange(width)[None, None, :] + jitter[..., 0]) / width * 2 - 1
+    ys = (np.arange(height)[None, :, None] + jitter[..., 1]) / height * 2 - 1
+    sx = xs * aspect
+    sy = ys
     sz = 1.0 / math.tan(fov * 0.5)
     z = _normalize(t - o)
     xa = _normalize(np.cross(up, z))
@@ -62,7 +69,6 @@ def camera_rays(width: int, height: int, poses, aspect: float | None = None, fov
     w = (xa[:, None, None, :] * sx[..., None] + ya[:, None, None, :] * sy[..., None] +
          z[:, None, None, :] * sz)
     w = _normalize(w)
-    n = poses.shape[0]
     out = np.empty((n, height, width, 6))
     out[..., 0:3] = o[:, None, None, :]
     out[..., 3:6] = w

@@ -84,6 +84,7 @@ from .grids import (
     Conv2D,
     Conv2dGrid,
     Downsample2x,
+    MajorantGrid,
     TensorGrid,
     TensorGridBarrier,
     Upsample2x,
@@ -92,7 +93,13 @@ from .grids import (
     conv2d_o,
 )
 from ._train import mse_backward
-from .rendering import Cameras, EmissionAbsorption, RaymarchingTransmittance
+from .rendering import (
+    Cameras,
+    EmissionAbsorption,
+    RatiotrackingTransmittance,
+    RaymarchingTransmittance,
+    VoxelMajorantField,
+)
 from .nn import (
     ConcatTensorOp,
     Conv2DTensorOp,

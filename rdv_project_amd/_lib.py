@@ -101,6 +101,32 @@ class Conv2dDesc(C.Structure):
     ]
 
 
+class RatiotrackingDesc(C.Structure):
+    """Mirror of rdv_ratiotracking_desc."""
+    _fields_ = [
+        ("transform", C.c_float * 12),
+        ("density_scale", C.c_float),
+        ("maj_width", C.c_int32),
+        ("maj_height", C.c_int32),
+        ("maj_depth", C.c_int32),
+        ("seeds", C.c_uint32 * 4),
+        ("rng_skip", C.c_int32),
+        ("reserved", C.c_int32),
+    ]
+
+
+class MajorantGridDesc(C.Structure):
+    """Mirror of rdv_majorant_grid_desc."""
+    _fields_ = [
+        ("rank", C.c_int32),
+        ("channels", C.c_int32),
+        ("fine_shape", C.c_int32 * 4),
+        ("shape", C.c_int32 * 4),
+        ("aligned", C.c_int32),
+        ("linear", C.c_int32),
+    ]
+
+
 class RDVError(RuntimeError):
     """A HIP runtime failure reported by the library."""
 
@@ -124,6 +150,14 @@ _SIGNATURES = {
     "rdv_mlp_train_step_static": (C.c_int, [C.POINTER(MlpDesc), C.c_void_p, C.c_void_p, C.c_void_p, C.c_int64,
                                             C.c_void_p, C.POINTER(C.c_void_p), C.POINTER(C.c_void_p), C.c_void_p]),
     "rdv_cameras_rays": (C.c_int, [C.POINTER(CameraDesc), C.c_void_p, C.c_void_p, C.c_void_p]),
+    "rdv_cameras_rays_jittered": (C.c_int, [C.POINTER(CameraDesc), C.c_void_p, C.POINTER(C.c_uint32), C.c_void_p,
+                                            C.c_void_p]),
+    "rdv_random_uniform": (C.c_int, [C.POINTER(C.c_uint32), C.c_int64, C.c_int32, C.c_void_p, C.c_void_p]),
+    "rdv_ratiotracking_transmittance": (C.c_int, [C.POINTER(MlpDesc), C.c_void_p, C.POINTER(RatiotrackingDesc),
+                                                  C.c_void_p, C.c_void_p, C.c_int64, C.c_void_p, C.c_void_p]),
+    "rdv_voxel_majorant": (C.c_int, [C.c_void_p, C.c_int32, C.c_int32, C.c_int32, C.c_void_p, C.c_int64, C.c_void_p,
+                                     C.c_void_p]),
+    "rdv_majorant_grid": (C.c_int, [C.POINTER(MajorantGridDesc), C.c_void_p, C.c_void_p, C.c_void_p]),
     "rdv_render_emission_absorption": (C.c_int, [C.POINTER(CameraDesc), C.c_void_p, C.POINTER(MlpDesc), C.c_void_p,
                                                  C.c_int32, C.c_void_p, C.c_void_p]),
     "rdv_render_emission_absorption_rays": (C.c_int, [C.POINTER(MlpDesc), C.c_void_p, C.c_void_p, C.c_int64,

@@ -9,13 +9,15 @@ Sensor (maths:252-271) applies its map to each cell's value.
 from __future__ import annotations
 
 import ctypes as C
+import math
 
 import torch
 
 from . import _chain, _lib
 from .core import RDVObject, current_stream_handle, device, launch_scope, wrap
 from .maths import Grid, Sensor
-from .rendering import Cameras, EmissionAbsorption, RaymarchingTransmittance
+from .rendering import (Cameras, EmissionAbsorption, RaymarchingTransmittance, RatiotrackingTransmittance,
+                        VoxelMajorantField)
 
 _GRID_CACHE: dict = {}
 
@@ -43,14 +45,42 @@ def _poses(cam: Cameras) -> torch.Tensor:
     return p
 
 
-def camera_rays(cam: Cameras, out: RDVObject | None = None) -> RDVObject:
+def _seed_array(seeds):
+    arr = (C.c_uint32 * 4)()
+    for i, v in enumerate(seeds):
+        arr[i] = int(v) & 0xFFFFFFFF
+    return arr
+
+
+def camera_rays(cam: Cameras, out: RDVObject | None = None, seeds=None) -> RDVObject:
+    """The cameras' rays [n, H, W, 6].  A jittered camera draws with `seeds`
+    (4 words; fresh RandomLibrary seeds when None)."""
     n, H, W = cam.shape
     out = out if out is not None else _cached(("cameras",), (n, H, W, 6))
     d = camera_desc(cam)
+    lib = _lib.load()
     with launch_scope():
-        _lib.check(_lib.load().rdv_cameras_rays(C.byref(d), C.c_void_p(_poses(cam).data_ptr()),
-                                                C.c_void_p(out.device_ptr), C.c_void_p(current_stream_handle())),
-                   "Cameras")
+        if cam.pixel_jitter:
+            from .types import RandomLibrary
+            seeds = RandomLibrary.next_seeds() if seeds is None else seeds
+            _lib.check(lib.rdv_cameras_rays_jittered(C.byref(d), C.c_void_p(_poses(cam).data_ptr()),
+                                                     _seed_array(seeds), C.c_void_p(out.device_ptr),
+                                                     C.c_void_p(current_stream_handle())), "Cameras")
+        else:
+            _lib.check(lib.rdv_cameras_rays(C.byref(d), C.c_void_p(_poses(cam).data_ptr()),
+                                            C.c_void_p(out.device_ptr), C.c_void_p(current_stream_handle())),
+                       "Cameras")
+    return out
+
+
+def random_uniform(seeds, n_threads: int, per_thread: int) -> torch.Tensor:
+    """[n_threads, per_thread]: the first random() values of each thread of a
+    dispatch with these seeds (the generator every random node draws from)."""
+    out = torch.empty((n_threads, per_thread), dtype=torch.float32, device=device())
+    with launch_scope():
+        _lib.check(_lib.load().rdv_random_uniform(_seed_array(seeds), C.c_int64(n_threads), C.c_int32(per_thread),
+                                                  C.c_void_p(out.data_ptr()), C.c_void_p(current_stream_handle())),
+                   "random_uniform")
     return out
 
 
@@ -120,6 +150,100 @@ def raymarch_rows(rt: RaymarchingTransmittance, x, out: RDVObject | None = None)
     return out
 
 
+def _ray_rows(x, name: str, out_width: int, key) -> tuple[torch.Tensor, int, RDVObject]:
+    x = wrap(x)
+    if x.scalar_type != torch.float32:
+        raise TypeError(f"Map input must be float32, got {x.scalar_type}")
+    assert x.shape[-1] == 6, f"{name} expects rows of 6 values (x, w)"
+    rows = 1
+    for s_ in x.shape[:-1]:
+        rows *= int(s_)
+    xt = x.as_tensor("torch")
+    if not xt.is_contiguous():
+        xt = xt.contiguous()
+    return xt, rows, _cached(key, (*x.shape[:-1], out_width))
+
+
+def _majorant_values(f: VoxelMajorantField) -> tuple[torch.Tensor, int, int, int]:
+    """The field's grid values as a contiguous fp32 [D, H, W] tensor and (W, H, D)."""
+    D, H, W = (int(v) for v in f.grid.shape)
+    g = f._grid_values().as_tensor("torch")
+    if g.dtype != torch.float32 or not g.is_contiguous():
+        g = g.to(torch.float32).contiguous()
+    assert g.numel() == D * H * W, "the majorant grid must hold one value per voxel"
+    return g, W, H, D
+
+
+def voxel_majorant_ptrs(f: VoxelMajorantField, x_ptr: int, y_ptr: int, rows: int) -> None:
+    """VoxelMajorantField over `rows` rays (fp32 [rows, 6] at x_ptr) into fp32 [rows, 2] at y_ptr."""
+    g, W, H, D = _majorant_values(f)
+    _lib.check(_lib.load().rdv_voxel_majorant(C.c_void_p(g.data_ptr()), C.c_int32(W), C.c_int32(H), C.c_int32(D),
+                                              C.c_void_p(x_ptr), C.c_int64(rows), C.c_void_p(y_ptr),
+                                              C.c_void_p(current_stream_handle())), "VoxelMajorantField")
+
+
+def voxel_majorant_rows(f: VoxelMajorantField, x) -> RDVObject:
+    xt, rows, out = _ray_rows(x, "VoxelMajorantField", 2, ("vmf", id(type(f))))
+    with launch_scope():
+        voxel_majorant_ptrs(f, xt.data_ptr(), out.device_ptr, rows)
+    return out
+
+
+def _ratio_desc(rt: RatiotrackingTransmittance, seeds, rng_skip: int, W: int, H: int, D: int):
+    d = _lib.RatiotrackingDesc()
+    for i, v in enumerate(rt.transform.tolist_flat()):
+        d.transform[i] = v
+    d.density_scale = rt.density_scale
+    d.maj_width, d.maj_height, d.maj_depth = W, H, D
+    for i, v in enumerate(seeds):
+        d.seeds[i] = int(v) & 0xFFFFFFFF
+    d.rng_skip = rng_skip
+    d.reserved = 0
+    return d
+
+
+def ratiotracking_ptrs(rt: RatiotrackingTransmittance, x_ptr: int, y_ptr: int, rows: int, seeds=None,
+                       rng_skip: int = 0) -> None:
+    """RatiotrackingTransmittance over `rows` rays (fp32 [rows, 6] at x_ptr) into
+    fp32 [rows] at y_ptr; ray i draws from thread i's generator of `seeds`
+    (fresh RandomLibrary seeds when None) after skipping rng_skip values."""
+    from .types import RandomLibrary
+    seeds = RandomLibrary.next_seeds() if seeds is None else seeds
+    p, packed = _field_plan(rt.extinction, 3)
+    g, W, H, D = _majorant_values(rt.majorant)
+    d = _ratio_desc(rt, seeds, rng_skip, W, H, D)
+    _lib.check(_lib.load().rdv_ratiotracking_transmittance(
+        C.byref(p.desc), C.c_void_p(packed.data_ptr()), C.byref(d), C.c_void_p(g.data_ptr()), C.c_void_p(x_ptr),
+        C.c_int64(rows), C.c_void_p(y_ptr), C.c_void_p(current_stream_handle())), "RatiotrackingTransmittance")
+
+
+def ratiotracking_rows(rt: RatiotrackingTransmittance, x, out: RDVObject | None = None, seeds=None,
+                       rng_skip: int = 0) -> RDVObject:
+    """RatiotrackingTransmittance over rows x [..., 6] -> [..., 1]."""
+    xt, rows, cached = _ray_rows(x, "RatiotrackingTransmittance", 1, ("rtt", id(type(rt))))
+    out = cached if out is None else out
+    with launch_scope():
+        ratiotracking_ptrs(rt, xt.data_ptr(), out.device_ptr, rows, seeds, rng_skip)
+    return out
+
+
+def majorant_grid(fine: torch.Tensor, fine_shape, shape, channels: int, aligned: bool, linear: bool,
+                  out: torch.Tensor) -> torch.Tensor:
+    """MajorantGrid's values: fine [*fine_shape, channels] -> out [*shape, channels]."""
+    d = _lib.MajorantGridDesc()
+    d.rank = len(shape)
+    d.channels = channels
+    for i in range(len(shape)):
+        d.fine_shape[i] = int(fine_shape[i])
+        d.shape[i] = int(shape[i])
+    d.aligned = 1 if aligned else 0
+    d.linear = 1 if linear else 0
+    with launch_scope():
+        _lib.check(_lib.load().rdv_majorant_grid(C.byref(d), C.c_void_p(fine.data_ptr()), C.c_void_p(out.data_ptr()),
+                                                 C.c_void_p(current_stream_handle())), "MajorantGrid")
+    return out
+
+
 def composite(sigma_rgb: torch.Tensor, dt: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
     """Front-to-back compositing of samples sigma_rgb [n_rays, S, 4] = (sigma,
     r, g, b) with spacing dt [n_rays] -> [n_rays, 3] (build-defined)."""
@@ -147,11 +271,24 @@ def evaluate_grid(g: Grid, out: RDVObject | None = None) -> RDVObject:
         return camera_rays(g, out)
     if isinstance(g, Sensor) and isinstance(g.grid, Cameras):
         cam, m = g.grid, g.map
-        if isinstance(m, EmissionAbsorption):
+        if isinstance(m, EmissionAbsorption) and not cam.pixel_jitter:
             return render_ea(cam, m, out)
-        rays = camera_rays(cam, _cached(("sensor-rays",), (*cam.shape, 6)))
+        # One dispatch's seeds for the camera and the map: the reference's sensor
+        # runs both in one thread per cell, whose generator the camera's jitter
+        # advances by two draws before the map draws.
+        from .types import RandomLibrary
+        seeds = RandomLibrary.next_seeds()
+        rays = camera_rays(cam, _cached(("sensor-rays",), (*cam.shape, 6)), seeds=seeds)
+        if isinstance(m, EmissionAbsorption):
+            out = out if out is not None else _cached(("sensor-ea",), (*cam.shape, 3))
+            with launch_scope():
+                render_ea_rays(m, rays.device_ptr, out.device_ptr, math.prod(cam.shape))
+            return out
         if isinstance(m, RaymarchingTransmittance):
             return raymarch_rows(m, rays, out if out is not None else _cached(("sensor-rt",), (*cam.shape, 1)))
+        if isinstance(m, RatiotrackingTransmittance):
+            return ratiotracking_rows(m, rays, out if out is not None else _cached(("sensor-rtt",), (*cam.shape, 1)),
+                                      seeds=seeds, rng_skip=2 if cam.pixel_jitter else 0)
         y = m(rays)
         if out is not None:
             out.as_tensor("torch").copy_(y.as_tensor("torch").reshape(out.shape))

@@ -68,7 +68,15 @@ int launch_train_step(const rdv_mlp_desc& d, const MlpLayout& lay, const void* p
 int launch_train_step_static(const rdv_mlp_desc& d, const MlpLayout& lay, const void* packed, const void* x,
                              const float* target, int64_t n, float* loss, float* const* dW, float* const* db,
                              hipStream_t stream);
-int launch_camera_rays(const rdv_camera_desc& c, const float* poses, float* rays, hipStream_t stream);
+int launch_camera_rays(const rdv_camera_desc& c, const float* poses, const uint32_t* seeds, float* rays,
+                       hipStream_t stream);
+int launch_random_uniform(const uint32_t* seeds, int64_t n_threads, int per_thread, float* out, hipStream_t stream);
+int launch_ratiotracking(const rdv_mlp_desc& d, const MlpLayout& lay, const void* packed,
+                         const rdv_ratiotracking_desc& rt, const float* majorant, const float* rays, int64_t nrays,
+                         float* out, hipStream_t stream);
+int launch_voxel_majorant(const float* grid, int mw, int mh, int md, const float* rays, int64_t n, float* out,
+                          hipStream_t stream);
+int launch_majorant_grid(const rdv_majorant_grid_desc& g, const float* fine, float* out, hipStream_t stream);
 int launch_render_ea(const rdv_camera_desc& c, const float* poses, const float* rays, int64_t n_rays,
                      const rdv_mlp_desc& d, const MlpLayout& lay, const void* packed, int samples, float* image,
                      hipStream_t stream);
@@ -418,7 +426,25 @@ int rdv_cameras_rays(const rdv_camera_desc* cam, const float* poses, float* rays
   int rc = check_camera(cam);
   if (rc != RDV_OK) return rc;
   if (!poses || !rays) return fail(RDV_ERR_INVALID, "rdv_cameras_rays: NULL pointer argument");
-  return launch_camera_rays(*cam, poses, rays, static_cast<hipStream_t>(stream));
+  return launch_camera_rays(*cam, poses, nullptr, rays, static_cast<hipStream_t>(stream));
+}
+
+int rdv_cameras_rays_jittered(const rdv_camera_desc* cam, const float* poses, const uint32_t* seeds, float* rays,
+                              void* stream) {
+  int rc = check_camera(cam);
+  if (rc != RDV_OK) return rc;
+  if (!poses || !rays || !seeds) return fail(RDV_ERR_INVALID, "rdv_cameras_rays_jittered: NULL pointer argument");
+  if (int64_t(cam->n_cams) * cam->height * cam->width >= (int64_t(1) << 31))
+    return fail(RDV_ERR_INVALID, "a jittered dispatch holds fewer than 2^31 cells (the generator's thread index is an int)");
+  return launch_camera_rays(*cam, poses, seeds, rays, static_cast<hipStream_t>(stream));
+}
+
+int rdv_random_uniform(const uint32_t* seeds, int64_t n_threads, int32_t per_thread, float* out, void* stream) {
+  if (n_threads < 0 || n_threads >= (int64_t(1) << 31)) return fail(RDV_ERR_INVALID, "n_threads must be in [0, 2^31)");
+  if (per_thread < 0 || per_thread > (1 << 20)) return fail(RDV_ERR_INVALID, "per_thread must be in [0, 2^20]");
+  if (n_threads == 0 || per_thread == 0) return RDV_OK;
+  if (!seeds || !out) return fail(RDV_ERR_INVALID, "rdv_random_uniform: NULL pointer argument");
+  return launch_random_uniform(seeds, n_threads, per_thread, out, static_cast<hipStream_t>(stream));
 }
 
 int rdv_render_emission_absorption(const rdv_camera_desc* cam, const float* poses, const rdv_mlp_desc* field,
@@ -472,6 +498,53 @@ int rdv_raymarch_transmittance(const rdv_mlp_desc* extinction, const void* packe
   if (!packed || !rays || !out) return fail(RDV_ERR_INVALID, "rdv_raymarch_transmittance: NULL pointer argument");
   return launch_raymarch_transmittance(*extinction, lay, packed, rays, n_rays, transform12, step_size, density_scale,
                                        out, static_cast<hipStream_t>(stream));
+}
+
+int rdv_ratiotracking_transmittance(const rdv_mlp_desc* extinction, const void* packed,
+                                    const rdv_ratiotracking_desc* rt, const float* majorant, const float* rays,
+                                    int64_t n_rays, float* out, void* stream) {
+  MlpLayout lay;
+  int rc = check_mlp(extinction, &lay);
+  if (rc != RDV_OK) return rc;
+  if (!rt) return fail(RDV_ERR_INVALID, "rdv_ratiotracking_transmittance: NULL descriptor");
+  if (n_rays < 0 || n_rays >= (int64_t(1) << 31))
+    return fail(RDV_ERR_INVALID, "n_rays must be in [0, 2^31) (the generator's thread index is an int)");
+  if (rt->maj_width < 1 || rt->maj_height < 1 || rt->maj_depth < 1 ||
+      int64_t(rt->maj_width) * rt->maj_height * rt->maj_depth >= (int64_t(1) << 40))
+    return fail(RDV_ERR_INVALID, "the majorant grid needs width, height, depth >= 1");
+  if (!(rt->density_scale > 0.0f)) return fail(RDV_ERR_INVALID, "density_scale must be > 0");
+  if (rt->rng_skip < 0 || rt->rng_skip > 1024) return fail(RDV_ERR_INVALID, "rng_skip must be in [0, 1024]");
+  if (rt->reserved != 0) return fail(RDV_ERR_INVALID, "reserved must be 0");
+  if (n_rays == 0) return RDV_OK;
+  if (!packed || !majorant || !rays || !out)
+    return fail(RDV_ERR_INVALID, "rdv_ratiotracking_transmittance: NULL pointer argument");
+  return launch_ratiotracking(*extinction, lay, packed, *rt, majorant, rays, n_rays, out,
+                              static_cast<hipStream_t>(stream));
+}
+
+int rdv_voxel_majorant(const float* grid, int32_t width, int32_t height, int32_t depth, const float* rays,
+                       int64_t n_rays, float* out, void* stream) {
+  if (width < 1 || height < 1 || depth < 1) return fail(RDV_ERR_INVALID, "the grid needs width, height, depth >= 1");
+  if (n_rays < 0) return fail(RDV_ERR_INVALID, "n_rays must be >= 0");
+  if (n_rays == 0) return RDV_OK;
+  if (!grid || !rays || !out) return fail(RDV_ERR_INVALID, "rdv_voxel_majorant: NULL pointer argument");
+  return launch_voxel_majorant(grid, width, height, depth, rays, n_rays, out, static_cast<hipStream_t>(stream));
+}
+
+int rdv_majorant_grid(const rdv_majorant_grid_desc* desc, const float* fine, float* out, void* stream) {
+  if (!desc) return fail(RDV_ERR_INVALID, "rdv_majorant_grid: NULL descriptor");
+  if (desc->rank < 1 || desc->rank > 4) return fail(RDV_ERR_INVALID, "rank must be 1..4");
+  if (desc->channels < 1) return fail(RDV_ERR_INVALID, "channels must be >= 1");
+  int64_t fine_cells = 1, cells = 1;
+  for (int d = 0; d < desc->rank; ++d) {
+    if (desc->fine_shape[d] < 1 || desc->shape[d] < 1)
+      return fail(RDV_ERR_INVALID, "every extent of both shapes must be >= 1");
+    fine_cells *= desc->fine_shape[d];
+    cells *= desc->shape[d];
+    if (fine_cells > (int64_t(1) << 40) || cells > (int64_t(1) << 40)) return fail(RDV_ERR_INVALID, "grid too large");
+  }
+  if (!fine || !out) return fail(RDV_ERR_INVALID, "rdv_majorant_grid: NULL pointer argument");
+  return launch_majorant_grid(*desc, fine, out, static_cast<hipStream_t>(stream));
 }
 
 const char* rdv_mlp_kernel_name(const rdv_mlp_desc* desc) {

@@ -66,4 +66,44 @@ __device__ __forceinline__ float apply_act(int act, int channel, float v) {
   }
 }
 
+// ------------------------------------------------------------------ random
+// The reference's per-thread generator (src/rdv/shaders/libraries/random_library.h,
+// after GPU Gems 3 ch. 37: three Tausworthe steps combined with an LCG), restated
+// bit for bit so that a dispatch with the same seeds draws the same numbers:
+// a thread's state is spawned from the dispatch's uvec4 seeds and its index
+// (random_library.h:50-55, 255-267), random() steps the state and maps the
+// xor of its words to [0, 1) through the mantissa bits (random_library.h:31-38).
+struct RngState {
+  uint32_t x, y, z, w;
+};
+
+__device__ __forceinline__ uint32_t taus_step(uint32_t z, int s1, int s2, int s3, uint32_t m) {
+  const uint32_t b = ((z << s1) ^ z) >> s2;
+  return ((z & m) << s3) ^ b;
+}
+
+__device__ __forceinline__ void rng_step(RngState& s) {
+  s.x = taus_step(s.x, 13, 19, 12, 4294967294u);
+  s.y = taus_step(s.y, 2, 25, 4, 4294967288u);
+  s.z = taus_step(s.z, 3, 11, 17, 4294967280u);
+  s.w = 1664525u * s.w + 1013904223u;
+}
+
+__device__ __forceinline__ RngState rng_spawn(const uint32_t (&seeds)[4], int index) {
+  const uint32_t i = uint32_t(index);
+  RngState s;
+  s.x = seeds[0] ^ (i ^ 17u);
+  s.y = seeds[1] ^ (i * 123111171u);
+  s.z = seeds[2] ^ (i + 11u);
+  s.w = seeds[3] ^ (i ^ (seeds[0] + 13u * seeds[1]));
+  rng_step(s);
+  return s;
+}
+
+__device__ __forceinline__ float rng_uniform(RngState& s) {
+  rng_step(s);
+  const uint32_t v = s.x ^ s.y ^ s.z ^ s.w;
+  return __builtin_bit_cast(float, (v & 0x007FFFFFu) | 0x3F800000u) - 1.0f;
+}
+
 }  // namespace rdv

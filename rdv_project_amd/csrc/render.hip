@@ -38,8 +38,10 @@ struct CameraParams {
 // cameras.h: pixel centre p = ((x, y) + 0.5) / (W, H) * 2 - 1, s = (p.x * aspect,
 // p.y, 1 / tan(fov / 2)), frame z = normalize(target - origin),
 // x = normalize(cross(up, z)), y = cross(z, x), w = normalize(s.x x + s.y y + s.z z).
+// (jx, jy) is the sub-pixel position: the centre (1/2, 1/2), or two random
+// numbers for a jittered camera (cameras.h:7).
 __device__ __forceinline__ void camera_ray(const CameraParams& c, int cam, int y, int x, float (&o)[3],
-                                           float (&w)[3]) {
+                                           float (&w)[3], float jx = 0.5f, float jy = 0.5f) {
   const float* P = c.poses + int64_t(cam) * 9;
   float t[3], n[3];
 #pragma unroll
@@ -48,8 +50,8 @@ __device__ __forceinline__ void camera_ray(const CameraParams& c, int cam, int y
     t[i] = P[3 + i];
     n[i] = P[6 + i];
   }
-  const float px = (float(x) + 0.5f) / float(c.W) * 2.0f - 1.0f;
-  const float py = (float(y) + 0.5f) / float(c.H) * 2.0f - 1.0f;
+  const float px = (float(x) + jx) / float(c.W) * 2.0f - 1.0f;
+  const float py = (float(y) + jy) / float(c.H) * 2.0f - 1.0f;
   const float sx = px * c.aspect, sy = py, sz = 1.0f / tanf(c.fov * 0.5f);
   float z[3] = {t[0] - o[0], t[1] - o[1], t[2] - o[2]};
   float inv = 1.0f / sqrtf(z[0] * z[0] + z[1] * z[1] + z[2] * z[2]);
@@ -82,15 +84,26 @@ __device__ __forceinline__ void ray_box(const float (&x)[3], const float (&w)[3]
   tmax = fminf(fminf(c1[0], c1[1]), c1[2]);
 }
 
-__global__ void camera_rays_kernel(CameraParams c, float* __restrict__ rays) {
+struct JitterSeeds {
+  int on;             // 0: pixel centres
+  uint32_t seeds[4];  // the dispatch's random seeds
+};
+
+__global__ void camera_rays_kernel(CameraParams c, JitterSeeds js, float* __restrict__ rays) {
   const int64_t total = int64_t(c.n) * c.H * c.W;
   for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < total; i += int64_t(gridDim.x) * blockDim.x) {
     const int x = int(i % c.W);
     const int64_t r = i / c.W;
     const int y = int(r % c.H);
     const int cam = int(r / c.H);
+    float jx = 0.5f, jy = 0.5f;
+    if (js.on) {  // thread i's generator (the grid evaluator's thread index is the cell index)
+      RngState st = rng_spawn(js.seeds, int(i));
+      jx = rng_uniform(st);
+      jy = rng_uniform(st);
+    }
     float o[3], w[3];
-    camera_ray(c, cam, y, x, o, w);
+    camera_ray(c, cam, y, x, o, w, jx, jy);
     float* dst = rays + i * 6;
 #pragma unroll
     for (int k = 0; k < 3; ++k) {
@@ -580,6 +593,210 @@ __global__ __launch_bounds__(64 * gen_waves<MT>(), 1) void raymarch_generic_kern
   });
 }
 
+// ------------------------------------------------ ratio-tracking transmittance
+// RatiotrackingTransmittance with a VoxelMajorantField (src/rdv/domain/volumes.py:144-211,
+// shaders/volumes/ratiotracking_transmittance.h, ratiotracking_transmittance_trait.h,
+// voxel_majorant_field.h).  Per ray, in the object space of the transform,
+// from the box entry with d = tMax - max(0, tMin) left to travel:
+//   for (safety = 0; d > 0 && safety < 1024; safety++) {
+//     (maj, dist) = majorant(x, w);  maj = max(maj, 1e-12);  dist = max(dist, 1e-6)
+//     dt = min(dist, -log(1 - random()) / (maj * density_scale));  d -= dt;  x += dt * w
+//     if (dt >= dist) continue;            // left the majorant voxel first
+//     if (d <= 0) break;                   // left the box first
+//     T *= 1 - extinction(x) / maj
+//     if (T < 0.05) { if (random() >= T) return 0;  T = 1; }   // Russian roulette
+//   }
+//   return T
+// Every update is rounded to fp32 on its own (no contraction), so sample
+// positions, voxel choices and random draws follow the reference's arithmetic.
+//
+// Mapping: a wave tracks 32 rays at once, one per MFMA column (lanes l and
+// l + 32 mirror ray l).  Each lane runs its ray's free flights on its own until
+// it needs an extinction value; then the wave evaluates the extinction chain
+// once for all 32 pending positions on the matrix cores.  A lane whose ray ends
+// claims the next ray of the block's range at once, so the 32 columns stay
+// filled until the range runs dry.
+struct RatioArgs {
+  const float* rays;      // [n, 6]: x, w (world)
+  int64_t nrays;
+  const float* majorant;  // [D, H, W] fp32: one upper bound of the extinction per voxel of [-1,1]^3
+  int mw, mh, md;         // W, H, D
+  float M[12];            // mat4x3, column-major
+  float density_scale;
+  uint32_t seeds[4];      // the dispatch's random seeds
+  int rng_skip;           // random() draws a thread has taken before this map (2 after a jittered camera)
+  float* out;             // [n]
+};
+
+// voxel_majorant_field.h: the majorant of the voxel holding x and the distance
+// along w to that voxel's exit.
+__device__ __forceinline__ float voxel_majorant(const float* __restrict__ grid, int mw, int mh, int md,
+                                                const float (&x)[3], const float (&w)[3], float& dist) {
+#pragma clang fp contract(off)
+  const int dim[3] = {mw, mh, md};
+  int cell[3];
+  float te[3];
+#pragma unroll
+  for (int i = 0; i < 3; ++i) {
+    const float fd = float(dim[i]);
+    // int() truncates toward zero; clamping first keeps the conversion in range
+    // (and sends NaN to 0) without changing any in-range result.
+    const float f = (x[i] * 0.5f + 0.5f) * fd;
+    cell[i] = int(fminf(fmaxf(f, 0.0f), fd - 1.0f));
+    const float vs = 2.0f / fd;
+    const float bmin = float(cell[i]) * vs - 1.0f;
+    const float bmax = bmin + vs;
+    const float t0 = (bmin - x[i]) / w[i];
+    const float t1 = (bmax - x[i]) / w[i];
+    te[i] = fmaxf(t0, t1);
+  }
+  dist = fminf(fminf(te[0], te[1]), te[2]);
+  return grid[(int64_t(cell[2]) * mh + cell[1]) * mw + cell[0]];
+}
+
+// One ray of a ratio-tracking wave: its free flights run per lane.
+struct RatioRay {
+  float x[3], w[3];
+  float d, T, maj;
+  int safety;
+  RngState st;
+};
+
+// Free flights until the next collision (true: x is the collision point and
+// `maj` its majorant) or the end of the ray (false: T is the result).
+__device__ __forceinline__ bool ratio_flight(const RatioArgs& a, RatioRay& r) {
+#pragma clang fp contract(off)
+  for (;;) {
+    if (!(r.d > 0.0f && r.safety < 1024)) return false;
+    float dist;
+    float mj = voxel_majorant(a.majorant, a.mw, a.mh, a.md, r.x, r.w, dist);
+    mj = fmaxf(mj, 1e-12f);
+    dist = fmaxf(dist, 1e-6f);
+    const float u = rng_uniform(r.st);
+    const float ff = -logf(1.0f - u) / (mj * a.density_scale);
+    const float dt = fminf(dist, ff);
+    r.d = r.d - dt;
+#pragma unroll
+    for (int i = 0; i < 3; ++i) r.x[i] = r.x[i] + dt * r.w[i];
+    ++r.safety;
+    if (dt >= dist) continue;
+    if (r.d <= 0.0f) return false;
+    r.maj = mj;
+    return true;
+  }
+}
+
+// The start of ray `ray`: object-space entry point (false: the ray misses, T = 1).
+__device__ __forceinline__ bool ratio_start(const RatioArgs& a, const float (&L)[9], int64_t ray, RatioRay& r) {
+  const float* rr = a.rays + ray * 6;
+  const float xw[3] = {rr[0] - a.M[9], rr[1] - a.M[10], rr[2] - a.M[11]};
+#pragma unroll
+  for (int i = 0; i < 3; ++i) {  // L * v with L column-major
+    r.x[i] = L[i] * xw[0] + L[3 + i] * xw[1] + L[6 + i] * xw[2];
+    r.w[i] = L[i] * rr[3] + L[3 + i] * rr[4] + L[6 + i] * rr[5];
+  }
+  r.T = 1.0f;
+  r.safety = 0;
+  r.st = rng_spawn(a.seeds, int(ray));
+  for (int k = 0; k < a.rng_skip; ++k) rng_step(r.st);
+  float tmin, tmax;
+  ray_box(r.x, r.w, tmin, tmax);
+  if (tmax <= 0.0f || tmin > tmax) return false;
+  tmin = fmaxf(0.0f, tmin);
+#pragma unroll
+  for (int i = 0; i < 3; ++i) {
+    float wt = r.w[i] * tmin;
+    asm volatile("" : "+v"(wt));  // x += w * tMin: product and sum rounded separately
+    r.x[i] = r.x[i] + wt;
+  }
+  r.d = tmax - tmin;
+  return true;
+}
+
+struct RatioGenArgs {
+  RatioArgs r;
+  const uint8_t* packed;
+  GenNet net;
+};
+
+template <int MT, bool LDSW>
+__global__ __launch_bounds__(64 * gen_waves<MT>(), 1) void ratiotracking_generic_kernel(RatioGenArgs ga) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  __shared__ int s_next;
+  const RatioArgs& a = ga.r;
+  const GenNet& g = ga.net;
+  const int lane = threadIdx.x & 63;
+  const int h = lane >> 5, col = lane & 31;
+  const bool has_bias = (reinterpret_cast<const MlpPackHeader*>(ga.packed)->flags & kMlpHasBias) != 0;
+  const half8* w0;
+  const float* b0;
+  gen_sources<LDSW>(ga.packed, g, smem, &w0, &b0);
+  if (threadIdx.x == 0) s_next = 0;
+  __syncthreads();
+  const int act = g.act[g.L - 1];
+  const int64_t per_block = (a.nrays + gridDim.x - 1) / gridDim.x;
+  const int64_t r_begin = int64_t(blockIdx.x) * per_block;
+  const int64_t r_end = r_begin + per_block < a.nrays ? r_begin + per_block : a.nrays;
+  const int nr = int(r_end > r_begin ? r_end - r_begin : 0);
+  float L[9];
+  inverse3(a.M, L);
+
+  RatioRay r;
+#pragma unroll
+  for (int i = 0; i < 3; ++i) r.x[i] = r.w[i] = 0.0f;
+  r.d = r.T = r.maj = 0.0f;
+  r.safety = 0;
+  r.st = RngState{0, 0, 0, 0};
+  int64_t ray = -1;        // the ray in this column (-1: none)
+  bool pending = false;    // x is a collision point waiting for its extinction
+  bool exhausted = false;  // the block's range has run dry
+  const uint64_t below = (uint64_t(1) << col) - 1;
+  auto finish = [&](float T) {
+    if (h == 0) a.out[ray] = T;
+    ray = -1;
+  };
+  for (;;) {
+    // Fill: advance every ray to its next collision; columns that run out of
+    // ray take the next ones of the range.
+    for (;;) {
+      if (ray >= 0 && !pending) {
+        if (ratio_flight(a, r)) pending = true;
+        else finish(r.T);
+      }
+      const bool idle = ray < 0 && !exhausted;
+      const uint64_t want = __builtin_amdgcn_ballot_w64(h == 0 && idle);
+      if (want == 0) break;
+      int base = 0;
+      if (lane == 0) base = atomicAdd(&s_next, __builtin_popcountll(want));
+      base = __builtin_amdgcn_readfirstlane(base);
+      if (idle) {  // both halves see the same `want` bits of the h == 0 lanes
+        const int k = base + __builtin_popcountll(want & below);
+        if (k < nr) {
+          ray = r_begin + k;
+          if (!ratio_start(a, L, ray, r)) finish(1.0f);
+        } else {
+          exhausted = true;
+        }
+      }
+    }
+    if (__builtin_amdgcn_ballot_w64(h == 0 && pending) == 0) break;  // every column is out of work
+    float p[3];
+#pragma unroll
+    for (int i = 0; i < 3; ++i) p[i] = pending ? r.x[i] : 0.0f;
+    float sigma = gen_field_row0<MT>(g, w0, b0, has_bias, lane, h, p, act);
+    sigma = __shfl(sigma, col);  // the value of lane col (row 0 of its column)
+    if (pending) {
+#pragma clang fp contract(off)
+      pending = false;
+      r.T = r.T * (1.0f - sigma / r.maj);
+      if (r.T < 0.05f) {
+        if (rng_uniform(r.st) >= r.T) finish(0.0f);
+        else r.T = 1.0f;
+      }
+    }
+  }
+}
+
 struct RenderGenArgs {
   RenderArgs r;
   GenNet net;
@@ -738,12 +955,31 @@ static bool is_extinction_field(const rdv_mlp_desc& d, const MlpLayout& lay) {
   return (d.act[3] == RDV_ACT_NONE || d.act[3] == RDV_ACT_SOFTPLUS || d.act[3] == RDV_ACT_RELU) && lay.kc[0] == 1;
 }
 
-int launch_camera_rays(const rdv_camera_desc& c, const float* poses, float* rays, hipStream_t stream) {
+__global__ void random_uniform_kernel(JitterSeeds js, int64_t n_threads, int per_thread, float* __restrict__ out) {
+  for (int64_t t = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; t < n_threads; t += int64_t(gridDim.x) * blockDim.x) {
+    RngState st = rng_spawn(js.seeds, int(t));
+    for (int k = 0; k < per_thread; ++k) out[t * per_thread + k] = rng_uniform(st);
+  }
+}
+
+int launch_random_uniform(const uint32_t* seeds, int64_t n_threads, int per_thread, float* out, hipStream_t stream) {
+  JitterSeeds js{1, {seeds[0], seeds[1], seeds[2], seeds[3]}};
+  int64_t blocks = (n_threads + 255) / 256;
+  if (blocks > 65536) blocks = 65536;
+  random_uniform_kernel<<<dim3(unsigned(blocks)), dim3(256), 0, stream>>>(js, n_threads, per_thread, out);
+  RDV_HIP_TRY(hipGetLastError());
+  return RDV_OK;
+}
+
+int launch_camera_rays(const rdv_camera_desc& c, const float* poses, const uint32_t* seeds, float* rays,
+                       hipStream_t stream) {
   CameraParams p{poses, c.n_cams, c.height, c.width, c.aspect_ratio, c.fov};
+  JitterSeeds js{0, {0, 0, 0, 0}};
+  if (seeds != nullptr) js = JitterSeeds{1, {seeds[0], seeds[1], seeds[2], seeds[3]}};
   const int64_t total = int64_t(c.n_cams) * c.height * c.width;
   int64_t blocks = (total + 255) / 256;
   if (blocks > 65536) blocks = 65536;
-  camera_rays_kernel<<<dim3(unsigned(blocks)), dim3(256), 0, stream>>>(p, rays);
+  camera_rays_kernel<<<dim3(unsigned(blocks)), dim3(256), 0, stream>>>(p, js, rays);
   RDV_HIP_TRY(hipGetLastError());
   return RDV_OK;
 }
@@ -839,6 +1075,146 @@ int launch_raymarch_transmittance(const rdv_mlp_desc& d, const MlpLayout& lay, c
       raymarch_transmittance_kernel<ExtinctionNet64x3, RDV_ACT_NONE><<<grid, block, 0, stream>>>(a);
       break;
   }
+  RDV_HIP_TRY(hipGetLastError());
+  return RDV_OK;
+}
+
+
+__global__ __launch_bounds__(256) void voxel_majorant_kernel(const float* __restrict__ grid, int mw, int mh, int md,
+                                                             const float* __restrict__ rays, int64_t n,
+                                                             float* __restrict__ out) {
+  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += int64_t(gridDim.x) * blockDim.x) {
+    const float* rr = rays + i * 6;
+    const float x[3] = {rr[0], rr[1], rr[2]}, w[3] = {rr[3], rr[4], rr[5]};
+    float dist;
+    const float m = voxel_majorant(grid, mw, mh, md, x, w, dist);
+    out[2 * i] = m;
+    out[2 * i + 1] = dist;
+  }
+}
+
+int launch_voxel_majorant(const float* grid, int mw, int mh, int md, const float* rays, int64_t n, float* out,
+                          hipStream_t stream) {
+  int64_t blocks = (n + 255) / 256;
+  if (blocks > 65536) blocks = 65536;
+  voxel_majorant_kernel<<<dim3(unsigned(blocks)), dim3(256), 0, stream>>>(grid, mw, mh, md, rays, n, out);
+  RDV_HIP_TRY(hipGetLastError());
+  return RDV_OK;
+}
+
+int launch_ratiotracking(const rdv_mlp_desc& d, const MlpLayout& lay, const void* packed,
+                         const rdv_ratiotracking_desc& rt, const float* majorant, const float* rays, int64_t nrays,
+                         float* out, hipStream_t stream) {
+  if (!is_f16_field(d, 1))
+    return fail(RDV_ERR_UNSUPPORTED, "the extinction must be a LinearFast chain from 3 inputs to 1 output");
+  DeviceInfo di;
+  int rc = device_info(&di);
+  if (rc != RDV_OK) return rc;
+  RatioGenArgs ga;
+  RatioArgs& a = ga.r;
+  a.rays = rays;
+  a.nrays = nrays;
+  a.majorant = majorant;
+  a.mw = rt.maj_width;
+  a.mh = rt.maj_height;
+  a.md = rt.maj_depth;
+  for (int i = 0; i < 12; ++i) a.M[i] = rt.transform[i];
+  a.density_scale = rt.density_scale;
+  for (int i = 0; i < 4; ++i) a.seeds[i] = rt.seeds[i];
+  a.rng_skip = rt.rng_skip;
+  a.out = out;
+  ga.packed = static_cast<const uint8_t*>(packed);
+  gen_net(d, lay, &ga.net);
+  // 32 rays per wave
+  RDV_GEN_FIELD_DISPATCH(ratiotracking_generic_kernel, ga, (nrays + 31) / 32, di.cu_count, ga.net, stream);
+}
+
+// ------------------------------------------------------------- majorant grid
+struct MajorantGridArgs {
+  const float* fine;
+  float* out;
+  int rank, channels, aligned, linear;
+  int fshape[4], cshape[4];
+  int64_t cells;
+};
+
+// majorant_grid.h: the fine index range [lo, lo + ext) along one dimension that
+// a sampler can read from inside coarse cell i of n.
+__device__ __forceinline__ void majorant_range(int i, int n, int fine, bool aligned, bool lin, int& lo, int& ext) {
+#pragma clang fp contract(off)
+  const float fsz = float(fine);
+  const float t_lo = float(i) / float(n);
+  const float t_hi = float(i + 1) / float(n);
+  const float pos_lo = aligned ? t_lo * (fsz - 1.0f) : t_lo * fsz - 0.5f;
+  const float pos_hi = aligned ? t_hi * (fsz - 1.0f) : t_hi * fsz - 0.5f;
+  int d_lo, d_hi;
+  if (lin) {
+    d_lo = int(floorf(pos_lo));
+    d_hi = int(floorf(pos_hi)) + 2;
+  } else {
+    d_lo = int(floorf(pos_lo + 0.5f));
+    d_hi = int(floorf(pos_hi + 0.5f)) + 1;
+  }
+  if (d_lo < 0) d_lo = 0;
+  if (d_hi > fine) d_hi = fine;
+  if (d_hi <= d_lo) d_hi = d_lo + 1;
+  if (d_hi > fine) d_hi = fine;
+  if (d_lo >= d_hi) d_lo = d_hi - 1;
+  lo = d_lo;
+  ext = d_hi - d_lo;
+}
+
+// One wave per coarse cell: the lanes stride over the cell's fine window and
+// the maxima meet in a butterfly (max is exact, so the order does not matter).
+__global__ __launch_bounds__(256) void majorant_grid_kernel(MajorantGridArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t waves = int64_t(gridDim.x) * (blockDim.x >> 6);
+  for (int64_t c = int64_t(blockIdx.x) * (blockDim.x >> 6) + (threadIdx.x >> 6); c < a.cells; c += waves) {
+    int lo[4] = {0, 0, 0, 0}, ext[4] = {1, 1, 1, 1};
+    int64_t rem = c, count = 1;
+    for (int d = a.rank - 1; d >= 0; --d) {
+      const int idx = int(rem % a.cshape[d]);
+      rem /= a.cshape[d];
+      majorant_range(idx, a.cshape[d], a.fshape[d], a.aligned != 0, a.linear != 0, lo[d], ext[d]);
+      count *= ext[d];
+    }
+    for (int k = 0; k < a.channels; ++k) {
+      float m = -INFINITY;
+      for (int64_t j = lane; j < count; j += 64) {
+        int64_t r = j, flat = 0, stride = 1;
+        for (int d = a.rank - 1; d >= 0; --d) {
+          const int64_t id = lo[d] + r % ext[d];
+          r /= ext[d];
+          flat += id * stride;
+          stride *= a.fshape[d];
+        }
+        m = fmaxf(m, a.fine[flat * a.channels + k]);
+      }
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+      if (lane == 0) a.out[c * a.channels + k] = m;
+    }
+  }
+}
+
+int launch_majorant_grid(const rdv_majorant_grid_desc& g, const float* fine, float* out, hipStream_t stream) {
+  MajorantGridArgs a;
+  a.fine = fine;
+  a.out = out;
+  a.rank = g.rank;
+  a.channels = g.channels;
+  a.aligned = g.aligned;
+  a.linear = g.linear;
+  a.cells = 1;
+  for (int d = 0; d < 4; ++d) {
+    a.fshape[d] = d < g.rank ? g.fine_shape[d] : 1;
+    a.cshape[d] = d < g.rank ? g.shape[d] : 1;
+    if (d < g.rank) a.cells *= g.shape[d];
+  }
+  if (a.cells == 0) return RDV_OK;
+  int64_t blocks = (a.cells + 3) / 4;
+  if (blocks > 65536) blocks = 65536;
+  majorant_grid_kernel<<<dim3(unsigned(blocks)), dim3(256), 0, stream>>>(a);
   RDV_HIP_TRY(hipGetLastError());
   return RDV_OK;
 }

@@ -324,3 +324,31 @@ class Upsample2x(_GridNode, Generic[Generics.G]):
         _tensor_ops.upsample2x(x.as_tensor("torch").reshape(H * W, self.OUT), H, W,
                                out.as_tensor("torch").reshape(-1, self.OUT))
         return out
+
+
+class MajorantGrid(_GridNode, Generic[Generics.G]):
+    """`grid` at a new (typically coarser) `shape`: each cell holds the
+    channel-wise maximum over every cell of `grid` that a sampler with the same
+    aligned / linear convention could read from anywhere inside it (a linear
+    sampler reaches one cell past the naive range); the bound that voxel
+    majorant fields need (reference: maths:534-569, shaders/grids/majorant_grid.h).
+    Grids of 1 to 4 dimensions."""
+
+    def __init__(self, grid, shape: list[int], aligned: bool = False, linear: bool = True) -> None:
+        assert len(shape) == len(grid.shape), "MajorantGrid keeps the grid's dimension count"
+        assert 1 <= len(shape) <= 4, "MajorantGrid supports 1 to 4 dimensions"
+        super().__init__(list(shape))
+        self.IN = grid.IN
+        self.OUT = grid.OUT
+        self.grid = grid
+        self.aligned = 1 if aligned else 0
+        self.linear = 1 if linear else 0
+
+    def _values(self, ctx: dict) -> RDVObject:
+        from . import _render
+        fine = grid_values(self.grid, ctx).as_tensor("torch")
+        fine = _f32(fine)
+        out = self._out((*self.shape, self.OUT))
+        _render.majorant_grid(fine, self.grid.shape, self.shape, int(self.OUT), bool(self.aligned),
+                              bool(self.linear), out.as_tensor("torch"))
+        return out

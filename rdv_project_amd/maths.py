@@ -142,6 +142,11 @@ class Grid(Component, Generic[_IN, _OUT]):
         self._shape = list(shape)
         self.shape = list(shape)
 
+    def cast(self, target):
+        """This grid as a `target` (e.g. Grid[3, 1]): its known IN / OUT must
+        agree (reference: Node.cast, _core.py:1778-1814; the rules of Map.cast)."""
+        return Map.cast(self, target)
+
     def __rshift__(self, m):
         if isinstance(m, Identity):
             return self

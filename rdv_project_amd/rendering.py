@@ -2,6 +2,8 @@
 
   Cameras                    reference domain/rendering.py:10-42 (Grid[3, 6])
   RaymarchingTransmittance   reference domain/volumes.py:124-141 (Map[6, 1])
+  RatiotrackingTransmittance reference domain/volumes.py:144-190 (Map[6, 1])
+  VoxelMajorantField         reference domain/volumes.py:191-211 (Map[6, 2])
   EmissionAbsorption         build-defined (Map[6, 3]): the MLP-in-the-loop
                              renderer of the benchmark configuration
 Grids compose with maps (`Cameras(...) >> RaymarchingTransmittance(m)`) into a
@@ -22,7 +24,10 @@ class Cameras(Grid[3, 6]):
     """Pinhole cameras: cell (c, y, x) -> (origin, unit direction) of the ray
     through pixel (x, y) of camera c (reference: rendering.py:10-42,
     shaders/rendering/cameras.h).  poses: [num_cameras, 9] = origin | target | up.
-    aspect_ratio defaults to width / height and fov (vertical, radians) to pi / 4."""
+    aspect_ratio defaults to width / height and fov (vertical, radians) to pi / 4.
+    jitter: each evaluation places every ray at a uniform random point of its
+    pixel (two random() draws of the cell's thread, RandomLibrary) instead of
+    the centre."""
 
     IN = 3
     OUT = 6
@@ -36,15 +41,13 @@ class Cameras(Grid[3, 6]):
         if not isinstance(poses, RDVObject):
             poses = wrap(torch.as_tensor(poses, dtype=torch.float32))
         assert poses.shape[1] == 9, "poses must be a [num_cameras, 9] tensor (ori | target | up)"
-        if jitter:
-            raise NotImplementedError("pixel jitter (RandomLibrary) is outside this build")
         super().__init__([poses.shape[0], height, width])
         self.poses = poses
         self.width = int(width)
         self.height = int(height)
         self.aspect_ratio = float(aspect_ratio)
         self.fov = float(fov)
-        self.pixel_jitter = 0
+        self.pixel_jitter = 1 if jitter else 0
 
 
 def _as_mat4x3(t) -> mat4x3:
@@ -85,6 +88,75 @@ class RaymarchingTransmittance(Map[6, 1]):
     def _launch_rows(self, x_ptr: int, y_ptr: int, rows: int) -> None:
         from . import _render
         _render.raymarch_ptrs(self, x_ptr, y_ptr, rows)
+
+
+class VoxelMajorantField(Map[6, 2]):
+    """(x, w) -> (majorant, distance): the value of the voxel of `grid` (a
+    Grid[3, 1] over the box [-1,1]^3, shape [D, H, W]) that holds x, and the
+    distance along w to that voxel's exit (reference: volumes.py:191-211,
+    shaders/volumes/voxel_majorant_field.h).  Every voxel value must bound the
+    extinction over its voxel, or ratio tracking is biased."""
+
+    IN = 6
+    OUT = 2
+
+    def __init__(self, grid) -> None:
+        grid = grid.cast(Grid[3, 1])
+        assert len(grid.shape) == 3, "VoxelMajorantField needs a 3-D grid"
+        self.grid = grid
+
+    def _grid_values(self) -> RDVObject:
+        from .grids import grid_values
+        return grid_values(self.grid, {})
+
+    def _evaluate_rows(self, x) -> RDVObject:
+        from . import _render
+        return _render.voxel_majorant_rows(self, x)
+
+    def _launch_rows(self, x_ptr: int, y_ptr: int, rows: int) -> None:
+        from . import _render
+        _render.voxel_majorant_ptrs(self, x_ptr, y_ptr, rows)
+
+
+def _as_majorant_field(majorant) -> VoxelMajorantField:
+    """A majorant field as given, or a bare Grid[3, 1] wrapped as one
+    (reference: volumes.py:235-254)."""
+    if isinstance(majorant, VoxelMajorantField):
+        return majorant
+    if isinstance(majorant, Grid) and majorant.OUT == 1:
+        return VoxelMajorantField(majorant)
+    raise NotImplementedError("majorant must be a VoxelMajorantField or a Grid[3, 1]")
+
+
+class RatiotrackingTransmittance(Map[6, 1]):
+    """T(x, w) along a ray through the box [-1,1]^3 of the object space given by
+    `transform`, estimated by ratio tracking against a voxel majorant field:
+    free flights of -log(1 - random()) / (majorant * density_scale) capped at
+    the voxel exit, T *= 1 - extinction(x) / majorant at each collision,
+    Russian roulette below T = 0.05, at most 1024 steps; 1 when the ray misses
+    (reference: volumes.py:144-190, shaders/volumes/ratiotracking_transmittance.h,
+    ratiotracking_transmittance_trait.h).  An unbiased, noisy estimate: each
+    evaluation draws fresh random seeds (RandomLibrary).
+    extinction: a Map[3, 1] (any LinearFast chain from 3 inputs to 1 output);
+    majorant: a VoxelMajorantField or a Grid[3, 1] (wrapped as one)."""
+
+    IN = 6
+    OUT = 1
+
+    def __init__(self, extinction: Map, majorant, transform=None, density_scale: float = 1.0) -> None:
+        self.extinction = extinction.cast(Map[3, 1])  # TypeError for any other width (volumes.py:16)
+        self.majorant = _as_majorant_field(majorant).cast(Map[6, 2])
+        self.transform = mat4x3(1.0, 0.0, 0.0, 0.0, 1.0, 0.0, 0.0, 0.0, 1.0, 0.0, 0.0, 0.0) \
+            if transform is None else _as_mat4x3(transform)
+        self.density_scale = float(density_scale)
+
+    def _evaluate_rows(self, x) -> RDVObject:
+        from . import _render
+        return _render.ratiotracking_rows(self, x)
+
+    def _launch_rows(self, x_ptr: int, y_ptr: int, rows: int) -> None:
+        from . import _render
+        _render.ratiotracking_ptrs(self, x_ptr, y_ptr, rows)
 
 
 class EmissionAbsorption(Map[6, 3]):
