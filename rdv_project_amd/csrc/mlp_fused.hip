@@ -37,14 +37,15 @@ struct FusedArgs {
 //    pulling the same 26 KiB straight from L2 serialised on a few hot lines for
 //    ~3 us.)
 //  - Input: at the top of an iteration a wave claims its next pair tile and
-//    issues that tile's row loads into registers; at the bottom, a whole
-//    iteration later, it parks them in a wave-private LDS slot, which the next
-//    iteration reads.  The wait for the load therefore lands where the data has
-//    long arrived, and no barrier is needed after start-up.  The first tile's
-//    loads are issued before the weight staging, so their latency overlaps it.
-//  - Output: each pair tile's stores are issued after the next input has been
-//    parked, so the wait that precedes the parking never covers a store younger
-//    than an iteration.
+//    DMAs its 64 rows from HBM straight into a wave-private LDS buffer
+//    (global_load_lds_dword, one per input column: lane l's row lands at
+//    [d][l]), double-buffered, so no registers hold input in flight; the next
+//    iteration waits for it (s_waitcnt vmcnt(0)) a whole iteration later, when
+//    it has long arrived.  No barrier is needed after start-up.  The first
+//    tile's DMA is issued before the weight staging, so its latency overlaps it.
+//  - Output: each pair tile's stores are issued one iteration late, before the
+//    next DMA, so that wait (loads and stores retire in order on gfx9) never
+//    covers a store younger than an iteration.
 constexpr int kWaves2 = 8;
 constexpr int kThreads2 = 64 * kWaves2;
 
@@ -55,7 +56,7 @@ __global__ __launch_bounds__(kThreads2, 1) void mlp_fused_f16_kernel(FusedArgs a
   constexpr int MTO = N::mt(LL);
   __shared__ float sb[N::kBias];
   __shared__ half8 sw[N::kFrags * 64];
-  __shared__ float sx[kWaves2][64 * D];  // each wave's parked input pair tile
+  __shared__ float sx[kWaves2][2][D * 64];  // each wave's input pair tiles (double buffer), [d][row]
   __shared__ int s_next;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -68,28 +69,29 @@ __global__ __launch_bounds__(kThreads2, 1) void mlp_fused_f16_kernel(FusedArgs a
   const int nt = int(t_end > t_begin ? t_end - t_begin : 0);
   const bool has_bias = (reinterpret_cast<const MlpPackHeader*>(a.packed)->flags & kMlpHasBias) != 0;
 
-  // Rows of pair tile lt, half s (0: rows 0-31, 1: rows 32-63), clamped to valid rows.
+  // DMA of pair tile lt (64 rows, lane l -> row l, clamped to the last row) into buffer `buf`
   const int64_t last = a.nrows - 1;
-  auto load_tile = [&](int lt, float (&r)[2][D]) {
+  auto dma_tile = [&](int lt, int buf) {
+    int64_t row = (t_begin + (lt < nt ? lt : 0)) * 64 + lane;
+    row = row < last ? row : last;
+    const float* src = a.x + row * D;
 #pragma unroll
-    for (int s2 = 0; s2 < 2; ++s2) {
-      int64_t row = (t_begin + (lt < nt ? lt : 0)) * 64 + 32 * s2 + col;
-      row = row < last ? row : last;
-#pragma unroll
-      for (int d = 0; d < D; ++d) r[s2][d] = __builtin_nontemporal_load(a.x + row * D + d);
-    }
-  };
-  auto park = [&](const float (&r)[2][D]) {
-    if (h == 0) {
-#pragma unroll
-      for (int s2 = 0; s2 < 2; ++s2)
-#pragma unroll
-        for (int d = 0; d < D; ++d) sx[wave][(32 * s2 + col) * D + d] = r[s2][d];
+    for (int d = 0; d < D; ++d) {
+      const uint32_t dst = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(&sx[wave][buf][d * 64]));
+      uint32_t saved;
+      asm volatile(
+          "s_mov_b32 %0, m0\n\t"
+          "s_mov_b32 m0, %2\n\t"
+          "s_nop 0\n\t"
+          "global_load_lds_dword %1, off\n\t"
+          "s_mov_b32 m0, %0"
+          : "=&s"(saved)
+          : "v"(src + d), "s"(__builtin_amdgcn_readfirstlane(dst))
+          : "memory");
     }
   };
   int cur = wave;
-  float r0[2][D];
-  load_tile(cur, r0);
+  dma_tile(cur, 0);
 
   stage_net_weights<N, kThreads2>(a.packed, a.lay, sb, sw);
   if (threadIdx.x == 0) s_next = kWaves2;
@@ -100,21 +102,26 @@ __global__ __launch_bounds__(kThreads2, 1) void mlp_fused_f16_kernel(FusedArgs a
     if (lane == 0) t = atomicAdd(&s_next, 1);
     return __builtin_amdgcn_readfirstlane(t);
   };
-  park(r0);
 
   f32x4 po[2][MTO][4];
   int64_t prow = -1;
+  int buf = 0;
   while (cur < nt) {
     const int nxt = claim();
-    float r[2][D];
-    load_tile(nxt, r);
-
+    // this tile's DMA (and everything older: the stores of two iterations ago) has landed
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     float pA[D], pB[D];
 #pragma unroll
     for (int d = 0; d < D; ++d) {
-      pA[d] = sx[wave][col * D + d];
-      pB[d] = sx[wave][(32 + col) * D + d];
+      pA[d] = sx[wave][buf][d * 64 + col];
+      pB[d] = sx[wave][buf][d * 64 + 32 + col];
     }
+    // the previous pair tile's stores, then the next tile's DMA
+    if (prow >= 0) {
+      if (prow < a.nrows) store_head<N>(a.y + prow * N::kOut, po[0], h);
+      if (prow + 32 < a.nrows) store_head<N>(a.y + (prow + 32) * N::kOut, po[1], h);
+    }
+    dma_tile(nxt, buf ^ 1);
     f32x16 accA[N::kMaxMT], accB[N::kMaxMT];
     half8 bA[N::kMaxKC], bB[N::kMaxKC];
     const LdsWeights ws{sw + opaque_zero(), lane};
@@ -124,31 +131,20 @@ __global__ __launch_bounds__(kThreads2, 1) void mlp_fused_f16_kernel(FusedArgs a
     } else {
       run_pair<N, 0, RELU, false>(ws, pB, h, bA, bB, accA, accB, sb);
     }
-    f32x4 o[2][MTO][4];
 #pragma unroll
     for (int t = 0; t < MTO; ++t)
 #pragma unroll
       for (int q = 0; q < 4; ++q)
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) {
-          o[0][t][q][jj] = head_act<HEAD_ACT>(32 * t + 8 * q + 4 * h + jj, accA[t][4 * q + jj]);
-          o[1][t][q][jj] = head_act<HEAD_ACT>(32 * t + 8 * q + 4 * h + jj, accB[t][4 * q + jj]);
+          po[0][t][q][jj] = head_act<HEAD_ACT>(32 * t + 8 * q + 4 * h + jj, accA[t][4 * q + jj]);
+          po[1][t][q][jj] = head_act<HEAD_ACT>(32 * t + 8 * q + 4 * h + jj, accB[t][4 * q + jj]);
         }
-
-    park(r);  // the next pair tile's input, loaded a whole iteration ago
-    if (prow >= 0) {
-      if (prow < a.nrows) store_head<N>(a.y + prow * N::kOut, po[0], h);
-      if (prow + 32 < a.nrows) store_head<N>(a.y + (prow + 32) * N::kOut, po[1], h);
-    }
-#pragma unroll
-    for (int s2 = 0; s2 < 2; ++s2)
-#pragma unroll
-      for (int t = 0; t < MTO; ++t)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) po[s2][t][q] = o[s2][t][q];
     prow = (t_begin + cur) * 64 + col;
     cur = nxt;
+    buf ^= 1;
   }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no DMA outstanding at exit
   if (prow >= 0) {
     if (prow < a.nrows) store_head<N>(a.y + prow * N::kOut, po[0], h);
     if (prow + 32 < a.nrows) store_head<N>(a.y + (prow + 32) * N::kOut, po[1], h);
