@@ -212,6 +212,13 @@ __device__ __forceinline__ void ea_ray(const RenderArgs& a, int64_t ray, float (
   camera_ray(a.cam, cam, y, x, o, w);
 }
 
+// A wave-uniform float moved to a scalar register (the ray's geometry and
+// transmittance are the same in every lane of its wave; in SGPRs they do not
+// compete with the MLP chain's VGPRs).
+__device__ __forceinline__ float wave_uniform(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, v)));
+}
+
 template <class N>
 __global__ __launch_bounds__(kEaThreads, 1) void render_ea_kernel(RenderArgs a) {
   static_assert(N::kIn == 3 && N::kOut == 4, "the renderer evaluates a 3 -> 4 (density, RGB) field");
@@ -238,12 +245,17 @@ __global__ __launch_bounds__(kEaThreads, 1) void render_ea_kernel(RenderArgs a) 
     const int64_t ray = r_begin + r;
     float o[3], w[3];
     ea_ray(a, ray, o, w);
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+      o[i] = wave_uniform(o[i]);
+      w[i] = wave_uniform(w[i]);
+    }
     float t0, t1;
     ray_box(o, w, t0, t1);
     float cr = 0.0f, cg = 0.0f, cb = 0.0f;
     if (!(t1 <= 0.0f || t0 > t1)) {
-      t0 = fmaxf(t0, 0.0f);
-      const float dt = (t1 - t0) / float(a.samples);
+      t0 = wave_uniform(fmaxf(t0, 0.0f));
+      const float dt = wave_uniform((t1 - t0) / float(a.samples));
       float Tin = 1.0f;
       auto composite = [&](const f32x16& f) {
         const float sigma = fast_softplus(f[0]);
@@ -254,7 +266,7 @@ __global__ __launch_bounds__(kEaThreads, 1) void render_ea_kernel(RenderArgs a) 
         cr += wgt * fast_sigmoid(f[1]);
         cg += wgt * fast_sigmoid(f[2]);
         cb += wgt * fast_sigmoid(f[3]);
-        Tin *= __expf(-total);
+        Tin = wave_uniform(Tin * __expf(-total));
       };
       for (int c = 0; c + 1 < chunks; c += 2) {
         const float ta = t0 + (float(32 * c + col) + 0.5f) * dt;
@@ -833,12 +845,17 @@ __global__ __launch_bounds__(64 * gen_waves<MT>(), 1) void render_ea_generic_ker
     const int64_t ray = r_begin + r;
     float o[3], w[3];
     ea_ray(a, ray, o, w);
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+      o[i] = wave_uniform(o[i]);
+      w[i] = wave_uniform(w[i]);
+    }
     float t0, t1;
     ray_box(o, w, t0, t1);
     float cr = 0.0f, cg = 0.0f, cb = 0.0f;
     if (!(t1 <= 0.0f || t0 > t1)) {
-      t0 = fmaxf(t0, 0.0f);
-      const float dt = (t1 - t0) / float(a.samples);
+      t0 = wave_uniform(fmaxf(t0, 0.0f));
+      const float dt = wave_uniform((t1 - t0) / float(a.samples));
       float Tin = 1.0f;
       for (int c = 0; c < chunks; ++c) {
         const float ts = t0 + (float(32 * c + col) + 0.5f) * dt;
