@@ -475,6 +475,74 @@ def bench_generic_mlp(steps, warmup):
     }
 
 
+def bench_volumes(steps, warmup):
+    """Ratio-tracking transmittance (RatiotrackingTransmittance with a VoxelMajorantField) over the C4 camera's
+    512 x 512 rays: extinction = a 3 -> 64 -> 64 -> 64 -> 1 softplus LinearFast chain (Kaiming-uniform fp16,
+    seed 11), density_scale 4, majorant = MajorantGrid(64^3 lattice of the extinction x 1.3, [8, 8, 8])."""
+    import torch
+    import rdv_project_amd as rdv
+    from rdv_project_amd import _chain, _lib, _render
+    from rdv_project_amd import workloads as WL
+    from rdv_project_amd.types import RandomLibrary
+    lib = _lib.load()
+    layers = WL.kaiming_uniform_f16([(64, 3), (64, 64), (64, 64), (1, 64)], seed=11)
+    ext = None
+    for i, (w, b) in enumerate(layers):
+        lin = rdv.linear(w.cuda(), b.cuda(), f16=True)
+        ext = lin if ext is None else ext >> lin
+        ext = ext >> (rdv.relu if i + 1 < len(layers) else rdv.softplus)
+    c = (torch.arange(64, dtype=torch.float32) + 0.5) / 64 * 2 - 1
+    zz, yy, xx = torch.meshgrid(c, c, c, indexing="ij")
+    lattice = torch.stack([xx, yy, zz], -1).reshape(-1, 3).cuda()
+    dens = ext(rdv.wrap(lattice)).as_tensor("torch").reshape(64, 64, 64, 1) * 1.3 + 1e-3
+    mg = rdv.MajorantGrid(rdv.TensorGrid(dens.clone()), [8, 8, 8])
+    rt = rdv.RatiotrackingTransmittance(ext, mg, density_scale=4.0)
+    majv = mg().as_tensor("torch").contiguous().clone()
+    p = _chain.plan_chain(ext, 3)
+    packed = _chain.packed_params(ext, p)
+    rays = rdv.Cameras(WL.C4_WIDTH, WL.C4_HEIGHT, WL.c4_pose().cuda())().as_tensor("torch").reshape(-1, 6).clone()
+    n = rays.shape[0]
+    out = torch.empty(n, device="cuda")
+    RandomLibrary.seed(0)
+    d = _render._ratio_desc(rt, RandomLibrary.next_seeds(), 0, 8, 8, 8)
+    stream = C.c_void_p(torch.cuda.current_stream().cuda_stream)
+    args = (C.byref(p.desc), C.c_void_p(packed.data_ptr()), C.byref(d), C.c_void_p(majv.data_ptr()),
+            C.c_void_p(rays.data_ptr()), C.c_int64(n), C.c_void_p(out.data_ptr()), stream)
+
+    def launch(i):
+        d.seeds[0] = 128 + i  # a fresh generator per call, as each dispatch draws new seeds
+        rc = lib.rdv_ratiotracking_transmittance(*args)
+        if rc != 0:
+            _lib.check(rc, "ratio tracking")
+
+    wall, ev = _time_launches(launch, steps, warmup)
+    T = out.double()
+    # majorant grid alone (64^3 -> 8^3, linear, unaligned): 1 MiB read per call
+    fine = dens.contiguous()
+    mout = torch.empty(8, 8, 8, 1, device="cuda")
+    gd = _lib.MajorantGridDesc()
+    gd.rank, gd.channels, gd.aligned, gd.linear = 3, 1, 0, 1
+    for i in range(3):
+        gd.fine_shape[i], gd.shape[i] = 64, 8
+
+    def launch_mg(i):
+        rc = lib.rdv_majorant_grid(C.byref(gd), C.c_void_p(fine.data_ptr()), C.c_void_p(mout.data_ptr()), stream)
+        if rc != 0:
+            _lib.check(rc, "majorant grid")
+
+    _, mev = _time_launches(launch_mg, max(steps, 20), warmup, prewarm_s=0.05)
+    return {
+        "workload": "ratio tracking over 512x512 C4 camera rays, extinction 3->64->64->64->1 softplus (fp16 MFMA, "
+                    "seed 11), density_scale 4, 8^3 voxel majorant from a 64^3 MajorantGrid",
+        "kernel": "ratiotracking_generic_kernel",
+        "ms_per_call": round(ev, 4),
+        "Mrays_per_s": round(n / (ev * 1e-3) / 1e6, 1),
+        "mean_T": round(float(T.mean()), 4),
+        "majorant_grid_us": round(mev * 1e3, 2),
+        "bound": "per-ray free-flight loop; one chain evaluation per collision for the 32 rays of a wave",
+    }
+
+
 def main() -> int:
     global PREWARM_S
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
@@ -559,6 +627,9 @@ def main() -> int:
         _log("generic MLP")
         extras["generic_mlp"] = bench_generic_mlp(max(args.steps // 5, 10), args.warmup)
         _log(f"generic MLP {extras['generic_mlp']}")
+        _log("ratio tracking")
+        extras["ratiotracking"] = bench_volumes(max(args.steps // 20, 10), 3)
+        _log(f"ratio tracking {extras['ratiotracking']}")
 
     cpu = None
     if not args.no_cpu_baseline:

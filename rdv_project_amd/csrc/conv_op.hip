@@ -58,6 +58,7 @@ struct ConvArgs {
   int kp;             // K per LDS pass (multiple of the chunk width)
   int passes;
   int ob, n_ob;
+  int w_rows;         // RSCK with 16-byte rows: cv_stage_rows
 };
 
 template <bool F16>
@@ -112,6 +113,53 @@ __device__ void cv_stage(const ConvArgs& a, int o0, int k0, int nkc, f32x4* sw, 
   }
   for (int i = threadIdx.x; i < a.ob; i += kCvThreads)
     sb[i] = (a.bias != nullptr && o0 + i < a.cout) ? a.bias[o0 + i] : 0.0f;
+}
+
+// cv_stage for an RSCK filter whose rows are 16-byte vectors (cout % 4 == 0,
+// w 16-byte aligned): w[k][o] is contiguous in o, so a thread reads kLane rows
+// k .. k + kLane - 1 of four consecutive outputs (one 16-byte load per row,
+// coalesced across threads) and writes the four slots of those outputs.  Same
+// slot contents as cv_stage.
+template <bool F16>
+__device__ void cv_stage_rows(const ConvArgs& a, int o0, int k0, int nkc, f32x4* sw, float* sb) {
+  using S = CvStep<F16>;
+  const int nt = a.ob / 16;
+  const int groups = nt * nkc * 16;  // (t, c, lane / 16, four outputs)
+  for (int gi = threadIdx.x; gi < groups; gi += kCvThreads) {
+    const int j = gi & 3, kq = (gi >> 2) & 3;
+    const int tc = gi >> 4;
+    const int t = tc / nkc, c = tc - t * nkc;
+    const int o = o0 + 16 * t + 4 * j;
+    const int k = k0 + c * S::kK + kq * S::kLane;
+    f32x4 r[S::kLane];
+#pragma unroll
+    for (int i = 0; i < S::kLane; ++i) {
+      const bool ok = o < a.cout && k + i < a.K;
+      r[i] = ok ? *reinterpret_cast<const f32x4*>(a.w + int64_t(k + i) * a.cout + o) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      f32x4 v;
+      if constexpr (F16) {
+        half8 h;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) h[i] = half_t(r[i][e]);
+        v = __builtin_bit_cast(f32x4, h);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = r[i][e];
+      }
+      sw[(t * nkc + c) * 64 + kq * 16 + 4 * j + e] = v;
+    }
+  }
+  for (int i = threadIdx.x; i < a.ob; i += kCvThreads)
+    sb[i] = (a.bias != nullptr && o0 + i < a.cout) ? a.bias[o0 + i] : 0.0f;
+}
+
+template <bool F16>
+__device__ __forceinline__ void cv_stage_any(const ConvArgs& a, int o0, int k0, int nkc, f32x4* sw, float* sb) {
+  if (a.w_rows) cv_stage_rows<F16>(a, o0, k0, nkc, sw, sb);
+  else cv_stage<F16>(a, o0, k0, nkc, sw, sb);
 }
 
 // One lane's view of its kCvRT pixels: image coordinates and validity.
@@ -228,7 +276,7 @@ __global__ __launch_bounds__(kCvThreads) void conv_op_kernel(ConvArgs a) {
   const int o0 = ob_idx * a.ob;
 
   if (a.passes == 1) {
-    cv_stage<F16>(a, o0, 0, nkc, sw, sb);
+    cv_stage_any<F16>(a, o0, 0, nkc, sw, sb);
     __syncthreads();
   }
   for (int64_t task = rwg; task < a.tasks; task += rstride) {
@@ -246,7 +294,7 @@ __global__ __launch_bounds__(kCvThreads) void conv_op_kernel(ConvArgs a) {
       const int k0 = pass * a.kp;
       if (a.passes > 1) {
         __syncthreads();
-        cv_stage<F16>(a, o0, k0, nkc, sw, sb);
+        cv_stage_any<F16>(a, o0, k0, nkc, sw, sb);
         __syncthreads();
       }
       if (pass == 0) {
@@ -369,6 +417,7 @@ int launch_conv2d(const rdv_conv2d_desc& d, const float* x, const float* w, cons
   a.passes = passes;
   a.ob = ob;
   a.n_ob = (d.cout + ob - 1) / ob;
+  a.w_rows = d.w_layout == RDV_WLAYOUT_RSCK && d.cout % 4 == 0 && reinterpret_cast<uintptr_t>(w) % 16 == 0 ? 1 : 0;
   const int64_t rows_per_task = int64_t(kCvWaves) * 16 * kCvRT;
   a.tasks = (rows + rows_per_task - 1) / rows_per_task;
   const int nt = ob / 16;
