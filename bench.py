@@ -81,6 +81,72 @@ def _mlp_setup(x_cpu, layers, acts, enc=None, rotate=ROTATE):
 PREWARM_S = 0.5  # seconds of untimed launches before the warm-up steps
 
 
+def bench_volume_profile(steps, warmup):
+    """VolumeProfile over the C4 camera's 512 x 512 rays: the ratio-tracking leg's extinction (3 -> 64 -> 64 -> 64
+    -> 1 softplus, seed 11) and 8^3 majorant, density_scale 4, thresholds (0.9, 0.5, 0.1), step_size 0.004, g 0.3,
+    4 environment samples, constant RGB environment and albedo (the two maps cost nothing); both stages timed."""
+    import torch
+    import rdv_project_amd as rdv
+    from rdv_project_amd import _chain, _lib, _render
+    from rdv_project_amd import workloads as WL
+    from rdv_project_amd.types import RandomLibrary
+    lib = _lib.load()
+    layers = WL.kaiming_uniform_f16([(64, 3), (64, 64), (64, 64), (1, 64)], seed=11)
+    ext = None
+    for i, (w, b) in enumerate(layers):
+        lin = rdv.linear(w.cuda(), b.cuda(), f16=True)
+        ext = lin if ext is None else ext >> lin
+        ext = ext >> (rdv.relu if i + 1 < len(layers) else rdv.softplus)
+    c = (torch.arange(64, dtype=torch.float32) + 0.5) / 64 * 2 - 1
+    zz, yy, xx = torch.meshgrid(c, c, c, indexing="ij")
+    lattice = torch.stack([xx, yy, zz], -1).reshape(-1, 3).cuda()
+    dens = ext(rdv.wrap(lattice)).as_tensor("torch").reshape(64, 64, 64, 1) * 1.3 + 1e-3
+    mg = rdv.MajorantGrid(rdv.TensorGrid(dens.clone()), [8, 8, 8])
+    majv = mg().as_tensor("torch").contiguous().clone()
+    vp = rdv.VolumeProfile(ext, mg, rdv.Constant([1.0, 0.9, 0.8]), rdv.Constant([0.6, 0.7, 0.8]), [0.9, 0.5, 0.1],
+                           density_scale=4.0, g=0.3, step_size=0.004, environment_samples=4)
+    p = _chain.plan_chain(ext, 3)
+    packed = _chain.packed_params(ext, p)
+    rays = rdv.Cameras(WL.C4_WIDTH, WL.C4_HEIGHT, WL.c4_pose().cuda())().as_tensor("torch").reshape(-1, 6).clone()
+    n = rays.shape[0]
+    out = torch.empty(n, vp.OUT, device="cuda")
+    RandomLibrary.seed(0)
+    d = _render._vp_desc(vp, RandomLibrary.next_seeds(), 0, 8, 8, 8)
+    ws = _render._vp_workspace(vp, n)
+    env_v, alb_v = vp.environment._value_ptr(), vp.scattering_albedo._value_ptr()
+    stream = C.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    def launch(i):
+        d.seeds[0] = 256 + i
+        rc = lib.rdv_volume_profile(C.byref(p.desc), C.c_void_p(packed.data_ptr()), C.byref(d),
+                                    C.c_void_p(majv.data_ptr()), C.c_void_p(rays.data_ptr()), C.c_int64(n),
+                                    C.c_void_p(out.data_ptr()), C.c_void_p(ws["spos"].data_ptr()),
+                                    C.c_void_p(ws["dirs"].data_ptr()), C.c_void_p(ws["wts"].data_ptr()),
+                                    C.c_void_p(ws["valid"].data_ptr()), stream)
+        if rc == 0:
+            rc = lib.rdv_volume_profile_finish(C.byref(d), C.c_void_p(alb_v), C.c_int64(0), C.c_void_p(env_v),
+                                               C.c_int64(0), C.c_void_p(ws["wts"].data_ptr()),
+                                               C.c_void_p(ws["valid"].data_ptr()), C.c_int64(n),
+                                               C.c_void_p(out.data_ptr()), stream)
+        if rc != 0:
+            _lib.check(rc, "volume profile")
+
+    wall, ev = _time_launches(launch, steps, warmup, prewarm_s=0.0)
+    valid = float(ws["valid"][:n].float().mean())
+    return {
+        "workload": "VolumeProfile over 512x512 C4 camera rays: extinction 3->64->64->64->1 softplus (fp16 MFMA, "
+                    "seed 11), 8^3 voxel majorant, density_scale 4, thresholds (0.9, 0.5, 0.1), step 0.004, g 0.3, "
+                    "4 environment samples, constant RGB environment and albedo",
+        "kernels": "volume_profile_kernel + volume_profile_finish_kernel",
+        "ms_per_call": round(ev, 3),
+        "Mrays_per_s": round(n / (ev * 1e-3) / 1e6, 2),
+        "valid_fraction": round(valid, 4),
+        "mean_S": round(float(out[:, -1].double().mean()), 4),
+        "bound": "per-ray state machine (two fixed-step marches, the light ray's march, four ratio-tracked "
+                 "environment rays); one chain evaluation per step for the 32 rays of a wave",
+    }
+
+
 def _time_launches(launch, steps: int, warmup: int, prewarm_s: float | None = None):
     """Returns (wall ms per step, event ms per step) for `steps` back-to-back
     launches.  Before the `warmup` steps the same launches run, untimed, for
@@ -630,6 +696,8 @@ def main() -> int:
         _log("ratio tracking")
         extras["ratiotracking"] = bench_volumes(max(args.steps // 20, 10), 3)
         _log(f"ratio tracking {extras['ratiotracking']}")
+        extras["volume_profile"] = bench_volume_profile(3, 1)
+        _log(f"volume profile {extras['volume_profile']}")
 
     cpu = None
     if not args.no_cpu_baseline:

@@ -415,6 +415,68 @@ typedef struct rdv_majorant_grid_desc {
  * shaders/grids/majorant_grid.h). */
 int rdv_majorant_grid(const rdv_majorant_grid_desc* desc, const float* fine, float* out, void* stream);
 
+/* ------------------------------------------------------------- volume profile */
+#define RDV_VP_MAX_DEPTH 16    /* transmittance thresholds (DEPTH_SAMPLES)   */
+#define RDV_VP_MAX_SPECTRAL 8  /* SPECTRAL_DIM                               */
+
+typedef struct rdv_volume_profile_desc {
+  float transform[12];         /* mat4x3, column-major, as rdv_raymarch_transmittance     */
+  float density_scale;
+  float g;                     /* Henyey-Greenstein anisotropy                           */
+  float step_size;             /* fixed step of the marches                              */
+  float light_direction[3];    /* world space                                            */
+  float light_intensity[RDV_VP_MAX_SPECTRAL];
+  float transmittance_threshold[RDV_VP_MAX_DEPTH];
+  int32_t depth_samples;       /* DEPTH_SAMPLES, 1..RDV_VP_MAX_DEPTH                     */
+  int32_t spectral_dim;        /* SPECTRAL_DIM, 1..RDV_VP_MAX_SPECTRAL                   */
+  int32_t sample_index;        /* the depth sample whose position is shaded, 0..depth_samples-1 */
+  int32_t environment_samples; /* >= 0                                                   */
+  int32_t maj_width, maj_height, maj_depth;  /* the voxel majorant grid [depth, height, width] */
+  uint32_t seeds[4];           /* the dispatch's random seeds                            */
+  int32_t rng_skip;            /* random() draws each thread took before this map        */
+  int32_t reserved;            /* 0                                                      */
+} rdv_volume_profile_desc;
+
+/* VolumeProfile, first stage: per ray rays[n, 6] = (x, w), everything but the
+ * two spectral maps.  In the object space of the transform: the ray's box
+ * [-1,1]^3 interval trimmed at both ends while the voxel majorant is 0; tau by
+ * a fixed-step march (left endpoints, stop past 20); a second march that
+ * records the depth t where tau crosses each threshold's expected crossing
+ * value; S = 1 - exp(-tau); the depths re-encoded; then at the sample depth's
+ * position the light ray's raymarched transmittance and, per environment
+ * sample, a Henyey-Greenstein direction and its ratio-tracked transmittance
+ * (thread i = ray i draws from rdv_random_uniform's generator with vp->seeds
+ * after vp->rng_skip draws).  out[n, 4 + 3 SD + DS] receives every output
+ * except the environment and albedo features; per ray, sample_pos[n, 3] gets
+ * the object-space sample position, env_dirs[n, ES, 3] each environment
+ * direction (world space), env_weights[n, ES] = S * T of each, valid[n] 1 where
+ * the ray reached at least one depth (0 elsewhere: those rows are final).
+ * extinction: any LinearFast chain from 3 inputs to 1 output; majorant: device
+ * [depth, height, width] fp32 of a VoxelMajorantField.
+ * Replaces VolumeProfile's shader (src/rdv/domain/volumes.py:503-550,
+ * shaders/volumes/volume_profile.h:1-167 and the traits it calls:
+ * raymarching_transmittance_trait.h, ratiotracking_transmittance_trait.h,
+ * voxel_majorant_field.h, random_library.h:224-239 hg_phase_sample,
+ * math_library.h:48-57, 323-330). */
+int rdv_volume_profile(const rdv_mlp_desc* extinction, const void* packed, const rdv_volume_profile_desc* vp,
+                       const float* majorant, const float* rays, int64_t n_rays, float* out, float* sample_pos,
+                       float* env_dirs, float* env_weights, int32_t* valid, void* stream);
+
+/* VolumeProfile, second stage, for rows with valid[i] = 1: the environment
+ * feature out[i, DS+2+c] = sum over s of env_weights[i, s] * env[i ES + s, c] / ES
+ * (accumulated in s order) and the albedo feature out[i, DS+2+SD+c] =
+ * 1 / (1 - log(1 - albedo[i, c])), where env and albedo are the
+ * ENVIRONMENT and SCATTERING_ALBEDO maps evaluated at env_dirs and sample_pos
+ * (row strides env_stride / albedo_stride floats; 0 repeats one row, for a
+ * constant map).  Replaces volume_profile.h:155-160. */
+int rdv_volume_profile_finish(const rdv_volume_profile_desc* vp, const float* albedo, int64_t albedo_stride,
+                              const float* env, int64_t env_stride, const float* env_weights,
+                              const int32_t* valid, int64_t n_rays, float* out, void* stream);
+
+/* out[rows, width] = value[width] repeated on every row: a Constant map over
+ * rows (src/rdv/maths/__init__.py:1659-1668, shaders/maps/constant.h). */
+int rdv_broadcast_rows(const float* value, int32_t width, int64_t rows, float* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -24,6 +24,7 @@ from .core import (
 )
 from .maths import (
     Composite,
+    Constant,
     Grid,
     GridEvaluator,
     Identity,
@@ -98,6 +99,7 @@ from .rendering import (
     EmissionAbsorption,
     RatiotrackingTransmittance,
     RaymarchingTransmittance,
+    VolumeProfile,
     VoxelMajorantField,
 )
 from .nn import (

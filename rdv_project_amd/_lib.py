@@ -115,6 +115,33 @@ class RatiotrackingDesc(C.Structure):
     ]
 
 
+VP_MAX_DEPTH = 16
+VP_MAX_SPECTRAL = 8
+
+
+class VolumeProfileDesc(C.Structure):
+    """Mirror of rdv_volume_profile_desc."""
+    _fields_ = [
+        ("transform", C.c_float * 12),
+        ("density_scale", C.c_float),
+        ("g", C.c_float),
+        ("step_size", C.c_float),
+        ("light_direction", C.c_float * 3),
+        ("light_intensity", C.c_float * VP_MAX_SPECTRAL),
+        ("transmittance_threshold", C.c_float * VP_MAX_DEPTH),
+        ("depth_samples", C.c_int32),
+        ("spectral_dim", C.c_int32),
+        ("sample_index", C.c_int32),
+        ("environment_samples", C.c_int32),
+        ("maj_width", C.c_int32),
+        ("maj_height", C.c_int32),
+        ("maj_depth", C.c_int32),
+        ("seeds", C.c_uint32 * 4),
+        ("rng_skip", C.c_int32),
+        ("reserved", C.c_int32),
+    ]
+
+
 class MajorantGridDesc(C.Structure):
     """Mirror of rdv_majorant_grid_desc."""
     _fields_ = [
@@ -158,6 +185,12 @@ _SIGNATURES = {
     "rdv_voxel_majorant": (C.c_int, [C.c_void_p, C.c_int32, C.c_int32, C.c_int32, C.c_void_p, C.c_int64, C.c_void_p,
                                      C.c_void_p]),
     "rdv_majorant_grid": (C.c_int, [C.POINTER(MajorantGridDesc), C.c_void_p, C.c_void_p, C.c_void_p]),
+    "rdv_volume_profile": (C.c_int, [C.POINTER(MlpDesc), C.c_void_p, C.POINTER(VolumeProfileDesc), C.c_void_p,
+                                     C.c_void_p, C.c_int64, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
+                                     C.c_void_p, C.c_void_p]),
+    "rdv_volume_profile_finish": (C.c_int, [C.POINTER(VolumeProfileDesc), C.c_void_p, C.c_int64, C.c_void_p,
+                                            C.c_int64, C.c_void_p, C.c_void_p, C.c_int64, C.c_void_p, C.c_void_p]),
+    "rdv_broadcast_rows": (C.c_int, [C.c_void_p, C.c_int32, C.c_int64, C.c_void_p, C.c_void_p]),
     "rdv_render_emission_absorption": (C.c_int, [C.POINTER(CameraDesc), C.c_void_p, C.POINTER(MlpDesc), C.c_void_p,
                                                  C.c_int32, C.c_void_p, C.c_void_p]),
     "rdv_render_emission_absorption_rays": (C.c_int, [C.POINTER(MlpDesc), C.c_void_p, C.c_void_p, C.c_int64,

@@ -1,6 +1,7 @@
 """Grid evaluation and the rendering kernels through the C ABI
 (rdv_cameras_rays, rdv_render_emission_absorption, rdv_composite,
-rdv_raymarch_transmittance).
+rdv_raymarch_transmittance, rdv_ratiotracking_transmittance,
+rdv_volume_profile).
 
 Reference: Grid.__call__ (src/rdv/maths/__init__.py:77-103) evaluates every cell
 of a grid in row-major order into a per-class cached [*shape, OUT] buffer; a
@@ -17,7 +18,7 @@ from . import _chain, _lib
 from .core import RDVObject, current_stream_handle, device, launch_scope, wrap
 from .maths import Grid, Sensor
 from .rendering import (Cameras, EmissionAbsorption, RaymarchingTransmittance, RatiotrackingTransmittance,
-                        VoxelMajorantField)
+                        VolumeProfile, VoxelMajorantField)
 
 _GRID_CACHE: dict = {}
 
@@ -227,6 +228,111 @@ def ratiotracking_rows(rt: RatiotrackingTransmittance, x, out: RDVObject | None 
     return out
 
 
+def _vp_desc(vp: VolumeProfile, seeds, rng_skip: int, W: int, H: int, D: int) -> _lib.VolumeProfileDesc:
+    if vp.spectral_dim is None:
+        raise RuntimeError("Generic arguments could not be deduced from input data. You must explicitly cast.")
+    assert 1 <= vp.depth_samples <= _lib.VP_MAX_DEPTH, \
+        f"VolumeProfile supports 1..{_lib.VP_MAX_DEPTH} transmittance thresholds"
+    assert 1 <= vp.spectral_dim <= _lib.VP_MAX_SPECTRAL, \
+        f"VolumeProfile supports a spectral width of 1..{_lib.VP_MAX_SPECTRAL}"
+    assert len(vp.light_intensity) == vp.spectral_dim, "light_intensity needs one value per spectral channel"
+    d = _lib.VolumeProfileDesc()
+    for i, v in enumerate(vp.transform.tolist_flat()):
+        d.transform[i] = v
+    d.density_scale = vp.density_scale
+    d.g = vp.g
+    d.step_size = vp.step_size
+    for i, v in enumerate(vp.light_direction):
+        d.light_direction[i] = v
+    for i, v in enumerate(vp.light_intensity):
+        d.light_intensity[i] = v
+    for i, v in enumerate(vp.transmittance_threshold):
+        d.transmittance_threshold[i] = v
+    d.depth_samples = vp.depth_samples
+    d.spectral_dim = vp.spectral_dim
+    d.sample_index = vp.sample_index
+    d.environment_samples = vp.environment_samples
+    d.maj_width, d.maj_height, d.maj_depth = W, H, D
+    for i, v in enumerate(seeds):
+        d.seeds[i] = int(v) & 0xFFFFFFFF
+    d.rng_skip = rng_skip
+    d.reserved = 0
+    return d
+
+
+def _vp_workspace(vp: VolumeProfile, rows: int) -> dict:
+    """Per-ray scratch of the two stages (sample positions, environment
+    directions and weights, valid flags and the two maps' values), kept on the
+    node and reused while the row count is unchanged."""
+    es, sd = vp.environment_samples, vp.spectral_dim
+    key = (rows, es, sd)
+    ws = vp.__dict__.get("_rdv_ws")
+    if ws is not None and ws["key"] == key:
+        return ws
+    dev = device()
+    ws = {
+        "key": key,
+        "spos": torch.empty((max(rows, 1), 3), dtype=torch.float32, device=dev),
+        "dirs": torch.empty((max(rows * es, 1), 3), dtype=torch.float32, device=dev),
+        "wts": torch.empty((max(rows * es, 1),), dtype=torch.float32, device=dev),
+        "valid": torch.empty((max(rows, 1),), dtype=torch.int32, device=dev),
+        "albedo": torch.empty((max(rows, 1), sd), dtype=torch.float32, device=dev),
+        "env": torch.empty((max(rows * es, 1), sd), dtype=torch.float32, device=dev),
+    }
+    vp.__dict__["_rdv_ws"] = ws
+    return ws
+
+
+def _map_over(m, x: torch.Tensor, rows: int, out: torch.Tensor) -> tuple[int, int]:
+    """(pointer, row stride in floats) of map m's values over the first `rows`
+    rows of x: a Constant's one row (stride 0), else m evaluated into `out`."""
+    from .maths import Constant
+    if isinstance(m, Constant):
+        return m._value_ptr(), 0
+    if rows > 0:
+        _chain.launch_map_rows(m, x.data_ptr(), out.data_ptr(), rows)
+    return out.data_ptr(), int(out.shape[1])
+
+
+def volume_profile_ptrs(vp: VolumeProfile, x_ptr: int, y_ptr: int, rows: int, seeds=None, rng_skip: int = 0) -> None:
+    """VolumeProfile over `rows` rays (fp32 [rows, 6] at x_ptr) into fp32
+    [rows, OUT] at y_ptr: the ray stage, the scattering-albedo and environment
+    maps over its recorded positions and directions, then the finishing stage.
+    Ray i draws from thread i's generator of `seeds` (fresh RandomLibrary seeds
+    when None) after rng_skip values."""
+    from .types import RandomLibrary
+    seeds = RandomLibrary.next_seeds() if seeds is None else seeds
+    p, packed = _field_plan(vp.extinction, 3)
+    g, W, H, D = _majorant_values(vp.majorant)
+    d = _vp_desc(vp, seeds, rng_skip, W, H, D)
+    ws = _vp_workspace(vp, rows)
+    lib = _lib.load()
+    stream = C.c_void_p(current_stream_handle())
+    _lib.check(lib.rdv_volume_profile(C.byref(p.desc), C.c_void_p(packed.data_ptr()), C.byref(d),
+                                      C.c_void_p(g.data_ptr()), C.c_void_p(x_ptr), C.c_int64(rows),
+                                      C.c_void_p(y_ptr), C.c_void_p(ws["spos"].data_ptr()),
+                                      C.c_void_p(ws["dirs"].data_ptr()), C.c_void_p(ws["wts"].data_ptr()),
+                                      C.c_void_p(ws["valid"].data_ptr()), stream), "VolumeProfile")
+    a_ptr, a_stride = _map_over(vp.scattering_albedo, ws["spos"], rows, ws["albedo"])
+    e_ptr, e_stride = _map_over(vp.environment, ws["dirs"], rows * vp.environment_samples, ws["env"])
+    _lib.check(lib.rdv_volume_profile_finish(C.byref(d), C.c_void_p(a_ptr), C.c_int64(a_stride), C.c_void_p(e_ptr),
+                                             C.c_int64(e_stride), C.c_void_p(ws["wts"].data_ptr()),
+                                             C.c_void_p(ws["valid"].data_ptr()), C.c_int64(rows),
+                                             C.c_void_p(y_ptr), stream), "VolumeProfile")
+
+
+def volume_profile_rows(vp: VolumeProfile, x, out: RDVObject | None = None, seeds=None,
+                        rng_skip: int = 0) -> RDVObject:
+    """VolumeProfile over rows x [..., 6] -> [..., OUT]."""
+    if vp.OUT is None:
+        raise RuntimeError("Generic arguments could not be deduced from input data. You must explicitly cast.")
+    xt, rows, cached = _ray_rows(x, "VolumeProfile", vp.OUT, ("vp", id(type(vp)), vp.OUT))
+    out = cached if out is None else out
+    with launch_scope():
+        volume_profile_ptrs(vp, xt.data_ptr(), out.device_ptr, rows, seeds, rng_skip)
+    return out
+
+
 def majorant_grid(fine: torch.Tensor, fine_shape, shape, channels: int, aligned: bool, linear: bool,
                   out: torch.Tensor) -> torch.Tensor:
     """MajorantGrid's values: fine [*fine_shape, channels] -> out [*shape, channels]."""
@@ -286,6 +392,10 @@ def evaluate_grid(g: Grid, out: RDVObject | None = None) -> RDVObject:
             return out
         if isinstance(m, RaymarchingTransmittance):
             return raymarch_rows(m, rays, out if out is not None else _cached(("sensor-rt",), (*cam.shape, 1)))
+        if isinstance(m, VolumeProfile) and m.OUT is not None:
+            return volume_profile_rows(m, rays, out if out is not None else _cached(("sensor-vp", m.OUT),
+                                                                                     (*cam.shape, m.OUT)),
+                                       seeds=seeds, rng_skip=2 if cam.pixel_jitter else 0)
         if isinstance(m, RatiotrackingTransmittance):
             return ratiotracking_rows(m, rays, out if out is not None else _cached(("sensor-rtt",), (*cam.shape, 1)),
                                       seeds=seeds, rng_skip=2 if cam.pixel_jitter else 0)

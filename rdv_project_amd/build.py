@@ -28,6 +28,7 @@ SOURCES = [
     "mlp_generic.hip",
     "winograd.hip",
     "render.hip",
+    "volume_profile.hip",
     "train.hip",
     "linear_op.hip",
     "tensor_data.hip",

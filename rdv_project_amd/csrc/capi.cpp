@@ -74,6 +74,14 @@ int launch_random_uniform(const uint32_t* seeds, int64_t n_threads, int per_thre
 int launch_ratiotracking(const rdv_mlp_desc& d, const MlpLayout& lay, const void* packed,
                          const rdv_ratiotracking_desc& rt, const float* majorant, const float* rays, int64_t nrays,
                          float* out, hipStream_t stream);
+int launch_volume_profile(const rdv_mlp_desc& d, const MlpLayout& lay, const void* packed,
+                          const rdv_volume_profile_desc& vp, const float* majorant, const float* rays, int64_t nrays,
+                          float* out, float* spos, float* env_dirs, float* env_w, int32_t* valid,
+                          hipStream_t stream);
+int launch_volume_profile_finish(const rdv_volume_profile_desc& vp, const float* albedo, int64_t albedo_stride,
+                                 const float* env, int64_t env_stride, const float* env_w, const int32_t* valid,
+                                 int64_t nrays, float* out, hipStream_t stream);
+int launch_broadcast_rows(const float* value, int width, int64_t rows, float* out, hipStream_t stream);
 int launch_voxel_majorant(const float* grid, int mw, int mh, int md, const float* rays, int64_t n, float* out,
                           hipStream_t stream);
 int launch_majorant_grid(const rdv_majorant_grid_desc& g, const float* fine, float* out, hipStream_t stream);
@@ -520,6 +528,66 @@ int rdv_ratiotracking_transmittance(const rdv_mlp_desc* extinction, const void* 
     return fail(RDV_ERR_INVALID, "rdv_ratiotracking_transmittance: NULL pointer argument");
   return launch_ratiotracking(*extinction, lay, packed, *rt, majorant, rays, n_rays, out,
                               static_cast<hipStream_t>(stream));
+}
+
+static int check_volume_profile(const rdv_volume_profile_desc* vp) {
+  if (!vp) return fail(RDV_ERR_INVALID, "volume profile: NULL descriptor");
+  if (vp->depth_samples < 1 || vp->depth_samples > RDV_VP_MAX_DEPTH)
+    return fail(RDV_ERR_INVALID, "depth_samples must be in [1, " + std::to_string(RDV_VP_MAX_DEPTH) + "]");
+  if (vp->spectral_dim < 1 || vp->spectral_dim > RDV_VP_MAX_SPECTRAL)
+    return fail(RDV_ERR_INVALID, "spectral_dim must be in [1, " + std::to_string(RDV_VP_MAX_SPECTRAL) + "]");
+  if (vp->sample_index < 0 || vp->sample_index >= vp->depth_samples)
+    return fail(RDV_ERR_INVALID, "sample_index must index one of the depth samples");
+  if (vp->environment_samples < 0 || vp->environment_samples > 4096)
+    return fail(RDV_ERR_INVALID, "environment_samples must be in [0, 4096]");
+  if (!(vp->step_size > 0.0f)) return fail(RDV_ERR_INVALID, "step_size must be > 0");
+  if (!(vp->density_scale > 0.0f)) return fail(RDV_ERR_INVALID, "density_scale must be > 0");
+  if (vp->maj_width < 1 || vp->maj_height < 1 || vp->maj_depth < 1 ||
+      int64_t(vp->maj_width) * vp->maj_height * vp->maj_depth >= (int64_t(1) << 40))
+    return fail(RDV_ERR_INVALID, "the majorant grid needs width, height, depth >= 1");
+  if (vp->rng_skip < 0 || vp->rng_skip > 1024) return fail(RDV_ERR_INVALID, "rng_skip must be in [0, 1024]");
+  if (vp->reserved != 0) return fail(RDV_ERR_INVALID, "reserved must be 0");
+  return RDV_OK;
+}
+
+int rdv_volume_profile(const rdv_mlp_desc* extinction, const void* packed, const rdv_volume_profile_desc* vp,
+                       const float* majorant, const float* rays, int64_t n_rays, float* out, float* sample_pos,
+                       float* env_dirs, float* env_weights, int32_t* valid, void* stream) {
+  MlpLayout lay;
+  int rc = check_mlp(extinction, &lay);
+  if (rc != RDV_OK) return rc;
+  rc = check_volume_profile(vp);
+  if (rc != RDV_OK) return rc;
+  if (n_rays < 0 || n_rays >= (int64_t(1) << 31))
+    return fail(RDV_ERR_INVALID, "n_rays must be in [0, 2^31) (the generator's thread index is an int)");
+  if (n_rays == 0) return RDV_OK;
+  if (!packed || !majorant || !rays || !out || !sample_pos || !valid ||
+      (vp->environment_samples > 0 && (!env_dirs || !env_weights)))
+    return fail(RDV_ERR_INVALID, "rdv_volume_profile: NULL pointer argument");
+  return launch_volume_profile(*extinction, lay, packed, *vp, majorant, rays, n_rays, out, sample_pos, env_dirs,
+                               env_weights, valid, static_cast<hipStream_t>(stream));
+}
+
+int rdv_volume_profile_finish(const rdv_volume_profile_desc* vp, const float* albedo, int64_t albedo_stride,
+                              const float* env, int64_t env_stride, const float* env_weights,
+                              const int32_t* valid, int64_t n_rays, float* out, void* stream) {
+  int rc = check_volume_profile(vp);
+  if (rc != RDV_OK) return rc;
+  if (n_rays < 0) return fail(RDV_ERR_INVALID, "n_rays must be >= 0");
+  if (albedo_stride < 0 || env_stride < 0) return fail(RDV_ERR_INVALID, "row strides must be >= 0");
+  if (n_rays == 0) return RDV_OK;
+  if (!albedo || !valid || !out || (vp->environment_samples > 0 && (!env || !env_weights)))
+    return fail(RDV_ERR_INVALID, "rdv_volume_profile_finish: NULL pointer argument");
+  return launch_volume_profile_finish(*vp, albedo, albedo_stride, env, env_stride, env_weights, valid, n_rays, out,
+                                      static_cast<hipStream_t>(stream));
+}
+
+int rdv_broadcast_rows(const float* value, int32_t width, int64_t rows, float* out, void* stream) {
+  if (width < 1) return fail(RDV_ERR_INVALID, "width must be >= 1");
+  if (rows < 0) return fail(RDV_ERR_INVALID, "rows must be >= 0");
+  if (rows == 0) return RDV_OK;
+  if (!value || !out) return fail(RDV_ERR_INVALID, "rdv_broadcast_rows: NULL pointer argument");
+  return launch_broadcast_rows(value, width, rows, out, static_cast<hipStream_t>(stream));
 }
 
 int rdv_voxel_majorant(const float* grid, int32_t width, int32_t height, int32_t depth, const float* rays,

@@ -175,4 +175,20 @@ int launch_concat(const float* x1, int C1, const float* x2, int C2, int64_t rows
   return RDV_OK;
 }
 
+// Constant map over rows (src/rdv/maths/__init__.py:1659-1668): out[r, c] = value[c].
+__global__ __launch_bounds__(256) void broadcast_rows_kernel(const float* __restrict__ value, int width, int64_t total,
+                                                             float* __restrict__ out) {
+  for (int64_t e = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; e < total; e += int64_t(gridDim.x) * blockDim.x)
+    out[e] = value[e % width];
+}
+
+int launch_broadcast_rows(const float* value, int width, int64_t rows, float* out, hipStream_t stream) {
+  const int64_t total = rows * width;
+  unsigned blocks = 0;
+  if (int rc = grid_for(total, &blocks)) return rc;
+  broadcast_rows_kernel<<<dim3(blocks), dim3(256), 0, stream>>>(value, width, total, out);
+  RDV_HIP_TRY(hipGetLastError());
+  return RDV_OK;
+}
+
 }  // namespace rdv

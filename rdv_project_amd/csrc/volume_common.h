@@ -1,0 +1,156 @@
+// Device helpers shared by the ray kernels (render.hip, volume_profile.hip):
+// the unit-box slab test, the 3x3 inverse of a mat4x3's linear part, the voxel
+// majorant lookup, and the runtime-shaped extinction / field chain evaluated on
+// 32 points of a wave with its launch helper.
+#pragma once
+
+#include "mlp_core.h"
+#include "mlp_generic.h"
+
+namespace rdv {
+
+// math_library.h:48-57: slab test against [-1, 1]^3.
+// Every operation rounded on its own: a contracted -x * inv +- s moves the exit
+// distance by an ulp against the voxel exits computed from the same ray, which
+// changes where a tracked ray's last flight ends.
+__device__ __forceinline__ void ray_box(const float (&x)[3], const float (&w)[3], float& tmin, float& tmax) {
+#pragma clang fp contract(off)
+  float c0[3], c1[3];
+#pragma unroll
+  for (int i = 0; i < 3; ++i) {
+    const float inv = 1.0f / w[i];
+    const float xc = -x[i] * inv;
+    const float s = fabsf(inv);
+    c0[i] = xc - s;
+    c1[i] = xc + s;
+  }
+  tmin = fmaxf(fmaxf(c0[0], c0[1]), c0[2]);
+  tmax = fminf(fminf(c1[0], c1[1]), c1[2]);
+}
+
+// GLSL inverse() of the 3x3 linear part by the adjugate (columns c0, c1, c2).
+__device__ __forceinline__ void inverse3(const float (&M)[12], float (&L)[9]) {
+  const float a00 = M[0], a01 = M[1], a02 = M[2];  // column 0
+  const float a10 = M[3], a11 = M[4], a12 = M[5];  // column 1
+  const float a20 = M[6], a21 = M[7], a22 = M[8];  // column 2
+  const float b01 = a22 * a11 - a12 * a21;
+  const float b11 = -a22 * a10 + a12 * a20;
+  const float b21 = a21 * a10 - a11 * a20;
+  const float det = a00 * b01 + a01 * b11 + a02 * b21;
+  const float id = 1.0f / det;
+  L[0] = b01 * id;
+  L[1] = (-a22 * a01 + a02 * a21) * id;
+  L[2] = (a12 * a01 - a02 * a11) * id;
+  L[3] = b11 * id;
+  L[4] = (a22 * a00 - a02 * a20) * id;
+  L[5] = (-a12 * a00 + a02 * a10) * id;
+  L[6] = b21 * id;
+  L[7] = (-a21 * a00 + a01 * a20) * id;
+  L[8] = (a11 * a00 - a01 * a10) * id;
+}
+
+constexpr int64_t kGenFieldLdsCap = 152 * 1024;
+
+// A-fragment and bias sources of a block: the LDS copy (staged here) or the
+// packed block in global memory.
+template <bool LDSW>
+__device__ __forceinline__ void gen_sources(const uint8_t* packed, const GenNet& g, uint8_t* smem, const half8** w,
+                                            const float** b) {
+  if constexpr (LDSW) {
+    gen_stage(packed, g, smem);
+    *w = reinterpret_cast<const half8*>(smem);
+    *b = reinterpret_cast<const float*>(smem + int64_t(g.n_frag) * 1024);
+  } else {
+    *w = reinterpret_cast<const half8*>(packed + g.frag_off0);
+    *b = reinterpret_cast<const float*>(packed + g.bias_off0);
+  }
+}
+
+// The chain's head value of row 0 at this lane's sample p (3 coordinates).
+template <int MT>
+__device__ __forceinline__ float gen_field_row0(const GenNet& g, const half8* w0, const float* b0, bool has_bias,
+                                                int lane, int h, const float (&p)[3], int act) {
+  const int z = opaque_zero();
+  const half8* wsrc = w0 + z;
+  auto wf = [&](int f) { return wsrc[f * 64 + lane]; };
+  auto get = [&](int d) { return d == 0 ? p[0] : (d == 1 ? p[1] : p[2]); };
+  auto l0 = [&](int c) { return gen_l0_chunk(g, c, h, get); };
+  float v = 0.0f;
+  auto sink = [&](const auto& acc) { v = gen_head_act(act, 0, acc[0][0]); };
+  gen_chain<MT>(g, GenCtx{b0 + z, has_bias, h}, wf, l0, sink);
+  return v;
+}
+
+// voxel_majorant_field.h: the majorant of the voxel holding x and the distance
+// along w to that voxel's exit.
+__device__ __forceinline__ float voxel_majorant(const float* __restrict__ grid, int mw, int mh, int md,
+                                                const float (&x)[3], const float (&w)[3], float& dist) {
+#pragma clang fp contract(off)
+  const int dim[3] = {mw, mh, md};
+  int cell[3];
+  float te[3];
+#pragma unroll
+  for (int i = 0; i < 3; ++i) {
+    const float fd = float(dim[i]);
+    // int() truncates toward zero; clamping first keeps the conversion in range
+    // (and sends NaN to 0) without changing any in-range result.
+    const float f = (x[i] * 0.5f + 0.5f) * fd;
+    cell[i] = int(fminf(fmaxf(f, 0.0f), fd - 1.0f));
+    const float vs = 2.0f / fd;
+    const float bmin = float(cell[i]) * vs - 1.0f;
+    const float bmax = bmin + vs;
+    const float t0 = (bmin - x[i]) / w[i];
+    const float t1 = (bmax - x[i]) / w[i];
+    te[i] = fmaxf(t0, t1);
+  }
+  dist = fminf(fminf(te[0], te[1]), te[2]);
+  return grid[(int64_t(cell[2]) * mh + cell[1]) * mw + cell[0]];
+}
+
+template <class Args, int MT, bool LDSW>
+static int launch_gen_field(void (*kernel)(Args), const Args& a, int64_t work_items, int cu, size_t lds,
+                            hipStream_t stream) {
+  static bool attr = false;
+  if (LDSW && !attr) {
+    RDV_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    int(kGenFieldLdsCap)));
+    attr = true;
+  }
+  constexpr int waves = gen_waves<MT>();
+  int64_t blocks = cu;
+  const int64_t need = (work_items + waves - 1) / waves;
+  if (need < blocks) blocks = need;
+  kernel<<<dim3(unsigned(blocks)), dim3(64 * waves), lds, stream>>>(a);
+  RDV_HIP_TRY(hipGetLastError());
+  return RDV_OK;
+}
+
+#define RDV_GEN_FIELD_DISPATCH(KERNEL, ARGS, ITEMS, CU, NET, STREAM)                                          \
+  do {                                                                                                       \
+    const int64_t lds_ = gen_lds_bytes(NET);                                                                 \
+    const bool in_lds_ = lds_ <= kGenFieldLdsCap;                                                            \
+    switch (gen_mt_bound(NET)) {                                                                             \
+      case 1:                                                                                                \
+        return in_lds_ ? launch_gen_field<decltype(ARGS), 1, true>(&KERNEL<1, true>, ARGS, ITEMS, CU, lds_, STREAM) \
+                       : launch_gen_field<decltype(ARGS), 1, false>(&KERNEL<1, false>, ARGS, ITEMS, CU, 0, STREAM); \
+      case 2:                                                                                                \
+        return in_lds_ ? launch_gen_field<decltype(ARGS), 2, true>(&KERNEL<2, true>, ARGS, ITEMS, CU, lds_, STREAM) \
+                       : launch_gen_field<decltype(ARGS), 2, false>(&KERNEL<2, false>, ARGS, ITEMS, CU, 0, STREAM); \
+      case 4:                                                                                                \
+        return in_lds_ ? launch_gen_field<decltype(ARGS), 4, true>(&KERNEL<4, true>, ARGS, ITEMS, CU, lds_, STREAM) \
+                       : launch_gen_field<decltype(ARGS), 4, false>(&KERNEL<4, false>, ARGS, ITEMS, CU, 0, STREAM); \
+      default:                                                                                               \
+        return in_lds_ ? launch_gen_field<decltype(ARGS), 8, true>(&KERNEL<8, true>, ARGS, ITEMS, CU, lds_, STREAM) \
+                       : launch_gen_field<decltype(ARGS), 8, false>(&KERNEL<8, false>, ARGS, ITEMS, CU, 0, STREAM); \
+    }                                                                                                        \
+  } while (0)
+
+// A LinearFast chain from 3 inputs (raw or FREQ-encoded) to `out` outputs?
+static bool is_f16_field(const rdv_mlp_desc& d, int out) {
+  if (d.in_features != 3 || d.dims[d.n_layers] != out) return false;
+  for (int i = 0; i < d.n_layers; ++i)
+    if (d.prec[i] != RDV_PREC_F16) return false;
+  return true;
+}
+
+}  // namespace rdv

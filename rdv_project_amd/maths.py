@@ -94,6 +94,49 @@ class Identity(Map):
 X = Identity()
 
 
+class Constant(Map):
+    """f(x) = data for every row, whatever the input width (reference:
+    maths:1659-1668, shaders/maps/constant.h).  data: [..., OUT]; its last row
+    of OUT values is the constant (the reference copies the buffer's first OUT
+    floats)."""
+
+    def __init__(self, data) -> None:
+        if not isinstance(data, RDVObject):
+            data = wrap(data)
+        self.OUT = int(data.shape[-1])
+        self.buf_ = data
+
+    def _value_ptr(self) -> int:
+        import torch
+        t = self.buf_.as_tensor("torch")
+        if t.dtype != torch.float32 or not t.is_contiguous():
+            t = t.to(torch.float32).contiguous()
+            self.__dict__["_rdv_value"] = t  # keep the converted copy alive
+        return t.data_ptr()
+
+    def _launch_rows(self, x_ptr: int, y_ptr: int, rows: int) -> None:
+        import ctypes as C
+        from . import _lib
+        from .core import current_stream_handle
+        _lib.check(_lib.load().rdv_broadcast_rows(C.c_void_p(self._value_ptr()), C.c_int32(self.OUT),
+                                                  C.c_int64(rows), C.c_void_p(y_ptr),
+                                                  C.c_void_p(current_stream_handle())), "Constant")
+
+    def _evaluate_rows(self, x) -> RDVObject:
+        import torch
+        from .core import device, launch_scope
+        x = wrap(x)
+        rows = _math.prod(x.shape[:-1]) if len(x.shape) >= 1 else 1
+        hit = self.__dict__.get("_rdv_out")
+        shape = (*x.shape[:-1], self.OUT)
+        if hit is None or tuple(hit.shape) != shape:
+            hit = RDVObject(torch.empty(shape, dtype=torch.float32, device=device()))
+            self.__dict__["_rdv_out"] = hit
+        with launch_scope():
+            self._launch_rows(x.device_ptr, hit.device_ptr, rows)
+        return hit
+
+
 class Composite(Map):
     """f(g(x)) (reference: maths:1700-1728)."""
 

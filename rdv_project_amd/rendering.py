@@ -4,6 +4,7 @@
   RaymarchingTransmittance   reference domain/volumes.py:124-141 (Map[6, 1])
   RatiotrackingTransmittance reference domain/volumes.py:144-190 (Map[6, 1])
   VoxelMajorantField         reference domain/volumes.py:191-211 (Map[6, 2])
+  VolumeProfile              reference domain/volumes.py:503-550 (Map[6, DS + 3 SD + 4])
   EmissionAbsorption         build-defined (Map[6, 3]): the MLP-in-the-loop
                              renderer of the benchmark configuration
 Grids compose with maps (`Cameras(...) >> RaymarchingTransmittance(m)`) into a
@@ -157,6 +158,75 @@ class RatiotrackingTransmittance(Map[6, 1]):
     def _launch_rows(self, x_ptr: int, y_ptr: int, rows: int) -> None:
         from . import _render
         _render.ratiotracking_ptrs(self, x_ptr, y_ptr, rows)
+
+
+class VolumeProfile(Map):
+    """Per-ray features of a participating medium for a learned renderer
+    (reference: volumes.py:503-550, shaders/volumes/volume_profile.h:1-167).
+    For a ray (x, w) [6] in the object space of `transform` (the box [-1,1]^3),
+    OUT = DS + 3 SD + 4 values (DS = len(transmittance_threshold), SD = the
+    spectral width of scattering_albedo / environment):
+      [0, DS)            re-encoded depths where tau crosses each threshold's
+                         expected crossing value (1 / (0.1 + t_0), then
+                         1 / (1 + 10 sqrt(t_i - t_{i-1})))
+      DS                 0.2 log(1 + tau)
+      DS + 1             S * T of the light ray (raymarched, step_size)
+      DS + 2 + [0, SD)   environment next-event estimate: mean over
+                         environment_samples Henyey-Greenstein directions of
+                         S * T (ratio-tracked) * environment(direction)
+      DS + 2 + SD + [0, SD)   1 / (1 - log(1 - albedo)) at the sample position
+      DS + 2 + 2 SD      g
+      DS + 3 + 2 SD + [0, SD)  light_intensity
+      OUT - 1            S = 1 - exp(-tau)
+    (everything but S is 0 where no depth was reached; all 0 for a miss).
+    extinction: a Map[3, 1] (any LinearFast chain from 3 inputs to 1 output);
+    majorant: a VoxelMajorantField or a Grid[3, 1]; scattering_albedo and
+    environment: Map[3, SD] (Constant maps or any map this package evaluates
+    over rows).  Random draws: ray i uses thread i's generator of a fresh
+    dispatch (RandomLibrary).  nee_near_distance is kept for the interface; the
+    reference's active shader does not read it."""
+
+    IN = 6
+
+    def __init__(self, extinction: Map, majorant, environment: Map, scattering_albedo: Map,
+                 transmittance_threshold: list, density_scale: float = 1.0, transform=None,
+                 light_direction=(0.0, 1.0, 0.0), light_intensity=None, g: float = 0.0, step_size: float = 0.001,
+                 environment_samples: int = 4, sample_index: int = 0, nee_near_distance: float = 0.05) -> None:
+        # trait order of the reference (volumes.py:7-120): extinction, majorant,
+        # scattering albedo (fixes SPECTRAL_DIM when the map's width is known), environment
+        self.extinction = extinction.cast(Map[3, 1])
+        self.majorant = _as_majorant_field(majorant).cast(Map[6, 2])
+        spectral_dim = scattering_albedo.OUT
+        if spectral_dim is None:
+            spectral_dim = environment.OUT
+        self.scattering_albedo = scattering_albedo.cast(Map[3, spectral_dim])
+        self.environment = environment.cast(Map[3, spectral_dim])
+        depth_samples = len(transmittance_threshold)
+        self.spectral_dim = None if spectral_dim is None else int(spectral_dim)
+        self.depth_samples = depth_samples
+        self.OUT = None if spectral_dim is None else 4 + spectral_dim * 3 + depth_samples
+        self.transform = mat4x3(1.0, 0.0, 0.0, 0.0, 1.0, 0.0, 0.0, 0.0, 1.0, 0.0, 0.0, 0.0) \
+            if transform is None else _as_mat4x3(transform)
+        self.light_direction = tuple(float(v) for v in light_direction)
+        assert len(self.light_direction) == 3, "light_direction must have 3 components"
+        if spectral_dim is not None:
+            self.light_intensity = [1.0] * spectral_dim if light_intensity is None else \
+                [float(v) for v in light_intensity]
+        self.density_scale = float(density_scale)
+        self.g = float(g)
+        self.step_size = float(step_size)
+        self.environment_samples = int(environment_samples)
+        self.sample_index = int(sample_index)
+        self.transmittance_threshold = [float(v) for v in transmittance_threshold]
+        self.nee_near_distance = float(nee_near_distance)
+
+    def _evaluate_rows(self, x) -> RDVObject:
+        from . import _render
+        return _render.volume_profile_rows(self, x)
+
+    def _launch_rows(self, x_ptr: int, y_ptr: int, rows: int) -> None:
+        from . import _render
+        _render.volume_profile_ptrs(self, x_ptr, y_ptr, rows)
 
 
 class EmissionAbsorption(Map[6, 3]):

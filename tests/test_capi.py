@@ -194,3 +194,63 @@ def test_linear_op_host_errors_need_no_device():
     assert lib.rdv_relu_op(None, None, -1, None) == _lib.RDV_ERR_INVALID
     assert lib.rdv_relu_op(None, None, 0, None) == 0
     assert lib.rdv_relu_op(0x1008, 0x2000, 16, None) == _lib.RDV_ERR_INVALID
+
+
+def _vp(**kw):
+    d = _lib.VolumeProfileDesc()
+    for i, v in enumerate([1.0, 0.0, 0.0, 0.0, 1.0, 0.0, 0.0, 0.0, 1.0, 0.0, 0.0, 0.0]):
+        d.transform[i] = v
+    d.density_scale, d.g, d.step_size = 1.0, 0.0, 0.001
+    d.light_direction[1] = 1.0
+    d.depth_samples, d.spectral_dim, d.sample_index, d.environment_samples = 3, 3, 0, 4
+    d.maj_width = d.maj_height = d.maj_depth = 8
+    d.rng_skip, d.reserved = 0, 0
+    for k, v in kw.items():
+        setattr(d, k, v)
+    return d
+
+
+def _ext_desc():
+    d = _lib.MlpDesc()
+    d.n_layers, d.in_features, d.encoding, d.enc_octaves = 2, 3, _lib.ENC_NONE, 0
+    d.dims[0], d.dims[1], d.dims[2] = 3, 16, 1
+    d.act[0], d.act[1] = _lib.ACT_RELU, _lib.ACT_NONE
+    d.prec[0] = d.prec[1] = _lib.PREC_F16
+    return d
+
+
+@pytest.mark.parametrize("kw,fragment", [
+    (dict(depth_samples=0), "depth_samples"),
+    (dict(depth_samples=17), "depth_samples"),
+    (dict(spectral_dim=0), "spectral_dim"),
+    (dict(spectral_dim=9), "spectral_dim"),
+    (dict(sample_index=3), "sample_index"),
+    (dict(environment_samples=-1), "environment_samples"),
+    (dict(step_size=0.0), "step_size"),
+    (dict(density_scale=-1.0), "density_scale"),
+    (dict(maj_depth=0), "majorant grid"),
+    (dict(rng_skip=-2), "rng_skip"),
+    (dict(reserved=1), "reserved"),
+])
+def test_volume_profile_rejects_before_any_launch(kw, fragment):
+    lib = _lib.load()
+    d = _vp(**kw)
+    rc = lib.rdv_volume_profile(C.byref(_ext_desc()), 0x1000, C.byref(d), 0x2000, 0x3000, 64, 0x4000, 0x5000,
+                                0x6000, 0x7000, 0x8000, None)
+    assert rc == _lib.RDV_ERR_INVALID and fragment in _lib.last_error()
+    rc = lib.rdv_volume_profile_finish(C.byref(d), 0x1000, 3, 0x2000, 3, 0x3000, 0x4000, 64, 0x5000, None)
+    assert rc == _lib.RDV_ERR_INVALID and fragment in _lib.last_error()
+
+
+def test_volume_profile_host_errors_need_no_device():
+    lib = _lib.load()
+    d = _vp()
+    assert lib.rdv_volume_profile(C.byref(_ext_desc()), None, C.byref(d), None, None, 0, None, None, None, None,
+                                  None, None) == 0
+    assert lib.rdv_volume_profile(C.byref(_ext_desc()), None, C.byref(d), None, None, 16, None, None, None, None,
+                                  None, None) == _lib.RDV_ERR_INVALID
+    assert "NULL" in _lib.last_error()
+    assert lib.rdv_volume_profile_finish(C.byref(d), 0x1000, -1, 0x2000, 3, 0x3000, 0x4000, 8, 0x5000,
+                                         None) == _lib.RDV_ERR_INVALID
+    assert lib.rdv_broadcast_rows(None, 0, 4, None, None) == _lib.RDV_ERR_INVALID
+    assert lib.rdv_broadcast_rows(None, 3, 0, None, None) == 0
