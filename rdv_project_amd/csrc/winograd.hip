@@ -623,8 +623,9 @@ __device__ __forceinline__ void wg_store_asm(const f32x4 (&yv)[2][2], const Wino
 //   waves 4-7 (input role): row pairs into a 4-slot ring by DMA (3 pairs
 //     ahead), then V of tile row s into sv buffer s % 2;
 //   waves 0-3 (GEMM role): U in registers (its loads run under the first V
-//     transform); the GEMMs, inverse transform and stores of tile row s - 1
-//     from sv buffer (s - 1) % 2.
+//     transform, and the first tile row's GEMMs start on each group of U as it
+//     lands); the GEMMs, inverse transform and stores of tile row s - 1 from sv
+//     buffer (s - 1) % 2.
 // Step s = 0 .. R ends with one barrier.  Each role's vector-memory stream is
 // its own (DMAs only; U's loads then stores only), so the input role's waits
 // count its DMA instructions alone.  The V transform is one (tile, 4-channel)
@@ -778,76 +779,105 @@ __global__ __launch_bounds__(512, 1) void winograd3x3_pipe_kernel(WinogradArgs a
   // ================= GEMM role: wave w owns output channels 16 (4 blockIdx.y + w) + 0..15
   const int g = blockIdx.y * 4 + w;
   const bool active = 16 * g < a.cout;
+  // Bias, ReLU and the stores of tile row tr's outputs yv (after wg_gemm_pipe).
+  auto finish_row = [&](f32x4 (&yv)[2][2], const f32x4& bias, int img, int seg, int tr) {
+    const int n = lane & 15;
+    const int tc = seg * kWgTiles + n;
+    const int co0 = 16 * g + 4 * (lane >> 4);
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj)
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int jx = 0; jx < 2; ++jx) {
+          float val = yv[i][jx][jj] + bias[jj];
+          if (a.relu) val = fmaxf(val, 0.0f);
+          yv[i][jx][jj] = val;
+        }
+    if (a.out_layout == RDV_LAYOUT_CHW && a.out_dtype == RDV_DTYPE_F16) {
+      // lane 4q + k of the 16 tile lanes takes channel co0 + k of tiles 4q .. 4q+3
+      // (8 consecutive fp16 columns of each output row): two 16-byte stores
+      // instead of eight 4-byte ones.  W % 8 == 0, so a quad's tiles are all
+      // inside the image or all outside.
+      uint32_t r0[4], r1[4];
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        r0[jj] = __builtin_bit_cast(uint32_t, half2v{half_t(yv[0][0][jj]), half_t(yv[0][1][jj])});
+        r1[jj] = __builtin_bit_cast(uint32_t, half2v{half_t(yv[1][0][jj]), half_t(yv[1][1][jj])});
+      }
+      const int k = lane & 3;
+      wg_quad_transpose(r0, k);
+      wg_quad_transpose(r1, k);
+      const int tq = tc - k;  // the quad's first tile
+      if (tq < a.W / 2) {
+        half_t* dst = static_cast<half_t*>(a.y) + (int64_t(img) * a.cout + co0 + k) * (int64_t(a.H) * a.W) +
+                      int64_t(2 * tr) * a.W + 2 * tq;
+        wg_st128(dst, __builtin_bit_cast(f32x4, r0));
+        wg_st128(dst + a.W, __builtin_bit_cast(f32x4, r1));
+      }
+    } else if (tc < a.W / 2) {
+      wg_store_asm(yv, a, img, co0, 2 * tr, 2 * tc);
+    }
+  };
+  // The GEMMs, inverse transform, bias, ReLU and stores of tile row tr from sv buffer `buf`.
+  auto gemm_row = [&](const half8 (&uu)[16][KC], const f32x4& bias, int img, int seg, int tr, int buf) {
+    f32x4 yv[2][2];
+    wg_gemm_pipe(uu, svb + buf * LD::kSvHalf8, lane, yv);
+    finish_row(yv, bias, img, seg, tr);
+  };
   // U's loads are issued after the first item's first barrier (its first pairs
   // landed), so the input role's DMAs go first, and they run under the input
-  // role's V of tile row 0, which needs no U; the wait for them follows step 0
+  // role's V of tile row 0, which needs no U.  The bias comes first and U in the
+  // order of wg_gemm_pipe's fragment groups (column b = G / 2, rows 2 (G % 2) +
+  // 0..1), and the first tile row is peeled out of the loop below: the
+  // compiler's per-register waits then let each group's MFMAs start as soon as
+  // that group's U has landed, instead of after all 128 KiB of it.  Those waits
+  // count only these loads (no store is issued before that row's GEMMs), and the
+  // peeled row uses every U register and the bias, so nothing is pending for the
+  // compiler inside the loop.
   const bool any = int64_t(blockIdx.x) < a.items;
   if (any) __syncthreads();
-  half8 u[16][KC];
   const int g_n = (a.cout + 15) / 16;
   const int gu = active ? g : 0;
-#pragma unroll
-  for (int p = 0; p < 16; ++p)
-#pragma unroll
-    for (int kc = 0; kc < KC; ++kc)
-      u[p][kc] = reinterpret_cast<const half8*>(a.U)[((int64_t(p) * KC + kc) * g_n + gu) * 64 + lane];
   const f32x4 bias = wg_lane_bias(a, gu, lane);
-  if (any) __syncthreads();  // end of the first item's step 0
+  half8 u[16][KC];
+  wg_static_for(std::make_integer_sequence<int, 8>{}, [&](auto gc) {
+    constexpr int G = decltype(gc)::value, b = G / 2, ra0 = 2 * (G % 2);
 #pragma unroll
-  for (int p = 0; p < 16; ++p)
+    for (int r = 0; r < 2; ++r)
 #pragma unroll
-    for (int kc = 0; kc < KC; ++kc) asm volatile("" ::"v"(u[p][kc]));
-  asm volatile("" ::"v"(bias));
-  wg_wait_vmcnt(0);  // U and the bias resident: no compiler-generated wait inside the loop
+      for (int kc = 0; kc < KC; ++kc) {
+        const int p = 4 * (ra0 + r) + b;
+        u[p][kc] = reinterpret_cast<const half8*>(a.U)[((int64_t(p) * KC + kc) * g_n + gu) * 64 + lane];
+      }
+  });
+  if (!any) return;
+  __syncthreads();  // end of the first item's step 0 (V of its first tile row in sv buffer 0)
+  {
+    int img, seg, tr0;
+    decode(blockIdx.x, img, seg, tr0);
+    // step 1 of the first item
+    f32x4 yv[2][2] = {};
+    if (active) wg_gemm_pipe(u, svb, lane, yv);
+    // every path uses U and the bias here, before any store, so none enters the
+    // loop with a load pending for the compiler (it would wait there, on the
+    // stores); on the active path every load has already been waited for
+#pragma unroll
+    for (int p = 0; p < 16; ++p)
+#pragma unroll
+      for (int kc = 0; kc < KC; ++kc) asm volatile("" ::"v"(u[p][kc]));
+    asm volatile("" ::"v"(bias));
+    if (active) finish_row(yv, bias, img, seg, tr0);
+    __syncthreads();
+  }
   for (int64_t item = blockIdx.x; item < a.items; item += gridDim.x) {
     int img, seg, tr0;
     decode(item, img, seg, tr0);
     const int R = min(a.rows_per_item, a.th - tr0);
-    const int s0 = item == blockIdx.x ? 1 : 0;  // the first item's step 0 barriers are above
+    const int s0 = item == blockIdx.x ? 2 : 0;  // the first item's steps 0 and 1 are above
     if (s0 == 0) __syncthreads();               // the input role's first two pairs
     for (int s = s0; s <= R; ++s) {
-      if (s >= 1 && active) {
-        const int tr = tr0 + s - 1;
-        f32x4 yv[2][2];
-        wg_gemm_pipe(u, svb + ((s - 1) & 1) * LD::kSvHalf8, lane, yv);
-        const int n = lane & 15;
-        const int tc = seg * kWgTiles + n;
-        const int co0 = 16 * g + 4 * (lane >> 4);
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj)
-#pragma unroll
-          for (int i = 0; i < 2; ++i)
-#pragma unroll
-            for (int jx = 0; jx < 2; ++jx) {
-              float val = yv[i][jx][jj] + bias[jj];
-              if (a.relu) val = fmaxf(val, 0.0f);
-              yv[i][jx][jj] = val;
-            }
-        if (a.out_layout == RDV_LAYOUT_CHW && a.out_dtype == RDV_DTYPE_F16) {
-          // lane 4q + k of the 16 tile lanes takes channel co0 + k of tiles 4q .. 4q+3
-          // (8 consecutive fp16 columns of each output row): two 16-byte stores
-          // instead of eight 4-byte ones.  W % 8 == 0, so a quad's tiles are all
-          // inside the image or all outside.
-          uint32_t r0[4], r1[4];
-#pragma unroll
-          for (int jj = 0; jj < 4; ++jj) {
-            r0[jj] = __builtin_bit_cast(uint32_t, half2v{half_t(yv[0][0][jj]), half_t(yv[0][1][jj])});
-            r1[jj] = __builtin_bit_cast(uint32_t, half2v{half_t(yv[1][0][jj]), half_t(yv[1][1][jj])});
-          }
-          const int k = lane & 3;
-          wg_quad_transpose(r0, k);
-          wg_quad_transpose(r1, k);
-          const int tq = tc - k;  // the quad's first tile
-          if (tq < a.W / 2) {
-            half_t* dst = static_cast<half_t*>(a.y) + (int64_t(img) * a.cout + co0 + k) * (int64_t(a.H) * a.W) +
-                          int64_t(2 * tr) * a.W + 2 * tq;
-            wg_st128(dst, __builtin_bit_cast(f32x4, r0));
-            wg_st128(dst + a.W, __builtin_bit_cast(f32x4, r1));
-          }
-        } else if (tc < a.W / 2) {
-          wg_store_asm(yv, a, img, co0, 2 * tr, 2 * tc);
-        }
-      }
+      if (s >= 1 && active) gemm_row(u, bias, img, seg, tr0 + s - 1, (s - 1) & 1);
       __syncthreads();
     }
   }
