@@ -434,7 +434,7 @@ def bench_conv_and_data_ops(steps, warmup):
     out = {"direct_conv": {
         "workload": "implicit-GEMM direct conv, fp16 operands: channels-last fp32 x [256*256, 64] (seed 15), "
                     "3x3 64 -> 64, 'same' padding, fp32 y (Conv2DTensorOp{Fast,Simple,Simple3x3,Window3x3})",
-        "kernel": "conv_op_kernel<true, 4>",
+        "kernel": "conv_tile_kernel<4>",
         "us_per_call": round(ev * 1e3, 2),
         "TFLOP_s": round(flop / (ev * 1e-3) / 1e12, 1),
         "mfma_peak_pct": round(100 * flop / (ev * 1e-3) / 1e12 / PEAK_FP16_TFLOPS, 2),

@@ -86,11 +86,13 @@ __device__ __forceinline__ float w_at(const ConvArgs& a, int o, int k) {
 // k0 + c kK + (lane / 16) kLane + 0 .. kLane-1 (fp16 halves or fp32 floats);
 // outputs past cout and K past KH KW CIN are zero.  Also the bias block.
 template <bool F16>
-__device__ void cv_stage(const ConvArgs& a, int o0, int k0, int nkc, f32x4* sw, float* sb) {
+__device__ void cv_stage(const ConvArgs& a, int o0, int k0, int nkc, f32x4* sw, float* sb, int tid = -1,
+                         int nthr = kCvThreads) {
   using S = CvStep<F16>;
+  if (tid < 0) tid = int(threadIdx.x);
   const int nt = a.ob / 16;
   const int slots = nt * nkc * 64;
-  for (int s = threadIdx.x; s < slots; s += kCvThreads) {
+  for (int s = tid; s < slots; s += nthr) {
     const int t = s / (nkc * 64);
     const int rem = s - t * (nkc * 64);
     const int c = rem >> 6, ln = rem & 63;
@@ -111,8 +113,7 @@ __device__ void cv_stage(const ConvArgs& a, int o0, int k0, int nkc, f32x4* sw, 
     }
     sw[s] = v;
   }
-  for (int i = threadIdx.x; i < a.ob; i += kCvThreads)
-    sb[i] = (a.bias != nullptr && o0 + i < a.cout) ? a.bias[o0 + i] : 0.0f;
+  for (int i = tid; i < a.ob; i += nthr) sb[i] = (a.bias != nullptr && o0 + i < a.cout) ? a.bias[o0 + i] : 0.0f;
 }
 
 // cv_stage for an RSCK filter whose rows are 16-byte vectors (cout % 4 == 0,
@@ -347,6 +348,235 @@ __global__ __launch_bounds__(kCvThreads) void conv_op_kernel(ConvArgs a) {
   }
 }
 
+// ------------------------------------------------------------ spatial tiles
+// The fp16 path for a filter block that fits LDS next to a haloed input tile
+// (cin % 32 == 0, cout <= 128): a block owns TH x TW tiles of output pixels in
+// turn.  Each tile's (TH + KH - 1) x (TW + KW - 1) x cin input window is
+// converted to fp16 into LDS once (zero outside the image) and every tap reads
+// its B fragments from there, so x crosses the load path about
+// (TH + KH - 1)(TW + KW - 1) / (TH TW) times instead of KH KW times.  The
+// filter block is staged once per launch, its loads issued in one round next
+// to the first window's, and the next tile's window loads are in flight (in
+// registers) while the current tile's MFMAs run.  Wave w computes output rows
+// 2w and 2w + 1 of the tile, 32 columns each (N blocks j = 0..3: row 2w + j / 2,
+// columns 16 (j % 2) ..: four blocks share every filter fragment read) against
+// every 16-channel output tile.  K runs over taps in (kh, kw) order and 32-channel
+// chunks within a tap: the filter staging's K order.
+constexpr int kTileH = 8;     // output rows per tile (two per wave)
+constexpr int kTileW = 32;    // output columns per tile
+constexpr int kTileNB = 4;    // N blocks per wave
+constexpr int kWinBatch = 22; // window loads per thread held across a tile (a 3x3, 64-channel window: 21.25)
+constexpr int kFiltBatch = 5; // filter groups per thread and round (64 -> 64 3x3: 4.5)
+
+struct TileArgs {
+  ConvArgs c;
+  int tiles_w, tiles;  // column tiles per row band, tiles in all
+  int win_w, win_h;    // input window: kTileW + kw - 1, kTileH + kh - 1
+  int ps;              // LDS bytes per window pixel: 2 cin + 16 (spreads a wave's reads over every bank)
+  int win_bytes;       // window bytes, rounded up to 16
+};
+
+// The RSCK filter block [o0, o0 + 16 NT) x every K into LDS in fragment order
+// (as cv_stage_rows), each thread's groups kFiltBatch at a time; between the
+// loads and their conversion, `mid` runs (the first window's loads), so those
+// do not delay this round's waits.
+template <int NT, class Mid>
+__device__ void cv_stage_filter(const ConvArgs& a, int o0, int nkc, f32x4* sw, float* sb, Mid&& mid) {
+  // group gi: four outputs 4 cg .. (cg = gi % 4 NT: output tile t = cg / 4, j = cg % 4) of rows
+  // k .. k + 7 (k = 32 c + 8 kq, kq = (gi / 4 NT) % 4, c = gi / 16 NT).  Consecutive lanes take
+  // consecutive 16-byte pieces of a row, so a wave's load covers whole rows of the filter block.
+  const int groups = NT * nkc * 16;
+  bool ran = false;
+  for (int g0 = int(threadIdx.x); g0 < groups || !ran; g0 += kFiltBatch * kCvThreads) {
+    f32x4 r[kFiltBatch][8];
+#pragma unroll
+    for (int u = 0; u < kFiltBatch; ++u) {
+      const int gi = g0 + u * kCvThreads;
+      const int cg = gi % (4 * NT), rest = gi / (4 * NT);
+      const int t = cg >> 2, j = cg & 3, kq = rest & 3, c = rest >> 2;
+      const int o = o0 + 16 * t + 4 * j;
+      const int k = c * 32 + kq * 8;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const bool ok = gi < groups && o < a.cout && k + i < a.K;
+        const int64_t off = ok ? int64_t(k + i) * a.cout + o : 0;
+        r[u][i] = *reinterpret_cast<const f32x4*>(a.w + off);
+        if (!ok) r[u][i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      }
+    }
+    if (!ran) {
+      mid();
+      ran = true;
+    }
+#pragma unroll
+    for (int u = 0; u < kFiltBatch; ++u) {
+      const int gi = g0 + u * kCvThreads;
+      if (gi < groups) {
+        const int cg = gi % (4 * NT), rest = gi / (4 * NT);
+        const int t = cg >> 2, j = cg & 3, kq = rest & 3, c = rest >> 2;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          half8 h;
+#pragma unroll
+          for (int i = 0; i < 8; ++i) h[i] = half_t(r[u][i][e]);
+          sw[(t * nkc + c) * 64 + kq * 16 + 4 * j + e] = __builtin_bit_cast(f32x4, h);
+        }
+      }
+    }
+  }
+  for (int i = threadIdx.x; i < 16 * NT; i += kCvThreads)
+    sb[i] = (a.bias != nullptr && o0 + i < a.cout) ? a.bias[o0 + i] : 0.0f;
+}
+
+template <int NT>
+__global__ __launch_bounds__(kCvThreads, 1) void conv_tile_kernel(TileArgs ta) {
+  const ConvArgs& a = ta.c;
+  extern __shared__ f32x4 cv_smem[];
+  const int nkc = a.K / 32;
+  uint8_t* win = reinterpret_cast<uint8_t*>(cv_smem);
+  f32x4* sw = reinterpret_cast<f32x4*>(win + ta.win_bytes);
+  float* sb = reinterpret_cast<float*>(sw + NT * nkc * 64);
+  const int lane = threadIdx.x & 63;
+  const int q = lane >> 4, n = lane & 15;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int o0 = (blockIdx.x % a.n_ob) * a.ob;
+  const int64_t tstride = gridDim.x / a.n_ob;
+  const int cq = a.cin / 4;  // 16-byte groups of 4 channels per pixel
+  const int groups = ta.win_h * ta.win_w * cq;
+
+  // one window batch: groups [base, base + kWinBatch kCvThreads) of `tile`, fp32 in registers
+  f32x4 raw[kWinBatch];
+  int dst[kWinBatch];
+  auto load_batch = [&](int64_t tile, int base) {
+    const int th = int(tile / ta.tiles_w), tw = int(tile % ta.tiles_w);
+    const int h0 = th * kTileH, w0 = tw * kTileW;
+#pragma unroll
+    for (int i = 0; i < kWinBatch; ++i) {
+      const int gi = base + i * kCvThreads + int(threadIdx.x);
+      const int pix = gi / cq, g4 = gi - pix * cq;
+      const int r = pix / ta.win_w, cc = pix - r * ta.win_w;
+      const int ih = h0 + r - a.ph, iw = w0 + cc - a.pw;
+      const bool in = gi < groups && ih >= 0 && ih < a.H && iw >= 0 && iw < a.W;
+      const int64_t off = in ? (int64_t(ih) * a.W + iw) * a.cin + 4 * g4 : 0;
+      raw[i] = *reinterpret_cast<const f32x4*>(a.x + off);
+      if (!in) raw[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      dst[i] = gi < groups ? pix * ta.ps + 8 * g4 : -1;
+    }
+  };
+  auto commit_batch = [&]() {
+#pragma unroll
+    for (int i = 0; i < kWinBatch; ++i) {
+      if (dst[i] >= 0) {
+        half4 hv;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) hv[j] = half_t(raw[i][j]);
+        *reinterpret_cast<half4*>(win + dst[i]) = hv;
+      }
+    }
+  };
+
+  int64_t tile = blockIdx.x / a.n_ob;
+  // the filter's first round of loads, then the first window's (or its first batch), then the conversions
+  cv_stage_filter<NT>(a, o0, nkc, sw, sb, [&]() {
+    if (tile < ta.tiles) load_batch(tile, 0);
+  });
+  for (; tile < ta.tiles; tile += tstride) {
+    const int th = int(tile / ta.tiles_w), tw = int(tile % ta.tiles_w);
+    const int h0 = th * kTileH, w0 = tw * kTileW;
+    // this tile's window into LDS: the batch in flight, and any further batches now
+    commit_batch();
+    for (int base = kWinBatch * kCvThreads; base < groups; base += kWinBatch * kCvThreads) {
+      load_batch(tile, base);
+      commit_batch();
+    }
+    __syncthreads();
+    // the next tile's window loads run under this tile's MFMAs
+    const int64_t next = tile + tstride;
+    if (next < ta.tiles) load_batch(next, 0);  // (its first batch, when the window needs more than one)
+    f32x4 acc[kTileNB][NT];
+    {
+      const f32x4* sb4 = reinterpret_cast<const f32x4*>(sb);
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        const f32x4 b = sb4[t * 4 + q];
+#pragma unroll
+        for (int j = 0; j < kTileNB; ++j) acc[j][t] = b;
+      }
+    }
+    // lane (q, n) of N block j reads window pixel (2 wave + j / 2 + kh, 16 (j % 2) + n + kw),
+    // channels 32 kc + 8 q .. + 7.  Two register sets alternate: chunk c + 1's
+    // fragments are read into one while chunk c's MFMAs run on the other; a
+    // scheduling barrier keeps the reads ahead of those MFMAs.
+    const uint8_t* wrow = win + (2 * wave * ta.win_w + n) * ta.ps + 16 * q;
+    const int jstride = ta.win_w * ta.ps;
+    const int kcs = a.cin / 32;
+    int kc = 0, kw = 0;
+    int off = 0;  // window byte offset of the chunk read next: (kh win_w + kw) ps + 64 kc
+    auto advance = [&]() {  // channels first, then taps along the row, then rows
+      if (++kc == kcs) {
+        kc = 0;
+        if (++kw == a.kw) {
+          kw = 0;
+          off += (ta.win_w - a.kw + 1) * ta.ps - 64 * (kcs - 1);
+        } else {
+          off += ta.ps - 64 * (kcs - 1);
+        }
+      } else {
+        off += 64;
+      }
+    };
+    auto frags = [&](int c, half8 (&xb)[kTileNB], half8 (&wb)[NT]) {
+      const int o = c < nkc ? off : 0;  // past the last chunk: re-read chunk 0 (in bounds, unused)
+      const int cc = c < nkc ? c : 0;
+#pragma unroll
+      for (int j = 0; j < kTileNB; ++j)
+        xb[j] = *reinterpret_cast<const half8*>(wrow + o + (j >> 1) * jstride + (j & 1) * 16 * ta.ps);
+#pragma unroll
+      for (int t = 0; t < NT; ++t) wb[t] = __builtin_bit_cast(half8, sw[(t * nkc + cc) * 64 + lane]);
+      advance();
+    };
+    auto mma = [&](const half8 (&xb)[kTileNB], const half8 (&wb)[NT]) {
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int j = 0; j < kTileNB; ++j)
+          acc[j][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wb[t], xb[j], acc[j][t], 0, 0, 0);
+    };
+    half8 xa[kTileNB], wa[NT], xb2[kTileNB], wb2[NT];
+    frags(0, xa, wa);
+    for (int c = 0; c < nkc; c += 2) {
+      frags(c + 1, xb2, wb2);
+      __builtin_amdgcn_sched_barrier(0);
+      mma(xa, wa);
+      if (c + 1 < nkc) {
+        frags(c + 2, xa, wa);
+        __builtin_amdgcn_sched_barrier(0);
+        mma(xb2, wb2);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < kTileNB; ++j) {
+      const int oh = h0 + 2 * wave + (j >> 1), ow = w0 + 16 * (j & 1) + n;
+      if (oh < a.H && ow < a.W) {
+        float* yr = a.y + (int64_t(oh) * a.W + ow) * a.cout;
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+          const int col = o0 + 16 * t + 4 * q;
+          if (col < a.cout) {
+            f32x4 v = acc[j][t];
+            if (a.relu) {
+#pragma unroll
+              for (int e = 0; e < 4; ++e) v[e] = fmaxf(v[e], 0.0f);
+            }
+            *reinterpret_cast<f32x4*>(yr + col) = v;
+          }
+        }
+      }
+    }
+    __syncthreads();  // every wave is done with this window
+  }
+}
+
 template <bool F16, int NT, bool VEC>
 const void* cv_fn() {
   return reinterpret_cast<const void*>(&conv_op_kernel<F16, NT, VEC>);
@@ -418,6 +648,39 @@ int launch_conv2d(const rdv_conv2d_desc& d, const float* x, const float* w, cons
   a.ob = ob;
   a.n_ob = (d.cout + ob - 1) / ob;
   a.w_rows = d.w_layout == RDV_WLAYOUT_RSCK && d.cout % 4 == 0 && reinterpret_cast<uintptr_t>(w) % 16 == 0 ? 1 : 0;
+  // spatial tiles: fp16, whole 32-channel chunks per tap, an RSCK filter of
+  // 16-byte rows, one output block, and the haloed window plus the filter block in LDS
+  if (f16 && vec && a.w_rows && d.cin % 32 == 0 && d.cout % 16 == 0 && passes == 1 && a.n_ob == 1) {
+    TileArgs ta;
+    ta.c = a;
+    ta.c.kp = K;
+    ta.win_w = kTileW + d.kw - 1;
+    ta.win_h = kTileH + d.kh - 1;
+    ta.ps = 2 * d.cin + 16;
+    ta.win_bytes = (ta.win_w * ta.win_h * ta.ps + 15) / 16 * 16;
+    const size_t tlds = size_t(ta.win_bytes) + size_t(ob / 16) * (K / 32) * 64 * sizeof(f32x4) + size_t(ob) * sizeof(float);
+    if (tlds <= size_t(156) * 1024) {
+      ta.tiles_w = (d.W + kTileW - 1) / kTileW;
+      const int64_t tiles = int64_t((d.H + kTileH - 1) / kTileH) * ta.tiles_w;
+      if (tiles > 0x7fffffff) return fail(RDV_ERR_UNSUPPORTED, "grid too large");
+      ta.tiles = int(tiles);
+      const int ti = ob / 16 - 1;  // the kernel's NT is the exact tile count
+      static const void* const tfns[8] = {
+          reinterpret_cast<const void*>(&conv_tile_kernel<1>), reinterpret_cast<const void*>(&conv_tile_kernel<2>),
+          reinterpret_cast<const void*>(&conv_tile_kernel<3>), reinterpret_cast<const void*>(&conv_tile_kernel<4>),
+          reinterpret_cast<const void*>(&conv_tile_kernel<5>), reinterpret_cast<const void*>(&conv_tile_kernel<6>),
+          reinterpret_cast<const void*>(&conv_tile_kernel<7>), reinterpret_cast<const void*>(&conv_tile_kernel<8>)};
+      static bool tattr[8] = {};
+      if (!tattr[ti]) {
+        RDV_HIP_TRY(hipFuncSetAttribute(tfns[ti], hipFuncAttributeMaxDynamicSharedMemorySize, 156 * 1024));
+        tattr[ti] = true;
+      }
+      const int64_t grid = std::min<int64_t>(tiles, dev.cu_count);
+      void* tparams[] = {&ta};
+      RDV_HIP_TRY(hipLaunchKernel(tfns[ti], dim3(static_cast<unsigned>(grid)), dim3(kCvThreads), tparams, tlds, stream));
+      return RDV_OK;
+    }
+  }
   const int64_t rows_per_task = int64_t(kCvWaves) * 16 * kCvRT;
   a.tasks = (rows + rows_per_task - 1) / rows_per_task;
   const int nt = ob / 16;

@@ -298,6 +298,9 @@ def _check_conv(got, x, w, b, H, W, f16, what):
     (rdv.Conv2DTensorOpSimple, True, (8, 8, 16, 160, 3, 1)),      # two output blocks
     (rdv.Conv2DTensorOpSimple3x3, True, (32, 16, 32, 64, 3, 3)),
     (rdv.Conv2DTensorOpWindow3x3, True, (24, 16, 64, 32, 3, 3)),
+    (rdv.Conv2DTensorOpFast, True, (36, 72, 32, 48, 3, 3)),       # spatial tiles, a ragged column tile
+    (rdv.Conv2DTensorOpSimple, True, (20, 136, 96, 32, 3, 3)),    # three 32-channel chunks per tap
+    (rdv.Conv2DTensorOpFast, True, (19, 96, 32, 32, 5, 5)),       # 5 x 5 window, a ragged row tile
 ])
 def test_direct_conv_variants_match_oracle(cls, f16, shape):
     H, W, C, K, KH, KW = shape
