@@ -20,19 +20,22 @@ BUILD_DIR = os.path.join(PKG_DIR, "_build")
 LIB_NAME = "librdv_hip.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
 
+# Longest compiles first: the pool starts them in this order.
 SOURCES = [
+    "mlp_generic8.hip",
+    "mlp_generic8g.hip",
+    "render.hip",
+    "volume_profile.hip",
+    "mlp_generic.hip",
+    "train.hip",
+    "winograd.hip",
+    "conv_op.hip",
+    "mlp_fused.hip",
+    "linear_op.hip",
     "capi.cpp",
     "mlp_pack.hip",
     "mlp_f32.hip",
-    "mlp_fused.hip",
-    "mlp_generic.hip",
-    "winograd.hip",
-    "render.hip",
-    "volume_profile.hip",
-    "train.hip",
-    "linear_op.hip",
     "tensor_data.hip",
-    "conv_op.hip",
 ]
 
 ARCH = os.environ.get("RDV_OFFLOAD_ARCH", "gfx950")

@@ -155,6 +155,12 @@ __device__ __forceinline__ void gen_init(f32x16 (&acc)[M], const float* bias, bo
   }
 }
 
+// Shape of one hidden or last layer, read once at the layer's start.
+struct GenLayerShape {
+  int kc, frag, bias, act;  // as GenNet's entries of the layer
+  bool last;                // the chain's last layer
+};
+
 // Per-layer context of gen_chain.
 struct GenCtx {
   const float* bias;  // the chain's biases (LDS or global)
@@ -171,48 +177,88 @@ __device__ __forceinline__ void gen_finish(const f32x16 (&acc)[M], half8 (&b)[2 
   else gen_handoff<MT, M>(acc, b, act, h);
 }
 
-// Layer 0 with M tiles: K chunks one at a time, B fragment from l0(c).
-template <int MT, int M, class W, class L0, class Sink>
+// No-op hook of gen_chain.
+struct GenNoHook {
+  __device__ __forceinline__ void operator()() const {}
+};
+
+// Layer 0 with M tiles, B fragment of K chunk c from l0(c).  KC0 == 0: a
+// run-time loop over the chunks, one at a time.  KC0 > 0 (the chain has at most
+// KC0 chunks in layer 0): the loop is unrolled, so l0 may index registers by c,
+// and the A fragments are double-buffered as in gen_layer.  after0() runs after
+// the layer's MFMAs are issued, before its hand-off.
+template <int MT, int M, int KC0, class W, class L0, class Sink, class Hook>
 __device__ __forceinline__ void gen_layer0(const GenNet& g, const GenCtx& x, const W& wf, L0&& l0, half8 (&b)[2 * MT],
-                                           Sink&& sink) {
+                                           Sink&& sink, Hook&& after0) {
   f32x16 acc[M];
   gen_init<M>(acc, x.bias + g.bias[0], x.has_bias, x.h);
   const int kc = g.kc[0], f0 = g.frag[0];
-  for (int c = 0; c < kc; ++c) {
-    half8 A[M];
+  if constexpr (KC0 == 0) {
+    for (int c = 0; c < kc; ++c) {
+      half8 A[M];
 #pragma unroll
-    for (int t = 0; t < M; ++t) A[t] = wf(f0 + t * kc + c);
-    const half8 bc = l0(c);
+      for (int t = 0; t < M; ++t) A[t] = wf(f0 + t * kc + c);
+      const half8 bc = l0(c);
 #pragma unroll
-    for (int t = 0; t < M; ++t) acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[t], bc, acc[t], 0, 0, 0);
+      for (int t = 0; t < M; ++t) acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[t], bc, acc[t], 0, 0, 0);
+    }
+  } else {
+    half8 A[2][M];
+#pragma unroll
+    for (int t = 0; t < M; ++t) A[0][t] = wf(f0 + t * kc);
+#pragma unroll
+    for (int c = 0; c < KC0; ++c) {
+      if (c < kc) {
+        const int cn = c + 1 < kc ? c + 1 : c;
+#pragma unroll
+        for (int t = 0; t < M; ++t) A[(c + 1) & 1][t] = wf(f0 + t * kc + cn);
+        const half8 bc = l0(c);
+#pragma unroll
+        for (int t = 0; t < M; ++t)
+          acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[c & 1][t], bc, acc[t], 0, 0, 0);
+      }
+    }
   }
+  after0();
   gen_finish<MT, M>(acc, b, g.L == 1, g.act[0], x.h, sink);
 }
 
+// K chunks of A fragments a layer with M tiles keeps in flight: eight
+// fragments (32 VGPRs) for every M up to 4, so a narrow layer, whose few MFMAs
+// per chunk cannot cover one LDS read latency, reads several chunks ahead.
+template <int M>
+constexpr int gen_ring() { return M == 1 ? 8 : M == 2 ? 4 : 2; }
+
 // Hidden or last layer l with M tiles and kc = 2 mt[l - 1] K chunks from b: A
-// fragments double-buffered in registers, chunk c + 1's reads issued before
-// chunk c's MFMAs (the last chunk re-reads a valid fragment, no branch).
+// fragments in a register ring of R = gen_ring<M>() chunks, chunk c + R - 1's
+// reads issued before chunk c's MFMAs.  Reads past the last chunk re-read it
+// (a valid fragment, no branch), so every path issues the same reads.
 template <int MT, int M, class W, class Sink>
-__device__ __forceinline__ void gen_layer(const GenNet& g, const GenCtx& x, const W& wf, int l, half8 (&b)[2 * MT],
+__device__ __forceinline__ void gen_layer(const GenLayerShape& s, const GenCtx& x, const W& wf, half8 (&b)[2 * MT],
                                           Sink&& sink) {
+  constexpr int R = gen_ring<M>() < 2 * MT ? gen_ring<M>() : 2 * MT;
   f32x16 acc[M];
-  gen_init<M>(acc, x.bias + g.bias[l], x.has_bias, x.h);
-  const int kc = g.kc[l], f0 = g.frag[l];
-  half8 A[2][M];
+  gen_init<M>(acc, x.bias + s.bias, x.has_bias, x.h);
+  const int kc = s.kc, f0 = s.frag;
+  half8 A[R][M];
 #pragma unroll
-  for (int t = 0; t < M; ++t) A[0][t] = wf(f0 + t * kc);
+  for (int p = 0; p + 1 < R; ++p) {
+    const int cp = p < kc ? p : kc - 1;
+#pragma unroll
+    for (int t = 0; t < M; ++t) A[p][t] = wf(f0 + t * kc + cp);
+  }
 #pragma unroll
   for (int c = 0; c < 2 * MT; ++c) {
     if (c < kc) {
-      const int cn = c + 1 < kc ? c + 1 : c;
+      const int cn = c + R - 1 < kc ? c + R - 1 : kc - 1;
 #pragma unroll
-      for (int t = 0; t < M; ++t) A[(c + 1) & 1][t] = wf(f0 + t * kc + cn);
+      for (int t = 0; t < M; ++t) A[(c + R - 1) % R][t] = wf(f0 + t * kc + cn);
 #pragma unroll
       for (int t = 0; t < M; ++t)
-        acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[c & 1][t], b[c], acc[t], 0, 0, 0);
+        acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[c % R][t], b[c], acc[t], 0, 0, 0);
     }
   }
-  gen_finish<MT, M>(acc, b, l == g.L - 1, g.act[l], x.h, sink);
+  gen_finish<MT, M>(acc, b, s.last, s.act, x.h, sink);
 }
 
 #define RDV_GEN_SWITCH(mt, CALL)                                     \
@@ -231,16 +277,23 @@ __device__ __forceinline__ void gen_layer(const GenNet& g, const GenCtx& x, cons
 // of layer 0's K chunk c; wf(f) returns A fragment f (this lane's 16 bytes).
 // The last layer's accumulators (f32x16[mt], before its activation) go to
 // sink(acc); the register arrays between layers are only the 2 MT fragments.
-template <int MT, class W, class L0, class Sink>
-__device__ __forceinline__ void gen_chain(const GenNet& g, const GenCtx& x, const W& wf, L0&& l0, Sink&& sink) {
+// KC0 and after0: as in gen_layer0.
+template <int MT, int KC0 = 0, class W, class L0, class Sink, class Hook = GenNoHook>
+__device__ __forceinline__ void gen_chain(const GenNet& g, const GenCtx& x, const W& wf, L0&& l0, Sink&& sink,
+                                          Hook&& after0 = Hook{}) {
   half8 b[2 * MT];
-#define RDV_GEN_L0(M) gen_layer0<MT, M>(g, x, wf, l0, b, sink)
+#define RDV_GEN_L0(M) gen_layer0<MT, M, KC0>(g, x, wf, l0, b, sink, after0)
   RDV_GEN_SWITCH(g.mt[0], RDV_GEN_L0)
 #undef RDV_GEN_L0
 #pragma nounroll
   for (int l = 1; l < g.L; ++l) {
-#define RDV_GEN_LH(M) gen_layer<MT, M>(g, x, wf, l, b, sink)
-    RDV_GEN_SWITCH(g.mt[l], RDV_GEN_LH)
+    const GenLayerShape s{g.kc[l], g.frag[l], g.bias[l], g.act[l], l == g.L - 1};
+    const int mt = g.mt[l];
+    // The layer's shape is in SGPRs before its first LDS read: the wait for
+    // these scalar loads would otherwise also wait for the bias reads.
+    asm volatile("" ::"s"(s.kc), "s"(s.frag), "s"(s.bias), "s"(s.act), "s"(mt));
+#define RDV_GEN_LH(M) gen_layer<MT, M>(s, x, wf, b, sink)
+    RDV_GEN_SWITCH(mt, RDV_GEN_LH)
 #undef RDV_GEN_LH
   }
 }
