@@ -138,6 +138,10 @@ def test_golden_vectors(path):
     ([3, 256, 256, 4], True, 3000, "mlp_generic_f16<8,global>"),      # fragments beyond the LDS cap
     ([256, 32, 1], True, 500, "mlp_generic_f16<1,lds>"),              # 16 K chunks in layer 0
     ([8] + [32] * 15 + [2], True, 2048, "mlp_generic_f16<1,lds>"),    # 16 layers
+    # raw 16-byte rows of at most 64 features: layer 0's input is loaded a tile ahead
+    ([36, 96, 48, 8], True, 1000, "mlp_generic_f16<4,lds>"),          # 3 K chunks, pieces past D are zeros
+    ([12, 40, 3], True, 4115, "mlp_generic_f16<2,lds>"),              # 1 K chunk, partial last tile
+    ([20, 64, 64, 4], True, 33, "mlp_generic_f16<2,lds>"),            # fewer tiles than waves
 ])
 def test_generic_chains(dims, f16, n, kernel):
     g = WL.gen(5)
