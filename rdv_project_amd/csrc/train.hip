@@ -1040,38 +1040,38 @@ __global__ void train_reduce2_kernel(ReduceJobs J, const float* __restrict__ mid
   J.out[j][i] = acc * scale;
 }
 
-// W^T A fragments of layer li from the fp32 copy: element
-// ((ti * kco + c) * 64 + lane) * 8 + j = W[16c + 8 (lane / 32) + j][32 ti + lane % 32].
-__global__ void train_pack_wt_kernel(const float* __restrict__ w32, int in, int out, half_t* __restrict__ wt) {
-  const int kco = (out + 15) / 16;
-  const int64_t total = int64_t(in / 32) * kco * 64 * 8;
-  const int64_t e = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (e >= total) return;
-  const int j = int(e & 7);
-  const int lane = int((e >> 3) & 63);
-  const int64_t r = e >> 9;
-  const int c = int(r % kco), ti = int(r / kco);
-  const int o = 16 * c + 8 * (lane >> 5) + j;
-  const int i = 32 * ti + (lane & 31);
-  wt[e] = half_t(o < out ? w32[int64_t(o) * in + i] : 0.0f);
-}
+// Every transposed-weight pack of a step in one launch.  Job k writes the
+// W^T fragments of one layer from its fp32 copy, element
+// ((ti * kc + c) * 64 + lane) * 8 + j = W[o][32 ti + lane % 32] (zero past
+// `out`), kc = ceil(out / 16), with o in the order of the kernel that reads it:
+//   kTrPackWt  (train_pair_kernel):  o = 16 c + 8 (lane / 32) + j;
+//   kTrPackWts (train_pair2_kernel): o = tfl_feature(c, lane / 32, j), the
+//     tile-fragment K order; as an MFMA operand: rows (A) or columns (B)
+//     32 ti .. of W^T, K = W's output features, chunk c.
+enum { kTrPackWt = 0, kTrPackWts = 1 };
+struct TrainPackJobs {
+  const float* w32[RDV_MLP_MAX_LAYERS];
+  half_t* wt[RDV_MLP_MAX_LAYERS];
+  int in[RDV_MLP_MAX_LAYERS], out[RDV_MLP_MAX_LAYERS], kind[RDV_MLP_MAX_LAYERS];
+  int64_t start[RDV_MLP_MAX_LAYERS + 1];  // first element of job k (start[n] = all elements)
+  int n;
+};
 
-// W^T fragments in the tile-fragment K order: element
-// ((ti * kc + c) * 64 + lane) * 8 + j = W[tfl_feature(c, lane / 32, j)][32 ti + lane % 32]
-// (zero past `out`), kc = ceil(out / 16).  As an MFMA operand: rows (A) or
-// columns (B) 32 ti .. of W^T, K = W's output features, chunk c.
-__global__ void train_pack_wts_kernel(const float* __restrict__ w32, int in, int out, half_t* __restrict__ wt) {
+__global__ void train_pack_batch_kernel(TrainPackJobs J) {
+  const int64_t g = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (g >= J.start[J.n]) return;
+  int k = 0;
+  while (g >= J.start[k + 1]) ++k;
+  const int64_t e = g - J.start[k];
+  const int in = J.in[k], out = J.out[k];
   const int kc = (out + 15) / 16;
-  const int64_t total = int64_t(in / 32) * kc * 64 * 8;
-  const int64_t e = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (e >= total) return;
   const int j = int(e & 7);
   const int lane = int((e >> 3) & 63);
   const int64_t r = e >> 9;
   const int c = int(r % kc), ti = int(r / kc);
-  const int o = tfl_feature(c, lane >> 5, j);
+  const int o = J.kind[k] == kTrPackWts ? tfl_feature(c, lane >> 5, j) : 16 * c + 8 * (lane >> 5) + j;
   const int i = 32 * ti + (lane & 31);
-  wt[e] = half_t(o < out ? w32[int64_t(o) * in + i] : 0.0f);
+  J.wt[k][e] = half_t(o < out ? J.w32[k][int64_t(o) * in + i] : 0.0f);
 }
 
 // ------------------------------------------ backward, layer pairs, point-major
@@ -1081,7 +1081,7 @@ __global__ void train_pack_wts_kernel(const float* __restrict__ w32, int in, int
 // the MFMA's M side, so their D registers hold, per lane, one feature over 16
 // points: the layout of a K = points operand.
 //   h_l     [points x m] = h_{l-1} W_{l-1}^T + b  (A: h_{l-1} slots, B: the forward's fragments)
-//   g_{l-1} [points x m] = (g_l W_l) * [h_l > 0]   (A: g_l slots,     B: W_l^T, train_pack_wts)
+//   g_{l-1} [points x m] = (g_l W_l) * [h_l > 0]   (A: g_l slots,     B: W_l^T, kTrPackWts order)
 //   dW_l    [o x m]      += g_l^T h_l               (A: g_l^T,         B: h_l)
 //   dW_{l-1}[m x i]      += g_{l-1}^T h_{l-1}       (A: g_{l-1},       B: h_{l-1}^T)
 //   g_{l-2}^T [i x points] = W_{l-1}^T g_{l-1}^T, masked by h_{l-1} > 0, stored as slots
@@ -1099,8 +1099,8 @@ struct TrainPair2Args {
   const half_t* hin;   // h_{l-1}, tile-fragment layout of width 128
   const half_t* wf;    // layer l-1 forward A fragments (packed layout)
   const float* bias;   // layer l-1 padded bias [128]
-  const half_t* wls;   // W_l^T, train_pack_wts(W_l, 128, OUT)
-  const half_t* wl1s;  // W_{l-1}^T, train_pack_wts(W_{l-1}, 128, 128)
+  const half_t* wls;   // W_l^T in the kTrPackWts order (in 128, out OUT)
+  const half_t* wl1s;  // W_{l-1}^T in the kTrPackWts order (128 x 128)
   half_t* gout;        // g_{l-2}, tile-fragment layout of width 128
   float* dw_l;         // [gridDim.x][OUT][128]
   float* db_l;         // [gridDim.x][OUT]
@@ -1666,38 +1666,48 @@ int launch_train_step(const rdv_mlp_desc& d, const MlpLayout& lay, const void* p
   if (rc != RDV_OK) return rc;
   // backward: layer pairs from the head down, then layer 0 alone if L is odd;
   // gradients ping-pong between dz_off[0] and dz_off[1]
-  auto pack_wt = [&](int l) -> half_t* {
-    const int in = d.dims[l], out = d.dims[l + 1];
-    half_t* wt = reinterpret_cast<half_t*>(ws + p.wt_off[l]);
-    const int64_t total = int64_t(in / 32) * ((out + 15) / 16) * 64 * 8;
-    if (total > 0) {
-      train_pack_wt_kernel<<<dim3(unsigned((total + 255) / 256)), dim3(256), 0, stream>>>(
-          reinterpret_cast<const float*>(pk + lay.w32_off[l]), in, out, wt);
+  // The pair kernels' transposed weights, every layer >= 1 in the order its
+  // pair kernel reads, packed in one launch before the first of them.
+  auto use_pair2 = [&](int l) {
+    return l - 1 >= 1 && d.dims[l - 1] == 128 && d.dims[l] == 128 && (d.dims[l + 1] == 128 || d.dims[l + 1] == 16);
+  };
+  auto wt_of = [&](int l) { return reinterpret_cast<half_t*>(ws + p.wt_off[l]); };
+  {
+    TrainPackJobs pj;
+    pj.n = 0;
+    pj.start[0] = 0;
+    auto add = [&](int l, int kind) {
+      const int k = pj.n++;
+      pj.w32[k] = reinterpret_cast<const float*>(pk + lay.w32_off[l]);
+      pj.wt[k] = wt_of(l);
+      pj.in[k] = d.dims[l];
+      pj.out[k] = d.dims[l + 1];
+      pj.kind[k] = kind;
+      pj.start[k + 1] = pj.start[k] + int64_t(d.dims[l] / 32) * ((d.dims[l + 1] + 15) / 16) * 64 * 8;
+    };
+    for (int l = L - 1; l >= 1; l -= 2) {
+      const int kind = use_pair2(l) ? kTrPackWts : kTrPackWt;
+      add(l, kind);
+      if (l - 1 >= 1) add(l - 1, kind);
     }
-    return wt;
-  };
-  auto pack_wts = [&](int l, half_t* wt) {
-    const int in = d.dims[l], out = d.dims[l + 1];
-    const int64_t total = int64_t(in / 32) * ((out + 15) / 16) * 64 * 8;
-    train_pack_wts_kernel<<<dim3(unsigned((total + 255) / 256)), dim3(256), 0, stream>>>(
-        reinterpret_cast<const float*>(pk + lay.w32_off[l]), in, out, wt);
-    return wt;
-  };
+    if (pj.n > 0 && pj.start[pj.n] > 0) {
+      train_pack_batch_kernel<<<dim3(unsigned((pj.start[pj.n] + 255) / 256)), dim3(256), 0, stream>>>(pj);
+      RDV_HIP_TRY(hipGetLastError());
+    }
+  }
   const half_t* gsrc = reinterpret_cast<const half_t*>(ws + p.g_off);
   int dst = 0;
   int l = L - 1;
   for (; l >= 1; l -= 2) {
-    if (l - 1 >= 1 && d.dims[l - 1] == 128 && d.dims[l] == 128 && (d.dims[l + 1] == 128 || d.dims[l + 1] == 16)) {
+    if (use_pair2(l)) {
       // point-major pair kernel
       TrainPair2Args pa;
       pa.g = gsrc;
       pa.hin = reinterpret_cast<const half_t*>(ws + p.h_off[l - 1]);
       pa.wf = reinterpret_cast<const half_t*>(pk + lay.frag_off[l - 1]);
       pa.bias = reinterpret_cast<const float*>(pk + lay.bias_off[l - 1]);
-      pa.wls = pack_wts(l, reinterpret_cast<half_t*>(ws + p.wt_off[l]));
-      RDV_HIP_TRY(hipGetLastError());
-      pa.wl1s = pack_wts(l - 1, reinterpret_cast<half_t*>(ws + p.wt_off[l - 1]));
-      RDV_HIP_TRY(hipGetLastError());
+      pa.wls = wt_of(l);
+      pa.wl1s = wt_of(l - 1);
       pa.gout = reinterpret_cast<half_t*>(ws + p.dz_off[dst]);
       pa.dw_l = reinterpret_cast<float*>(ws + p.dw_off[l]);
       pa.db_l = reinterpret_cast<float*>(ws + p.db_off[l]);
@@ -1734,10 +1744,8 @@ int launch_train_step(const rdv_mlp_desc& d, const MlpLayout& lay, const void* p
     pa.hin = l - 1 == 0 ? static_cast<const half_t*>(x) : reinterpret_cast<const half_t*>(ws + p.h_off[l - 1]);
     pa.wf = reinterpret_cast<const half_t*>(pk + lay.frag_off[l - 1]);
     pa.bias = reinterpret_cast<const float*>(pk + lay.bias_off[l - 1]);
-    pa.wtl = pack_wt(l);
-    RDV_HIP_TRY(hipGetLastError());
-    pa.wtl1 = l - 1 > 0 ? pack_wt(l - 1) : nullptr;
-    RDV_HIP_TRY(hipGetLastError());
+    pa.wtl = wt_of(l);
+    pa.wtl1 = l - 1 > 0 ? wt_of(l - 1) : nullptr;
     pa.gout = l - 1 > 0 ? reinterpret_cast<half_t*>(ws + p.dz_off[dst]) : nullptr;
     pa.dw_l = reinterpret_cast<float*>(ws + p.dw_off[l]);
     pa.db_l = reinterpret_cast<float*>(ws + p.db_off[l]);
