@@ -115,6 +115,17 @@ __device__ __forceinline__ float wave_scan_incl(float v, int /*lane*/) {
   v += dpp_move<0x143, 0xC>(v);  // row_bcast:31 into rows 2, 3
   return v;
 }
+// Inclusive prefix sums over each 32-lane half of a wave separately: the
+// first five steps of wave_scan_incl (lanes 0..31 get the same bits as from
+// it, lanes 32..63 the same scan of their own half).
+__device__ __forceinline__ float wave_scan_incl32(float v) {
+  v += dpp_move<0x111, 0xF>(v);  // row_shr:1
+  v += dpp_move<0x112, 0xF>(v);  // row_shr:2
+  v += dpp_move<0x114, 0xF>(v);  // row_shr:4
+  v += dpp_move<0x118, 0xF>(v);  // row_shr:8
+  v += dpp_move<0x142, 0xA>(v);  // row_bcast:15 into rows 1, 3
+  return v;
+}
 // Sum over the wave, returned in every lane.
 __device__ __forceinline__ float wave_sum(float v) {
   const float incl = wave_scan_incl(v, 0);
@@ -252,6 +263,44 @@ __global__ __launch_bounds__(kEaThreads, 1) void render_ea_kernel(RenderArgs a) 
         cb += wgt * fast_sigmoid(f[3]);
         Tin = wave_uniform(Tin * __expf(-total));
       };
+      // The two chunks of a pair in one pass: chunk b's rows 0..3 move from
+      // lanes 0..31 to lanes 32..63 (ds_bpermute: lane l reads lane l % 32),
+      // each lane half scans its own 32 samples, and chunk b starts from chunk
+      // a's transmittance.  Every sample's weight and colour are computed as by
+      // composite(a) then composite(b), in half the instructions; only the
+      // final sum over the lanes adds the per-lane colours in another order.
+      // The four moves are issued from inline assembly and waited for there:
+      // this compiler folded the four ds_bpermute builtins of one MFMA result
+      // into one (and its v_permlane32_swap builtin does not model the write
+      // to its second register).
+      auto composite_pair = [&](const f32x16& fa, const f32x16& fb) {
+        float b0, b1, b2, b3;
+        const int src = col << 2;
+        // fb comes straight from an MFMA: 24 wait states before an LDS
+        // instruction reads it (the compiler pads only its own instructions).
+        asm volatile(
+            "s_nop 7\n"
+            "s_nop 7\n"
+            "s_nop 7\n"
+            "ds_bpermute_b32 %0, %4, %5\n"
+            "ds_bpermute_b32 %1, %4, %6\n"
+            "ds_bpermute_b32 %2, %4, %7\n"
+            "ds_bpermute_b32 %3, %4, %8\n"
+            "s_waitcnt lgkmcnt(0)"
+            : "=&v"(b0), "=&v"(b1), "=&v"(b2), "=&v"(b3)
+            : "v"(src), "v"(fb[0]), "v"(fb[1]), "v"(fb[2]), "v"(fb[3]));
+        const float f[4] = {h == 0 ? fa[0] : b0, h == 0 ? fa[1] : b1, h == 0 ? fa[2] : b2, h == 0 ? fa[3] : b3};
+        const float sigma = fast_softplus(f[0]);
+        const float ad = sigma * dt;
+        const float incl = wave_scan_incl32(ad);
+        const float total_a = lane_value(incl, 31), total_b = lane_value(incl, 63);
+        const float tin_b = wave_uniform(Tin * __expf(-total_a));
+        const float wgt = (h == 0 ? Tin : tin_b) * __expf(-(incl - ad)) * (1.0f - __expf(-ad));
+        cr += wgt * fast_sigmoid(f[1]);
+        cg += wgt * fast_sigmoid(f[2]);
+        cb += wgt * fast_sigmoid(f[3]);
+        Tin = wave_uniform(tin_b * __expf(-total_b));
+      };
       for (int c = 0; c + 1 < chunks; c += 2) {
         const float ta = t0 + (float(32 * c + col) + 0.5f) * dt;
         const float tb = t0 + (float(32 * c + 32 + col) + 0.5f) * dt;
@@ -263,8 +312,7 @@ __global__ __launch_bounds__(kEaThreads, 1) void render_ea_kernel(RenderArgs a) 
         build_input<N>(pa, h, bA);
         if (has_bias) run_pair<N, 0, true, true>(ws, pb, h, bA, bB, accA, accB, sb + opaque_zero());
         else run_pair<N, 0, true, false>(ws, pb, h, bA, bB, accA, accB, sb);
-        composite(accA[0]);
-        composite(accB[0]);
+        composite_pair(accA[0], accB[0]);
       }
       if (chunks & 1) {
         const int c = chunks - 1;
