@@ -25,7 +25,11 @@ SOURCES = [
     "mlp_generic8.hip",
     "mlp_generic8g.hip",
     "render.hip",
+    "render_field8_march.hip",
+    "render_field8_ratio.hip",
+    "render_field8_ea.hip",
     "volume_profile.hip",
+    "volume_profile8.hip",
     "mlp_generic.hip",
     "train.hip",
     "winograd.hip",

@@ -26,6 +26,15 @@
 // ray order, the colour a per-lane partial sum reduced once per ray.
 #include "volume_common.h"
 
+// RDV_FIELD_PART selects what this translation unit emits: 0 (render.hip
+// itself) everything except the 8-tile instantiations of the runtime-shaped
+// field kernels; 1, 2, 3 (render_field8_{march,ratio,ea}.hip) the 8-tile
+// launcher of one of those kernels.  The 8-tile kernels take most of the
+// compile time, and separate units build in parallel.
+#ifndef RDV_FIELD_PART
+#define RDV_FIELD_PART 0
+#endif
+
 namespace rdv {
 
 struct CameraParams {
@@ -73,6 +82,7 @@ struct JitterSeeds {
   uint32_t seeds[4];  // the dispatch's random seeds
 };
 
+#if RDV_FIELD_PART == 0
 __global__ void camera_rays_kernel(CameraParams c, JitterSeeds js, float* __restrict__ rays) {
   const int64_t total = int64_t(c.n) * c.H * c.W;
   for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < total; i += int64_t(gridDim.x) * blockDim.x) {
@@ -96,6 +106,7 @@ __global__ void camera_rays_kernel(CameraParams c, JitterSeeds js, float* __rest
     }
   }
 }
+#endif
 
 // ------------------------------------------------------------ wave helpers
 // Inclusive prefix sum over the 64 lanes of a wave with DPP lane moves (no LDS
@@ -398,6 +409,7 @@ __global__ __launch_bounds__(256) void composite_kernel(const f32x4* __restrict_
   }
 }
 
+#if RDV_FIELD_PART == 0
 __global__ __launch_bounds__(256) void composite_long_kernel(const f32x4* __restrict__ s,
                                                              const float* __restrict__ dts, int64_t nrays,
                                                              int samples, float* __restrict__ out) {
@@ -431,6 +443,7 @@ __global__ __launch_bounds__(256) void composite_long_kernel(const f32x4* __rest
     }
   }
 }
+#endif
 
 // ------------------------------------------------ raymarching transmittance
 struct TransmittanceArgs {
@@ -849,6 +862,15 @@ __global__ __launch_bounds__(64 * gen_waves<MT>(), 1) void render_ea_generic_ker
 }
 
 // ---------------------------------------------------------- instantiations
+// 8-tile launchers of the runtime-shaped field kernels (RDV_FIELD_PART 1..3).
+int launch_raymarch_generic8(const TransmittanceGenArgs& a, int64_t items, int cu, int64_t lds, bool in_lds,
+                             hipStream_t stream);
+int launch_ratiotracking_generic8(const RatioGenArgs& a, int64_t items, int cu, int64_t lds, bool in_lds,
+                                  hipStream_t stream);
+int launch_render_ea_generic8(const RenderGenArgs& a, int64_t items, int cu, int64_t lds, bool in_lds,
+                              hipStream_t stream);
+
+#if RDV_FIELD_PART == 0
 using RenderNet64x3 = Net<RDV_ENC_NONE, 3, 0, 4, 1, 2, 2, 2, 1>;   // 3->64->64->64->4
 using ExtinctionNet64x3 = Net<RDV_ENC_NONE, 3, 0, 1, 1, 2, 2, 2, 1>;  // 3->64->64->64->1
 
@@ -932,7 +954,8 @@ int launch_render_ea(const rdv_camera_desc& c, const float* poses, const float* 
     RenderGenArgs ga;
     ga.r = a;
     gen_net(d, lay, &ga.net);
-    RDV_GEN_FIELD_DISPATCH(render_ea_generic_kernel, ga, nrays, di.cu_count, ga.net, stream);
+    RDV_GEN_FIELD_DISPATCH(render_ea_generic_kernel, ga, nrays, di.cu_count, ga.net, stream,
+                           launch_render_ea_generic8);
   }
   int64_t blocks = di.cu_count;
   const int64_t need = (nrays + kEaWaves - 1) / kEaWaves;
@@ -982,7 +1005,8 @@ int launch_raymarch_transmittance(const rdv_mlp_desc& d, const MlpLayout& lay, c
     TransmittanceGenArgs ga;
     ga.t = a;
     gen_net(d, lay, &ga.net);
-    RDV_GEN_FIELD_DISPATCH(raymarch_generic_kernel, ga, nrays, di.cu_count, ga.net, stream);
+    RDV_GEN_FIELD_DISPATCH(raymarch_generic_kernel, ga, nrays, di.cu_count, ga.net, stream,
+                           launch_raymarch_generic8);
   }
   int64_t blocks = di.cu_count;
   const int64_t need = (nrays + kRenderWaves - 1) / kRenderWaves;
@@ -1050,7 +1074,8 @@ int launch_ratiotracking(const rdv_mlp_desc& d, const MlpLayout& lay, const void
   ga.packed = static_cast<const uint8_t*>(packed);
   gen_net(d, lay, &ga.net);
   // 32 rays per wave
-  RDV_GEN_FIELD_DISPATCH(ratiotracking_generic_kernel, ga, (nrays + 31) / 32, di.cu_count, ga.net, stream);
+  RDV_GEN_FIELD_DISPATCH(ratiotracking_generic_kernel, ga, (nrays + 31) / 32, di.cu_count, ga.net, stream,
+                         launch_ratiotracking_generic8);
 }
 
 // ------------------------------------------------------------- majorant grid
@@ -1142,5 +1167,13 @@ int launch_majorant_grid(const rdv_majorant_grid_desc& g, const float* fine, flo
   RDV_HIP_TRY(hipGetLastError());
   return RDV_OK;
 }
+
+#elif RDV_FIELD_PART == 1
+RDV_GEN_FIELD_DEFINE8(launch_raymarch_generic8, raymarch_generic_kernel, TransmittanceGenArgs)
+#elif RDV_FIELD_PART == 2
+RDV_GEN_FIELD_DEFINE8(launch_ratiotracking_generic8, ratiotracking_generic_kernel, RatioGenArgs)
+#elif RDV_FIELD_PART == 3
+RDV_GEN_FIELD_DEFINE8(launch_render_ea_generic8, render_ea_generic_kernel, RenderGenArgs)
+#endif  // RDV_FIELD_PART
 
 }  // namespace rdv

@@ -125,7 +125,12 @@ static int launch_gen_field(void (*kernel)(Args), const Args& a, int64_t work_it
   return RDV_OK;
 }
 
-#define RDV_GEN_FIELD_DISPATCH(KERNEL, ARGS, ITEMS, CU, NET, STREAM)                                          \
+// Launch of a runtime-shaped field kernel KERNEL<MT, LDSW> for NET, with the
+// 8-tile instantiations (chains with a layer wider than 128) handed to
+// LAUNCH8, defined by RDV_GEN_FIELD_DEFINE8 in a translation unit of its own:
+// they take most of a source's compile time, and separate units build in
+// parallel.
+#define RDV_GEN_FIELD_DISPATCH(KERNEL, ARGS, ITEMS, CU, NET, STREAM, LAUNCH8)                                 \
   do {                                                                                                       \
     const int64_t lds_ = gen_lds_bytes(NET);                                                                 \
     const bool in_lds_ = lds_ <= kGenFieldLdsCap;                                                            \
@@ -140,10 +145,16 @@ static int launch_gen_field(void (*kernel)(Args), const Args& a, int64_t work_it
         return in_lds_ ? launch_gen_field<decltype(ARGS), 4, true>(&KERNEL<4, true>, ARGS, ITEMS, CU, lds_, STREAM) \
                        : launch_gen_field<decltype(ARGS), 4, false>(&KERNEL<4, false>, ARGS, ITEMS, CU, 0, STREAM); \
       default:                                                                                               \
-        return in_lds_ ? launch_gen_field<decltype(ARGS), 8, true>(&KERNEL<8, true>, ARGS, ITEMS, CU, lds_, STREAM) \
-                       : launch_gen_field<decltype(ARGS), 8, false>(&KERNEL<8, false>, ARGS, ITEMS, CU, 0, STREAM); \
+        return LAUNCH8(ARGS, ITEMS, CU, lds_, in_lds_, STREAM);                                              \
     }                                                                                                        \
   } while (0)
+
+// Definition of the 8-tile launcher LAUNCH8 of KERNEL (arguments ARGS_T).
+#define RDV_GEN_FIELD_DEFINE8(LAUNCH8, KERNEL, ARGS_T)                                                       \
+  int LAUNCH8(const ARGS_T& a, int64_t items, int cu, int64_t lds, bool in_lds, hipStream_t stream) {        \
+    return in_lds ? launch_gen_field<ARGS_T, 8, true>(&KERNEL<8, true>, a, items, cu, lds, stream)           \
+                  : launch_gen_field<ARGS_T, 8, false>(&KERNEL<8, false>, a, items, cu, 0, stream);           \
+  }
 
 // A LinearFast chain from 3 inputs (raw or FREQ-encoded) to `out` outputs?
 static bool is_f16_field(const rdv_mlp_desc& d, int out) {

@@ -3,6 +3,13 @@
 // with the extinction chain on the matrix cores.
 #include "volume_common.h"
 
+// RDV_FIELD_PART: 0 (this file) everything except the 8-tile instantiations
+// of volume_profile_kernel; 1 (volume_profile8.hip) their launcher alone, in a
+// translation unit of its own (they take most of the compile time).
+#ifndef RDV_FIELD_PART
+#define RDV_FIELD_PART 0
+#endif
+
 namespace rdv {
 
 // ------------------------------------------------------------ volume profile
@@ -457,6 +464,10 @@ struct VpFinishArgs {
   float* out;
 };
 
+// 8-tile launcher of volume_profile_kernel (RDV_FIELD_PART 1).
+int launch_volume_profile8(const VpGenArgs& a, int64_t items, int cu, int64_t lds, bool in_lds, hipStream_t stream);
+
+#if RDV_FIELD_PART == 0
 __global__ __launch_bounds__(256) void volume_profile_finish_kernel(VpFinishArgs f) {
 #pragma clang fp contract(off)
   const int outw = 4 + 3 * f.sd + f.ds;
@@ -514,7 +525,8 @@ int launch_volume_profile(const rdv_mlp_desc& d, const MlpLayout& lay, const voi
   ga.packed = static_cast<const uint8_t*>(packed);
   gen_net(d, lay, &ga.net);
   // 32 rays per wave
-  RDV_GEN_FIELD_DISPATCH(volume_profile_kernel, ga, (nrays + 31) / 32, di.cu_count, ga.net, stream);
+  RDV_GEN_FIELD_DISPATCH(volume_profile_kernel, ga, (nrays + 31) / 32, di.cu_count, ga.net, stream,
+                         launch_volume_profile8);
 }
 
 int launch_volume_profile_finish(const rdv_volume_profile_desc& vp, const float* albedo, int64_t albedo_stride,
@@ -528,5 +540,9 @@ int launch_volume_profile_finish(const rdv_volume_profile_desc& vp, const float*
   RDV_HIP_TRY(hipGetLastError());
   return RDV_OK;
 }
+
+#else
+RDV_GEN_FIELD_DEFINE8(launch_volume_profile8, volume_profile_kernel, VpGenArgs)
+#endif  // RDV_FIELD_PART
 
 }  // namespace rdv

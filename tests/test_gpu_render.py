@@ -173,7 +173,8 @@ def test_emission_absorption_runtime_shaped_fields(dims):
 
 
 @pytest.mark.parametrize("dims,head", [([3, 32, 32, 1], "softplus"), ([3, 128, 128, 1], "relu"),
-                                       ([3, 64, 96, 64, 1], "softplus")])
+                                       ([3, 64, 96, 64, 1], "softplus"),
+                                       ([3, 160, 1], "softplus")])  # 5 M tiles: the 8-tile kernel
 def test_raymarching_transmittance_runtime_shaped_extinction(dims, head):
     """Any LinearFast Map[3, 1] as the extinction, as the reference marches any
     extinction map it is given."""

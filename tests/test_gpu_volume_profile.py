@@ -147,7 +147,8 @@ def test_constant_extinction_matches_oracle(g, es, sd):
     _check(out, ws, ref, n, len(thr), sd, es, 1e-5, 1e-6, 1.0, True, "constant extinction")
 
 
-@pytest.mark.parametrize("dims,res,ds", [([3, 64, 64, 64, 1], 4, 3.0), ([3, 32, 32, 1], 2, 1.5)])
+@pytest.mark.parametrize("dims,res,ds", [([3, 64, 64, 64, 1], 4, 3.0), ([3, 32, 32, 1], 2, 1.5),
+                                         ([3, 160, 1], 2, 1.5)])  # 5 M tiles: the 8-tile kernel
 def test_mlp_extinction_matches_oracle(dims, res, ds):
     layers = _rand_field(dims, seed=sum(dims) + res)
     ext = _field(layers, head="softplus")

@@ -126,7 +126,8 @@ def _agree(T, ref, what):
 
 
 @pytest.mark.parametrize("dims,res,ds", [([3, 64, 64, 64, 1], 4, 3.0), ([3, 32, 32, 1], 1, 1.0),
-                                         ([3, 128, 1], 8, 6.0)])
+                                         ([3, 128, 1], 8, 6.0),
+                                         ([3, 160, 1], 4, 3.0)])  # 5 M tiles: the 8-tile kernel
 def test_ratiotracking_matches_oracle(dims, res, ds):
     layers = _rand_field(dims, seed=dims[1] + res)
     ext = _field(layers, head="softplus")
