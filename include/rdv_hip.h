@@ -462,6 +462,22 @@ int rdv_volume_profile(const rdv_mlp_desc* extinction, const void* packed, const
                        const float* majorant, const float* rays, int64_t n_rays, float* out, float* sample_pos,
                        float* env_dirs, float* env_weights, int32_t* valid, void* stream);
 
+/* VolumeProfileDDA, first stage: as rdv_volume_profile, except the tau and
+ * depth marches.  Those do not trim the ray's ends.  Instead they walk
+ * majorant_grid (device [grid_depth, grid_height, grid_width] fp32 over the
+ * box, e.g. rdv_majorant_grid's output) cell by cell with an Amanatides-Woo
+ * DDA from the entry cell: at most 4096 cells, until tMax or off the grid.
+ * In a cell whose value is > 0 the march samples t, t + step, ... while t is
+ * below the cell's exit, then t jumps to the exit; cells whose value is not
+ * > 0 are skipped whole.  `majorant` (the VoxelMajorantField's grid) still
+ * serves the environment rays' ratio tracking.  Grid dimensions 1..4096.
+ * Replaces VolumeProfileDDA's shader (src/rdv/domain/volumes.py:560-603,
+ * shaders/volumes/volume_profile_dda.h:1-208). */
+int rdv_volume_profile_dda(const rdv_mlp_desc* extinction, const void* packed, const rdv_volume_profile_desc* vp,
+                           const float* majorant, const float* majorant_grid, int32_t grid_width,
+                           int32_t grid_height, int32_t grid_depth, const float* rays, int64_t n_rays, float* out,
+                           float* sample_pos, float* env_dirs, float* env_weights, int32_t* valid, void* stream);
+
 /* VolumeProfile, second stage, for rows with valid[i] = 1: the environment
  * feature out[i, DS+2+c] = sum over s of env_weights[i, s] * env[i ES + s, c] / ES
  * (accumulated in s order) and the albedo feature out[i, DS+2+SD+c] =

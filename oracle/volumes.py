@@ -303,17 +303,68 @@ def _march_ts(t0, tmax, step, cap: int) -> np.ndarray:
     return np.array(ts, F)
 
 
+def dda_march_ts(x, wo, tmin, tmax, step, grid: np.ndarray, cap: int = MAX_MARCH) -> np.ndarray:
+    """The sample positions t of VolumeProfileDDA's fixed-step marches
+    (shaders/volumes/volume_profile_dda.h:25-77): an Amanatides-Woo walk of
+    grid [D, H, W] over the box from the cell of x + wo tmin (clamped into the
+    grid); in a cell whose value is > 0, t, t + step, ... while t < the cell's
+    exit (= min of the three axis boundaries and tmax); then t = the exit and
+    the walk steps along the axis whose boundary comes first (x, then y, then
+    z on ties).  At most 4096 cells, while t < tmax, until the walk leaves the
+    grid; at most cap samples (the HIP kernel's bound).  Every operation is
+    rounded to float32 on its own."""
+    grid = np.asarray(grid, F)
+    D, H, W = grid.shape[:3]
+    dim = [W, H, D]
+    x = np.asarray(x, F)
+    wo = np.asarray(wo, F)
+    tmin, tmax, step = _f32(tmin), _f32(tmax), _f32(step)
+    entry = _point(x, wo, tmin)
+    cell, dstep, tma, tdl = [0, 0, 0], [0, 0, 0], [F(0)] * 3, [F(0)] * 3
+    with np.errstate(divide="ignore", invalid="ignore", over="ignore"):
+        for i in range(3):
+            fd = _f32(dim[i])
+            cs = _f32(_f32(2) / fd)
+            ci = int(np.floor(_f32(_f32(_f32(entry[i] * _f32(0.5)) + _f32(0.5)) * fd)))
+            cell[i] = min(max(ci, 0), dim[i] - 1)
+            dstep[i] = 1 if wo[i] > 0 else (-1 if wo[i] < 0 else 0)
+            inv = _f32(_f32(1) / wo[i])
+            nb = _f32(_f32(_f32(_f32(cell[i]) + _f32(max(dstep[i], 0))) * cs) - _f32(1))
+            tma[i] = _f32(_f32(nb - x[i]) * inv)
+            tdl[i] = _f32(cs * _f32(abs(inv)))
+        ts = []
+        t = tmin
+        for _ in range(4096):
+            if not t < tmax:
+                break
+            cexit = np.fmin(np.fmin(tma[0], tma[1]), np.fmin(tma[2], tmax))
+            if grid[cell[2], cell[1], cell[0]] > 0:
+                while t < cexit:
+                    if len(ts) >= cap:
+                        return np.array(ts, F)
+                    ts.append(t)
+                    t = _f32(t + step)
+            t = cexit
+            ax = 0 if (tma[0] <= tma[1] and tma[0] <= tma[2]) else (1 if tma[1] <= tma[2] else 2)
+            cell[ax] += dstep[ax]
+            tma[ax] = _f32(tma[ax] + tdl[ax])
+            if min(cell) < 0 or cell[0] >= W or cell[1] >= H or cell[2] >= D:
+                break
+    return np.array(ts, F)
+
+
 def volume_profile(rays: np.ndarray, extinction, majorant: np.ndarray, seeds, thresholds, spectral_dim: int,
                    environment_samples: int = 4, g: float = 0.0, step_size: float = 0.001,
                    density_scale: float = 1.0, transform=None, light_direction=(0.0, 1.0, 0.0),
                    light_intensity=None, sample_index: int = 0, rng_skip: int = 0, albedo=None,
-                   environment=None) -> dict:
+                   environment=None, dda_grid: np.ndarray | None = None) -> dict:
     """VolumeProfile of rays [n, 6].  extinction: object-space points [m, 3] ->
     [m] float32; majorant: the voxel grid [D, H, W]; albedo / environment:
     [m, 3] -> [m, SD] float32 (sample positions in object space, directions in
     world space).  Returns {"out": [n, DS + 3 SD + 4], "spos": [n, 3],
     "dirs": [n, ES, 3], "wts": [n, ES], "valid": [n]} (the first stage's records
-    are zero where a ray does not reach them)."""
+    are zero where a ray does not reach them).  dda_grid [D, H, W]: VolumeProfileDDA
+    (volumes.py:560-603): no end trimming, both marches at dda_march_ts's positions."""
     rays = np.asarray(rays, F).reshape(-1, 6)
     n = rays.shape[0]
     DS, SD, ES = len(thresholds), int(spectral_dim), int(environment_samples)
@@ -350,14 +401,14 @@ def volume_profile(rays: np.ndarray, extinction, majorant: np.ndarray, seeds, th
         tmin = max(_f32(0), tmin)
         if not (tmax > 0 and tmin <= tmax):
             continue
-        for _ in range(4096):
+        for _ in range(0 if dda_grid is not None else 4096):
             if not tmin < tmax:
                 break
             mj, dist = _majorant(majorant, _point(x, wo, tmin), wo)
             if mj > 0:
                 break
             tmin = _f32(tmin + max(dist, _f32(1e-5)))
-        for _ in range(4096):
+        for _ in range(0 if dda_grid is not None else 4096):
             if not tmin < tmax:
                 break
             mj, dist = _majorant(majorant, _point(x, wo, tmax), (-wo).astype(F))
@@ -365,7 +416,10 @@ def volume_profile(rays: np.ndarray, extinction, majorant: np.ndarray, seeds, th
                 break
             tmax = _f32(tmax - max(dist, _f32(1e-5)))
         # tau march (every sample up to tmax, then cut at the first tau > 20)
-        ts = _march_ts(tmin, tmax, step, MAX_MARCH)
+        if dda_grid is not None:
+            ts = dda_march_ts(x, wo, tmin, tmax, step, dda_grid)
+        else:
+            ts = _march_ts(tmin, tmax, step, MAX_MARCH)
         sg = sig((x[None, :] + (wo[None, :] * ts[:, None]).astype(F)).astype(F))
         tau = _f32(0)
         for k in range(ts.size):

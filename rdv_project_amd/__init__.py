@@ -100,6 +100,7 @@ from .rendering import (
     RatiotrackingTransmittance,
     RaymarchingTransmittance,
     VolumeProfile,
+    VolumeProfileDDA,
     VoxelMajorantField,
 )
 from .nn import (

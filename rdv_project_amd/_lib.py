@@ -188,6 +188,9 @@ _SIGNATURES = {
     "rdv_volume_profile": (C.c_int, [C.POINTER(MlpDesc), C.c_void_p, C.POINTER(VolumeProfileDesc), C.c_void_p,
                                      C.c_void_p, C.c_int64, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
                                      C.c_void_p, C.c_void_p]),
+    "rdv_volume_profile_dda": (C.c_int, [C.POINTER(MlpDesc), C.c_void_p, C.POINTER(VolumeProfileDesc), C.c_void_p,
+                                         C.c_void_p, C.c_int32, C.c_int32, C.c_int32, C.c_void_p, C.c_int64,
+                                         C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p]),
     "rdv_volume_profile_finish": (C.c_int, [C.POINTER(VolumeProfileDesc), C.c_void_p, C.c_int64, C.c_void_p,
                                             C.c_int64, C.c_void_p, C.c_void_p, C.c_int64, C.c_void_p, C.c_void_p]),
     "rdv_broadcast_rows": (C.c_int, [C.c_void_p, C.c_int32, C.c_int64, C.c_void_p, C.c_void_p]),

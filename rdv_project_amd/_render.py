@@ -18,7 +18,7 @@ from . import _chain, _lib
 from .core import RDVObject, current_stream_handle, device, launch_scope, wrap
 from .maths import Grid, Sensor
 from .rendering import (Cameras, EmissionAbsorption, RaymarchingTransmittance, RatiotrackingTransmittance,
-                        VolumeProfile, VoxelMajorantField)
+                        VolumeProfile, VolumeProfileDDA, VoxelMajorantField)
 
 _GRID_CACHE: dict = {}
 
@@ -165,14 +165,20 @@ def _ray_rows(x, name: str, out_width: int, key) -> tuple[torch.Tensor, int, RDV
     return xt, rows, _cached(key, (*x.shape[:-1], out_width))
 
 
-def _majorant_values(f: VoxelMajorantField) -> tuple[torch.Tensor, int, int, int]:
-    """The field's grid values as a contiguous fp32 [D, H, W] tensor and (W, H, D)."""
-    D, H, W = (int(v) for v in f.grid.shape)
-    g = f._grid_values().as_tensor("torch")
+def _grid_values_dhw(grid) -> tuple[torch.Tensor, int, int, int]:
+    """A 3-D Grid[3, 1]'s values as a contiguous fp32 [D, H, W] tensor and (W, H, D)."""
+    from .grids import grid_values
+    D, H, W = (int(v) for v in grid.shape)
+    g = grid_values(grid, {}).as_tensor("torch")
     if g.dtype != torch.float32 or not g.is_contiguous():
         g = g.to(torch.float32).contiguous()
     assert g.numel() == D * H * W, "the majorant grid must hold one value per voxel"
     return g, W, H, D
+
+
+def _majorant_values(f: VoxelMajorantField) -> tuple[torch.Tensor, int, int, int]:
+    """The field's grid values as a contiguous fp32 [D, H, W] tensor and (W, H, D)."""
+    return _grid_values_dhw(f.grid)
 
 
 def voxel_majorant_ptrs(f: VoxelMajorantField, x_ptr: int, y_ptr: int, rows: int) -> None:
@@ -308,11 +314,17 @@ def volume_profile_ptrs(vp: VolumeProfile, x_ptr: int, y_ptr: int, rows: int, se
     ws = _vp_workspace(vp, rows)
     lib = _lib.load()
     stream = C.c_void_p(current_stream_handle())
-    _lib.check(lib.rdv_volume_profile(C.byref(p.desc), C.c_void_p(packed.data_ptr()), C.byref(d),
-                                      C.c_void_p(g.data_ptr()), C.c_void_p(x_ptr), C.c_int64(rows),
-                                      C.c_void_p(y_ptr), C.c_void_p(ws["spos"].data_ptr()),
-                                      C.c_void_p(ws["dirs"].data_ptr()), C.c_void_p(ws["wts"].data_ptr()),
-                                      C.c_void_p(ws["valid"].data_ptr()), stream), "VolumeProfile")
+    tail = (C.c_void_p(x_ptr), C.c_int64(rows), C.c_void_p(y_ptr), C.c_void_p(ws["spos"].data_ptr()),
+            C.c_void_p(ws["dirs"].data_ptr()), C.c_void_p(ws["wts"].data_ptr()), C.c_void_p(ws["valid"].data_ptr()),
+            stream)
+    if isinstance(vp, VolumeProfileDDA):
+        dg, dW, dH, dD = _grid_values_dhw(vp.majorant_grid)
+        _lib.check(lib.rdv_volume_profile_dda(C.byref(p.desc), C.c_void_p(packed.data_ptr()), C.byref(d),
+                                              C.c_void_p(g.data_ptr()), C.c_void_p(dg.data_ptr()), C.c_int32(dW),
+                                              C.c_int32(dH), C.c_int32(dD), *tail), "VolumeProfileDDA")
+    else:
+        _lib.check(lib.rdv_volume_profile(C.byref(p.desc), C.c_void_p(packed.data_ptr()), C.byref(d),
+                                          C.c_void_p(g.data_ptr()), *tail), "VolumeProfile")
     a_ptr, a_stride = _map_over(vp.scattering_albedo, ws["spos"], rows, ws["albedo"])
     e_ptr, e_stride = _map_over(vp.environment, ws["dirs"], rows * vp.environment_samples, ws["env"])
     _lib.check(lib.rdv_volume_profile_finish(C.byref(d), C.c_void_p(a_ptr), C.c_int64(a_stride), C.c_void_p(e_ptr),

@@ -75,9 +75,9 @@ int launch_ratiotracking(const rdv_mlp_desc& d, const MlpLayout& lay, const void
                          const rdv_ratiotracking_desc& rt, const float* majorant, const float* rays, int64_t nrays,
                          float* out, hipStream_t stream);
 int launch_volume_profile(const rdv_mlp_desc& d, const MlpLayout& lay, const void* packed,
-                          const rdv_volume_profile_desc& vp, const float* majorant, const float* rays, int64_t nrays,
-                          float* out, float* spos, float* env_dirs, float* env_w, int32_t* valid,
-                          hipStream_t stream);
+                          const rdv_volume_profile_desc& vp, const float* majorant, const float* dda_grid, int dda_w,
+                          int dda_h, int dda_d, const float* rays, int64_t nrays, float* out, float* spos,
+                          float* env_dirs, float* env_w, int32_t* valid, hipStream_t stream);
 int launch_volume_profile_finish(const rdv_volume_profile_desc& vp, const float* albedo, int64_t albedo_stride,
                                  const float* env, int64_t env_stride, const float* env_w, const int32_t* valid,
                                  int64_t nrays, float* out, hipStream_t stream);
@@ -564,8 +564,31 @@ int rdv_volume_profile(const rdv_mlp_desc* extinction, const void* packed, const
   if (!packed || !majorant || !rays || !out || !sample_pos || !valid ||
       (vp->environment_samples > 0 && (!env_dirs || !env_weights)))
     return fail(RDV_ERR_INVALID, "rdv_volume_profile: NULL pointer argument");
-  return launch_volume_profile(*extinction, lay, packed, *vp, majorant, rays, n_rays, out, sample_pos, env_dirs,
-                               env_weights, valid, static_cast<hipStream_t>(stream));
+  return launch_volume_profile(*extinction, lay, packed, *vp, majorant, nullptr, 0, 0, 0, rays, n_rays, out,
+                               sample_pos, env_dirs, env_weights, valid, static_cast<hipStream_t>(stream));
+}
+
+int rdv_volume_profile_dda(const rdv_mlp_desc* extinction, const void* packed, const rdv_volume_profile_desc* vp,
+                           const float* majorant, const float* majorant_grid, int32_t grid_width,
+                           int32_t grid_height, int32_t grid_depth, const float* rays, int64_t n_rays, float* out,
+                           float* sample_pos, float* env_dirs, float* env_weights, int32_t* valid, void* stream) {
+  MlpLayout lay;
+  int rc = check_mlp(extinction, &lay);
+  if (rc != RDV_OK) return rc;
+  rc = check_volume_profile(vp);
+  if (rc != RDV_OK) return rc;
+  if (grid_width < 1 || grid_height < 1 || grid_depth < 1 || grid_width > 4096 || grid_height > 4096 ||
+      grid_depth > 4096)
+    return fail(RDV_ERR_INVALID, "rdv_volume_profile_dda: grid dimensions must be in [1, 4096]");
+  if (n_rays < 0 || n_rays >= (int64_t(1) << 31))
+    return fail(RDV_ERR_INVALID, "n_rays must be in [0, 2^31) (the generator's thread index is an int)");
+  if (n_rays == 0) return RDV_OK;
+  if (!packed || !majorant || !majorant_grid || !rays || !out || !sample_pos || !valid ||
+      (vp->environment_samples > 0 && (!env_dirs || !env_weights)))
+    return fail(RDV_ERR_INVALID, "rdv_volume_profile_dda: NULL pointer argument");
+  return launch_volume_profile(*extinction, lay, packed, *vp, majorant, majorant_grid, grid_width, grid_height,
+                               grid_depth, rays, n_rays, out, sample_pos, env_dirs, env_weights, valid,
+                               static_cast<hipStream_t>(stream));
 }
 
 int rdv_volume_profile_finish(const rdv_volume_profile_desc* vp, const float* albedo, int64_t albedo_stride,

@@ -25,6 +25,14 @@ namespace rdv {
 //   Henyey-Greenstein direction with its ratio-tracked transmittance.
 // Every fp32 update is rounded on its own (no contraction), in the shader's operation order.
 //
+// VolumeProfileDDA (volumes.py:560-603, shaders/volumes/volume_profile_dda.h:1-208): the same,
+// except that the two fixed-step marches neither trim the ends nor use the majorant field:
+// they walk `majorant_grid` (a separate [D, H, W] grid over the box) cell by cell with an
+// Amanatides-Woo DDA from the entry cell (at most 4096 cells, until tMax or off the grid).
+// In a cell whose value is > 0 the march samples t, t + step, ... while t < the cell's exit;
+// then t jumps to the exit (empty cells are skipped whole).  The light ray and the
+// environment rays are VolumeProfile's.
+//
 // Mapping: as the ratio-tracking kernel, a wave holds 32 rays (lanes l and l + 32 mirror ray
 // l); each lane runs its ray's state machine until it needs an extinction value, then the
 // wave evaluates the extinction chain once for the 32 pending points.  The environment and
@@ -48,9 +56,11 @@ struct VpArgs {
   float* env_dirs;    // [n, es, 3]
   float* env_w;       // [n, es]
   int32_t* valid;     // [n]
+  const float* dgrid; // VolumeProfileDDA: the walked grid [dd, dh, dw] (null: VolumeProfile)
+  int dw, dh, dd;
 };
 
-enum : int { kVpDone = 0, kVpTau = 1, kVpDepth = 2, kVpRm = 3, kVpRt = 4 };
+enum : int { kVpDone = 0, kVpTau = 1, kVpDepth = 2, kVpRm = 3, kVpRt = 4, kVpTauDda = 5, kVpDepthDda = 6 };
 
 // Steps of one fixed-step march at most.  The shader's marches stop only at
 // tMax (or tau > 20); a step below the spacing of fp32 values near t would
@@ -66,6 +76,11 @@ struct VpRay {
   float p[3], dl[3], d, T, maj;  // the secondary ray: position, direction, distance left, T or tau, majorant
   int idx, phase, k, s;
   RngState st;
+  // the DDA walk (VolumeProfileDDA): cell, per-axis exit distance and its increment, step sign,
+  // the current cell's exit, whether t is inside a marched cell, cells walked
+  int cell[3], dstep[3];
+  float tma[3], tdl[3], cexit;
+  int inner, guard;
 };
 
 // Expected tau at the crossing of a transmittance threshold (volume_profile.h:82).
@@ -198,6 +213,71 @@ __device__ __forceinline__ void vp_after_depth(const VpCtx& c, VpRay& r, int64_t
   r.phase = kVpRm;
 }
 
+// The DDA walk's start at tmin (volume_profile_dda.h:25-51): the entry cell (clamped into
+// the grid), the step signs, the distances to each axis' next cell boundary and their
+// increments (1 / 0 gives +-inf: that axis never comes first).
+__device__ __forceinline__ void vp_dda_setup(const VpCtx& c, VpRay& r) {
+#pragma clang fp contract(off)
+  const VpArgs& a = c.a;
+  const int dim[3] = {a.dw, a.dh, a.dd};
+  float entry[3];
+  vp_point(r.x, r.wo, r.tmin, entry);
+#pragma unroll
+  for (int i = 0; i < 3; ++i) {
+    const float fd = float(dim[i]);
+    const float cs = 2.0f / fd;
+    const int ci = int(floorf((entry[i] * 0.5f + 0.5f) * fd));
+    r.cell[i] = ci < 0 ? 0 : (ci > dim[i] - 1 ? dim[i] - 1 : ci);
+    r.dstep[i] = r.wo[i] > 0.0f ? 1 : (r.wo[i] < 0.0f ? -1 : 0);
+    const float inv = 1.0f / r.wo[i];
+    const float nb = (float(r.cell[i]) + fmaxf(float(r.dstep[i]), 0.0f)) * cs - 1.0f;
+    r.tma[i] = (nb - r.x[i]) * inv;
+    r.tdl[i] = cs * fabsf(inv);
+  }
+  r.t = r.tmin;
+  r.inner = 0;
+  r.guard = 0;
+}
+
+// Leaves the current cell (volume_profile_dda.h:68-76): t to its exit, the next cell along
+// the axis whose boundary comes first; false once the walk is off the grid.
+__device__ __forceinline__ bool vp_dda_next(const VpCtx& c, VpRay& r) {
+#pragma clang fp contract(off)
+  r.t = r.cexit;
+  int ax = 2;
+  if (r.tma[0] <= r.tma[1] && r.tma[0] <= r.tma[2]) ax = 0;
+  else if (r.tma[1] <= r.tma[2]) ax = 1;
+  r.cell[ax] += r.dstep[ax];
+  r.tma[ax] = r.tma[ax] + r.tdl[ax];
+  ++r.guard;
+  return r.cell[0] >= 0 && r.cell[1] >= 0 && r.cell[2] >= 0 && r.cell[0] < c.a.dw && r.cell[1] < c.a.dh &&
+         r.cell[2] < c.a.dd;
+}
+
+// Walks to the next sample point of a DDA march (true, the point in q) or to the walk's end
+// (false): inside a marched cell while t < its exit, else into the next cell, skipping cells
+// whose value is not > 0.
+__device__ __forceinline__ bool vp_dda_walk(const VpCtx& c, VpRay& r, float (&q)[3]) {
+#pragma clang fp contract(off)
+  const VpArgs& a = c.a;
+  for (;;) {
+    if (r.inner) {
+      if (r.t < r.cexit) {
+        vp_point(r.x, r.wo, r.t, q);
+        return true;
+      }
+      r.inner = 0;
+      if (!vp_dda_next(c, r)) return false;
+    }
+    if (!(r.guard < 4096 && r.t < r.tmax)) return false;
+    r.cexit = fminf(fminf(r.tma[0], r.tma[1]), fminf(r.tma[2], r.tmax));
+    const float m = a.dgrid[(int64_t(r.cell[2]) * a.dh + r.cell[1]) * a.dw + r.cell[0]];
+    if (m > 0.0f) r.inner = 1;
+    else if (!vp_dda_next(c, r)) return false;
+  }
+}
+
+// The depth march after the tau march (both variants; volume_profile.h:82-86).
 __device__ __forceinline__ void vp_depth_begin(const VpCtx& c, VpRay& r, int64_t ray) {
   r.t = r.tmin;
   r.k = 0;
@@ -205,6 +285,15 @@ __device__ __forceinline__ void vp_depth_begin(const VpCtx& c, VpRay& r, int64_t
   r.idx = 0;
   r.scale = c.a.thr[0];
   r.tcross = vp_crossing(r.scale, r.tau);
+  if (c.a.dgrid != nullptr) {
+    if (r.tau > 0.0001f) {
+      vp_dda_setup(c, r);
+      r.phase = kVpDepthDda;
+    } else {
+      vp_after_depth(c, r, ray);
+    }
+    return;
+  }
   if (r.tau > 0.0001f && r.t < r.tmax) r.phase = kVpDepth;
   else vp_after_depth(c, r, ray);
 }
@@ -230,6 +319,15 @@ __device__ __forceinline__ void vp_start(const VpCtx& c, VpRay& r, int64_t ray) 
   if (!(tmax > 0.0f && tmin <= tmax)) {
     a.valid[ray] = 0;
     r.phase = kVpDone;
+    return;
+  }
+  if (a.dgrid != nullptr) {  // VolumeProfileDDA: no trimming, the walk skips empty cells
+    r.tmin = tmin;
+    r.tmax = tmax;
+    r.tau = 0.0f;
+    r.k = 0;
+    vp_dda_setup(c, r);
+    r.phase = kVpTauDda;
     return;
   }
   // empty space at both ends: the voxel majorant is 0 up to its voxel's exit
@@ -300,6 +398,44 @@ __device__ __forceinline__ bool vp_advance(const VpCtx& c, VpRay& r, int64_t ray
         }
         vp_point(r.x, r.wo, r.t, q);
         return true;
+      case kVpTauDda:  // volume_profile_dda.h:53-77
+        if (has) {
+          has = false;
+          r.tau = r.tau + (sigma * a.density_scale) * a.step;
+          r.t = r.t + a.step;
+          if (r.tau > 20.0f || ++r.k >= kVpMaxMarch) {
+            vp_depth_begin(c, r, ray);
+            break;
+          }
+        }
+        if (vp_dda_walk(c, r, q)) return true;
+        vp_depth_begin(c, r, ray);
+        break;
+      case kVpDepthDda:  // volume_profile_dda.h:83-129
+        if (has) {
+          has = false;
+          r.ctau = r.ctau + (sigma * a.density_scale) * a.step;
+          float* o = a.out + ray * c.outw;
+          while (r.ctau * r.scale >= r.tcross) {
+            o[r.idx] = r.t;
+            ++r.idx;
+            if (r.idx >= a.ds) break;
+            r.scale = a.thr[r.idx];
+            r.tcross = vp_crossing(r.scale, r.tau);
+          }
+          bool stop = r.idx >= a.ds;
+          if (!stop) {
+            r.t = r.t + a.step;
+            stop = r.ctau > 20.0f || ++r.k >= kVpMaxMarch;
+          }
+          if (stop) {
+            vp_after_depth(c, r, ray);
+            break;
+          }
+        }
+        if (vp_dda_walk(c, r, q)) return true;
+        vp_after_depth(c, r, ray);
+        break;
       case kVpRm:  // raymarching_transmittance_trait.h
         if (has) {
           has = false;
@@ -488,9 +624,9 @@ __global__ __launch_bounds__(256) void volume_profile_finish_kernel(VpFinishArgs
 }
 
 int launch_volume_profile(const rdv_mlp_desc& d, const MlpLayout& lay, const void* packed,
-                          const rdv_volume_profile_desc& vp, const float* majorant, const float* rays, int64_t nrays,
-                          float* out, float* spos, float* env_dirs, float* env_w, int32_t* valid,
-                          hipStream_t stream) {
+                          const rdv_volume_profile_desc& vp, const float* majorant, const float* dda_grid, int dda_w,
+                          int dda_h, int dda_d, const float* rays, int64_t nrays, float* out, float* spos,
+                          float* env_dirs, float* env_w, int32_t* valid, hipStream_t stream) {
   if (!is_f16_field(d, 1))
     return fail(RDV_ERR_UNSUPPORTED, "the extinction must be a LinearFast chain from 3 inputs to 1 output");
   DeviceInfo di;
@@ -522,6 +658,10 @@ int launch_volume_profile(const rdv_mlp_desc& d, const MlpLayout& lay, const voi
   a.env_dirs = env_dirs;
   a.env_w = env_w;
   a.valid = valid;
+  a.dgrid = dda_grid;
+  a.dw = dda_w;
+  a.dh = dda_h;
+  a.dd = dda_d;
   ga.packed = static_cast<const uint8_t*>(packed);
   gen_net(d, lay, &ga.net);
   // 32 rays per wave

@@ -229,6 +229,33 @@ class VolumeProfile(Map):
         _render.volume_profile_ptrs(self, x_ptr, y_ptr, rows)
 
 
+class VolumeProfileDDA(VolumeProfile):
+    """VolumeProfile whose primary ray walks `majorant_grid` cell by cell
+    (reference: volumes.py:560-603, shaders/volumes/volume_profile_dda.h:1-208).
+    The tau and depth marches use an Amanatides-Woo DDA over majorant_grid, a
+    Grid[3, 1] of shape [D, H, W] over the box (e.g. a MajorantGrid's output),
+    instead of trimming the ray's ends with `majorant`. A cell whose value is
+    > 0 is marched in fixed steps from where the walk entered it up to its exit.
+    Cells whose value is not > 0 are skipped whole. At most 4096 cells are
+    walked, stopping at the box exit or on leaving the grid. `majorant` (the
+    VoxelMajorantField) still serves the environment rays' ratio tracking, and
+    the outputs are VolumeProfile's."""
+
+    def __init__(self, extinction: Map, majorant, majorant_grid, environment: Map, scattering_albedo: Map,
+                 transmittance_threshold: list, density_scale: float = 1.0, transform=None,
+                 light_direction=(0.0, 1.0, 0.0), light_intensity=None, g: float = 0.0, step_size: float = 0.001,
+                 environment_samples: int = 4, sample_index: int = 0, nee_near_distance: float = 0.05) -> None:
+        super().__init__(extinction=extinction, majorant=majorant, environment=environment,
+                         scattering_albedo=scattering_albedo, transmittance_threshold=transmittance_threshold,
+                         density_scale=density_scale, transform=transform, light_direction=light_direction,
+                         light_intensity=light_intensity, g=g, step_size=step_size,
+                         environment_samples=environment_samples, sample_index=sample_index,
+                         nee_near_distance=nee_near_distance)
+        majorant_grid = majorant_grid.cast(Grid[3, 1])
+        assert len(majorant_grid.shape) == 3, "VolumeProfileDDA needs a 3-D majorant_grid"
+        self.majorant_grid = majorant_grid
+
+
 class EmissionAbsorption(Map[6, 3]):
     """Build-defined volume renderer (no reference counterpart): along each ray
     (origin, direction) through [-1,1]^3, `samples` points t_i = t0 + (i + 1/2) dt

@@ -23,7 +23,8 @@ def test_curated_names_import():
                  "LinearTensorOpSimple", "LinearTensorOpFast", "LinearTensorOpMine", "Conv2DTensorOp",
                  "Conv2DTensorOpFast", "Conv2DTensorOpSimple", "Conv2DTensorOpSimple3x3", "Conv2DTensorOpWindow3x3",
                  "Conv2DTensorOpWinograd3x3", "Downsample2xTensorOp", "Upsample2xTensorOp", "ConcatTensorOp",
-                 "Cameras", "RaymarchingTransmittance", "wrap", "dispatch", "profiling", "profiling_submit_times",
+                 "Cameras", "RaymarchingTransmittance", "RatiotrackingTransmittance", "VoxelMajorantField",
+                 "VolumeProfile", "VolumeProfileDDA", "MajorantGrid", "TensorGrid", "wrap", "dispatch", "profiling", "profiling_submit_times",
                  "reset_submit_times", "Map", "Grid", "X", "Generics", "Generic", "Main", "Component", "Struct",
                  "Library", "Single", "Array", "Pointer", "Buffer", "FixArray", "Deferred", "deferreds",
                  "RDVObject", "ensure_on_rdv", "is_on_rdv", "MathLibrary", "RandomLibrary", "GridLibrary",

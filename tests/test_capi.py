@@ -242,6 +242,25 @@ def test_volume_profile_rejects_before_any_launch(kw, fragment):
     assert rc == _lib.RDV_ERR_INVALID and fragment in _lib.last_error()
 
 
+@pytest.mark.parametrize("w,h,dd,grid,fragment", [
+    (0, 4, 4, 0x9000, "grid dimensions"),
+    (4, 4097, 4, 0x9000, "grid dimensions"),
+    (4, 4, 4, None, "NULL"),
+])
+def test_volume_profile_dda_rejects_before_any_launch(w, h, dd, grid, fragment):
+    lib = _lib.load()
+    d = _vp()
+    rc = lib.rdv_volume_profile_dda(C.byref(_ext_desc()), 0x1000, C.byref(d), 0x2000, grid, w, h, dd, 0x3000, 64,
+                                    0x4000, 0x5000, 0x6000, 0x7000, 0x8000, None)
+    assert rc == _lib.RDV_ERR_INVALID and fragment in _lib.last_error()
+    # the VolumeProfile descriptor checks come first, as for rdv_volume_profile
+    rc = lib.rdv_volume_profile_dda(C.byref(_ext_desc()), 0x1000, C.byref(_vp(depth_samples=0)), 0x2000, 0x9000,
+                                    4, 4, 4, 0x3000, 64, 0x4000, 0x5000, 0x6000, 0x7000, 0x8000, None)
+    assert rc == _lib.RDV_ERR_INVALID and "depth_samples" in _lib.last_error()
+    assert lib.rdv_volume_profile_dda(C.byref(_ext_desc()), None, C.byref(d), None, None, 4, 4, 4, None, 0, None,
+                                      None, None, None, None, None) == 0
+
+
 def test_volume_profile_host_errors_need_no_device():
     lib = _lib.load()
     d = _vp()

@@ -1,5 +1,6 @@
 """GPU parity of VolumeProfile (src/rdv/domain/volumes.py:503-550,
-shaders/volumes/volume_profile.h:1-167) against oracle/volumes.py.
+shaders/volumes/volume_profile.h:1-167) and VolumeProfileDDA (volumes.py:560-603,
+shaders/volumes/volume_profile_dda.h:1-208) against oracle/volumes.py.
 
 Bars.  The deterministic outputs (depths, 0.2 log(1 + tau), the light ray's
 raymarched transmittance, albedo, g, intensities, S): with an extinction the
@@ -166,6 +167,68 @@ def test_mlp_extinction_matches_oracle(dims, res, ds):
                            albedo=lambda p: np.tile(np.float32([0.3, 0.5, 0.7]), (p.shape[0], 1)),
                            environment=lambda w: np.tile(np.float32([1.0, 0.8, 0.6]), (w.shape[0], 1)))
     _check(out, ws, ref, n, 4, sd, 2, 2e-3, 1e-4, 0.97, False, f"MLP extinction {dims}")
+
+
+@pytest.mark.parametrize("res,sparse,es", [(4, False, 4), (5, True, 2), (3, True, 0)])
+def test_dda_constant_extinction_matches_oracle(res, sparse, es):
+    """VolumeProfileDDA (volumes.py:560-603): the marches walk a separate grid
+    cell by cell, restarting the fixed steps at every cell entry and skipping
+    cells whose value is not > 0; the same exact bars as VolumeProfile."""
+    sigma, ds, sd, g = 0.9, 1.7, 3, 0.2
+    maj = np.random.default_rng(5).uniform(0.9, 1.8, (4, 4, 4)).astype(np.float32)
+    dgrid = np.random.default_rng(6 + res).uniform(0.5, 1.5, (res, res, res)).astype(np.float32)
+    if sparse:
+        dgrid[np.random.default_rng(7).uniform(size=dgrid.shape) < 0.4] = 0.0
+        dgrid[:, 0] = 0.0  # an empty slab inside the box
+    ext = _field(_const_layers(sigma))
+    alb = np.linspace(0.2, 0.7, sd).astype(np.float32)
+    env = np.linspace(0.5, 1.5, sd).astype(np.float32)
+    thr = [0.9, 0.6, 0.3]
+    vp = rdv.VolumeProfileDDA(ext, rdv.TensorGrid(torch.from_numpy(maj[..., None]).cuda()),
+                              rdv.TensorGrid(torch.from_numpy(dgrid[..., None]).cuda()), rdv.Constant(env),
+                              rdv.Constant(alb), thr, density_scale=ds, g=g, step_size=0.004, environment_samples=es,
+                              light_direction=(0.3, 0.9, -0.2))
+    rays = _camera_rays(24, 18)
+    seeds = (11, 22, 33, 44)
+    out, ws, n = _run(vp, rays, seeds)
+    ref = V.volume_profile(rays, lambda p: np.full(p.shape[0], sigma, np.float32), maj, seeds, thr, sd,
+                           environment_samples=es, g=g, step_size=0.004, density_scale=ds,
+                           light_direction=(0.3, 0.9, -0.2), dda_grid=dgrid,
+                           albedo=lambda p: np.tile(alb, (p.shape[0], 1)),
+                           environment=lambda w: np.tile(env, (w.shape[0], 1)))
+    v = ref["valid"] == 1
+    assert v.mean() > 0.3 and (~v).any()
+    _check(out, ws, ref, n, len(thr), sd, es, 1e-5, 1e-6, 1.0, True, f"DDA constant extinction {res} {sparse}")
+    if sparse:  # the walk skipped cells: the plain VolumeProfile march gives other depths
+        plain = V.volume_profile(rays, lambda p: np.full(p.shape[0], sigma, np.float32), maj, seeds, thr, sd,
+                                 environment_samples=0, g=g, step_size=0.004, density_scale=ds,
+                                 light_direction=(0.3, 0.9, -0.2),
+                                 albedo=lambda p: np.tile(alb, (p.shape[0], 1)),
+                                 environment=lambda w: np.tile(env, (w.shape[0], 1)))
+        assert (plain["out"][:, 0] != ref["out"][:, 0]).mean() > 0.1
+
+
+def test_dda_mlp_extinction_matches_oracle():
+    dims, res, ds = [3, 64, 64, 64, 1], 4, 3.0
+    layers = _rand_field(dims, seed=77)
+    ext = _field(layers, head="softplus")
+    maj = _majorant_of(_np(layers), "softplus", res)
+    dgrid = maj.copy()
+    dgrid[maj < np.quantile(maj, 0.3)] = 0.0  # skip the thinnest cells
+    sd = 3
+    vp = rdv.VolumeProfileDDA(ext, rdv.TensorGrid(torch.from_numpy(maj[..., None]).cuda()),
+                              rdv.TensorGrid(torch.from_numpy(dgrid[..., None]).cuda()),
+                              rdv.Constant([1.0, 0.8, 0.6]), rdv.Constant([0.3, 0.5, 0.7]), [0.8, 0.5, 0.25, 0.1],
+                              density_scale=ds, g=0.2, step_size=0.01, environment_samples=2)
+    rays = _camera_rays(20, 16)
+    seeds = (5, 6, 7, 8)
+    out, ws, n = _run(vp, rays, seeds)
+    f = V.mlp_extinction(_np(layers), "softplus")
+    ref = V.volume_profile(rays, f, maj, seeds, [0.8, 0.5, 0.25, 0.1], sd, environment_samples=2, g=0.2,
+                           step_size=0.01, density_scale=ds, dda_grid=dgrid,
+                           albedo=lambda p: np.tile(np.float32([0.3, 0.5, 0.7]), (p.shape[0], 1)),
+                           environment=lambda w: np.tile(np.float32([1.0, 0.8, 0.6]), (w.shape[0], 1)))
+    _check(out, ws, ref, n, 4, sd, 2, 2e-3, 1e-4, 0.97, False, "DDA MLP extinction")
 
 
 def test_chain_albedo_and_environment_maps():
