@@ -84,7 +84,8 @@ PREWARM_S = 0.5  # seconds of untimed launches before the warm-up steps
 def bench_volume_profile(steps, warmup):
     """VolumeProfile over the C4 camera's 512 x 512 rays: the ratio-tracking leg's extinction (3 -> 64 -> 64 -> 64
     -> 1 softplus, seed 11) and 8^3 majorant, density_scale 4, thresholds (0.9, 0.5, 0.1), step_size 0.004, g 0.3,
-    4 environment samples, constant RGB environment and albedo (the two maps cost nothing); both stages timed."""
+    4 environment samples, constant RGB environment and albedo (the two maps cost nothing); both stages timed.
+    Then VolumeProfileDDA on the same rays, its walked grid the same 8^3 MajorantGrid."""
     import torch
     import rdv_project_amd as rdv
     from rdv_project_amd import _chain, _lib, _render
@@ -133,6 +134,25 @@ def bench_volume_profile(steps, warmup):
 
     wall, ev = _time_launches(launch, steps, warmup, prewarm_s=0.0)
     valid = float(ws["valid"][:n].float().mean())
+    mean_s = float(out[:, -1].double().mean())
+
+    def launch_dda(i):  # VolumeProfileDDA: the primary ray walks the same 8^3 MajorantGrid cell by cell
+        d.seeds[0] = 256 + i
+        rc = lib.rdv_volume_profile_dda(C.byref(p.desc), C.c_void_p(packed.data_ptr()), C.byref(d),
+                                        C.c_void_p(majv.data_ptr()), C.c_void_p(majv.data_ptr()), C.c_int32(8),
+                                        C.c_int32(8), C.c_int32(8), C.c_void_p(rays.data_ptr()), C.c_int64(n),
+                                        C.c_void_p(out.data_ptr()), C.c_void_p(ws["spos"].data_ptr()),
+                                        C.c_void_p(ws["dirs"].data_ptr()), C.c_void_p(ws["wts"].data_ptr()),
+                                        C.c_void_p(ws["valid"].data_ptr()), stream)
+        if rc == 0:
+            rc = lib.rdv_volume_profile_finish(C.byref(d), C.c_void_p(alb_v), C.c_int64(0), C.c_void_p(env_v),
+                                               C.c_int64(0), C.c_void_p(ws["wts"].data_ptr()),
+                                               C.c_void_p(ws["valid"].data_ptr()), C.c_int64(n),
+                                               C.c_void_p(out.data_ptr()), stream)
+        if rc != 0:
+            _lib.check(rc, "volume profile DDA")
+
+    _, ev_dda = _time_launches(launch_dda, steps, warmup, prewarm_s=0.0)
     return {
         "workload": "VolumeProfile over 512x512 C4 camera rays: extinction 3->64->64->64->1 softplus (fp16 MFMA, "
                     "seed 11), 8^3 voxel majorant, density_scale 4, thresholds (0.9, 0.5, 0.1), step 0.004, g 0.3, "
@@ -141,7 +161,11 @@ def bench_volume_profile(steps, warmup):
         "ms_per_call": round(ev, 3),
         "Mrays_per_s": round(n / (ev * 1e-3) / 1e6, 2),
         "valid_fraction": round(valid, 4),
-        "mean_S": round(float(out[:, -1].double().mean()), 4),
+        "mean_S": round(mean_s, 4),
+        "dda": {"ms_per_call": round(ev_dda, 3), "Mrays_per_s": round(n / (ev_dda * 1e-3) / 1e6, 2),
+                "valid_fraction": round(float(ws["valid"][:n].float().mean()), 4),
+                "mean_S": round(float(out[:, -1].double().mean()), 4),
+                "variant": "VolumeProfileDDA, majorant_grid = the same 8^3 MajorantGrid"},
         "bound": "per-ray state machine (two fixed-step marches, the light ray's march, four ratio-tracked "
                  "environment rays); one chain evaluation per step for the 32 rays of a wave",
     }

@@ -30,6 +30,8 @@ SOURCES = [
     "render_field8_ea.hip",
     "volume_profile.hip",
     "volume_profile8.hip",
+    "volume_profile_dda.hip",
+    "volume_profile_dda8.hip",
     "mlp_generic.hip",
     "train.hip",
     "winograd.hip",

@@ -4,7 +4,9 @@
 #include "volume_common.h"
 
 // RDV_FIELD_PART: 0 (this file) everything except the 8-tile instantiations
-// of volume_profile_kernel; 1 (volume_profile8.hip) their launcher alone, in a
+// of volume_profile_kernel and every instantiation of volume_profile_dda_kernel;
+// 1 (volume_profile8.hip) the former's 8-tile launcher; 2 and 3
+// (volume_profile_dda{,8}.hip) the DDA kernel's launchers: each in a
 // translation unit of its own (they take most of the compile time).
 #ifndef RDV_FIELD_PART
 #define RDV_FIELD_PART 0
@@ -76,12 +78,18 @@ struct VpRay {
   float p[3], dl[3], d, T, maj;  // the secondary ray: position, direction, distance left, T or tau, majorant
   int idx, phase, k, s;
   RngState st;
-  // the DDA walk (VolumeProfileDDA): cell, per-axis exit distance and its increment, step sign,
-  // the current cell's exit, whether t is inside a marched cell, cells walked
-  int cell[3], dstep[3];
-  float tma[3], tdl[3], cexit;
-  int inner, guard;
+  // The DDA walk (VolumeProfileDDA) during the two marches, when the secondary ray's p, dl and
+  // d are free: p holds the distance to each axis' next cell boundary, dl its increment, d the
+  // current cell's exit; cell the current cell; walk = cells walked, + kVpInner while t is
+  // inside a marched cell.
+  int cell[3];
+  int walk;
 };
+
+constexpr int kVpInner = 1 << 20;  // walk flag: t is inside a marched cell (cells walked stay < 4097)
+
+// The DDA step sign of axis i.
+__device__ __forceinline__ int vp_sign(float w) { return w > 0.0f ? 1 : (w < 0.0f ? -1 : 0); }
 
 // Expected tau at the crossing of a transmittance threshold (volume_profile.h:82).
 __device__ __forceinline__ float vp_crossing(float scale, float tau) {
@@ -228,28 +236,32 @@ __device__ __forceinline__ void vp_dda_setup(const VpCtx& c, VpRay& r) {
     const float cs = 2.0f / fd;
     const int ci = int(floorf((entry[i] * 0.5f + 0.5f) * fd));
     r.cell[i] = ci < 0 ? 0 : (ci > dim[i] - 1 ? dim[i] - 1 : ci);
-    r.dstep[i] = r.wo[i] > 0.0f ? 1 : (r.wo[i] < 0.0f ? -1 : 0);
     const float inv = 1.0f / r.wo[i];
-    const float nb = (float(r.cell[i]) + fmaxf(float(r.dstep[i]), 0.0f)) * cs - 1.0f;
-    r.tma[i] = (nb - r.x[i]) * inv;
-    r.tdl[i] = cs * fabsf(inv);
+    const float nb = (float(r.cell[i]) + fmaxf(float(vp_sign(r.wo[i])), 0.0f)) * cs - 1.0f;
+    r.p[i] = (nb - r.x[i]) * inv;
+    r.dl[i] = cs * fabsf(inv);
   }
   r.t = r.tmin;
-  r.inner = 0;
-  r.guard = 0;
+  r.walk = 0;
 }
 
 // Leaves the current cell (volume_profile_dda.h:68-76): t to its exit, the next cell along
 // the axis whose boundary comes first; false once the walk is off the grid.
 __device__ __forceinline__ bool vp_dda_next(const VpCtx& c, VpRay& r) {
 #pragma clang fp contract(off)
-  r.t = r.cexit;
-  int ax = 2;
-  if (r.tma[0] <= r.tma[1] && r.tma[0] <= r.tma[2]) ax = 0;
-  else if (r.tma[1] <= r.tma[2]) ax = 1;
-  r.cell[ax] += r.dstep[ax];
-  r.tma[ax] = r.tma[ax] + r.tdl[ax];
-  ++r.guard;
+  r.t = r.d;
+  // constant indices only: a run-time index would put the ray's state in scratch memory
+  if (r.p[0] <= r.p[1] && r.p[0] <= r.p[2]) {
+    r.cell[0] += vp_sign(r.wo[0]);
+    r.p[0] = r.p[0] + r.dl[0];
+  } else if (r.p[1] <= r.p[2]) {
+    r.cell[1] += vp_sign(r.wo[1]);
+    r.p[1] = r.p[1] + r.dl[1];
+  } else {
+    r.cell[2] += vp_sign(r.wo[2]);
+    r.p[2] = r.p[2] + r.dl[2];
+  }
+  r.walk = (r.walk & ~kVpInner) + 1;
   return r.cell[0] >= 0 && r.cell[1] >= 0 && r.cell[2] >= 0 && r.cell[0] < c.a.dw && r.cell[1] < c.a.dh &&
          r.cell[2] < c.a.dd;
 }
@@ -261,23 +273,23 @@ __device__ __forceinline__ bool vp_dda_walk(const VpCtx& c, VpRay& r, float (&q)
 #pragma clang fp contract(off)
   const VpArgs& a = c.a;
   for (;;) {
-    if (r.inner) {
-      if (r.t < r.cexit) {
+    if (r.walk & kVpInner) {
+      if (r.t < r.d) {
         vp_point(r.x, r.wo, r.t, q);
         return true;
       }
-      r.inner = 0;
       if (!vp_dda_next(c, r)) return false;
     }
-    if (!(r.guard < 4096 && r.t < r.tmax)) return false;
-    r.cexit = fminf(fminf(r.tma[0], r.tma[1]), fminf(r.tma[2], r.tmax));
+    if (!((r.walk & ~kVpInner) < 4096 && r.t < r.tmax)) return false;
+    r.d = fminf(fminf(r.p[0], r.p[1]), fminf(r.p[2], r.tmax));
     const float m = a.dgrid[(int64_t(r.cell[2]) * a.dh + r.cell[1]) * a.dw + r.cell[0]];
-    if (m > 0.0f) r.inner = 1;
+    if (m > 0.0f) r.walk |= kVpInner;
     else if (!vp_dda_next(c, r)) return false;
   }
 }
 
 // The depth march after the tau march (both variants; volume_profile.h:82-86).
+template <bool DDA>
 __device__ __forceinline__ void vp_depth_begin(const VpCtx& c, VpRay& r, int64_t ray) {
   r.t = r.tmin;
   r.k = 0;
@@ -285,7 +297,7 @@ __device__ __forceinline__ void vp_depth_begin(const VpCtx& c, VpRay& r, int64_t
   r.idx = 0;
   r.scale = c.a.thr[0];
   r.tcross = vp_crossing(r.scale, r.tau);
-  if (c.a.dgrid != nullptr) {
+  if constexpr (DDA) {
     if (r.tau > 0.0001f) {
       vp_dda_setup(c, r);
       r.phase = kVpDepthDda;
@@ -299,6 +311,7 @@ __device__ __forceinline__ void vp_depth_begin(const VpCtx& c, VpRay& r, int64_t
 }
 
 // Ray `ray` from its input row to its first extinction request (or its end).
+template <bool DDA>
 __device__ __forceinline__ void vp_start(const VpCtx& c, VpRay& r, int64_t ray) {
 #pragma clang fp contract(off)
   const VpArgs& a = c.a;
@@ -321,7 +334,7 @@ __device__ __forceinline__ void vp_start(const VpCtx& c, VpRay& r, int64_t ray) 
     r.phase = kVpDone;
     return;
   }
-  if (a.dgrid != nullptr) {  // VolumeProfileDDA: no trimming, the walk skips empty cells
+  if constexpr (DDA) {  // VolumeProfileDDA: no trimming, the walk skips empty cells
     r.tmin = tmin;
     r.tmax = tmax;
     r.tau = 0.0f;
@@ -350,12 +363,13 @@ __device__ __forceinline__ void vp_start(const VpCtx& c, VpRay& r, int64_t ray) 
   r.t = tmin;
   r.k = 0;
   if (r.t < r.tmax) r.phase = kVpTau;
-  else vp_depth_begin(c, r, ray);
+  else vp_depth_begin<DDA>(c, r, ray);
 }
 
 // Advances ray `ray` until it needs the extinction at a point (true, the point
 // in q) or has finished (false).  has / sigma: the extinction at the point the
 // previous call asked for.
+template <bool DDA>
 __device__ __forceinline__ bool vp_advance(const VpCtx& c, VpRay& r, int64_t ray, bool has, float sigma,
                                            float (&q)[3]) {
 #pragma clang fp contract(off)
@@ -368,7 +382,7 @@ __device__ __forceinline__ bool vp_advance(const VpCtx& c, VpRay& r, int64_t ray
           r.tau = r.tau + (sigma * a.density_scale) * a.step;
           r.t = r.t + a.step;
           if (r.tau > 20.0f || !(r.t < r.tmax) || ++r.k >= kVpMaxMarch) {
-            vp_depth_begin(c, r, ray);
+            vp_depth_begin<DDA>(c, r, ray);
             break;
           }
         }
@@ -399,43 +413,51 @@ __device__ __forceinline__ bool vp_advance(const VpCtx& c, VpRay& r, int64_t ray
         vp_point(r.x, r.wo, r.t, q);
         return true;
       case kVpTauDda:  // volume_profile_dda.h:53-77
-        if (has) {
-          has = false;
-          r.tau = r.tau + (sigma * a.density_scale) * a.step;
-          r.t = r.t + a.step;
-          if (r.tau > 20.0f || ++r.k >= kVpMaxMarch) {
-            vp_depth_begin(c, r, ray);
-            break;
-          }
-        }
-        if (vp_dda_walk(c, r, q)) return true;
-        vp_depth_begin(c, r, ray);
-        break;
-      case kVpDepthDda:  // volume_profile_dda.h:83-129
-        if (has) {
-          has = false;
-          r.ctau = r.ctau + (sigma * a.density_scale) * a.step;
-          float* o = a.out + ray * c.outw;
-          while (r.ctau * r.scale >= r.tcross) {
-            o[r.idx] = r.t;
-            ++r.idx;
-            if (r.idx >= a.ds) break;
-            r.scale = a.thr[r.idx];
-            r.tcross = vp_crossing(r.scale, r.tau);
-          }
-          bool stop = r.idx >= a.ds;
-          if (!stop) {
+        if constexpr (DDA) {
+          if (has) {
+            has = false;
+            r.tau = r.tau + (sigma * a.density_scale) * a.step;
             r.t = r.t + a.step;
-            stop = r.ctau > 20.0f || ++r.k >= kVpMaxMarch;
+            if (r.tau > 20.0f || ++r.k >= kVpMaxMarch) {
+              vp_depth_begin<DDA>(c, r, ray);
+              break;
+            }
           }
-          if (stop) {
-            vp_after_depth(c, r, ray);
-            break;
-          }
+          if (vp_dda_walk(c, r, q)) return true;
+          vp_depth_begin<DDA>(c, r, ray);
+          break;
+        } else {
+          return false;
         }
-        if (vp_dda_walk(c, r, q)) return true;
-        vp_after_depth(c, r, ray);
-        break;
+      case kVpDepthDda:  // volume_profile_dda.h:83-129
+        if constexpr (DDA) {
+          if (has) {
+            has = false;
+            r.ctau = r.ctau + (sigma * a.density_scale) * a.step;
+            float* o = a.out + ray * c.outw;
+            while (r.ctau * r.scale >= r.tcross) {
+              o[r.idx] = r.t;
+              ++r.idx;
+              if (r.idx >= a.ds) break;
+              r.scale = a.thr[r.idx];
+              r.tcross = vp_crossing(r.scale, r.tau);
+            }
+            bool stop = r.idx >= a.ds;
+            if (!stop) {
+              r.t = r.t + a.step;
+              stop = r.ctau > 20.0f || ++r.k >= kVpMaxMarch;
+            }
+            if (stop) {
+              vp_after_depth(c, r, ray);
+              break;
+            }
+          }
+          if (vp_dda_walk(c, r, q)) return true;
+          vp_after_depth(c, r, ray);
+          break;
+        } else {
+          return false;
+        }
       case kVpRm:  // raymarching_transmittance_trait.h
         if (has) {
           has = false;
@@ -511,8 +533,10 @@ struct VpGenArgs {
   GenNet net;
 };
 
-template <int MT, bool LDSW>
-__global__ __launch_bounds__(64 * gen_waves<MT>(), 1) void volume_profile_kernel(VpGenArgs ga) {
+// One block's rays (DDA: VolumeProfileDDA's marches, a compile-time choice so that
+// VolumeProfile's kernel carries none of the walk's state).
+template <int MT, bool LDSW, bool DDA>
+__device__ __forceinline__ void volume_profile_body(const VpGenArgs& ga) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   __shared__ int s_next;
   const VpArgs& a = ga.v;
@@ -552,7 +576,7 @@ __global__ __launch_bounds__(64 * gen_waves<MT>(), 1) void volume_profile_kernel
   for (;;) {
     for (;;) {
       if (ray >= 0 && !pending) {
-        pending = vp_advance(c, r, ray, has, sigma, q);
+        pending = vp_advance<DDA>(c, r, ray, has, sigma, q);
         has = false;
         if (!pending) ray = -1;
       }
@@ -566,7 +590,7 @@ __global__ __launch_bounds__(64 * gen_waves<MT>(), 1) void volume_profile_kernel
         const int k = base + __builtin_popcountll(want & below);
         if (k < nr) {
           ray = r_begin + k;
-          vp_start(c, r, ray);
+          vp_start<DDA>(c, r, ray);
           if (r.phase == kVpDone) ray = -1;
         } else {
           exhausted = true;
@@ -587,6 +611,16 @@ __global__ __launch_bounds__(64 * gen_waves<MT>(), 1) void volume_profile_kernel
   }
 }
 
+template <int MT, bool LDSW>
+__global__ __launch_bounds__(64 * gen_waves<MT>(), 1) void volume_profile_kernel(VpGenArgs ga) {
+  volume_profile_body<MT, LDSW, false>(ga);
+}
+
+template <int MT, bool LDSW>
+__global__ __launch_bounds__(64 * gen_waves<MT>(), 1) void volume_profile_dda_kernel(VpGenArgs ga) {
+  volume_profile_body<MT, LDSW, true>(ga);
+}
+
 // volume_profile.h:155-160 for the rows that reached a depth.
 struct VpFinishArgs {
   const float* albedo;
@@ -600,8 +634,12 @@ struct VpFinishArgs {
   float* out;
 };
 
-// 8-tile launcher of volume_profile_kernel (RDV_FIELD_PART 1).
+// 8-tile launcher of volume_profile_kernel (RDV_FIELD_PART 1); every launch of
+// volume_profile_dda_kernel (RDV_FIELD_PART 2) and its 8-tile launcher (RDV_FIELD_PART 3).
 int launch_volume_profile8(const VpGenArgs& a, int64_t items, int cu, int64_t lds, bool in_lds, hipStream_t stream);
+int launch_volume_profile_dda_any(const VpGenArgs& a, int64_t items, int cu, hipStream_t stream);
+int launch_volume_profile_dda8(const VpGenArgs& a, int64_t items, int cu, int64_t lds, bool in_lds,
+                               hipStream_t stream);
 
 #if RDV_FIELD_PART == 0
 __global__ __launch_bounds__(256) void volume_profile_finish_kernel(VpFinishArgs f) {
@@ -665,6 +703,7 @@ int launch_volume_profile(const rdv_mlp_desc& d, const MlpLayout& lay, const voi
   ga.packed = static_cast<const uint8_t*>(packed);
   gen_net(d, lay, &ga.net);
   // 32 rays per wave
+  if (dda_grid != nullptr) return launch_volume_profile_dda_any(ga, (nrays + 31) / 32, di.cu_count, stream);
   RDV_GEN_FIELD_DISPATCH(volume_profile_kernel, ga, (nrays + 31) / 32, di.cu_count, ga.net, stream,
                          launch_volume_profile8);
 }
@@ -681,8 +720,15 @@ int launch_volume_profile_finish(const rdv_volume_profile_desc& vp, const float*
   return RDV_OK;
 }
 
-#else
+#elif RDV_FIELD_PART == 1
 RDV_GEN_FIELD_DEFINE8(launch_volume_profile8, volume_profile_kernel, VpGenArgs)
+#elif RDV_FIELD_PART == 2
+int launch_volume_profile_dda_any(const VpGenArgs& a, int64_t items, int cu, hipStream_t stream) {
+  VpGenArgs ga = a;
+  RDV_GEN_FIELD_DISPATCH(volume_profile_dda_kernel, ga, items, cu, ga.net, stream, launch_volume_profile_dda8);
+}
+#elif RDV_FIELD_PART == 3
+RDV_GEN_FIELD_DEFINE8(launch_volume_profile_dda8, volume_profile_dda_kernel, VpGenArgs)
 #endif  // RDV_FIELD_PART
 
 }  // namespace rdv
