@@ -284,6 +284,42 @@ def test_sensor_jittered_volume_profile():
     _check(img.reshape(-1, vp.OUT), ws, ref, 20 * 14, 1, 1, 2, 1e-5, 1e-6, 1.0, True, "jittered sensor")
 
 
+def test_sensor_dda_non_cubic_grid_and_transform():
+    """Cameras >> VolumeProfileDDA with a non-cubic walked grid ([2, 5, 3]), a
+    turned, scaled and shifted transform and sample_index 1."""
+    sigma = 0.8
+    ext = _field(_const_layers(sigma))
+    maj = np.full((3, 3, 3), 1.2, np.float32)
+    dgrid = np.random.default_rng(21).uniform(0.2, 1.0, (2, 5, 3)).astype(np.float32)
+    dgrid[1, 2, 1] = 0.0
+    dgrid[0, 4, :] = 0.0
+    # mat4x3, column-major: a 90-degree turn about y with power-of-two scales and a shift, so that its
+    # inverse is exact in fp32 both here and in the kernel (a general rotation's inverse differs in the
+    # last bits between the two computations, and so would every position)
+    M = [0.0, 0.0, -2.0, 0.0, 0.5, 0.0, 1.0, 0.0, 0.0, 0.1, -0.2, 0.15]
+    thr = [0.8, 0.4, 0.2]
+    vp = rdv.VolumeProfileDDA(ext, rdv.TensorGrid(torch.from_numpy(maj[..., None]).cuda()),
+                              rdv.TensorGrid(torch.from_numpy(dgrid[..., None]).cuda()), rdv.Constant([1.0, 0.5]),
+                              rdv.Constant([0.4, 0.6]), thr, transform=rdv.mat4x3(*M), step_size=0.007,
+                              environment_samples=2, sample_index=1, g=-0.25, density_scale=1.4)
+    cam = rdv.Cameras(22, 16, WL.c4_pose().cuda())
+    RandomLibrary.seed(41)
+    img = (cam >> vp)().as_tensor("torch").cpu().numpy()
+    assert img.shape == (1, 16, 22, vp.OUT)
+    RandomLibrary.seed(41)
+    seeds = RandomLibrary.next_seeds()
+    rays = _render.camera_rays(cam, seeds=seeds).as_tensor("torch").reshape(-1, 6).cpu().numpy()
+    ref = V.volume_profile(rays, lambda p: np.full(p.shape[0], sigma, np.float32), maj, seeds, thr, 2,
+                           environment_samples=2, step_size=0.007, density_scale=1.4, g=-0.25, sample_index=1,
+                           transform=M, dda_grid=dgrid,
+                           albedo=lambda p: np.tile(np.float32([0.4, 0.6]), (p.shape[0], 1)),
+                           environment=lambda w: np.tile(np.float32([1.0, 0.5]), (w.shape[0], 1)))
+    v = ref["valid"] == 1
+    assert v.mean() > 0.2 and (~v).any()
+    ws = {k: t.cpu().numpy() for k, t in vp.__dict__["_rdv_ws"].items() if k != "key"}
+    _check(img.reshape(-1, vp.OUT), ws, ref, 22 * 16, len(thr), 2, 2, 1e-5, 1e-6, 1.0, True, "DDA sensor")
+
+
 def test_full_size_properties():
     """512 x 512 C4 camera rays through a constant medium: S is the closed form
     1 - exp(-sigma ds L) to the march's step, and the mean ratio-tracked
