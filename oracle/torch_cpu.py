@@ -4,7 +4,7 @@ oracle/__init__.py).  bench.py times these functions as its CPU baseline
 against the numpy oracle, which is what pins them.
 
 The reference itself cannot run here or on the GPU box (it needs the vulky
-package and a Vulkan device, SURVEY c1), so the baseline is this repository's
+package and a Vulkan device), so the baseline is this repository's
 own CPU statement of the same arithmetic, written the way a CPU user of torch
 would: fp32 GEMMs on fp16-rounded operands (LinearFast,
 src/rdv/shaders/maps/linear_fast.h:61-98: operands staged as float16, fp32

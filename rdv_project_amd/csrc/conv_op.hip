@@ -379,7 +379,7 @@ struct TileArgs {
 // The RSCK filter block [o0, o0 + 16 NT) x every K into LDS in fragment order
 // (as cv_stage_rows), each thread's groups kFiltBatch at a time; between the
 // loads and their conversion, `mid` runs (the first window's loads), so those
-// do not delay this round's waits.
+// do not delay this batch's waits.
 template <int NT, class Mid>
 __device__ void cv_stage_filter(const ConvArgs& a, int o0, int nkc, f32x4* sw, float* sb, Mid&& mid) {
   // group gi: four outputs 4 cg .. (cg = gi % 4 NT: output tile t = cg / 4, j = cg % 4) of rows
