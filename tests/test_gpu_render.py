@@ -68,7 +68,7 @@ def test_composite_kernel(n, S):
 def test_emission_absorption_small_image_matches_oracle():
     layers = WL.c4_mlp()
     cam = rdv.Cameras(24, 16, WL.c4_pose().cuda())
-    for samples in (32, 128):
+    for samples in (32, 96, 128):  # 96: a composited pair, then a single chunk
         img = (cam >> rdv.EmissionAbsorption(_field(layers), samples=samples))().as_tensor("torch")
         img = img.cpu().numpy().reshape(-1, 3)
         rays = R.camera_rays(24, 16, WL.c4_pose().numpy()).reshape(-1, 6)
