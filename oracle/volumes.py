@@ -311,8 +311,10 @@ def dda_march_ts(x, wo, tmin, tmax, step, grid: np.ndarray, cap: int = MAX_MARCH
     exit (= min of the three axis boundaries and tmax); then t = the exit and
     the walk steps along the axis whose boundary comes first (x, then y, then
     z on ties).  At most 4096 cells, while t < tmax, until the walk leaves the
-    grid; at most cap samples (the HIP kernel's bound).  Every operation is
-    rounded to float32 on its own."""
+    grid; at most cap samples (the HIP kernel's bound).  An axis whose direction
+    component is 0 never comes first (+inf boundary distance and increment: the
+    shader's stated intent; its arithmetic gives -inf there, and its march would
+    not end).  Every operation is rounded to float32 on its own."""
     grid = np.asarray(grid, F)
     D, H, W = grid.shape[:3]
     dim = [W, H, D]
@@ -330,8 +332,11 @@ def dda_march_ts(x, wo, tmin, tmax, step, grid: np.ndarray, cap: int = MAX_MARCH
             dstep[i] = 1 if wo[i] > 0 else (-1 if wo[i] < 0 else 0)
             inv = _f32(_f32(1) / wo[i])
             nb = _f32(_f32(_f32(_f32(cell[i]) + _f32(max(dstep[i], 0))) * cs) - _f32(1))
-            tma[i] = _f32(_f32(nb - x[i]) * inv)
-            tdl[i] = _f32(cs * _f32(abs(inv)))
+            if wo[i] == 0:  # never the first axis (the shader's stated intent; its arithmetic can give -inf)
+                tma[i], tdl[i] = F(np.inf), F(np.inf)
+            else:
+                tma[i] = _f32(_f32(nb - x[i]) * inv)
+                tdl[i] = _f32(cs * _f32(abs(inv)))
         ts = []
         t = tmin
         for _ in range(4096):

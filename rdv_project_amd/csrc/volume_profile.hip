@@ -223,7 +223,10 @@ __device__ __forceinline__ void vp_after_depth(const VpCtx& c, VpRay& r, int64_t
 
 // The DDA walk's start at tmin (volume_profile_dda.h:25-51): the entry cell (clamped into
 // the grid), the step signs, the distances to each axis' next cell boundary and their
-// increments (1 / 0 gives +-inf: that axis never comes first).
+// increments.  An axis whose direction component is 0 gets +inf for both, so it never comes
+// first, as the shader's comment intends: its arithmetic, (boundary - x) * (1 / +0), gives
+// -inf when x lies above the cell's lower boundary, and the walk would then stay at
+// t = -inf (the shader's loop would not end).
 __device__ __forceinline__ void vp_dda_setup(const VpCtx& c, VpRay& r) {
 #pragma clang fp contract(off)
   const VpArgs& a = c.a;
@@ -238,8 +241,9 @@ __device__ __forceinline__ void vp_dda_setup(const VpCtx& c, VpRay& r) {
     r.cell[i] = ci < 0 ? 0 : (ci > dim[i] - 1 ? dim[i] - 1 : ci);
     const float inv = 1.0f / r.wo[i];
     const float nb = (float(r.cell[i]) + fmaxf(float(vp_sign(r.wo[i])), 0.0f)) * cs - 1.0f;
-    r.p[i] = (nb - r.x[i]) * inv;
-    r.dl[i] = cs * fabsf(inv);
+    const bool still = r.wo[i] == 0.0f;
+    r.p[i] = still ? __builtin_huge_valf() : (nb - r.x[i]) * inv;
+    r.dl[i] = still ? __builtin_huge_valf() : cs * fabsf(inv);
   }
   r.t = r.tmin;
   r.walk = 0;

@@ -208,6 +208,34 @@ def test_dda_constant_extinction_matches_oracle(res, sparse, es):
         assert (plain["out"][:, 0] != ref["out"][:, 0]).mean() > 0.1
 
 
+def test_dda_rays_starting_inside_the_box():
+    """Origins inside [-1, 1]^3: the walk starts in the origin's own cell (tMin = 0)."""
+    sigma, sd = 0.6, 1
+    rng = np.random.default_rng(13)
+    o = rng.uniform(-0.95, 0.95, (700, 3))
+    w = rng.normal(size=(700, 3))
+    w /= np.linalg.norm(w, axis=1, keepdims=True)
+    w[:40, 0] = 0.0  # a direction parallel to two grid planes (its axis never comes first)
+    w[:40] /= np.linalg.norm(w[:40], axis=1, keepdims=True)
+    rays = np.concatenate([o, w], 1).astype(np.float32)
+    maj = np.full((2, 2, 2), 1.0, np.float32)
+    dgrid = np.random.default_rng(14).uniform(0.1, 1.0, (4, 3, 5)).astype(np.float32)
+    dgrid[2] = 0.0
+    vp = rdv.VolumeProfileDDA(_field(_const_layers(sigma)), rdv.TensorGrid(torch.from_numpy(maj[..., None]).cuda()),
+                              rdv.TensorGrid(torch.from_numpy(dgrid[..., None]).cuda()), rdv.Constant([1.0]),
+                              rdv.Constant([0.5]), [0.7, 0.3], step_size=0.005, environment_samples=1,
+                              density_scale=2.0)
+    seeds = (3, 1, 4, 1)
+    out, ws, n = _run(vp, rays, seeds)
+    ref = V.volume_profile(rays, lambda p: np.full(p.shape[0], sigma, np.float32), maj, seeds, [0.7, 0.3], sd,
+                           environment_samples=1, step_size=0.005, density_scale=2.0, dda_grid=dgrid,
+                           albedo=lambda p: np.full((p.shape[0], 1), 0.5, np.float32),
+                           environment=lambda d: np.ones((d.shape[0], 1), np.float32))
+    v = ref["valid"] == 1
+    assert v.mean() > 0.3 and (~v).any()
+    _check(out, ws, ref, n, 2, sd, 1, 1e-5, 1e-6, 1.0, True, "DDA rays from inside")
+
+
 def test_dda_mlp_extinction_matches_oracle():
     dims, res, ds = [3, 64, 64, 64, 1], 4, 3.0
     layers = _rand_field(dims, seed=77)

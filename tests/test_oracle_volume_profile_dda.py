@@ -86,6 +86,25 @@ def test_dda_skips_empty_cells(seed):
         assert grid[c[2], c[1], c[0]] > 0
 
 
+@pytest.mark.parametrize("axis", [0, 1, 2])
+def test_dda_zero_direction_component(axis):
+    """A direction parallel to one axis' planes: that axis never comes first, and
+    the walk matches the plane crossings of the other two (finite sample times)."""
+    rng = np.random.default_rng(40 + axis)
+    grid = np.ones((4, 3, 5), F)
+    for _ in range(4):
+        x = rng.uniform(-0.9, 0.9, 3).astype(F)
+        w = rng.normal(size=3)
+        w[axis] = 0.0
+        w = (w / np.linalg.norm(w)).astype(F)
+        tmin, tmax = V._box(x, w)
+        tmin = max(F(0), tmin)
+        step = F(0.013)
+        ts = V.dda_march_ts(x, w, tmin, tmax, step, grid)
+        assert np.isfinite(ts).all()
+        assert ts.size == sum(n for _, n in _expected(x, w, tmin, tmax, float(step), grid))
+
+
 def test_planted_march_without_reanchoring_is_caught():
     """A march that ignores the cell exits (VolumeProfile's plain march over the
     same interval) fails the per-cell count on a ray that crosses several cells."""
