@@ -621,9 +621,27 @@ def bench_volumes(steps, warmup):
             _lib.check(rc, "majorant grid")
 
     _, mev = _time_launches(launch_mg, max(steps, 20), warmup, prewarm_s=0.05)
+
+    # RaymarchingTransmittance over the same rays and extinction (fixed steps of 0.002, cut at tau > 16)
+    tarr = (C.c_float * 12)(1.0, 0.0, 0.0, 0.0, 1.0, 0.0, 0.0, 0.0, 1.0, 0.0, 0.0, 0.0)
+    tout = torch.empty(n, device="cuda")
+
+    def launch_rm(i):
+        rc = lib.rdv_raymarch_transmittance(C.byref(p.desc), C.c_void_p(packed.data_ptr()),
+                                            C.c_void_p(rays.data_ptr()), C.c_int64(n), tarr, C.c_float(0.002),
+                                            C.c_float(4.0), C.c_void_p(tout.data_ptr()), stream)
+        if rc != 0:
+            _lib.check(rc, "raymarching transmittance")
+
+    _, rev = _time_launches(launch_rm, max(steps, 20), warmup)
     return {
         "workload": "ratio tracking over 512x512 C4 camera rays, extinction 3->64->64->64->1 softplus (fp16 MFMA, "
                     "seed 11), density_scale 4, 8^3 voxel majorant from a 64^3 MajorantGrid",
+        "raymarch": {"workload": "RaymarchingTransmittance over the same rays and extinction, step 0.002, "
+                                 "density_scale 4 (fixed steps, cut at tau > 16)",
+                     "kernel": "raymarch_transmittance_kernel",
+                     "ms_per_call": round(rev, 4), "Mrays_per_s": round(n / (rev * 1e-3) / 1e6, 1),
+                     "mean_T": round(float(tout.double().mean()), 4)},
         "kernel": "ratiotracking_generic_kernel",
         "ms_per_call": round(ev, 4),
         "Mrays_per_s": round(n / (ev * 1e-3) / 1e6, 1),

@@ -136,6 +136,19 @@ def test_raymarching_transmittance_matches_reference_march():
     assert (ref < 1).any()
 
 
+def test_raymarching_transmittance_many_rays():
+    """64 x 48 camera rays (3,072) through a denser medium: every ray against the oracle's march."""
+    layers = WL.kaiming_uniform_f16([(64, 3), (64, 64), (64, 64), (1, 64)], seed=11)
+    ext = _field(layers, head="softplus")
+    cam = rdv.Cameras(64, 48, WL.c4_pose().cuda())
+    T = (cam >> rdv.RaymarchingTransmittance(ext, step_size=0.002, density_scale=4.0))()
+    T = T.as_tensor("torch").reshape(-1).cpu().numpy()
+    rays = cam().as_tensor("torch").reshape(-1, 6).cpu().numpy()
+    ref = R.raymarch_transmittance(rays, _np(layers), head="softplus", step=0.002, density_scale=4.0)
+    assert (ref < 1).mean() > 0.5 and (ref == 1).any()
+    _close(T, ref, 1e-4, 1e-6, "transmittance, 3072 rays")
+
+
 def test_raymarching_transmittance_transform_scale_and_cutoff():
     layers = WL.kaiming_uniform_f16([(64, 3), (64, 64), (64, 64), (1, 64)], seed=12)
     ext = _field(layers, head="softplus")
