@@ -225,11 +225,33 @@ __device__ __forceinline__ float wave_uniform(float v) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, v)));
 }
 
+// The march geometry of ray `ray`: p = (origin, w.x), q = (w.y, w.z, entry
+// distance, step); a step of -1 marks a ray that misses the box.
+__device__ __forceinline__ void ea_setup(const RenderArgs& a, int64_t ray, f32x4& p, f32x4& q) {
+  float o[3], w[3];
+  ea_ray(a, ray, o, w);
+  float t0, t1;
+  ray_box(o, w, t0, t1);
+  float dt = -1.0f;
+  if (!(t1 <= 0.0f || t0 > t1)) {
+    t0 = fmaxf(t0, 0.0f);
+    dt = (t1 - t0) / float(a.samples);
+  }
+  p = f32x4{o[0], o[1], o[2], w[0]};
+  q = f32x4{w[1], w[2], t0, dt};
+}
+
+// Rays whose geometry a block computes at once, one ray per thread, into LDS
+// (32 bytes each): the camera frame, slab test and step are then computed once
+// per ray instead of in all 64 lanes of the wave that marches it.
+constexpr int kEaBatch = 2048;
+
 template <class N>
 __global__ __launch_bounds__(kEaThreads, 1) void render_ea_kernel(RenderArgs a) {
   static_assert(N::kIn == 3 && N::kOut == 4, "the renderer evaluates a 3 -> 4 (density, RGB) field");
   __shared__ float sb[N::kBias];
   __shared__ half8 sw[N::kFrags * 64];
+  __shared__ f32x4 s_ray[2][kEaBatch];
   __shared__ int s_next;
   const int lane = threadIdx.x & 63;
   const int h = lane >> 5, col = lane & 31;
@@ -247,102 +269,105 @@ __global__ __launch_bounds__(kEaThreads, 1) void render_ea_kernel(RenderArgs a) 
     return __builtin_amdgcn_readfirstlane(t);
   };
   const int chunks = a.samples / 32;
-  for (int r = claim(); r < nr; r = claim()) {
-    const int64_t ray = r_begin + r;
-    float o[3], w[3];
-    ea_ray(a, ray, o, w);
-#pragma unroll
-    for (int i = 0; i < 3; ++i) {
-      o[i] = wave_uniform(o[i]);
-      w[i] = wave_uniform(w[i]);
-    }
-    float t0, t1;
-    ray_box(o, w, t0, t1);
-    float cr = 0.0f, cg = 0.0f, cb = 0.0f;
-    if (!(t1 <= 0.0f || t0 > t1)) {
-      t0 = wave_uniform(fmaxf(t0, 0.0f));
-      const float dt = wave_uniform((t1 - t0) / float(a.samples));
-      float Tin = 1.0f;
-      auto composite = [&](const f32x16& f) {
-        const float sigma = fast_softplus(f[0]);
-        const float ad = h == 0 ? sigma * dt : 0.0f;
-        const float incl = wave_scan_incl(ad, lane);
-        const float total = lane_value(incl, 31);
-        const float wgt = h == 0 ? Tin * __expf(-(incl - ad)) * (1.0f - __expf(-ad)) : 0.0f;
-        cr += wgt * fast_sigmoid(f[1]);
-        cg += wgt * fast_sigmoid(f[2]);
-        cb += wgt * fast_sigmoid(f[3]);
-        Tin = wave_uniform(Tin * __expf(-total));
-      };
-      // The two chunks of a pair in one pass: chunk b's rows 0..3 move from
-      // lanes 0..31 to lanes 32..63 (ds_bpermute: lane l reads lane l % 32),
-      // each lane half scans its own 32 samples, and chunk b starts from chunk
-      // a's transmittance.  Every sample's weight and colour are computed as by
-      // composite(a) then composite(b), in half the instructions; only the
-      // final sum over the lanes adds the per-lane colours in another order.
-      // The four moves are issued from inline assembly and waited for there:
-      // this compiler folded the four ds_bpermute builtins of one MFMA result
-      // into one (and its v_permlane32_swap builtin does not model the write
-      // to its second register).
-      auto composite_pair = [&](const f32x16& fa, const f32x16& fb) {
-        float b0, b1, b2, b3;
-        const int src = col << 2;
-        // fb comes straight from an MFMA: 24 wait states before an LDS
-        // instruction reads it (the compiler pads only its own instructions).
-        asm volatile(
-            "s_nop 7\n"
-            "s_nop 7\n"
-            "s_nop 7\n"
-            "ds_bpermute_b32 %0, %4, %5\n"
-            "ds_bpermute_b32 %1, %4, %6\n"
-            "ds_bpermute_b32 %2, %4, %7\n"
-            "ds_bpermute_b32 %3, %4, %8\n"
-            "s_waitcnt lgkmcnt(0)"
-            : "=&v"(b0), "=&v"(b1), "=&v"(b2), "=&v"(b3)
-            : "v"(src), "v"(fb[0]), "v"(fb[1]), "v"(fb[2]), "v"(fb[3]));
-        const float f[4] = {h == 0 ? fa[0] : b0, h == 0 ? fa[1] : b1, h == 0 ? fa[2] : b2, h == 0 ? fa[3] : b3};
-        const float sigma = fast_softplus(f[0]);
-        const float ad = sigma * dt;
-        const float incl = wave_scan_incl32(ad);
-        const float total_a = lane_value(incl, 31), total_b = lane_value(incl, 63);
-        const float tin_b = wave_uniform(Tin * __expf(-total_a));
-        const float wgt = (h == 0 ? Tin : tin_b) * __expf(-(incl - ad)) * (1.0f - __expf(-ad));
-        cr += wgt * fast_sigmoid(f[1]);
-        cg += wgt * fast_sigmoid(f[2]);
-        cb += wgt * fast_sigmoid(f[3]);
-        Tin = wave_uniform(tin_b * __expf(-total_b));
-      };
-      for (int c = 0; c + 1 < chunks; c += 2) {
-        const float ta = t0 + (float(32 * c + col) + 0.5f) * dt;
-        const float tb = t0 + (float(32 * c + 32 + col) + 0.5f) * dt;
-        const float pa[3] = {o[0] + ta * w[0], o[1] + ta * w[1], o[2] + ta * w[2]};
-        const float pb[3] = {o[0] + tb * w[0], o[1] + tb * w[1], o[2] + tb * w[2]};
-        f32x16 accA[N::kMaxMT], accB[N::kMaxMT];
-        half8 bA[N::kMaxKC], bB[N::kMaxKC];
-        const LdsWeights ws{sw + opaque_zero(), lane};
-        build_input<N>(pa, h, bA);
-        if (has_bias) run_pair<N, 0, true, true>(ws, pb, h, bA, bB, accA, accB, sb + opaque_zero());
-        else run_pair<N, 0, true, false>(ws, pb, h, bA, bB, accA, accB, sb);
-        composite_pair(accA[0], accB[0]);
+  // Batches of kEaBatch rays: every thread sets up its rays, then the waves
+  // claim them one by one; a barrier ends each batch (counter and ray slots
+  // are reused).
+  for (int base = 0; base < nr; base += kEaBatch) {
+    const int nb = nr - base < kEaBatch ? nr - base : kEaBatch;
+    for (int i = threadIdx.x; i < nb; i += kEaThreads) ea_setup(a, r_begin + base + i, s_ray[0][i], s_ray[1][i]);
+    if (threadIdx.x == 0) s_next = 0;
+    __syncthreads();
+    for (int r = claim(); r < nb; r = claim()) {
+      const int64_t ray = r_begin + base + r;
+      const f32x4 p4 = s_ray[0][r], q4 = s_ray[1][r];
+      const float o[3] = {wave_uniform(p4[0]), wave_uniform(p4[1]), wave_uniform(p4[2])};
+      const float w[3] = {wave_uniform(p4[3]), wave_uniform(q4[0]), wave_uniform(q4[1])};
+      const float t0 = wave_uniform(q4[2]), dt = wave_uniform(q4[3]);
+      float cr = 0.0f, cg = 0.0f, cb = 0.0f;
+      if (!(dt < 0.0f)) {
+        float Tin = 1.0f;
+        auto composite = [&](const f32x16& f) {
+          const float sigma = fast_softplus(f[0]);
+          const float ad = h == 0 ? sigma * dt : 0.0f;
+          const float incl = wave_scan_incl(ad, lane);
+          const float total = lane_value(incl, 31);
+          const float wgt = h == 0 ? Tin * __expf(-(incl - ad)) * (1.0f - __expf(-ad)) : 0.0f;
+          cr += wgt * fast_sigmoid(f[1]);
+          cg += wgt * fast_sigmoid(f[2]);
+          cb += wgt * fast_sigmoid(f[3]);
+          Tin = wave_uniform(Tin * __expf(-total));
+        };
+        // The two chunks of a pair in one pass: chunk b's rows 0..3 move from
+        // lanes 0..31 to lanes 32..63 (ds_bpermute: lane l reads lane l % 32),
+        // each lane half scans its own 32 samples, and chunk b starts from chunk
+        // a's transmittance.  Every sample's weight and colour are computed as by
+        // composite(a) then composite(b), in half the instructions; only the
+        // final sum over the lanes adds the per-lane colours in another order.
+        // The four moves are issued from inline assembly and waited for there:
+        // this compiler folded the four ds_bpermute builtins of one MFMA result
+        // into one (and its v_permlane32_swap builtin does not model the write
+        // to its second register).
+        auto composite_pair = [&](const f32x16& fa, const f32x16& fb) {
+          float b0, b1, b2, b3;
+          const int src = col << 2;
+          // fb comes straight from an MFMA: 24 wait states before an LDS
+          // instruction reads it (the compiler pads only its own instructions).
+          asm volatile(
+              "s_nop 7\n"
+              "s_nop 7\n"
+              "s_nop 7\n"
+              "ds_bpermute_b32 %0, %4, %5\n"
+              "ds_bpermute_b32 %1, %4, %6\n"
+              "ds_bpermute_b32 %2, %4, %7\n"
+              "ds_bpermute_b32 %3, %4, %8\n"
+              "s_waitcnt lgkmcnt(0)"
+              : "=&v"(b0), "=&v"(b1), "=&v"(b2), "=&v"(b3)
+              : "v"(src), "v"(fb[0]), "v"(fb[1]), "v"(fb[2]), "v"(fb[3]));
+          const float f[4] = {h == 0 ? fa[0] : b0, h == 0 ? fa[1] : b1, h == 0 ? fa[2] : b2, h == 0 ? fa[3] : b3};
+          const float sigma = fast_softplus(f[0]);
+          const float ad = sigma * dt;
+          const float incl = wave_scan_incl32(ad);
+          const float total_a = lane_value(incl, 31), total_b = lane_value(incl, 63);
+          const float tin_b = wave_uniform(Tin * __expf(-total_a));
+          const float wgt = (h == 0 ? Tin : tin_b) * __expf(-(incl - ad)) * (1.0f - __expf(-ad));
+          cr += wgt * fast_sigmoid(f[1]);
+          cg += wgt * fast_sigmoid(f[2]);
+          cb += wgt * fast_sigmoid(f[3]);
+          Tin = wave_uniform(tin_b * __expf(-total_b));
+        };
+        for (int c = 0; c + 1 < chunks; c += 2) {
+          const float ta = t0 + (float(32 * c + col) + 0.5f) * dt;
+          const float tb = t0 + (float(32 * c + 32 + col) + 0.5f) * dt;
+          const float pa[3] = {o[0] + ta * w[0], o[1] + ta * w[1], o[2] + ta * w[2]};
+          const float pb[3] = {o[0] + tb * w[0], o[1] + tb * w[1], o[2] + tb * w[2]};
+          f32x16 accA[N::kMaxMT], accB[N::kMaxMT];
+          half8 bA[N::kMaxKC], bB[N::kMaxKC];
+          const LdsWeights ws{sw + opaque_zero(), lane};
+          build_input<N>(pa, h, bA);
+          if (has_bias) run_pair<N, 0, true, true>(ws, pb, h, bA, bB, accA, accB, sb + opaque_zero());
+          else run_pair<N, 0, true, false>(ws, pb, h, bA, bB, accA, accB, sb);
+          composite_pair(accA[0], accB[0]);
+        }
+        if (chunks & 1) {
+          const int c = chunks - 1;
+          const float ts = t0 + (float(32 * c + col) + 0.5f) * dt;
+          const float p[3] = {o[0] + ts * w[0], o[1] + ts * w[1], o[2] + ts * w[2]};
+          f32x16 fin[N::kMaxMT];
+          eval_chunk<N, true>(sw, sb, has_bias, lane, h, p, fin);
+          composite(fin[0]);
+        }
+        cr = wave_sum(cr);
+        cg = wave_sum(cg);
+        cb = wave_sum(cb);
       }
-      if (chunks & 1) {
-        const int c = chunks - 1;
-        const float ts = t0 + (float(32 * c + col) + 0.5f) * dt;
-        const float p[3] = {o[0] + ts * w[0], o[1] + ts * w[1], o[2] + ts * w[2]};
-        f32x16 fin[N::kMaxMT];
-        eval_chunk<N, true>(sw, sb, has_bias, lane, h, p, fin);
-        composite(fin[0]);
+      if (lane == 0) {
+        float* dst = a.image + ray * 3;
+        dst[0] = cr;
+        dst[1] = cg;
+        dst[2] = cb;
       }
-      cr = wave_sum(cr);
-      cg = wave_sum(cg);
-      cb = wave_sum(cb);
     }
-    if (lane == 0) {
-      float* dst = a.image + ray * 3;
-      dst[0] = cr;
-      dst[1] = cg;
-      dst[2] = cb;
-    }
+    __syncthreads();
   }
 }
 
