@@ -479,6 +479,7 @@ struct TransmittanceArgs {
   float M[12];        // mat4x3, column-major: linear columns 0..2, translation column 3
   float step, density_scale;
   float* out;         // [n]
+  int lane_rays;      // 1: one ray per MFMA column (raymarch_rays_lanes), 0: one ray per wave
 };
 
 // The reference marches sequentially (transmittance_rm):
@@ -494,7 +495,7 @@ struct TransmittanceArgs {
 // extinction at its sample position x (lanes l and l + 32 hold the same sample;
 // the value of lanes 0..31 is used).
 template <class Sigma>
-__device__ __forceinline__ void raymarch_rays(const TransmittanceArgs& a, int* s_next, Sigma&& sigma_of) {
+__device__ __forceinline__ void raymarch_rays_chunks(const TransmittanceArgs& a, int* s_next, Sigma&& sigma_of) {
   const int lane = threadIdx.x & 63;
   const int h = lane >> 5, col = lane & 31;
   const int64_t per_block = (a.nrays + gridDim.x - 1) / gridDim.x;
@@ -575,6 +576,122 @@ __device__ __forceinline__ void raymarch_rays(const TransmittanceArgs& a, int* s
     }
     if (lane == 0) a.out[ray] = T;
   }
+}
+
+// One ray of a lane-per-ray march (lanes l and l + 32 hold the same ray).
+struct MarchRay {
+  float x[3], sw[3];  // object-space position, step * w
+  float d, tau;       // distance left, optical depth
+  int k;              // steps taken
+};
+
+// The start of ray `ray`: the same fp32 operations as raymarch_rays_chunks
+// (false: the ray misses the box, T = 1).
+__device__ __forceinline__ bool march_start(const TransmittanceArgs& a, const float (&L)[9], int64_t ray,
+                                            MarchRay& r) {
+  const float* rr = a.rays + ray * 6;
+  const float xw[3] = {rr[0] - a.M[9], rr[1] - a.M[10], rr[2] - a.M[11]};
+  float w[3];
+#pragma unroll
+  for (int i = 0; i < 3; ++i) {  // L * v with L column-major
+    r.x[i] = L[i] * xw[0] + L[3 + i] * xw[1] + L[6 + i] * xw[2];
+    w[i] = L[i] * rr[3] + L[3 + i] * rr[4] + L[6 + i] * rr[5];
+  }
+  float tmin, tmax;
+  ray_box(r.x, w, tmin, tmax);
+  if (tmax <= 0.0f || tmin > tmax) return false;
+  tmin = fmaxf(0.0f, tmin);
+#pragma unroll
+  for (int i = 0; i < 3; ++i) {
+    float wt = w[i] * tmin;
+    asm volatile("" : "+v"(wt));  // x += w * tMin: product and sum rounded separately
+    r.x[i] = r.x[i] + wt;
+    r.sw[i] = a.step * w[i];
+    asm volatile("" : "+v"(r.sw[i]));  // the product is rounded on its own, as x += step * w
+  }
+  r.d = tmax - tmin;
+  r.tau = 0.0f;
+  r.k = 0;
+  return true;
+}
+
+// The same march with one ray per MFMA column: each lane takes one step of its
+// own ray per evaluation of the extinction chain, in the reference's order
+// (tau summed sequentially, so T is the reference's fp32 result up to the
+// extinction values).  A column whose ray ends claims the next ray of the
+// block's range at once.  No replay of the position updates: for launches with
+// several rays per column (the host picks this mode from the ray count); with
+// few rays per column a ray's steps would each wait for a whole chain, where
+// raymarch_rays_chunks takes 32 of them per chain.
+template <class Sigma>
+__device__ __forceinline__ void raymarch_rays_lanes(const TransmittanceArgs& a, int* s_next, Sigma&& sigma_of) {
+  const int lane = threadIdx.x & 63;
+  const int h = lane >> 5, col = lane & 31;
+  const int64_t per_block = (a.nrays + gridDim.x - 1) / gridDim.x;
+  const int64_t r_begin = int64_t(blockIdx.x) * per_block;
+  const int64_t r_end = r_begin + per_block < a.nrays ? r_begin + per_block : a.nrays;
+  const int nr = int(r_end > r_begin ? r_end - r_begin : 0);
+  float L[9];
+  inverse3(a.M, L);
+  MarchRay r;
+#pragma unroll
+  for (int i = 0; i < 3; ++i) r.x[i] = r.sw[i] = 0.0f;
+  r.d = r.tau = 0.0f;
+  r.k = 0;
+  int64_t ray = -1;        // the ray in this column (-1: none)
+  bool exhausted = false;  // the block's range has run dry
+  const uint64_t below = (uint64_t(1) << col) - 1;
+  auto finish = [&](float T) {
+    if (h == 0) a.out[ray] = T;
+    ray = -1;
+  };
+  for (;;) {
+    // Fill: columns without a ray take the next ones of the range.
+    for (;;) {
+      const bool idle = ray < 0 && !exhausted;
+      const uint64_t want = __builtin_amdgcn_ballot_w64(h == 0 && idle);
+      if (want == 0) break;
+      int base = 0;
+      if (lane == 0) base = atomicAdd(s_next, __builtin_popcountll(want));
+      base = __builtin_amdgcn_readfirstlane(base);
+      if (idle) {  // both halves see the same `want` bits of the h == 0 lanes
+        const int k = base + __builtin_popcountll(want & below);
+        if (k < nr) {
+          ray = r_begin + k;
+          if (!march_start(a, L, ray, r) || !(r.d > 0.0f)) finish(1.0f);  // no step: exp(-0)
+        } else {
+          exhausted = true;
+        }
+      }
+    }
+    if (__builtin_amdgcn_ballot_w64(h == 0 && ray >= 0) == 0) break;  // every column is out of work
+    float p[3];
+#pragma unroll
+    for (int i = 0; i < 3; ++i) p[i] = ray >= 0 ? r.x[i] : 0.0f;
+    float sigma = sigma_of(p);
+    sigma = __shfl(sigma, col);  // the value of lane col (row 0 of its column)
+    if (ray >= 0) {
+      const float ce = sigma * a.density_scale;
+      float inc = ce * a.step;
+      asm volatile("" : "+v"(inc));
+      r.tau = r.tau + inc;
+      if (r.tau > 16.0f) {
+        finish(0.0f);
+      } else {
+        r.d = r.d - a.step;
+#pragma unroll
+        for (int i = 0; i < 3; ++i) r.x[i] = r.x[i] + r.sw[i];
+        ++r.k;
+        if (!(r.d > 0.0f && r.k < 4096)) finish(expf(-r.tau));
+      }
+    }
+  }
+}
+
+template <class Sigma>
+__device__ __forceinline__ void raymarch_rays(const TransmittanceArgs& a, int* s_next, Sigma&& sigma_of) {
+  if (a.lane_rays) raymarch_rays_lanes(a, s_next, sigma_of);
+  else raymarch_rays_chunks(a, s_next, sigma_of);
 }
 
 template <class N, int HEAD_ACT>
@@ -1026,6 +1143,9 @@ int launch_raymarch_transmittance(const rdv_mlp_desc& d, const MlpLayout& lay, c
   a.step = step;
   a.density_scale = density_scale;
   a.out = out;
+  // One ray per MFMA column once every column of a full grid gets two rays or
+  // more (8 waves per block for the runtime-shaped kernels, at most).
+  a.lane_rays = nrays >= int64_t(2) * 32 * (fixed ? kRenderWaves : 8) * di.cu_count ? 1 : 0;
   if (!fixed) {
     TransmittanceGenArgs ga;
     ga.t = a;

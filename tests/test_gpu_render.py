@@ -4,8 +4,9 @@ oracle/render.py.
 Bars: rays within 2e-6 (fp32 geometry vs the float64 oracle); compositing and
 emission-absorption colours |C - ref| <= 1e-3 |ref| + 1e-5 (fp32 compositing,
 the stated tolerance); transmittance |T - ref| <= 1e-4 |ref| + 1e-6 (the
-reference's own march: identical sample positions and step counts, tau summed
-in a different order)."""
+reference's own march: identical sample positions and step counts; tau summed
+in the reference's order by the one-ray-per-column march of large launches, in
+another order by the one-ray-per-wave march)."""
 import math
 
 import numpy as np
@@ -201,6 +202,40 @@ def test_raymarching_transmittance_runtime_shaped_extinction(dims, head):
     ref = R.raymarch_transmittance(rays, _np(layers), head=head, step=0.004, density_scale=4.0)
     _close(T.reshape(-1).cpu().numpy(), ref, 1e-4, 1e-6, f"transmittance {dims}")
     assert (ref < 0.99).any() and (ref == 1).any()
+
+
+def _lane_mode_rays(waves):
+    """Camera rays enough for the one-ray-per-column march: two rays or more for
+    every MFMA column of a full grid (one block per CU of `waves` waves)."""
+    cu = torch.cuda.get_device_properties(0).multi_processor_count
+    need = 2 * 32 * waves * cu
+    w = 512
+    return rdv.Cameras(w, -(-need // w) + 3, WL.c4_pose().cuda())
+
+
+@pytest.mark.parametrize("dims", [None, [3, 32, 32, 1]])
+def test_raymarching_transmittance_one_ray_per_column(dims):
+    """Large launches march one ray per MFMA column (tau summed sequentially, as
+    the reference does): 1,200 sampled rays against the oracle's march, and the
+    same rays marched by a small launch (one ray per wave, 32 steps per chain)."""
+    if dims is None:  # the compile-time 3 -> 64^3 -> 1 kernel, 16 waves per block
+        layers, waves = WL.kaiming_uniform_f16([(64, 3), (64, 64), (64, 64), (1, 64)], seed=11), 16
+    else:  # runtime-shaped kernel, 8 waves per block
+        layers, waves = _rand_field(dims, seed=dims[1] + 7), 8
+    ext = _field(layers, head="softplus")
+    rt = rdv.RaymarchingTransmittance(ext, step_size=0.002, density_scale=4.0)
+    cam = _lane_mode_rays(waves)
+    rays = cam().as_tensor("torch").reshape(-1, 6).contiguous()
+    T = rt(rdv.wrap(rays)).as_tensor("torch").reshape(-1)
+    assert torch.isfinite(T).all() and bool(((T >= 0) & (T <= 1)).all())
+    pick = torch.from_numpy(np.random.default_rng(3).choice(rays.shape[0], 1200, replace=False)).cuda()
+    sub = rays[pick].contiguous()
+    T_small = rt(rdv.wrap(sub)).as_tensor("torch").reshape(-1)  # 1,200 rays: one ray per wave
+    ref = R.raymarch_transmittance(sub.cpu().numpy(), _np(layers), head="softplus", step=0.002, density_scale=4.0)
+    assert (ref < 0.99).mean() > 0.3 and (ref == 1).any()
+    got = T[pick].cpu().numpy()
+    _close(got, ref, 1e-4, 1e-6, "one ray per column against the oracle")
+    _close(got, T_small.cpu().numpy(), 1e-4, 1e-6, "one ray per column against one ray per wave")
 
 
 def test_grid_evaluator_dispatch_matches_call():
