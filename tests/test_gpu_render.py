@@ -125,6 +125,30 @@ def test_c4_full_config():
     _close(flat, split, 1e-3, 1e-5, "C4 fused vs split")
 
 
+def test_c4_whole_image_against_cpu_restatement():
+    """Every pixel of the C4 frame against oracle/torch_cpu.render_ea (the
+    numpy oracle's computation as torch-CPU fp32 GEMMs on fp16-rounded
+    operands, checked against that oracle by test_oracle_torch_cpu), in
+    8,192-ray chunks."""
+    import os
+    from oracle import torch_cpu as TC
+    layers = WL.c4_mlp()
+    cam = rdv.Cameras(WL.C4_WIDTH, WL.C4_HEIGHT, WL.c4_pose().cuda())
+    img = (cam >> rdv.EmissionAbsorption(_field(layers), samples=WL.C4_SAMPLES))().as_tensor("torch")
+    flat = img.reshape(-1, 3).cpu().numpy()
+    rays = cam().as_tensor("torch").reshape(-1, 6).cpu()
+    threads = torch.get_num_threads()
+    torch.set_num_threads(max(1, min(16, len(os.sched_getaffinity(0)))))
+    try:
+        packed = TC.pack_layers(layers)
+        ref = torch.cat([TC.render_ea(rays[i:i + 8192], packed, WL.C4_SAMPLES)
+                         for i in range(0, rays.shape[0], 8192)]).numpy()
+    finally:
+        torch.set_num_threads(threads)
+    assert (ref == 0).any() and (ref > 0.1).any()
+    _close(flat, ref, 1e-3, 1e-5, "C4 whole image vs the CPU restatement")
+
+
 def test_raymarching_transmittance_matches_reference_march():
     layers = WL.kaiming_uniform_f16([(64, 3), (64, 64), (64, 64), (1, 64)], seed=11)
     ext = _field(layers, head="softplus")
