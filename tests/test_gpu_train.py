@@ -3,8 +3,9 @@ oracle/train.py.
 
 Bar: loss within 1e-4 relative; per layer, ||dW - ref||_F <= 1e-2 ||ref||_F and
 likewise for db (the GPU rounds g = 2 (y - t) and every propagated gradient to
-fp16, the oracle keeps float64).  At the full C5 size: the loss equals the mean
-squared error of the forward path, and the gradient of the whole set equals the
+fp16, the oracle keeps float64).  At the full C5 size: the same bars against
+the torch-CPU restatement of the oracle, the loss equals the mean squared error
+of the forward path, and the gradient of the whole set equals the
 point-weighted mean of the gradients of its two halves.
 
 The forward sums in a different fp32 order than the oracle, so a few
@@ -121,3 +122,38 @@ def test_c5_full_config_properties():
         ew = (torch.linalg.norm(fw.double() - cw) / torch.linalg.norm(cw)).item()
         eb = (torch.linalg.norm(fb.double() - cb) / torch.linalg.norm(cb)).item()
         assert ew <= 1e-4 and eb <= 1e-4, f"layer {l}: halves disagree ({ew:.3g}, {eb:.3g})"
+
+
+@pytest.mark.timeout(300)  # ~3 TFLOP of CPU work: ~15 s on 16 cores, longer on fewer
+def test_c5_full_config_against_cpu_restatement():
+    """The whole C5 step (4,194,304 points) against oracle/torch_cpu.train_step
+    (the oracle's computation as torch-CPU fp32 with autograd, checked against
+    it by test_oracle_torch_cpu), summed over 262,144-point chunks weighted by
+    their share of the points; the bars of the oracle comparisons above."""
+    import os
+    from oracle import torch_cpu as TC
+    x, t, layers = WL.c5()
+    n = x.shape[0]
+    m = _chain(layers)
+    loss, grads = rdv.mse_backward(m, x.cuda(), t.cuda())
+    loss = loss.item()
+    grads = [(dw.cpu().double().numpy(), db.cpu().double().numpy()) for dw, db in grads]
+    threads = torch.get_num_threads()
+    torch.set_num_threads(max(1, min(16, len(os.sched_getaffinity(0)))))
+    try:
+        params = [(w.float().clone().requires_grad_(True), b.float().clone().requires_grad_(True))
+                  for w, b in layers]
+        ref_loss = 0.0
+        ref = [(np.zeros(w.shape), np.zeros(b.shape)) for w, b in params]
+        xf = x.float()
+        for i in range(0, n, 262144):
+            c = min(262144, n - i)
+            lc = TC.train_step(xf[i:i + c], t[i:i + c], params)
+            ref_loss += lc.item() * c / n
+            for (rw, rb), (w, b) in zip(ref, params):
+                rw += w.grad.double().numpy() * (c / n)
+                rb += b.grad.double().numpy() * (c / n)
+    finally:
+        torch.set_num_threads(threads)
+    _check(loss, [(torch.from_numpy(dw), torch.from_numpy(db)) for dw, db in grads], ref_loss, ref,
+           "C5 full size vs the CPU restatement")
