@@ -256,10 +256,8 @@ __global__ __launch_bounds__(kEaThreads, 1) void render_ea_kernel(RenderArgs a) 
   const int lane = threadIdx.x & 63;
   const int h = lane >> 5, col = lane & 31;
   const int64_t nrays = ea_ray_count(a);
-  const int64_t per_block = (nrays + gridDim.x - 1) / gridDim.x;
-  const int64_t r_begin = int64_t(blockIdx.x) * per_block;
-  const int64_t r_end = r_begin + per_block < nrays ? r_begin + per_block : nrays;
-  const int nr = int(r_end > r_begin ? r_end - r_begin : 0);
+  const BlockRays br(nrays, false);
+  const int nr = br.count;
   const bool has_bias = (reinterpret_cast<const MlpPackHeader*>(a.packed)->flags & kMlpHasBias) != 0;
   stage_weights<N, kEaThreads>(a.packed, a.lay, sb, sw, &s_next);
 
@@ -274,11 +272,19 @@ __global__ __launch_bounds__(kEaThreads, 1) void render_ea_kernel(RenderArgs a) 
   // are reused).
   for (int base = 0; base < nr; base += kEaBatch) {
     const int nb = nr - base < kEaBatch ? nr - base : kEaBatch;
-    for (int i = threadIdx.x; i < nb; i += kEaThreads) ea_setup(a, r_begin + base + i, s_ray[0][i], s_ray[1][i]);
+    for (int i = threadIdx.x; i < nb; i += kEaThreads) {
+      const int64_t ray = br.ray(base + i);
+      if (ray < nrays) {
+        ea_setup(a, ray, s_ray[0][i], s_ray[1][i]);
+      } else {  // past the last ray: nothing to march, nothing to write
+        s_ray[0][i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        s_ray[1][i] = f32x4{0.0f, 0.0f, 0.0f, -1.0f};
+      }
+    }
     if (threadIdx.x == 0) s_next = 0;
     __syncthreads();
     for (int r = claim(); r < nb; r = claim()) {
-      const int64_t ray = r_begin + base + r;
+      const int64_t ray = br.ray(base + r);
       const f32x4 p4 = s_ray[0][r], q4 = s_ray[1][r];
       const float o[3] = {wave_uniform(p4[0]), wave_uniform(p4[1]), wave_uniform(p4[2])};
       const float w[3] = {wave_uniform(p4[3]), wave_uniform(q4[0]), wave_uniform(q4[1])};
@@ -360,7 +366,7 @@ __global__ __launch_bounds__(kEaThreads, 1) void render_ea_kernel(RenderArgs a) 
         cg = wave_sum(cg);
         cb = wave_sum(cb);
       }
-      if (lane == 0) {
+      if (lane == 0 && ray < nrays) {
         float* dst = a.image + ray * 3;
         dst[0] = cr;
         dst[1] = cg;
@@ -498,10 +504,8 @@ template <class Sigma>
 __device__ __forceinline__ void raymarch_rays_chunks(const TransmittanceArgs& a, int* s_next, Sigma&& sigma_of) {
   const int lane = threadIdx.x & 63;
   const int h = lane >> 5, col = lane & 31;
-  const int64_t per_block = (a.nrays + gridDim.x - 1) / gridDim.x;
-  const int64_t r_begin = int64_t(blockIdx.x) * per_block;
-  const int64_t r_end = r_begin + per_block < a.nrays ? r_begin + per_block : a.nrays;
-  const int nr = int(r_end > r_begin ? r_end - r_begin : 0);
+  const BlockRays br(a.nrays);
+  const int nr = br.count;
   float L[9];
   inverse3(a.M, L);
   auto claim = [&]() {
@@ -510,7 +514,8 @@ __device__ __forceinline__ void raymarch_rays_chunks(const TransmittanceArgs& a,
     return __builtin_amdgcn_readfirstlane(t);
   };
   for (int r = claim(); r < nr; r = claim()) {
-    const int64_t ray = r_begin + r;
+    const int64_t ray = br.ray(r);
+    if (ray >= a.nrays) continue;
     const float* rr = a.rays + ray * 6;
     const float xw[3] = {rr[0] - a.M[9], rr[1] - a.M[10], rr[2] - a.M[11]};
     float x[3], w[3];
@@ -627,10 +632,8 @@ template <class Sigma>
 __device__ __forceinline__ void raymarch_rays_lanes(const TransmittanceArgs& a, int* s_next, Sigma&& sigma_of) {
   const int lane = threadIdx.x & 63;
   const int h = lane >> 5, col = lane & 31;
-  const int64_t per_block = (a.nrays + gridDim.x - 1) / gridDim.x;
-  const int64_t r_begin = int64_t(blockIdx.x) * per_block;
-  const int64_t r_end = r_begin + per_block < a.nrays ? r_begin + per_block : a.nrays;
-  const int nr = int(r_end > r_begin ? r_end - r_begin : 0);
+  const BlockRays br(a.nrays);
+  const int nr = br.count;
   float L[9];
   inverse3(a.M, L);
   MarchRay r;
@@ -657,8 +660,9 @@ __device__ __forceinline__ void raymarch_rays_lanes(const TransmittanceArgs& a, 
       if (idle) {  // both halves see the same `want` bits of the h == 0 lanes
         const int k = base + __builtin_popcountll(want & below);
         if (k < nr) {
-          ray = r_begin + k;
-          if (!march_start(a, L, ray, r) || !(r.d > 0.0f)) finish(1.0f);  // no step: exp(-0)
+          ray = br.ray(k);
+          if (ray >= a.nrays) ray = -1;  // past the last ray: claim again
+          else if (!march_start(a, L, ray, r) || !(r.d > 0.0f)) finish(1.0f);  // no step: exp(-0)
         } else {
           exhausted = true;
         }
@@ -854,10 +858,8 @@ __global__ __launch_bounds__(64 * gen_waves<MT>(), 1) void ratiotracking_generic
   if (threadIdx.x == 0) s_next = 0;
   __syncthreads();
   const int act = g.act[g.L - 1];
-  const int64_t per_block = (a.nrays + gridDim.x - 1) / gridDim.x;
-  const int64_t r_begin = int64_t(blockIdx.x) * per_block;
-  const int64_t r_end = r_begin + per_block < a.nrays ? r_begin + per_block : a.nrays;
-  const int nr = int(r_end > r_begin ? r_end - r_begin : 0);
+  const BlockRays br(a.nrays);
+  const int nr = br.count;
   float L[9];
   inverse3(a.M, L);
 
@@ -892,8 +894,9 @@ __global__ __launch_bounds__(64 * gen_waves<MT>(), 1) void ratiotracking_generic
       if (idle) {  // both halves see the same `want` bits of the h == 0 lanes
         const int k = base + __builtin_popcountll(want & below);
         if (k < nr) {
-          ray = r_begin + k;
-          if (!ratio_start(a, L, ray, r)) finish(1.0f);
+          ray = br.ray(k);
+          if (ray >= a.nrays) ray = -1;  // past the last ray: claim again
+          else if (!ratio_start(a, L, ray, r)) finish(1.0f);
         } else {
           exhausted = true;
         }
@@ -933,10 +936,8 @@ __global__ __launch_bounds__(64 * gen_waves<MT>(), 1) void render_ea_generic_ker
   const int lane = threadIdx.x & 63;
   const int h = lane >> 5, col = lane & 31;
   const int64_t nrays = ea_ray_count(a);
-  const int64_t per_block = (nrays + gridDim.x - 1) / gridDim.x;
-  const int64_t r_begin = int64_t(blockIdx.x) * per_block;
-  const int64_t r_end = r_begin + per_block < nrays ? r_begin + per_block : nrays;
-  const int nr = int(r_end > r_begin ? r_end - r_begin : 0);
+  const BlockRays br(nrays, false);
+  const int nr = br.count;
   const bool has_bias = (reinterpret_cast<const MlpPackHeader*>(a.packed)->flags & kMlpHasBias) != 0;
   const half8* w0;
   const float* b0;
@@ -950,7 +951,8 @@ __global__ __launch_bounds__(64 * gen_waves<MT>(), 1) void render_ea_generic_ker
   };
   const int chunks = a.samples / 32;
   for (int r = claim(); r < nr; r = claim()) {
-    const int64_t ray = r_begin + r;
+    const int64_t ray = br.ray(r);
+    if (ray >= nrays) continue;
     float o[3], w[3];
     ea_ray(a, ray, o, w);
 #pragma unroll

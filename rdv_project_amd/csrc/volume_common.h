@@ -9,6 +9,41 @@
 
 namespace rdv {
 
+// A block's share of the n rays of a launch of G blocks.  Rays are taken in units
+// of 32 consecutive rays (one ray each when a block's share is below 256 rays, so
+// that small launches still spread over every block); G consecutive units form a
+// group, and block b takes unit (b + 37 k) mod G of group k.  Every block thus gets
+// rays from every part of a camera image: the work of a ray follows its path
+// through the box, and contiguous ranges of image rows gave the blocks at the
+// centre of the C4 frame up to 38% more fixed steps than the mean.  A unit keeps
+// neighbouring rays together, so the rays a wave claims at once stay coherent.
+// Slots of the last group may name rays >= n, which the kernels skip.  With
+// spread = false a block takes the contiguous range b ceil(n / G) + k instead (the
+// emission-absorption renderer, whose work per ray hardly varies: there the spread
+// order measured 2.5% slower).
+struct BlockRays {
+  int64_t n;
+  int g, b, shift;  // shift < 0: contiguous ranges
+  int count;        // slots of every block
+  __device__ explicit BlockRays(int64_t nrays, bool spread = true)
+      : n(nrays), g(int(gridDim.x)), b(int(blockIdx.x)) {
+    const int64_t per = (nrays + g - 1) / g;
+    if (!spread) {
+      shift = -1;
+      count = int(per);
+      return;
+    }
+    shift = per >= 256 ? 5 : 0;
+    const int64_t unit = int64_t(g) << shift;
+    count = int(((nrays + unit - 1) / unit) << shift);
+  }
+  __device__ int64_t ray(int k) const {
+    if (shift < 0) return int64_t(b) * count + k;
+    const int64_t grp = k >> shift;
+    return ((grp * g + (b + 37 * grp) % g) << shift) + (k & ((1 << shift) - 1));
+  }
+};
+
 // math_library.h:48-57: slab test against [-1, 1]^3.
 // Every operation rounded on its own: a contracted -x * inv +- s moves the exit
 // distance by an ulp against the voxel exits computed from the same ray, which

@@ -554,10 +554,8 @@ __device__ __forceinline__ void volume_profile_body(const VpGenArgs& ga) {
   if (threadIdx.x == 0) s_next = 0;
   __syncthreads();
   const int act = g.act[g.L - 1];
-  const int64_t per_block = (a.nrays + gridDim.x - 1) / gridDim.x;
-  const int64_t r_begin = int64_t(blockIdx.x) * per_block;
-  const int64_t r_end = r_begin + per_block < a.nrays ? r_begin + per_block : a.nrays;
-  const int nr = int(r_end > r_begin ? r_end - r_begin : 0);
+  const BlockRays br(a.nrays);
+  const int nr = br.count;
   float L[9];
   inverse3(a.M, L);
   float ldo[3];
@@ -593,9 +591,13 @@ __device__ __forceinline__ void volume_profile_body(const VpGenArgs& ga) {
       if (idle) {  // both halves see the same `want` bits of the h == 0 lanes
         const int k = base + __builtin_popcountll(want & below);
         if (k < nr) {
-          ray = r_begin + k;
-          vp_start<DDA>(c, r, ray);
-          if (r.phase == kVpDone) ray = -1;
+          ray = br.ray(k);
+          if (ray >= a.nrays) {
+            ray = -1;  // past the last ray: claim again
+          } else {
+            vp_start<DDA>(c, r, ray);
+            if (r.phase == kVpDone) ray = -1;
+          }
         } else {
           exhausted = true;
         }
