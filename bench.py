@@ -710,9 +710,9 @@ def main() -> int:
         x1, l1 = WL.c1()
         w1, e1, k1 = bench_mlp(x1, l1, ["relu"] * 4 + ["none"], None, max(args.steps // 2, 10), args.warmup)
         extras["C1_fused_mlp"] = {
-            "Mpoints_per_s": round(x1.shape[0] / (w1 * 1e-3) / 1e6, 1),
-            "us_per_call": round(w1 * 1e3, 3),
+            "Mpoints_per_s": round(x1.shape[0] / (e1 * 1e-3) / 1e6, 1),
             "kernel_us": round(e1 * 1e3, 3),
+            "wall_us_per_call": round(w1 * 1e3, 3),
             "TFLOP_s": round(C1_FLOP_PER_POINT * x1.shape[0] / (e1 * 1e-3) / 1e12, 2),
             "kernel": k1,
         }

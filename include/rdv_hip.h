@@ -319,6 +319,30 @@ int rdv_cameras_rays(const rdv_camera_desc* cam, const float* poses, float* rays
 int rdv_cameras_rays_jittered(const rdv_camera_desc* cam, const float* poses, const uint32_t* seeds, float* rays,
                               void* stream);
 
+/* ----------------------------------------------------- batched grid evaluation */
+#define RDV_GRID_MAX_RANK 8
+
+/* rays[i] = the camera ray of the index vector indices[i] = (cam, y, x), for a
+ * device int32 [n, 3] batch: the batch branch of Grid.__call__ on a Cameras
+ * grid (src/rdv/maths/__init__.py:104-119,
+ * src/rdv/shaders/grids/batch_grid_evaluator.h, rendering/cameras.h:1-20).
+ * seeds == NULL: pixel centres; else 4 host words, and row i draws its
+ * sub-pixel position from thread i's generator (the batch row is the
+ * reference batch evaluator's thread index).  cam outside [0, n_cams) gives a
+ * row of NaN; y and x are used as given.  n may be 0. */
+int rdv_cameras_rays_at(const rdv_camera_desc* cam, const float* poses, const int32_t* indices, int64_t n,
+                        const uint32_t* seeds, float* rays, void* stream);
+
+/* out[i, :] = values[cell(indices[i]), :] for a grid of `rank` dimensions
+ * (shape: host array) whose cells hold `width` fp32 values, row-major with the
+ * last dimension fastest (grid_library.h:3-16), and a device int32 [n, rank]
+ * batch of index vectors: the batch branch of Grid.__call__ over materialised
+ * grid values (TensorGrid's forward, src/rdv/shaders/grids/tensor_grid.h,
+ * behind BatchGridEvaluator, src/rdv/maths/__init__.py:815-844).  An index
+ * outside its dimension gives a row of NaN.  n may be 0. */
+int rdv_grid_gather(const float* values, int32_t rank, const int64_t* shape, int32_t width, const int32_t* indices,
+                    int64_t n, float* out, void* stream);
+
 /* out[t * per_thread + k] = the k-th random() value of thread t of a dispatch
  * whose seeds are `seeds` (4 host words): the reference's per-thread generator
  * (three Tausworthe steps and an LCG, GPU Gems 3 ch. 37), spawned from the

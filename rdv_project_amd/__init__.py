@@ -13,6 +13,7 @@ deferreds), the Map / Grid / TensorOperation families and their evaluators.  Com
 (librdv_hip.so); there is no CPU fallback.
 """
 from .core import (
+    MemoryLocation,
     RDVObject,
     ensure_on_rdv,
     is_on_rdv,
@@ -97,6 +98,13 @@ from ._train import mse_backward
 from .rendering import (
     Cameras,
     EmissionAbsorption,
+    EnvironmentSamplerTrait,
+    EnvironmentTrait,
+    ExtinctionTrait,
+    MajorantTrait,
+    RatiotrackingTransmittanceTrait,
+    RaymarchingTransmittanceTrait,
+    ScatteringAlbedoTrait,
     RatiotrackingTransmittance,
     RaymarchingTransmittance,
     VolumeProfile,

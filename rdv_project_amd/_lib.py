@@ -154,6 +154,9 @@ class MajorantGridDesc(C.Structure):
     ]
 
 
+GRID_MAX_RANK = 8
+
+
 class RDVError(RuntimeError):
     """A HIP runtime failure reported by the library."""
 
@@ -179,6 +182,10 @@ _SIGNATURES = {
     "rdv_cameras_rays": (C.c_int, [C.POINTER(CameraDesc), C.c_void_p, C.c_void_p, C.c_void_p]),
     "rdv_cameras_rays_jittered": (C.c_int, [C.POINTER(CameraDesc), C.c_void_p, C.POINTER(C.c_uint32), C.c_void_p,
                                             C.c_void_p]),
+    "rdv_cameras_rays_at": (C.c_int, [C.POINTER(CameraDesc), C.c_void_p, C.c_void_p, C.c_int64,
+                                      C.POINTER(C.c_uint32), C.c_void_p, C.c_void_p]),
+    "rdv_grid_gather": (C.c_int, [C.c_void_p, C.c_int32, C.POINTER(C.c_int64), C.c_int32, C.c_void_p, C.c_int64,
+                                  C.c_void_p, C.c_void_p]),
     "rdv_random_uniform": (C.c_int, [C.POINTER(C.c_uint32), C.c_int64, C.c_int32, C.c_void_p, C.c_void_p]),
     "rdv_ratiotracking_transmittance": (C.c_int, [C.POINTER(MlpDesc), C.c_void_p, C.POINTER(RatiotrackingDesc),
                                                   C.c_void_p, C.c_void_p, C.c_int64, C.c_void_p, C.c_void_p]),

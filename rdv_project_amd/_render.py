@@ -5,7 +5,10 @@ rdv_volume_profile).
 
 Reference: Grid.__call__ (src/rdv/maths/__init__.py:77-103) evaluates every cell
 of a grid in row-major order into a per-class cached [*shape, OUT] buffer; a
-Sensor (maths:252-271) applies its map to each cell's value.
+Sensor (maths:252-271) applies its map to each cell's value.  With a batch of
+index vectors (maths:104-119, BatchGridEvaluator) only those cells are
+evaluated, one thread per index vector (rdv_cameras_rays_at, rdv_grid_gather
+and the map kernels over the gathered rows).
 """
 from __future__ import annotations
 
@@ -424,3 +427,117 @@ def evaluate_grid(g: Grid, out: RDVObject | None = None) -> RDVObject:
         out.as_tensor("torch").copy_(v.as_tensor("torch").reshape(out.shape))
         return out
     return v
+
+
+# ------------------------------------------------------ batched evaluation
+
+
+def _batch_indices(g: Grid, batch) -> tuple[torch.Tensor, tuple, int]:
+    """The batch as a contiguous int32 [rows, IN] device tensor, its leading
+    shape and row count.  The reference reads the batch as int32 index vectors
+    (BatchGridEvaluator's FixArray[INT32, IN]); other integer types are
+    converted, floating-point batches raise TypeError."""
+    b = wrap(batch)
+    t = b.as_tensor("torch")
+    if t.dtype.is_floating_point or t.dtype == torch.bool or t.dtype.is_complex:
+        raise TypeError(f"grid indices must be integers, got {t.dtype}")
+    rank = len(g.shape)
+    assert len(t.shape) >= 1 and int(t.shape[-1]) == rank, \
+        f"the batch's last dimension ({int(t.shape[-1]) if len(t.shape) else None}) must be the grid's IN ({rank})"
+    lead = tuple(int(v) for v in t.shape[:-1])
+    rows = math.prod(lead)
+    if t.dtype != torch.int32:
+        if rows and (int(t.min()) < -(1 << 31) or int(t.max()) >= (1 << 31)):
+            raise AssertionError("grid indices must fit in int32")
+        t = t.to(torch.int32)
+    return t.contiguous().reshape(rows, rank), lead, rows
+
+
+def _batch_rays(cam: Cameras, idx: torch.Tensor, rows: int, out_ptr: int, seeds) -> None:
+    d = camera_desc(cam)
+    _lib.check(_lib.load().rdv_cameras_rays_at(C.byref(d), C.c_void_p(_poses(cam).data_ptr()),
+                                               C.c_void_p(idx.data_ptr()), C.c_int64(rows),
+                                               _seed_array(seeds) if seeds is not None else None,
+                                               C.c_void_p(out_ptr), C.c_void_p(current_stream_handle())), "Cameras")
+
+
+def _node_buffer(node, key: str, shape) -> torch.Tensor:
+    """A per-node device buffer reused while its shape is unchanged."""
+    shape = tuple(int(s) for s in shape)
+    buf = node.__dict__.get(key)
+    if buf is None or tuple(buf.shape) != shape:
+        buf = torch.empty(shape, dtype=torch.float32, device=device())
+        node.__dict__[key] = buf
+    return buf
+
+
+def _batch_values(g: Grid, idx: torch.Tensor, rows: int, out_ptr: int, ctx: dict) -> None:
+    """g at the rows index vectors of idx, into fp32 [rows, OUT] at out_ptr."""
+    from .grids import _GridNode, grid_values
+    if isinstance(g, Cameras):
+        seeds = None
+        if g.pixel_jitter:
+            from .types import RandomLibrary
+            seeds = RandomLibrary.next_seeds()
+        _batch_rays(g, idx, rows, out_ptr, seeds)
+        return
+    if isinstance(g, Sensor):
+        m = g.map
+        if isinstance(g.grid, Cameras):
+            cam = g.grid
+            # one dispatch's seeds for the camera and the map, as in the full-grid sensor
+            from .types import RandomLibrary
+            seeds = RandomLibrary.next_seeds()
+            rays = _node_buffer(g, "_rdv_batch_rays", (max(rows, 1), 6))
+            if rows:
+                _batch_rays(cam, idx, rows, rays.data_ptr(), seeds if cam.pixel_jitter else None)
+            skip = 2 if cam.pixel_jitter else 0
+            if rows == 0:
+                return
+            if isinstance(m, EmissionAbsorption):
+                render_ea_rays(m, rays.data_ptr(), out_ptr, rows)
+            elif isinstance(m, RaymarchingTransmittance):
+                raymarch_ptrs(m, rays.data_ptr(), out_ptr, rows)
+            elif isinstance(m, VolumeProfile):
+                volume_profile_ptrs(m, rays.data_ptr(), out_ptr, rows, seeds=seeds, rng_skip=skip)
+            elif isinstance(m, RatiotrackingTransmittance):
+                ratiotracking_ptrs(m, rays.data_ptr(), out_ptr, rows, seeds=seeds, rng_skip=skip)
+            else:
+                _chain.launch_map_rows(m, rays.data_ptr(), out_ptr, rows)
+            return
+        width = g.grid.OUT
+        if width is None:
+            raise RuntimeError("Generic arguments could not be deduced: the sensor's grid OUT is unknown")
+        inner = _node_buffer(g, "_rdv_batch_in", (max(rows, 1), int(width)))
+        _batch_values(g.grid, idx, rows, inner.data_ptr(), ctx)
+        if rows == 0:
+            return
+        if isinstance(m, EmissionAbsorption):
+            render_ea_rays(m, inner.data_ptr(), out_ptr, rows)
+        else:
+            _chain.launch_map_rows(m, inner.data_ptr(), out_ptr, rows)
+        return
+    # a grid whose values this build materialises (TensorGrid, barriers,
+    # convolutions, resampling, majorant grids, ...): its values, gathered
+    v = grid_values(g, ctx) if isinstance(g, _GridNode) else evaluate_grid(g)
+    vt = v.as_tensor("torch")
+    if vt.dtype != torch.float32 or not vt.is_contiguous():
+        vt = vt.to(torch.float32).contiguous()
+    rank = len(g.shape)
+    width = int(vt.numel() // max(1, math.prod(g.shape)))
+    shape = (C.c_int64 * rank)(*[int(s) for s in g.shape])
+    _lib.check(_lib.load().rdv_grid_gather(C.c_void_p(vt.data_ptr()), C.c_int32(rank), shape, C.c_int32(width),
+                                           C.c_void_p(idx.data_ptr()), C.c_int64(rows), C.c_void_p(out_ptr),
+                                           C.c_void_p(current_stream_handle())), "Grid batch")
+
+
+def evaluate_grid_batch(g: Grid, batch) -> RDVObject:
+    """g at a batch of index vectors [..., IN] -> [..., OUT] fp32, in an output
+    buffer cached per grid class and batch shape (maths:104-119)."""
+    if g.OUT is None:
+        raise RuntimeError("Generic arguments could not be deduced: the grid's OUT is unknown")
+    idx, lead, rows = _batch_indices(g, batch)
+    out = _cached(("batch", id(type(g)), int(g.OUT)), (*lead, int(g.OUT)))
+    with launch_scope():
+        _batch_values(g, idx, rows, out.device_ptr, {})
+    return out

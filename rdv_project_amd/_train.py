@@ -48,14 +48,15 @@ def _check_grads(grads, layers) -> None:
                 raise TypeError(f"grads[{i}] {what} must be a GPU tensor, got device {t.device}")
 
 
-def mse_backward(m: Map, x, target, grads=None):
+def mse_backward(m: Map, x, target, grads=None, loss=None):
     """Loss and gradients of mean((m(x) - target)^2) with respect to every
     layer's weight and bias.  x: [n, in] (fp16, or fp32 rounded to fp16 as
     LinearFast does), target: [n, out] fp32.  Returns (loss, [(dW, db), ...])
-    with fp32 dW [out, in] and db [out] per layer, in chain order; `grads`
-    may supply those output tensors (contiguous fp32 GPU tensors of exactly
-    those shapes, else TypeError).  The loss tensor is allocated on the first
-    call for a chain and device and reused after that."""
+    with a 0-d fp32 loss tensor and fp32 dW [out, in] and db [out] per layer,
+    in chain order.  Every call returns fresh tensors unless the caller passes
+    them: `grads` (contiguous fp32 GPU tensors of exactly those shapes) and
+    `loss` (a 0-d or 1-element contiguous fp32 GPU tensor), else TypeError.
+    Passing both makes a steady-state call allocate nothing."""
     xt = torch.as_tensor(x)
     tt = torch.as_tensor(target)
     assert xt.dim() == 2 and tt.dim() == 2 and xt.shape[0] == tt.shape[0], "x [n, in] and target [n, out]"
@@ -64,6 +65,8 @@ def mse_backward(m: Map, x, target, grads=None):
     assert tt.shape[1] == p.out_features, f"target has {tt.shape[1]} columns, the chain outputs {p.out_features}"
     if grads is not None:
         _check_grads(grads, p.layers)
+    if loss is not None:
+        _check_loss(loss)
     packed = _chain.packed_params(m, p)
     xh = xt.to(device=device(), dtype=torch.float16).contiguous()
     th = tt.to(device=device(), dtype=torch.float32).contiguous()
@@ -75,7 +78,8 @@ def mse_backward(m: Map, x, target, grads=None):
     if grads is None:
         grads = [(torch.empty(l.OUT, l.IN, dtype=torch.float32, device=device()),
                   torch.empty(l.OUT, dtype=torch.float32, device=device())) for l in p.layers]
-    loss = _loss_buffer(m, xh.device)
+    if loss is None:
+        loss = torch.empty((), dtype=torch.float32, device=device())
     dws = _lib.void_ptr_array([g[0].data_ptr() for g in grads])
     dbs = _lib.void_ptr_array([g[1].data_ptr() for g in grads])
     with launch_scope():
@@ -86,11 +90,11 @@ def mse_backward(m: Map, x, target, grads=None):
     return loss, grads
 
 
-def _loss_buffer(m: Map, dev) -> torch.Tensor:
-    """The chain's loss scalar, reused across calls (each call overwrites it, as
-    the reference's evaluators reuse their output buffers)."""
-    cached = getattr(m, "_rdv_loss", None)
-    if cached is None or cached.device != dev:
-        cached = torch.empty((), dtype=torch.float32, device=dev)
-        m._rdv_loss = cached
-    return cached
+def _check_loss(loss) -> None:
+    """A caller-supplied loss buffer: one contiguous fp32 element on the GPU."""
+    if not isinstance(loss, torch.Tensor):
+        raise TypeError("loss must be a torch tensor")
+    if loss.dtype != torch.float32 or loss.numel() != 1 or not loss.is_contiguous():
+        raise TypeError(f"loss must be one contiguous float32 element, got {loss.dtype} {list(loss.shape)}")
+    if loss.device.type != "cuda":
+        raise TypeError(f"loss must be a GPU tensor, got device {loss.device}")

@@ -42,6 +42,7 @@ SOURCES = [
     "mlp_pack.hip",
     "mlp_f32.hip",
     "tensor_data.hip",
+    "grid_batch.hip",
 ]
 
 ARCH = os.environ.get("RDV_OFFLOAD_ARCH", "gfx950")

@@ -70,6 +70,10 @@ int launch_train_step_static(const rdv_mlp_desc& d, const MlpLayout& lay, const 
                              hipStream_t stream);
 int launch_camera_rays(const rdv_camera_desc& c, const float* poses, const uint32_t* seeds, float* rays,
                        hipStream_t stream);
+int launch_cameras_rays_at(const rdv_camera_desc& c, const float* poses, const int32_t* idx, int64_t n,
+                           const uint32_t* seeds, float* rays, hipStream_t stream);
+int launch_grid_gather(const float* values, int rank, const int64_t* shape, int width, const int32_t* idx, int64_t n,
+                       float* out, hipStream_t stream);
 int launch_random_uniform(const uint32_t* seeds, int64_t n_threads, int per_thread, float* out, hipStream_t stream);
 int launch_ratiotracking(const rdv_mlp_desc& d, const MlpLayout& lay, const void* packed,
                          const rdv_ratiotracking_desc& rt, const float* majorant, const float* rays, int64_t nrays,
@@ -445,6 +449,36 @@ int rdv_cameras_rays_jittered(const rdv_camera_desc* cam, const float* poses, co
   if (int64_t(cam->n_cams) * cam->height * cam->width >= (int64_t(1) << 31))
     return fail(RDV_ERR_INVALID, "a jittered dispatch holds fewer than 2^31 cells (the generator's thread index is an int)");
   return launch_camera_rays(*cam, poses, seeds, rays, static_cast<hipStream_t>(stream));
+}
+
+int rdv_cameras_rays_at(const rdv_camera_desc* cam, const float* poses, const int32_t* indices, int64_t n,
+                        const uint32_t* seeds, float* rays, void* stream) {
+  int rc = check_camera(cam);
+  if (rc != RDV_OK) return rc;
+  if (n < 0 || n >= (int64_t(1) << 31))
+    return fail(RDV_ERR_INVALID, "the batch holds fewer than 2^31 index vectors (the generator's thread index is an int)");
+  if (n == 0) return RDV_OK;
+  if (!poses || !indices || !rays) return fail(RDV_ERR_INVALID, "rdv_cameras_rays_at: NULL pointer argument");
+  return launch_cameras_rays_at(*cam, poses, indices, n, seeds, rays, static_cast<hipStream_t>(stream));
+}
+
+int rdv_grid_gather(const float* values, int32_t rank, const int64_t* shape, int32_t width, const int32_t* indices,
+                    int64_t n, float* out, void* stream) {
+  if (rank < 1 || rank > RDV_GRID_MAX_RANK)
+    return fail(RDV_ERR_INVALID, "grid rank must be in [1, " + std::to_string(RDV_GRID_MAX_RANK) + "], got " +
+                                     std::to_string(rank));
+  if (!shape) return fail(RDV_ERR_INVALID, "rdv_grid_gather: NULL shape");
+  int64_t cells = 1;
+  for (int d = 0; d < rank; ++d) {
+    if (shape[d] < 1) return fail(RDV_ERR_INVALID, "grid dimensions must be >= 1");
+    if (cells > (int64_t(1) << 40) / shape[d]) return fail(RDV_ERR_INVALID, "grid too large");
+    cells *= shape[d];
+  }
+  if (width < 1) return fail(RDV_ERR_INVALID, "width must be >= 1");
+  if (n < 0 || n > ((int64_t(1) << 40) / width)) return fail(RDV_ERR_INVALID, "batch size out of range");
+  if (n == 0) return RDV_OK;
+  if (!values || !indices || !out) return fail(RDV_ERR_INVALID, "rdv_grid_gather: NULL pointer argument");
+  return launch_grid_gather(values, rank, shape, width, indices, n, out, static_cast<hipStream_t>(stream));
 }
 
 int rdv_random_uniform(const uint32_t* seeds, int64_t n_threads, int32_t per_thread, float* out, void* stream) {

@@ -155,6 +155,17 @@ struct VpCtx {
   int outw;
 };
 
+// A ray without a sample: valid 0, and zeros where the albedo and environment
+// maps would read its sample position and directions, so those maps never see
+// uninitialised workspace memory.
+__device__ __forceinline__ void vp_invalid(const VpArgs& a, int64_t ray) {
+  a.valid[ray] = 0;
+  float* sp = a.spos + ray * 3;
+  sp[0] = sp[1] = sp[2] = 0.0f;
+  float* ed = a.env_dirs + ray * a.es * 3;
+  for (int i = 0; i < 3 * a.es; ++i) ed[i] = 0.0f;
+}
+
 // The next environment sample's set-up, or the ray's last outputs after the last one.
 __device__ __forceinline__ void vp_env_next(const VpCtx& c, VpRay& r, int64_t ray) {
   const VpArgs& a = c.a;
@@ -191,7 +202,7 @@ __device__ __forceinline__ void vp_after_depth(const VpCtx& c, VpRay& r, int64_t
   r.S = 1.0f - expf(-r.tau);
   o[c.outw - 1] = r.S;
   if (r.idx <= 0) {
-    a.valid[ray] = 0;
+    vp_invalid(a, ray);
     r.phase = kVpDone;
     return;
   }
@@ -334,7 +345,7 @@ __device__ __forceinline__ void vp_start(const VpCtx& c, VpRay& r, int64_t ray) 
   ray_box(r.x, r.wo, tmin, tmax);
   tmin = fmaxf(0.0f, tmin);
   if (!(tmax > 0.0f && tmin <= tmax)) {
-    a.valid[ray] = 0;
+    vp_invalid(a, ray);
     r.phase = kVpDone;
     return;
   }

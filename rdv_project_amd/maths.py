@@ -96,9 +96,9 @@ X = Identity()
 
 class Constant(Map):
     """f(x) = data for every row, whatever the input width (reference:
-    maths:1659-1668, shaders/maps/constant.h).  data: [..., OUT]; its last row
-    of OUT values is the constant (the reference copies the buffer's first OUT
-    floats)."""
+    maths:1659-1668, shaders/maps/constant.h).  data: [..., OUT]; the constant
+    is the first OUT floats of the buffer (its first row), which is what the
+    reference's shader copies; further rows are ignored."""
 
     def __init__(self, data) -> None:
         if not isinstance(data, RDVObject):
@@ -198,14 +198,20 @@ class Grid(Component, Generic[_IN, _OUT]):
         return NotImplemented
 
     def __call__(self, *args, **kwargs):
-        """Every cell in row-major order into a cached [*shape, OUT] buffer;
-        keyword arguments bind deferred names for the call (maths:77-103)."""
-        if args:
-            raise NotImplementedError("batched grid evaluation (Grid.__call__(indices)) is outside this build")
+        """With no argument, every cell in row-major order into a cached
+        [*shape, OUT] buffer (maths:77-103).  With one argument, a batch of
+        index vectors [..., IN] (integers; the grid's IN-sized index in the
+        last dimension): the grid at those indices only, into a cached
+        [..., OUT] buffer, one thread per index vector (maths:104-119,
+        BatchGridEvaluator).  Keyword arguments bind deferred names for the
+        call."""
+        assert len(args) <= 1, "Grid.__call__ takes at most one batch of indices"
         if kwargs:
             DeferredLibrary.bind(**kwargs)
         try:
             from . import _render
+            if args:
+                return _render.evaluate_grid_batch(self, args[0])
             return _render.evaluate_grid(self)
         finally:
             if kwargs:

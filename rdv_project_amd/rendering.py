@@ -7,6 +7,11 @@
   VolumeProfile              reference domain/volumes.py:503-550 (Map[6, DS + 3 SD + 4])
   EmissionAbsorption         build-defined (Map[6, 3]): the MLP-in-the-loop
                              renderer of the benchmark configuration
+  ExtinctionTrait, MajorantTrait, RatiotrackingTransmittanceTrait,
+  RaymarchingTransmittanceTrait, ScatteringAlbedoTrait, EnvironmentTrait,
+  EnvironmentSamplerTrait    reference domain/volumes.py:7-120: the keyword
+                             constructors that hold, cast and bind a volume
+                             node's component maps
 Grids compose with maps (`Cameras(...) >> RaymarchingTransmittance(m)`) into a
 Sensor; calling the sensor renders every pixel on the GPU.
 """
@@ -18,7 +23,7 @@ import torch
 
 from .core import RDVObject, wrap
 from .maths import Grid, Map
-from .types import _MatBase, mat4x3
+from .types import Code, Generic, Generics, _MatBase, generic_value, mat4x3
 
 
 class Cameras(Grid[3, 6]):
@@ -62,7 +67,95 @@ def _as_mat4x3(t) -> mat4x3:
     return mat4x3(*vals)
 
 
-class RaymarchingTransmittance(Map[6, 1]):
+# ------------------------------------------------------------------ traits
+
+
+def _bound(node, name: str):
+    """The value bound to generic `name` on node: by its class, its own
+    attribute, or a match() made earlier in the same constructor."""
+    v = generic_value(node, name)
+    if v is None:
+        v = node.__dict__.get("_rdv_pending", {}).get(name)
+    return v
+
+
+class ExtinctionTrait(Code, Generic[Generics.EXTINCTION]):
+    """Holds `extinction`, cast to a Map[3, 1]; binds EXTINCTION to its type
+    (reference: volumes.py:7-19)."""
+
+    def __init__(self, *, extinction, **kwargs) -> None:
+        extinction = extinction.cast(Map[3, 1])
+        self.match(Generics.EXTINCTION, type(extinction))
+        self.extinction = extinction
+        super().__init__(**kwargs)
+
+
+class EnvironmentSamplerTrait(Code, Generic[Generics.ENVIRONMENT_SAMPLER, Generics.SPECTRAL_DIM]):
+    """Holds `environment_sampler`, cast to a Map[6, SPECTRAL_DIM + 4]; binds
+    SPECTRAL_DIM from its width when still open (reference: volumes.py:22-41)."""
+
+    def __init__(self, *, environment_sampler, **kwargs) -> None:
+        spectral_dim = _bound(self, "SPECTRAL_DIM")
+        if spectral_dim is None and environment_sampler.OUT is not None:
+            spectral_dim = environment_sampler.OUT - 4
+        environment_sampler = environment_sampler.cast(Map[6, None if spectral_dim is None else spectral_dim + 4])
+        self.match(Generics.ENVIRONMENT_SAMPLER, type(environment_sampler))
+        self.match(Generics.SPECTRAL_DIM, spectral_dim)
+        self.environment_sampler = environment_sampler
+        super().__init__(**kwargs)
+
+
+class EnvironmentTrait(Code, Generic[Generics.ENVIRONMENT, Generics.SPECTRAL_DIM]):
+    """Holds `environment`, cast to a Map[3, SPECTRAL_DIM]; binds SPECTRAL_DIM
+    from its width when still open (reference: volumes.py:44-63)."""
+
+    def __init__(self, *, environment, **kwargs) -> None:
+        spectral_dim = _bound(self, "SPECTRAL_DIM")
+        if spectral_dim is None:
+            spectral_dim = environment.OUT
+        environment = environment.cast(Map[3, spectral_dim])
+        self.match(Generics.ENVIRONMENT, type(environment))
+        self.match(Generics.SPECTRAL_DIM, spectral_dim)
+        self.environment = environment
+        super().__init__(**kwargs)
+
+
+class ScatteringAlbedoTrait(Code, Generic[Generics.SCATTERING_ALBEDO, Generics.SPECTRAL_DIM]):
+    """Holds `scattering_albedo`, cast to a Map[3, SPECTRAL_DIM]; binds
+    SPECTRAL_DIM from its width when still open (reference: volumes.py:66-85)."""
+
+    def __init__(self, *, scattering_albedo, **kwargs) -> None:
+        spectral_dim = _bound(self, "SPECTRAL_DIM")
+        if spectral_dim is None:
+            spectral_dim = scattering_albedo.OUT
+        scattering_albedo = scattering_albedo.cast(Map[3, spectral_dim])
+        self.match(Generics.SCATTERING_ALBEDO, type(scattering_albedo))
+        self.match(Generics.SPECTRAL_DIM, spectral_dim)
+        self.scattering_albedo = scattering_albedo
+        super().__init__(**kwargs)
+
+
+class MajorantTrait(Code, Generic[Generics.MAJORANT]):
+    """Holds `majorant`: a VoxelMajorantField, or a Grid[3, 1] wrapped as one,
+    cast to a Map[6, 2] (reference: volumes.py:88-102)."""
+
+    def __init__(self, *, majorant, **kwargs) -> None:
+        majorant = _as_majorant_field(majorant).cast(Map[6, 2])
+        self.match(Generics.MAJORANT, type(majorant))
+        self.majorant = majorant
+        super().__init__(**kwargs)
+
+
+class RatiotrackingTransmittanceTrait(ExtinctionTrait, MajorantTrait):
+    """Extinction and majorant: what ratio tracking needs (reference:
+    volumes.py:105-111)."""
+
+
+class RaymarchingTransmittanceTrait(ExtinctionTrait):
+    """Extinction: what a fixed-step raymarch needs (reference: volumes.py:114-120)."""
+
+
+class RaymarchingTransmittance(Map[6, 1], RaymarchingTransmittanceTrait):
     """T(x, w) along a ray through the box [-1,1]^3 of the object space given by
     `transform` (mat4x3, column-major: three linear columns, then the translation),
     marched with fixed steps: tau += extinction(x) * density_scale * step_size,
@@ -76,7 +169,7 @@ class RaymarchingTransmittance(Map[6, 1]):
     OUT = 1
 
     def __init__(self, extinction: Map, transform=None, step_size: float = 0.002, density_scale: float = 1.0) -> None:
-        self.extinction = extinction.cast(Map[3, 1])  # TypeError for any other width (volumes.py:16)
+        super().__init__(extinction=extinction)  # TypeError for any other width (volumes.py:16)
         self.transform = mat4x3(1.0, 0.0, 0.0, 0.0, 1.0, 0.0, 0.0, 0.0, 1.0, 0.0, 0.0, 0.0) \
             if transform is None else _as_mat4x3(transform)
         self.step_size = float(step_size)
@@ -129,7 +222,7 @@ def _as_majorant_field(majorant) -> VoxelMajorantField:
     raise NotImplementedError("majorant must be a VoxelMajorantField or a Grid[3, 1]")
 
 
-class RatiotrackingTransmittance(Map[6, 1]):
+class RatiotrackingTransmittance(Map[6, 1], RatiotrackingTransmittanceTrait):
     """T(x, w) along a ray through the box [-1,1]^3 of the object space given by
     `transform`, estimated by ratio tracking against a voxel majorant field:
     free flights of -log(1 - random()) / (majorant * density_scale) capped at
@@ -145,8 +238,7 @@ class RatiotrackingTransmittance(Map[6, 1]):
     OUT = 1
 
     def __init__(self, extinction: Map, majorant, transform=None, density_scale: float = 1.0) -> None:
-        self.extinction = extinction.cast(Map[3, 1])  # TypeError for any other width (volumes.py:16)
-        self.majorant = _as_majorant_field(majorant).cast(Map[6, 2])
+        super().__init__(extinction=extinction, majorant=majorant)
         self.transform = mat4x3(1.0, 0.0, 0.0, 0.0, 1.0, 0.0, 0.0, 0.0, 1.0, 0.0, 0.0, 0.0) \
             if transform is None else _as_mat4x3(transform)
         self.density_scale = float(density_scale)
@@ -160,7 +252,8 @@ class RatiotrackingTransmittance(Map[6, 1]):
         _render.ratiotracking_ptrs(self, x_ptr, y_ptr, rows)
 
 
-class VolumeProfile(Map):
+class VolumeProfile(Map, RatiotrackingTransmittanceTrait, RaymarchingTransmittanceTrait, ScatteringAlbedoTrait,
+                    EnvironmentTrait, Generic[Generics.DEPTH_SAMPLES]):
     """Per-ray features of a participating medium for a learned renderer
     (reference: volumes.py:503-550, shaders/volumes/volume_profile.h:1-167).
     For a ray (x, w) [6] in the object space of `transform` (the box [-1,1]^3),
@@ -192,16 +285,13 @@ class VolumeProfile(Map):
                  transmittance_threshold: list, density_scale: float = 1.0, transform=None,
                  light_direction=(0.0, 1.0, 0.0), light_intensity=None, g: float = 0.0, step_size: float = 0.001,
                  environment_samples: int = 4, sample_index: int = 0, nee_near_distance: float = 0.05) -> None:
-        # trait order of the reference (volumes.py:7-120): extinction, majorant,
+        # the traits in the reference's order (volumes.py:7-120): extinction, majorant,
         # scattering albedo (fixes SPECTRAL_DIM when the map's width is known), environment
-        self.extinction = extinction.cast(Map[3, 1])
-        self.majorant = _as_majorant_field(majorant).cast(Map[6, 2])
-        spectral_dim = scattering_albedo.OUT
-        if spectral_dim is None:
-            spectral_dim = environment.OUT
-        self.scattering_albedo = scattering_albedo.cast(Map[3, spectral_dim])
-        self.environment = environment.cast(Map[3, spectral_dim])
+        super().__init__(extinction=extinction, majorant=majorant, environment=environment,
+                         scattering_albedo=scattering_albedo)
+        spectral_dim = _bound(self, "SPECTRAL_DIM")
         depth_samples = len(transmittance_threshold)
+        self.match(Generics.DEPTH_SAMPLES, depth_samples)
         self.spectral_dim = None if spectral_dim is None else int(spectral_dim)
         self.depth_samples = depth_samples
         self.OUT = None if spectral_dim is None else 4 + spectral_dim * 3 + depth_samples

@@ -93,3 +93,78 @@ def test_vectors_and_matrices():
 def test_dispatch_rejects_non_main():
     with pytest.raises(TypeError):
         rdv.dispatch(_chain([3, 4]), 32)
+
+
+def test_volume_traits_are_public_and_bind_their_maps():
+    for name in ["ExtinctionTrait", "MajorantTrait", "RatiotrackingTransmittanceTrait",
+                 "RaymarchingTransmittanceTrait", "ScatteringAlbedoTrait", "EnvironmentTrait",
+                 "EnvironmentSamplerTrait", "MemoryLocation"]:
+        assert hasattr(rdv, name), name
+    ext = _chain([3, 64, 64, 1])
+    rt = rdv.RaymarchingTransmittance(ext)
+    assert isinstance(rt, rdv.RaymarchingTransmittanceTrait) and isinstance(rt, rdv.ExtinctionTrait)
+    assert rdv.Generics.EXTINCTION(rt) is type(ext) and rt.extinction is ext
+    maj = rdv.TensorGrid(torch.ones(2, 2, 2, 1))
+    rtt = rdv.RatiotrackingTransmittance(ext, maj)
+    assert isinstance(rtt, rdv.RatiotrackingTransmittanceTrait) and isinstance(rtt, rdv.MajorantTrait)
+    assert isinstance(rtt.majorant, rdv.VoxelMajorantField) and rdv.Generics.MAJORANT(rtt) is rdv.VoxelMajorantField
+    vp = rdv.VolumeProfile(ext, maj, rdv.Constant(torch.ones(1, 2)), rdv.Constant(torch.ones(1, 2)), [0.5, 0.2, 0.1])
+    for t in (rdv.RatiotrackingTransmittanceTrait, rdv.RaymarchingTransmittanceTrait, rdv.ScatteringAlbedoTrait,
+              rdv.EnvironmentTrait):
+        assert isinstance(vp, t)
+    assert rdv.Generics.SPECTRAL_DIM(vp) == 2 and rdv.Generics.DEPTH_SAMPLES(vp) == 3 and vp.OUT == 4 + 6 + 3
+    with pytest.raises(TypeError):  # the environment's width disagrees with the albedo's
+        rdv.VolumeProfile(ext, maj, rdv.Constant(torch.ones(1, 3)), rdv.Constant(torch.ones(1, 2)), [0.5])
+    with pytest.raises(TypeError):  # not a Map[3, 1]
+        rdv.RatiotrackingTransmittance(_chain([3, 64, 2]), maj)
+
+    class Custom(rdv.Map[6, 1], rdv.RaymarchingTransmittanceTrait):
+        def __init__(self, extinction):
+            super().__init__(extinction=extinction)
+
+    c = Custom(ext)
+    assert isinstance(c, rdv.ExtinctionTrait) and c.extinction is ext
+    with pytest.raises(TypeError):
+        rdv.ExtinctionTrait(extinction=_chain([3, 8, 2]))
+
+
+def test_constant_is_the_first_row():
+    data = torch.tensor([[1.0, 2.0], [3.0, 4.0]])
+    c = rdv.Constant(data)
+    assert c.OUT == 2
+    ptr = c._value_ptr()
+    assert ptr == c.buf_.device_ptr  # the buffer's first OUT floats, not its last row
+
+
+def test_ensure_on_rdv_returns_the_callers_backend_in_owned_memory():
+    import numpy as np
+    a = np.arange(6, dtype=np.float32).reshape(2, 3)
+    b = rdv.ensure_on_rdv(a)
+    assert isinstance(b, np.ndarray) and b.shape == (2, 3) and (b == a).all()
+    assert b.__array_interface__["data"][0] != a.__array_interface__["data"][0]
+    assert rdv.is_on_rdv(b) and not rdv.is_on_rdv(a) and rdv.is_on_rdv(b[1:])
+    assert rdv.ensure_on_rdv(b) is b  # already the library's: unchanged
+    t = torch.arange(5.0)
+    u = rdv.ensure_on_rdv(t)
+    assert isinstance(u, torch.Tensor) and u.data_ptr() != t.data_ptr() and torch.equal(u, t)
+    assert rdv.is_on_rdv(u) and not rdv.is_on_rdv(t) and rdv.ensure_on_rdv(u) is u
+    v = rdv.ensure_on_rdv(a, backend="torch")
+    assert isinstance(v, torch.Tensor) and v.shape == (2, 3) and rdv.is_on_rdv(v)
+    with pytest.raises(ValueError):
+        rdv.ensure_on_rdv(a, backend="numpy", location=rdv.MemoryLocation.DEVICE)
+    with pytest.raises(TypeError):
+        rdv.ensure_on_rdv([1.0, 2.0])
+    del u
+    import gc
+    gc.collect()
+    assert not rdv.is_on_rdv(t)
+
+
+def test_grid_batch_rejects_bad_indices_before_launch():
+    cam = rdv.Cameras(8, 6, torch.tensor([[0.0, 0.0, -3.5, 0.0, 0.0, 0.0, 0.0, 1.0, 0.0]]))
+    with pytest.raises(TypeError):
+        cam(torch.zeros(4, 3))
+    with pytest.raises(AssertionError):
+        cam(torch.zeros(4, 2, dtype=torch.int32))
+    with pytest.raises(AssertionError):
+        cam(torch.zeros(4, 3, dtype=torch.int32), torch.zeros(4, 3, dtype=torch.int32))

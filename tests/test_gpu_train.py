@@ -92,6 +92,24 @@ def test_generic_chains(dims, n):
     _check(loss.item(), grads, ref_loss, ref_grads, "-".join(map(str, dims)))
 
 
+def test_each_call_returns_its_own_loss():
+    """Two calls on different data return two loss tensors holding two losses
+    (a list of un-read losses keeps every step's value); a caller-supplied
+    loss buffer is the one written."""
+    x, t, layers = WL.c5(2048)
+    m = _chain(layers)
+    xd, td = x.cuda(), t.cuda()
+    la, _ = rdv.mse_backward(m, xd, td)
+    lb, _ = rdv.mse_backward(m, xd, td * 2.0 + 1.0)
+    assert la is not lb and la.data_ptr() != lb.data_ptr()
+    ref_a, _ = T.mse_grads(x.float().numpy(), [(w.numpy(), b.numpy()) for w, b in layers], t.numpy())
+    ref_b, _ = T.mse_grads(x.float().numpy(), [(w.numpy(), b.numpy()) for w, b in layers], t.numpy() * 2.0 + 1.0)
+    assert abs(la.item() - ref_a) <= 1e-4 * abs(ref_a) and abs(lb.item() - ref_b) <= 1e-4 * abs(ref_b)
+    own = torch.full((), -1.0, device="cuda")
+    lc, _ = rdv.mse_backward(m, xd, td, loss=own)
+    assert lc is own and abs(own.item() - ref_a) <= 1e-4 * abs(ref_a)
+
+
 def test_unsupported_chain_raises():
     layers = [(torch.zeros(64, 3), torch.zeros(64)), (torch.zeros(4, 64), torch.zeros(4))]
     with pytest.raises(NotImplementedError):

@@ -44,3 +44,11 @@ def test_bad_grads_rejected_before_launch(case):
 def test_target_width_checked():
     with pytest.raises(AssertionError):
         rdv.mse_backward(_chain(), torch.zeros(64, 16), torch.zeros(64, 7))
+
+
+@pytest.mark.parametrize("case", ["numpy", "fp64", "two", "host"])
+def test_bad_loss_buffer_rejected_before_launch(case):
+    loss = {"numpy": 0.0, "fp64": torch.zeros((), dtype=torch.float64), "two": torch.zeros(2),
+            "host": torch.zeros(())}[case]
+    with pytest.raises(TypeError):
+        rdv.mse_backward(_chain(), torch.zeros(64, 16), torch.zeros(64, 8), None, loss)
