@@ -101,10 +101,11 @@ def ray_box32(x, w):
     return np.fmax.reduce(c0, axis=-1), np.fmin.reduce(c1, axis=-1)
 
 
-def field_eval(p: np.ndarray, layers, acts) -> np.ndarray:
-    """The field chain on points p [..., 3], all rows in fp16 (LinearFast) arithmetic."""
+def field_eval(p: np.ndarray, layers, acts, precs=None) -> np.ndarray:
+    """The field chain on points p [..., 3]: every row with each layer's own
+    arithmetic (precs: 'f16' LinearFast, 'f32' Linear; all 'f16' by default)."""
     shp = p.shape[:-1]
-    y = M.chain(p.reshape(-1, 3), layers, acts, ["f16"] * len(layers))
+    y = M.chain(p.reshape(-1, 3), layers, acts, precs or ["f16"] * len(layers))
     return y.reshape(*shp, -1)
 
 
@@ -143,9 +144,10 @@ def composite(sigma_rgb: np.ndarray, dt: np.ndarray) -> np.ndarray:
 
 
 def raymarch_transmittance(rays: np.ndarray, layers, head: str = "softplus", transform=None, step: float = 0.002,
-                           density_scale: float = 1.0) -> np.ndarray:
+                           density_scale: float = 1.0, precs=None) -> np.ndarray:
     """transmittance_rm per ray [N, 6], the reference's sequential loop in
-    float32 (vectorised over rays).  head: activation of the extinction's last layer."""
+    float32 (vectorised over rays).  head: activation of the extinction's last
+    layer; precs: each layer's arithmetic ('f16' / 'f32', all 'f16' by default)."""
     f = np.float32
     rays = np.asarray(rays, np.float32).reshape(-1, 6)
     Mt = np.eye(4, 3, dtype=np.float64) if transform is None else np.asarray(transform, np.float64).reshape(4, 3)
@@ -171,7 +173,7 @@ def raymarch_transmittance(rays: np.ndarray, layers, head: str = "softplus", tra
         if not act.any():
             break
         ii = np.nonzero(act)[0]
-        sig = field_eval(x[ii], layers, acts)[:, 0].astype(np.float32)
+        sig = field_eval(x[ii], layers, acts, precs)[:, 0].astype(np.float32)
         ce = (sig * f(density_scale)).astype(np.float32)
         tau[ii] = (tau[ii] + (ce * step).astype(np.float32)).astype(np.float32)
         over = tau[ii] > 16

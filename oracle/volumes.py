@@ -165,13 +165,14 @@ def ratiotracking(rays: np.ndarray, extinction, majorant: np.ndarray, seeds, tra
     return T
 
 
-def mlp_extinction(layers, head: str = "none"):
-    """An extinction function for ratiotracking(): the LinearFast chain (fp16
-    arithmetic, ReLU hidden layers, `head` on the last)."""
+def mlp_extinction(layers, head: str = "none", precs=None):
+    """An extinction function for ratiotracking(): the chain with each layer's
+    arithmetic (precs: 'f16' LinearFast, 'f32' Linear; all 'f16' by default),
+    ReLU hidden layers, `head` on the last."""
     acts = ["relu"] * (len(layers) - 1) + [head]
 
     def f(p):
-        return field_eval(np.asarray(p, F), layers, acts)[:, 0].astype(F)
+        return field_eval(np.asarray(p, F), layers, acts, precs)[:, 0].astype(F)
     return f
 
 

@@ -4,7 +4,10 @@ A composition is accepted when its stages, in application order, are
   [FrequencyEncoding]? (Linear | LinearFast) [activation]? ( (Linear | LinearFast) [activation]? )*
 which is what the reference's MapEvaluator runs for a chain of
 `linear(...) >> relu >> ...` (src/rdv/maths/__init__.py:1451-1487,
-src/rdv/shaders/maps/composite.h:8-12).  Anything else raises
+src/rdv/shaders/maps/composite.h:8-12).  A Constant alone (maths:1659-1668) is
+lowered as one layer with zero weights and the constant as its bias, which
+the field kernels (extinctions, the renderer's field) evaluate exactly: every
+product is 0 and the accumulator starts at the bias.  Anything else raises
 NotImplementedError: this build has no general Map code generator.
 """
 from __future__ import annotations
@@ -16,7 +19,7 @@ import torch
 
 from . import _lib
 from .core import RDVObject, current_stream_handle, device, launch_scope, wrap
-from .maths import Identity, Map
+from .maths import Constant, Identity, Map
 from .nn import FrequencyEncoding, _Activation, _LinearBase
 
 
@@ -31,8 +34,47 @@ class ChainPlan:
         self.out_features = out_features
 
 
+class _ConstantLayer:
+    """A Constant seen as a layer [OUT, in_width]: zero fp32 weights (one buffer
+    kept on the Constant) and the constant's first OUT floats as the bias, read
+    at every pack like any layer's bias."""
+
+    def __init__(self, c: Constant, in_width: int) -> None:
+        self.IN, self.OUT = int(in_width), int(c.OUT)
+        self._precision = _lib.PREC_F16  # zero weights: the products are exact in any precision
+        zero = c.__dict__.get("_rdv_zero_w")
+        if zero is None or tuple(zero.shape) != (self.OUT, self.IN):
+            zero = wrap(torch.zeros((self.OUT, self.IN), dtype=torch.float32, device=device()))
+            c.__dict__["_rdv_zero_w"] = zero
+        self.weight = zero
+        self.bias = _ValuePtr(c._value_ptr())
+
+
+class _ValuePtr:
+    __slots__ = ("device_ptr",)
+
+    def __init__(self, ptr: int) -> None:
+        self.device_ptr = ptr
+
+
+def _plan_constant(c: Constant, in_width: int) -> ChainPlan:
+    lay = _ConstantLayer(c, in_width)
+    d = _lib.MlpDesc()
+    d.n_layers = 1
+    d.in_features = in_width
+    d.encoding = _lib.ENC_NONE
+    d.enc_octaves = 0
+    d.dims[0], d.dims[1] = in_width, lay.OUT
+    d.act[0] = _lib.ACT_NONE
+    d.prec[0] = lay._precision
+    _lib.check(_lib.load().rdv_mlp_validate(C.byref(d)), "mlp")
+    return ChainPlan(d, [lay], ("constant", in_width, lay.OUT), in_width, lay.OUT)
+
+
 def plan_chain(m: Map, in_width: int) -> ChainPlan:
     stages = [s for s in m.stages() if not isinstance(s, Identity)]
+    if len(stages) == 1 and isinstance(stages[0], Constant):
+        return _plan_constant(stages[0], in_width)
     enc, octaves, i, cur = _lib.ENC_NONE, 0, 0, in_width
     if stages and isinstance(stages[0], FrequencyEncoding):
         e = stages[0]

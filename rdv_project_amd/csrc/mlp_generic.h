@@ -34,6 +34,9 @@ struct GenNet {
   int frag[RDV_MLP_MAX_LAYERS]; // first A fragment (1 KiB units) of layer l
   int bias[RDV_MLP_MAX_LAYERS]; // first bias float of layer l
   int act[RDV_MLP_MAX_LAYERS];  // RDV_ACT_* after layer l
+  int f32[RDV_MLP_MAX_LAYERS];  // 1: exact fp32 layer (v_mfma_f32_32x32x2f32, gen_chain_mixed only)
+  int kb[RDV_MLP_MAX_LAYERS];   // 32-row K blocks of layer l (fp32 layers)
+  int in0;                      // layer 0's input width (the encoded width)
   int n_frag;                   // fragments of the whole chain
   int n_bias;                   // floats spanned by the bias sections (with alignment gaps)
   int max_mt;                   // largest mt[l]
@@ -56,10 +59,13 @@ inline void gen_net(const rdv_mlp_desc& d, const MlpLayout& lay, GenNet* g) {
     g->frag[l] = live ? int((lay.frag_off[l] - lay.frag_off[0]) / 1024) : 0;
     g->bias[l] = live ? int((lay.bias_off[l] - lay.bias_off[0]) / 4) : 0;
     g->act[l] = live ? d.act[l] : RDV_ACT_NONE;
+    g->f32[l] = live ? lay.f32[l] : 0;
+    g->kb[l] = live ? lay.kb[l] : 0;
     if (live && lay.mt[l] > g->max_mt) g->max_mt = lay.mt[l];
   }
+  g->in0 = d.dims[0];
   const int last = d.n_layers - 1;
-  g->n_frag = int((lay.frag_off[last] - lay.frag_off[0]) / 1024) + lay.mt[last] * lay.kc[last];
+  g->n_frag = int((lay.frag_off[last] - lay.frag_off[0]) / 1024) + lay.frag_units[last];
   g->n_bias = int((lay.bias_off[last] - lay.bias_off[0]) / 4) + 32 * lay.mt[last];
 }
 
@@ -330,6 +336,133 @@ __device__ __forceinline__ half8 gen_l0_chunk(const GenNet& g, int c, int h, Get
     }
   }
   return b;
+}
+
+
+// ----------------------------------------------------------- mixed chains
+// Chains with exact fp32 layers (Linear, maps/linear.h) alone or mixed with
+// LinearFast layers, on the matrix cores: an fp32 layer runs
+// v_mfma_f32_32x32x2f32 with its fp32 fragments (mlp_layout.h), one MFMA per
+// input row pair, B = the producing layer's fp32 D register after its
+// activation (no fp16 rounding anywhere in an fp32 layer, as in the
+// reference's Linear); an fp16 layer is the LinearFast layer of gen_chain,
+// and its input is rounded to fp16 by the hand-off whatever produced it.  The
+// fp32 products and sums are the matrix core's fp32 arithmetic, in its own
+// order (the reference sums one input at a time).
+//
+// MT bounds every layer's M tiles (register arrays: MT fp32 input blocks and
+// 2 MT fp16 fragments between layers).  feat(k) returns this lane's value of
+// encoded input feature k (0 past the input width).
+
+// fp32 layer with M tiles over the kb input blocks in v (hidden layer) or from
+// feat (layer 0, kb input blocks of its width); accumulates into acc.
+template <int MT, int M, bool L0, class W, class Feat>
+__device__ __forceinline__ void gen_f32_layer(f32x16 (&acc)[M], int f0, int kb, int width, int h, const W& wf,
+                                              Feat& feat, const f32x16 (&v)[MT]) {
+  if constexpr (L0) {
+    for (int blk = 0; blk < kb; ++blk) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        f32x4 A[M];
+#pragma unroll
+        for (int t = 0; t < M; ++t) A[t] = __builtin_bit_cast(f32x4, wf(f0 + (t * kb + blk) * 4 + q));
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+          const int k0 = 32 * blk + 8 * q + jj;  // lane half 0's row; half 1 reads k0 + 4
+          if (k0 < width) {
+            const float bv = feat(k0 + 4 * h);
+#pragma unroll
+            for (int t = 0; t < M; ++t) {
+              const float av = A[t][jj];
+              acc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(av, bv, acc[t], 0, 0, 0);
+            }
+          }
+        }
+      }
+    }
+  } else {
+#pragma unroll
+    for (int blk = 0; blk < MT; ++blk) {
+      if (blk < kb) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          f32x4 A[M];
+#pragma unroll
+          for (int t = 0; t < M; ++t) A[t] = __builtin_bit_cast(f32x4, wf(f0 + (t * kb + blk) * 4 + q));
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj) {
+            const float bv = v[blk][4 * q + jj];
+#pragma unroll
+            for (int t = 0; t < M; ++t) {
+              const float av = A[t][jj];
+              acc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(av, bv, acc[t], 0, 0, 0);
+            }
+          }
+        }
+      }
+    }
+  }
+}
+
+// One layer l of a mixed chain with M tiles.
+template <int MT, int M, class W, class Feat, class Get, class Sink>
+__device__ __forceinline__ void gen_mixed_layer(const GenNet& g, int l, const GenCtx& x, const W& wf, Feat& feat,
+                                                Get& get, half8 (&b)[2 * MT], f32x16 (&v)[MT], Sink& sink) {
+  f32x16 acc[M];
+  gen_init<M>(acc, x.bias + g.bias[l], x.has_bias, x.h);
+  const int f0 = g.frag[l];
+  if (g.f32[l]) {
+    if (l == 0) gen_f32_layer<MT, M, true>(acc, f0, g.kb[0], g.in0, x.h, wf, feat, v);
+    else gen_f32_layer<MT, M, false>(acc, f0, g.kb[l], 0, x.h, wf, feat, v);
+  } else if (l == 0) {
+    const int kc = g.kc[0];
+    for (int c = 0; c < kc; ++c) {
+      const half8 bc = gen_l0_chunk(g, c, x.h, get);
+#pragma unroll
+      for (int t = 0; t < M; ++t) acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wf(f0 + t * kc + c), bc, acc[t], 0, 0, 0);
+    }
+  } else {
+    const int kc = g.kc[l];
+#pragma unroll
+    for (int c = 0; c < 2 * MT; ++c) {
+      if (c < kc) {
+#pragma unroll
+        for (int t = 0; t < M; ++t)
+          acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wf(f0 + t * kc + c), b[c], acc[t], 0, 0, 0);
+      }
+    }
+  }
+  const bool last = l == g.L - 1;
+  if (last) {
+    sink(acc);
+  } else if (g.f32[l + 1]) {  // the next layer reads fp32 rows: the activation in fp32, no rounding
+#pragma unroll
+    for (int t = 0; t < M; ++t)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) v[t][j] = gen_head_act(g.act[l], gen_row(t, j, x.h), acc[t][j]);
+  } else {
+    gen_handoff<MT, M>(acc, b, g.act[l], x.h);
+  }
+}
+
+// The whole mixed chain for one 32-point tile: get(d) returns raw coordinate d
+// of this lane's point; sink(acc) receives the last layer's accumulators.
+template <int MT, class W, class Get, class Sink>
+__device__ __forceinline__ void gen_chain_mixed(const GenNet& g, const GenCtx& x, const W& wf, Get&& get, Sink&& sink) {
+  half8 b[2 * MT];
+  f32x16 v[MT];
+  const int enc_w = g.enc == RDV_ENC_FREQ ? g.D * (1 + 2 * g.oct) : g.D;
+  auto feat = [&](int k) -> float {
+    if (k >= enc_w) return 0.0f;
+    if (g.enc == RDV_ENC_FREQ) return gen_freq_feature(k, g.D, get);
+    return get(k);
+  };
+#pragma nounroll
+  for (int l = 0; l < g.L; ++l) {
+#define RDV_GEN_LM(M) gen_mixed_layer<MT, M>(g, l, x, wf, feat, get, b, v, sink)
+    RDV_GEN_SWITCH(g.mt[l], RDV_GEN_LM)
+#undef RDV_GEN_LM
+  }
 }
 
 }  // namespace rdv

@@ -14,13 +14,26 @@
 // The next layer's weight columns are permuted by the same sigma when packed,
 // so activations never leave registers between layers.
 //
-// Layout (every section 256-byte aligned), for layer i with KC = K chunks of 16
-// and MT = M tiles of 32:
+// Exact fp32 layers (RDV_PREC_F32) on the matrix cores use
+// v_mfma_f32_32x32x2f32 in the same transposed formulation: A = W[32t + l%32]
+// [k], B = the input row k of point l%32, one fp32 value per lane, K = 2 (lane
+// half h supplies k = the half's row).  MFMA j (0..15) of 32-row input block kb
+// takes k = 32kb + 8(j/4) + 4h + (j%4), which is exactly the row that D
+// register j of the producing layer holds: a layer's fp32 D registers (after
+// its activation) ARE the next fp32 layer's B operands, one per MFMA, with no
+// permutation.  The A values of MFMAs 4q .. 4q+3 for lane l are the four
+// consecutive columns W[m][32kb + 8q + 4h + 0..3], one 16-byte read.  Layer 0
+// reads its input rows in the same order (feature k = the encoded feature k).
+//
+// Layout (every section 256-byte aligned), for layer i with KC = K chunks of 16,
+// KB = K blocks of 32 and MT = M tiles of 32:
 //   header  : MlpPackHeader, 256 bytes (flags computed by the packer)
-//   frag[i] : MT x KC x 64 lanes x 8 fp16   (A fragments in lane order)
+//   frag[i] : fp16 layer: MT x KC x 64 lanes x 8 fp16 (A fragments in lane order)
+//             fp32 layer: MT x KB x 4 quartets x 64 lanes x 4 fp32
 //   bias[i] : MT*32 fp32                      (zero padded)
 //   w32[i]  : dims[i+1] x dims[i] fp32        (row-major copy, for fp32 paths)
 //   b32[i]  : dims[i+1] fp32
+// Both fragment kinds come in 1 KiB units (frag_units[i] of them).
 #pragma once
 
 #include <stdint.h>
@@ -43,7 +56,10 @@ struct MlpLayout {
   int in_w[RDV_MLP_MAX_LAYERS];   // actual input width of layer i
   int out_w[RDV_MLP_MAX_LAYERS];  // actual output width of layer i
   int kc[RDV_MLP_MAX_LAYERS];     // K chunks of 16 (virtual, after slot mapping)
+  int kb[RDV_MLP_MAX_LAYERS];     // K blocks of 32 (fp32 layers' matrix-core path)
   int mt[RDV_MLP_MAX_LAYERS];     // M tiles of 32
+  int f32[RDV_MLP_MAX_LAYERS];    // 1: exact fp32 layer (fp32 fragments)
+  int frag_units[RDV_MLP_MAX_LAYERS];  // 1 KiB units of layer i's fragments
   int64_t frag_off[RDV_MLP_MAX_LAYERS];
   int64_t bias_off[RDV_MLP_MAX_LAYERS];
   int64_t w32_off[RDV_MLP_MAX_LAYERS];
@@ -116,10 +132,13 @@ inline bool mlp_layout(const rdv_mlp_desc& d, MlpLayout* lay) {
     lay->mt[i] = div_up(d.dims[i + 1], 32);
     lay->kc[i] = i == 0 ? layer0_kc(d.encoding, d.in_features, d.enc_octaves, d.dims[0])
                         : 2 * lay->mt[i - 1];
+    lay->kb[i] = i == 0 ? div_up(d.dims[0], 32) : lay->mt[i - 1];
+    lay->f32[i] = d.prec[i] == RDV_PREC_F32 ? 1 : 0;
+    lay->frag_units[i] = lay->f32[i] ? lay->mt[i] * lay->kb[i] * 4 : lay->mt[i] * lay->kc[i];
   }
   for (int i = 0; i < L; ++i) {
     lay->frag_off[i] = off;
-    off = align256(off + int64_t(lay->mt[i]) * lay->kc[i] * 64 * 8 * 2);
+    off = align256(off + int64_t(lay->frag_units[i]) * 1024);
   }
   for (int i = 0; i < L; ++i) {
     lay->bias_off[i] = off;

@@ -20,8 +20,25 @@ __global__ void mlp_pack_layer_kernel(const float* __restrict__ W, const float* 
   const int in_w = lay.in_w[li], out_w = lay.out_w[li];
   const int kc = lay.kc[li], mt = lay.mt[li];
 
+  if (lay.f32[li]) {
+    // fp32 A fragments: element e = (((t * kb + blk) * 4 + q) * 64 + lane) * 4 + jj
+    // holds W[32t + lane % 32][32 blk + 8q + 4 (lane / 32) + jj]
+    const int kb = lay.kb[li];
+    if (e < int64_t(mt) * kb * 4 * 64 * 4) {
+      const int jj = int(e & 3);
+      const int lane = int((e >> 2) & 63);
+      const int64_t grp = e >> 8;
+      const int q = int(grp & 3);
+      const int64_t tb = grp >> 2;
+      const int blk = int(tb % kb), t = int(tb / kb);
+      const int m = 32 * t + (lane & 31);
+      const int k = 32 * blk + 8 * q + 4 * (lane >> 5) + jj;
+      const float v = (m < out_w && k < in_w) ? W[int64_t(m) * in_w + k] : 0.0f;
+      reinterpret_cast<float*>(packed + lay.frag_off[li])[e] = v;
+    }
+  }
   // fp16 A fragments: element e = ((t * kc + c) * 64 + lane) * 8 + j
-  const int64_t n_frag = int64_t(mt) * kc * 64 * 8;
+  const int64_t n_frag = lay.f32[li] ? 0 : int64_t(mt) * kc * 64 * 8;
   if (e < n_frag) {
     const int j = int(e & 7);
     const int lane = int((e >> 3) & 63);
@@ -50,7 +67,8 @@ int launch_mlp_pack(const rdv_mlp_desc& d, const MlpLayout& lay, const float* co
   mlp_pack_header_kernel<<<1, 64, 0, stream>>>(static_cast<uint8_t*>(packed));
   RDV_HIP_TRY(hipGetLastError());
   for (int i = 0; i < lay.n_layers; ++i) {
-    int64_t n = int64_t(lay.mt[i]) * lay.kc[i] * 64 * 8;
+    int64_t n = int64_t(lay.frag_units[i]) * 256;  // fragment elements (512 fp16 or 256 fp32 per KiB) bound
+    if (!lay.f32[i]) n = int64_t(lay.mt[i]) * lay.kc[i] * 64 * 8;
     const int64_t nw = int64_t(lay.out_w[i]) * lay.in_w[i];
     if (nw > n) n = nw;
     const int threads = 256;

@@ -679,7 +679,7 @@ struct TransmittanceGenArgs {
   GenNet net;
 };
 
-template <int MT, bool LDSW>
+template <int MT, bool LDSW, bool F32L = false>
 __global__ __launch_bounds__(64 * gen_waves<MT>(), 1) void raymarch_generic_kernel(TransmittanceGenArgs ga) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   __shared__ int s_next;
@@ -695,7 +695,7 @@ __global__ __launch_bounds__(64 * gen_waves<MT>(), 1) void raymarch_generic_kern
   __syncthreads();
   const int act = g.act[g.L - 1];
   raymarch_rays(a, &s_next, [&](const float (&xc)[3]) {
-    return gen_field_row0<MT>(g, w0, b0, has_bias, lane, h, xc, act);
+    return gen_field_row0<MT, F32L>(g, w0, b0, has_bias, lane, h, xc, act);
   });
 }
 
@@ -799,7 +799,7 @@ struct RatioGenArgs {
   GenNet net;
 };
 
-template <int MT, bool LDSW>
+template <int MT, bool LDSW, bool F32L = false>
 __global__ __launch_bounds__(64 * gen_waves<MT>(), 1) void ratiotracking_generic_kernel(RatioGenArgs ga) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   __shared__ int s_next;
@@ -862,7 +862,7 @@ __global__ __launch_bounds__(64 * gen_waves<MT>(), 1) void ratiotracking_generic
     float p[3];
 #pragma unroll
     for (int i = 0; i < 3; ++i) p[i] = pending ? r.x[i] : 0.0f;
-    float sigma = gen_field_row0<MT>(g, w0, b0, has_bias, lane, h, p, act);
+    float sigma = gen_field_row0<MT, F32L>(g, w0, b0, has_bias, lane, h, p, act);
     sigma = __shfl(sigma, col);  // the value of lane col (row 0 of its column)
     if (pending) {
 #pragma clang fp contract(off)
@@ -1087,8 +1087,11 @@ int launch_raymarch_transmittance(const rdv_mlp_desc& d, const MlpLayout& lay, c
                                   int64_t nrays, const float* transform12, float step, float density_scale,
                                   float* out, hipStream_t stream) {
   const bool fixed = is_extinction_field(d, lay);
-  if (!fixed && !is_f16_field(d, 1))
-    return fail(RDV_ERR_UNSUPPORTED, "the extinction must be a LinearFast chain from 3 inputs to 1 output");
+  std::string why;
+  const bool mixed = !fixed && is_mixed_field(d, lay, 1, &why);
+  if (!fixed && !mixed && !is_f16_field(d, 1))
+    return fail(RDV_ERR_UNSUPPORTED, why.empty() ? "the extinction must be a chain of LinearFast / Linear layers from 3 "
+                                                   "inputs to 1 output" : why);
   DeviceInfo di;
   int rc = device_info(&di);
   if (rc != RDV_OK) return rc;
@@ -1108,6 +1111,7 @@ int launch_raymarch_transmittance(const rdv_mlp_desc& d, const MlpLayout& lay, c
     TransmittanceGenArgs ga;
     ga.t = a;
     gen_net(d, lay, &ga.net);
+    if (mixed) RDV_GEN_FIELD_DISPATCH_MIXED(raymarch_generic_kernel, ga, nrays, di.cu_count, ga.net, stream);
     RDV_GEN_FIELD_DISPATCH(raymarch_generic_kernel, ga, nrays, di.cu_count, ga.net, stream,
                            launch_raymarch_generic8);
   }
@@ -1156,8 +1160,11 @@ int launch_voxel_majorant(const float* grid, int mw, int mh, int md, const float
 int launch_ratiotracking(const rdv_mlp_desc& d, const MlpLayout& lay, const void* packed,
                          const rdv_ratiotracking_desc& rt, const float* majorant, const float* rays, int64_t nrays,
                          float* out, hipStream_t stream) {
-  if (!is_f16_field(d, 1))
-    return fail(RDV_ERR_UNSUPPORTED, "the extinction must be a LinearFast chain from 3 inputs to 1 output");
+  std::string why;
+  const bool mixed = is_mixed_field(d, lay, 1, &why);
+  if (!mixed && !is_f16_field(d, 1))
+    return fail(RDV_ERR_UNSUPPORTED, why.empty() ? "the extinction must be a chain of LinearFast / Linear layers from 3 "
+                                                   "inputs to 1 output" : why);
   DeviceInfo di;
   int rc = device_info(&di);
   if (rc != RDV_OK) return rc;
@@ -1177,6 +1184,7 @@ int launch_ratiotracking(const rdv_mlp_desc& d, const MlpLayout& lay, const void
   ga.packed = static_cast<const uint8_t*>(packed);
   gen_net(d, lay, &ga.net);
   // 32 rays per wave
+  if (mixed) RDV_GEN_FIELD_DISPATCH_MIXED(ratiotracking_generic_kernel, ga, (nrays + 31) / 32, di.cu_count, ga.net, stream);
   RDV_GEN_FIELD_DISPATCH(ratiotracking_generic_kernel, ga, (nrays + 31) / 32, di.cu_count, ga.net, stream,
                          launch_ratiotracking_generic8);
 }

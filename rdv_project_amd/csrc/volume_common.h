@@ -4,6 +4,9 @@
 // 32 points of a wave with its launch helper.
 #pragma once
 
+#include <mutex>
+#include <vector>
+
 #include "mlp_core.h"
 #include "mlp_generic.h"
 
@@ -102,17 +105,22 @@ __device__ __forceinline__ void gen_sources(const uint8_t* packed, const GenNet&
 }
 
 // The chain's head value of row 0 at this lane's sample p (3 coordinates).
-template <int MT>
+// F32L: the chain may hold exact fp32 layers (gen_chain_mixed).
+template <int MT, bool F32L = false>
 __device__ __forceinline__ float gen_field_row0(const GenNet& g, const half8* w0, const float* b0, bool has_bias,
                                                 int lane, int h, const float (&p)[3], int act) {
   const int z = opaque_zero();
   const half8* wsrc = w0 + z;
   auto wf = [&](int f) { return wsrc[f * 64 + lane]; };
   auto get = [&](int d) { return d == 0 ? p[0] : (d == 1 ? p[1] : p[2]); };
-  auto l0 = [&](int c) { return gen_l0_chunk(g, c, h, get); };
   float v = 0.0f;
   auto sink = [&](const auto& acc) { v = gen_head_act(act, 0, acc[0][0]); };
-  gen_chain<MT>(g, GenCtx{b0 + z, has_bias, h}, wf, l0, sink);
+  if constexpr (F32L) {
+    gen_chain_mixed<MT>(g, GenCtx{b0 + z, has_bias, h}, wf, get, sink);
+  } else {
+    auto l0 = [&](int c) { return gen_l0_chunk(g, c, h, get); };
+    gen_chain<MT>(g, GenCtx{b0 + z, has_bias, h}, wf, l0, sink);
+  }
   return v;
 }
 
@@ -142,14 +150,24 @@ __device__ __forceinline__ float voxel_majorant(const float* __restrict__ grid, 
   return grid[(int64_t(cell[2]) * mh + cell[1]) * mw + cell[0]];
 }
 
+// Raises `kernel`'s dynamic-LDS limit to kGenFieldLdsCap, once per kernel.
+static int gen_field_lds_attr(const void* kernel) {
+  static std::mutex mu;
+  static std::vector<const void*> done;
+  std::lock_guard<std::mutex> lock(mu);
+  for (const void* k : done)
+    if (k == kernel) return RDV_OK;
+  RDV_HIP_TRY(hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, int(kGenFieldLdsCap)));
+  done.push_back(kernel);
+  return RDV_OK;
+}
+
 template <class Args, int MT, bool LDSW>
 static int launch_gen_field(void (*kernel)(Args), const Args& a, int64_t work_items, int cu, size_t lds,
                             hipStream_t stream) {
-  static bool attr = false;
-  if (LDSW && !attr) {
-    RDV_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                    int(kGenFieldLdsCap)));
-    attr = true;
+  if (LDSW) {
+    const int rc = gen_field_lds_attr(reinterpret_cast<const void*>(kernel));
+    if (rc != RDV_OK) return rc;
   }
   constexpr int waves = gen_waves<MT>();
   int64_t blocks = cu;
@@ -198,5 +216,47 @@ static bool is_f16_field(const rdv_mlp_desc& d, int out) {
     if (d.prec[i] != RDV_PREC_F16) return false;
   return true;
 }
+
+// Largest M-tile count of a chain with exact fp32 layers that the field kernels
+// instantiate (widths up to 64: the fp32 input blocks held between layers stay
+// within the ray kernels' register budget).
+constexpr int kGenMixedMaxMT = 2;
+
+// A chain from 3 inputs to `out` outputs with at least one exact fp32 layer,
+// whose widths the mixed field kernels take?  Its fragments (fp32 ones are
+// twice the bytes of fp16) must fit in the field kernels' LDS.
+static bool is_mixed_field(const rdv_mlp_desc& d, const MlpLayout& lay, int out, std::string* why) {
+  if (d.in_features != 3 || d.dims[d.n_layers] != out) return false;
+  bool any = false;
+  for (int i = 0; i < d.n_layers; ++i) any = any || d.prec[i] == RDV_PREC_F32;
+  if (!any) return false;
+  GenNet g;
+  gen_net(d, lay, &g);
+  if (g.max_mt > kGenMixedMaxMT) {
+    *why = "a field chain with exact fp32 (Linear) layers supports widths up to " + std::to_string(32 * kGenMixedMaxMT);
+    return false;
+  }
+  if (gen_lds_bytes(g) > kGenFieldLdsCap) {
+    *why = "a field chain with exact fp32 (Linear) layers must fit in " + std::to_string(kGenFieldLdsCap / 1024) +
+           " KiB of fragments and biases";
+    return false;
+  }
+  return true;
+}
+
+template <class Args, int MT>
+static int launch_gen_field_mixed(void (*kernel)(Args), const Args& a, int64_t work_items, int cu, size_t lds,
+                                  hipStream_t stream) {
+  return launch_gen_field<Args, MT, true>(kernel, a, work_items, cu, lds, stream);
+}
+
+// Launch of KERNEL<MT, true, true> (weights in LDS, exact fp32 layers) for NET.
+#define RDV_GEN_FIELD_DISPATCH_MIXED(KERNEL, ARGS, ITEMS, CU, NET, STREAM)                                  \
+  do {                                                                                                      \
+    const int64_t lds_ = gen_lds_bytes(NET);                                                                \
+    if (gen_mt_bound(NET) == 1)                                                                             \
+      return launch_gen_field_mixed<decltype(ARGS), 1>(&KERNEL<1, true, true>, ARGS, ITEMS, CU, lds_, STREAM); \
+    return launch_gen_field_mixed<decltype(ARGS), 2>(&KERNEL<2, true, true>, ARGS, ITEMS, CU, lds_, STREAM);   \
+  } while (0)
 
 }  // namespace rdv

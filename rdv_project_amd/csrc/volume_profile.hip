@@ -550,7 +550,7 @@ struct VpGenArgs {
 
 // One block's rays (DDA: VolumeProfileDDA's marches, a compile-time choice so that
 // VolumeProfile's kernel carries none of the walk's state).
-template <int MT, bool LDSW, bool DDA>
+template <int MT, bool LDSW, bool DDA, bool F32L>
 __device__ __forceinline__ void volume_profile_body(const VpGenArgs& ga) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   __shared__ int s_next;
@@ -618,7 +618,7 @@ __device__ __forceinline__ void volume_profile_body(const VpGenArgs& ga) {
     float p[3];
 #pragma unroll
     for (int i = 0; i < 3; ++i) p[i] = pending ? q[i] : 0.0f;
-    float s = gen_field_row0<MT>(g, w0, b0, has_bias, lane, h, p, act);
+    float s = gen_field_row0<MT, F32L>(g, w0, b0, has_bias, lane, h, p, act);
     s = __shfl(s, col);  // the value of lane col (row 0 of its column)
     if (pending) {
       sigma = s;
@@ -628,14 +628,14 @@ __device__ __forceinline__ void volume_profile_body(const VpGenArgs& ga) {
   }
 }
 
-template <int MT, bool LDSW>
+template <int MT, bool LDSW, bool F32L = false>
 __global__ __launch_bounds__(64 * gen_waves<MT>(), 1) void volume_profile_kernel(VpGenArgs ga) {
-  volume_profile_body<MT, LDSW, false>(ga);
+  volume_profile_body<MT, LDSW, false, F32L>(ga);
 }
 
-template <int MT, bool LDSW>
+template <int MT, bool LDSW, bool F32L = false>
 __global__ __launch_bounds__(64 * gen_waves<MT>(), 1) void volume_profile_dda_kernel(VpGenArgs ga) {
-  volume_profile_body<MT, LDSW, true>(ga);
+  volume_profile_body<MT, LDSW, true, F32L>(ga);
 }
 
 // volume_profile.h:155-160 for the rows that reached a depth.
@@ -654,7 +654,7 @@ struct VpFinishArgs {
 // 8-tile launcher of volume_profile_kernel (RDV_FIELD_PART 1); every launch of
 // volume_profile_dda_kernel (RDV_FIELD_PART 2) and its 8-tile launcher (RDV_FIELD_PART 3).
 int launch_volume_profile8(const VpGenArgs& a, int64_t items, int cu, int64_t lds, bool in_lds, hipStream_t stream);
-int launch_volume_profile_dda_any(const VpGenArgs& a, int64_t items, int cu, hipStream_t stream);
+int launch_volume_profile_dda_any(const VpGenArgs& a, int64_t items, int cu, bool mixed, hipStream_t stream);
 int launch_volume_profile_dda8(const VpGenArgs& a, int64_t items, int cu, int64_t lds, bool in_lds,
                                hipStream_t stream);
 
@@ -682,8 +682,11 @@ int launch_volume_profile(const rdv_mlp_desc& d, const MlpLayout& lay, const voi
                           const rdv_volume_profile_desc& vp, const float* majorant, const float* dda_grid, int dda_w,
                           int dda_h, int dda_d, const float* rays, int64_t nrays, float* out, float* spos,
                           float* env_dirs, float* env_w, int32_t* valid, hipStream_t stream) {
-  if (!is_f16_field(d, 1))
-    return fail(RDV_ERR_UNSUPPORTED, "the extinction must be a LinearFast chain from 3 inputs to 1 output");
+  std::string why;
+  const bool mixed = is_mixed_field(d, lay, 1, &why);
+  if (!mixed && !is_f16_field(d, 1))
+    return fail(RDV_ERR_UNSUPPORTED, why.empty() ? "the extinction must be a chain of LinearFast / Linear layers from 3 "
+                                                   "inputs to 1 output" : why);
   DeviceInfo di;
   int rc = device_info(&di);
   if (rc != RDV_OK) return rc;
@@ -720,7 +723,8 @@ int launch_volume_profile(const rdv_mlp_desc& d, const MlpLayout& lay, const voi
   ga.packed = static_cast<const uint8_t*>(packed);
   gen_net(d, lay, &ga.net);
   // 32 rays per wave
-  if (dda_grid != nullptr) return launch_volume_profile_dda_any(ga, (nrays + 31) / 32, di.cu_count, stream);
+  if (dda_grid != nullptr) return launch_volume_profile_dda_any(ga, (nrays + 31) / 32, di.cu_count, mixed, stream);
+  if (mixed) RDV_GEN_FIELD_DISPATCH_MIXED(volume_profile_kernel, ga, (nrays + 31) / 32, di.cu_count, ga.net, stream);
   RDV_GEN_FIELD_DISPATCH(volume_profile_kernel, ga, (nrays + 31) / 32, di.cu_count, ga.net, stream,
                          launch_volume_profile8);
 }
@@ -740,8 +744,9 @@ int launch_volume_profile_finish(const rdv_volume_profile_desc& vp, const float*
 #elif RDV_FIELD_PART == 1
 RDV_GEN_FIELD_DEFINE8(launch_volume_profile8, volume_profile_kernel, VpGenArgs)
 #elif RDV_FIELD_PART == 2
-int launch_volume_profile_dda_any(const VpGenArgs& a, int64_t items, int cu, hipStream_t stream) {
+int launch_volume_profile_dda_any(const VpGenArgs& a, int64_t items, int cu, bool mixed, hipStream_t stream) {
   VpGenArgs ga = a;
+  if (mixed) RDV_GEN_FIELD_DISPATCH_MIXED(volume_profile_dda_kernel, ga, items, cu, ga.net, stream);
   RDV_GEN_FIELD_DISPATCH(volume_profile_dda_kernel, ga, items, cu, ga.net, stream, launch_volume_profile_dda8);
 }
 #elif RDV_FIELD_PART == 3

@@ -161,9 +161,10 @@ class RaymarchingTransmittance(Map[6, 1], RaymarchingTransmittanceTrait):
     marched with fixed steps: tau += extinction(x) * density_scale * step_size,
     0 once tau > 16, exp(-tau) at the end; 1 when the ray misses
     (reference: volumes.py:124-141, shaders/volumes/raymarching_transmittance.h).
-    extinction: a Map[3, 1]: any LinearFast chain from 3 inputs (raw or
-    frequency-encoded) to 1 output, evaluated on the matrix cores 32 march
-    steps at a time."""
+    extinction: a Map[3, 1]: a chain of LinearFast (fp16) and Linear (exact
+    fp32) layers from 3 inputs (raw or frequency-encoded) to 1 output, or a
+    Constant; evaluated on the matrix cores for 32 march steps at a time
+    (chains with a Linear layer: widths up to 64)."""
 
     IN = 6
     OUT = 1
@@ -231,7 +232,8 @@ class RatiotrackingTransmittance(Map[6, 1], RatiotrackingTransmittanceTrait):
     (reference: volumes.py:144-190, shaders/volumes/ratiotracking_transmittance.h,
     ratiotracking_transmittance_trait.h).  An unbiased, noisy estimate: each
     evaluation draws fresh random seeds (RandomLibrary).
-    extinction: a Map[3, 1] (any LinearFast chain from 3 inputs to 1 output);
+    extinction: a Map[3, 1] (a chain of LinearFast / Linear layers from 3 inputs
+    to 1 output, widths up to 64 with a Linear layer, or a Constant);
     majorant: a VoxelMajorantField or a Grid[3, 1] (wrapped as one)."""
 
     IN = 6
@@ -272,7 +274,8 @@ class VolumeProfile(Map, RatiotrackingTransmittanceTrait, RaymarchingTransmittan
       DS + 3 + 2 SD + [0, SD)  light_intensity
       OUT - 1            S = 1 - exp(-tau)
     (everything but S is 0 where no depth was reached; all 0 for a miss).
-    extinction: a Map[3, 1] (any LinearFast chain from 3 inputs to 1 output);
+    extinction: a Map[3, 1] (a chain of LinearFast / Linear layers from 3 inputs
+    to 1 output, widths up to 64 with a Linear layer, or a Constant);
     majorant: a VoxelMajorantField or a Grid[3, 1]; scattering_albedo and
     environment: Map[3, SD] (Constant maps or any map this package evaluates
     over rows).  Random draws: ray i uses thread i's generator of a fresh
