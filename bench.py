@@ -226,6 +226,24 @@ def bench_mlp(x_cpu, layers, acts, enc, steps, warmup, rotate=ROTATE):
     return wall, ev, name
 
 
+def bench_mlp_api(x_cpu, layers, acts, enc, steps, warmup, rotate=ROTATE):
+    """The same chain through the drop-in API, `m(rdv.wrap(x))`, with
+    set_synchronous(False) so that calls queue as C ABI launches do: each call
+    reads the layers' fp32 parameters afresh (rdv_mlp_forward_unpacked)."""
+    import rdv_project_amd as rdv
+    m, _, _, xs, _ = _mlp_setup(x_cpu, layers, acts, enc, rotate)
+    xw = [rdv.wrap(t) for t in xs]
+    prev = rdv.set_synchronous(False)
+    try:
+        def launch(i):
+            m(xw[i % rotate])
+
+        wall, ev = _time_launches(launch, steps, warmup)
+    finally:
+        rdv.set_synchronous(prev)
+    return wall, ev
+
+
 def bench_winograd(steps, warmup):
     """C3 through the C ABI: NCHW fp16 in / out, ReLU, rotating x / y sets."""
     import torch
@@ -705,6 +723,17 @@ def main() -> int:
          f"{mpts:.0f} Mpts/s, {achieved:.1f} TFLOP/s")
 
     extras = {}
+    _log("C2 through the API")
+    aw, ae = bench_mlp_api(x, layers, acts, enc, args.steps, args.warmup)
+    extras["C2_api"] = {
+        "call": "m(rdv.wrap(x)) with set_synchronous(False): plan cached on the map, one rdv_mlp_forward_unpacked "
+                "launch converting the layers' fp32 parameters in the kernel",
+        "us_per_call": round(ae * 1e3, 3),
+        "wall_us_per_call": round(aw * 1e3, 3),
+        "Mpoints_per_s": round(n / (ae * 1e-3) / 1e6, 1),
+        "vs_c_abi_ms_per_step": round(ae / ev, 4),
+    }
+    _log(f"C2 API {extras['C2_api']}")
     if not args.no_extras:
         _log("C1")
         x1, l1 = WL.c1()

@@ -92,9 +92,10 @@ int rdv_mlp_validate(const rdv_mlp_desc* desc);
 int64_t rdv_mlp_packed_bytes(const rdv_mlp_desc* desc);
 
 /* Packs the layers' parameters into `packed` (device, rdv_mlp_packed_bytes
- * bytes, 256-byte aligned).  weights[i] points to layer i's fp32 weight,
- * row-major [dims[i+1], dims[i]] (PyTorch nn.Linear layout), biases[i] to its
- * fp32 bias [dims[i+1]]; both arrays hold DEVICE pointers and live on the host.
+ * bytes, 256-byte aligned), every layer and the header in one launch.
+ * weights[i] points to layer i's fp32 weight, row-major [dims[i+1], dims[i]]
+ * (PyTorch nn.Linear layout), biases[i] to its fp32 bias [dims[i+1]]; both
+ * arrays hold DEVICE pointers and live on the host.
  * Replaces the per-node weight/bias upload of _LinearBase.__init__
  * (src/rdv/domain/nn.py:34-54). */
 int rdv_mlp_pack(const rdv_mlp_desc* desc, const float* const* weights,
@@ -114,6 +115,28 @@ int rdv_mlp_pack(const rdv_mlp_desc* desc, const float* const* weights,
  * src/rdv/shaders/libraries/cooperative_library.h:20-33). */
 int rdv_mlp_forward(const rdv_mlp_desc* desc, const void* packed, const float* x,
                     float* y, int64_t n, void* stream);
+
+/* Bytes of workspace rdv_mlp_forward_unpacked needs for `desc`: 0 when a
+ * compile-time kernel serves the chain and every hidden width is a multiple of
+ * 32 (the kernel then builds its LDS fragments from the parameters itself),
+ * else rdv_mlp_packed_bytes(desc) (< 0 on error). */
+int64_t rdv_mlp_unpacked_workspace_bytes(const rdv_mlp_desc* desc);
+
+/* rdv_mlp_forward from the layers' own parameters -- weights[i] fp32 row-major
+ * [dims[i+1], dims[i]], biases[i] fp32 [dims[i+1]], device pointers in host
+ * arrays, as rdv_mlp_pack takes them -- read at every call, so any update of a
+ * parameter buffer is seen by the next call.  Chains with a compile-time
+ * kernel: one launch (each block converts W into its LDS fragments), plus the
+ * exact-fp32 launch of a partial last 32-row group, which reads W directly;
+ * no workspace.  Other chains: packed into `workspace` (256-byte aligned,
+ * rdv_mlp_unpacked_workspace_bytes bytes; RDV_ERR_WORKSPACE when smaller) by
+ * one pack launch, then rdv_mlp_forward.  Same results as rdv_mlp_pack +
+ * rdv_mlp_forward.  Replaces Map.__call__ -> dispatch(MapEvaluator), whose
+ * LinearFast reads the weights through their buffer pointers at every dispatch
+ * (src/rdv/maths/__init__.py:1451-1487, src/rdv/shaders/maps/linear_fast.h:39-60). */
+int rdv_mlp_forward_unpacked(const rdv_mlp_desc* desc, const float* const* weights, const float* const* biases,
+                             const float* x, float* y, int64_t n, void* workspace, int64_t workspace_bytes,
+                             void* stream);
 
 /* Same as rdv_mlp_forward but evaluates every row (tail included) on the fp16
  * matrix-core path; exposed for benchmarking the kernel alone. */

@@ -24,7 +24,7 @@ from .nn import FrequencyEncoding, _Activation, _LinearBase
 
 
 class ChainPlan:
-    __slots__ = ("desc", "layers", "signature", "in_features", "out_features")
+    __slots__ = ("desc", "layers", "signature", "in_features", "out_features", "ws_bytes", "arrays")
 
     def __init__(self, desc, layers, signature, in_features, out_features):
         self.desc = desc
@@ -32,6 +32,8 @@ class ChainPlan:
         self.signature = signature
         self.in_features = in_features
         self.out_features = out_features
+        self.ws_bytes = None  # rdv_mlp_unpacked_workspace_bytes, once known
+        self.arrays = None    # (pointer key, weight array, bias array) of the last call
 
 
 class _ConstantLayer:
@@ -72,6 +74,20 @@ def _plan_constant(c: Constant, in_width: int) -> ChainPlan:
 
 
 def plan_chain(m: Map, in_width: int) -> ChainPlan:
+    """m's lowering for rows of in_width features.  A composition's structure
+    never changes after it is built, so the plan is kept on m per input width
+    (a Constant's is rebuilt: its value buffer may be converted per call)."""
+    plans = m.__dict__.get("_rdv_plans")
+    hit = plans.get(in_width) if plans is not None else None
+    if hit is not None:
+        return hit
+    p = _plan_chain(m, in_width)
+    if p.signature[0] != "constant":
+        m.__dict__.setdefault("_rdv_plans", {})[in_width] = p
+    return p
+
+
+def _plan_chain(m: Map, in_width: int) -> ChainPlan:
     stages = [s for s in m.stages() if not isinstance(s, Identity)]
     if len(stages) == 1 and isinstance(stages[0], Constant):
         return _plan_constant(stages[0], in_width)
@@ -124,31 +140,50 @@ def plan_chain(m: Map, in_width: int) -> ChainPlan:
     return ChainPlan(d, layers, sig, in_width, cur)
 
 
+def _param_arrays(p: ChainPlan):
+    """The layers' weight and bias pointers as the C arrays the ABI takes,
+    rebuilt only when a pointer changed."""
+    key = tuple((l.weight.device_ptr, l.bias.device_ptr) for l in p.layers)
+    if p.arrays is None or p.arrays[0] != key:
+        p.arrays = (key, _lib.void_ptr_array([k[0] for k in key]), _lib.void_ptr_array([k[1] for k in key]))
+    return p.arrays
+
+
+def _packed_buffer(m: Map, p: ChainPlan) -> torch.Tensor:
+    """m's packed-block buffer (256-byte aligned, cached per chain structure).
+    Every call packs into it on the current stream; a call on another stream
+    than the last first waits for that stream's work, so no kernel still
+    reading the block sees it rewritten."""
+    nbytes = int(_lib.load().rdv_mlp_packed_bytes(C.byref(p.desc)))
+    if nbytes < 0:
+        _lib.check(nbytes, "mlp")
+    cached = m.__dict__.get("_rdv_packed")
+    if cached is not None and cached[0] == p.signature:
+        buf, last = cached[1], cached[2]
+        cur = torch.cuda.current_stream()
+        if last is not None and last != cur:
+            cur.wait_stream(last)
+        m.__dict__["_rdv_packed"] = (p.signature, buf, cur)
+        return buf
+    raw = torch.empty(nbytes + 256, dtype=torch.uint8, device=device())
+    off = (-raw.data_ptr()) % 256
+    buf = raw[off: off + nbytes]
+    m.__dict__["_rdv_packed"] = (p.signature, buf, torch.cuda.current_stream())
+    return buf
+
+
 def packed_params(m: Map, p: ChainPlan) -> torch.Tensor:
     """Packed parameter block of `m`, re-packed from the layers' fp32 weight and
-    bias buffers at every call (one small kernel, stream-ordered before the
-    launch that reads it).  The reference reads weights through pointers at
-    every dispatch, so any update of a weight buffer -- in place, through
-    `.data`, through another alias or from outside torch -- is seen by the next
-    evaluation.  Only the packed buffer itself is cached (per chain structure
-    and weight pointers), so steady-state calls allocate nothing."""
-    key = (p.signature, tuple((l.weight.device_ptr, l.bias.device_ptr) for l in p.layers))
-    lib = _lib.load()
-    cached = getattr(m, "_rdv_packed", None)
-    if cached is not None and cached[0] == key:
-        buf = cached[1]
-    else:
-        nbytes = lib.rdv_mlp_packed_bytes(C.byref(p.desc))
-        if nbytes < 0:
-            _lib.check(int(nbytes), "mlp")
-        raw = torch.empty(int(nbytes) + 256, dtype=torch.uint8, device=device())
-        off = (-raw.data_ptr()) % 256
-        buf = raw[off: off + int(nbytes)]
-        m._rdv_packed = (key, buf)
-    ws = _lib.void_ptr_array([l.weight.device_ptr for l in p.layers])
-    bs = _lib.void_ptr_array([l.bias.device_ptr for l in p.layers])
-    _lib.check(lib.rdv_mlp_pack(C.byref(p.desc), ws, bs, C.c_void_p(buf.data_ptr()),
-                                C.c_void_p(current_stream_handle())), "mlp pack")
+    bias buffers at every call (one launch, stream-ordered before the launch
+    that reads it).  The reference reads weights through pointers at every
+    dispatch, so any update of a weight buffer -- in place, through `.data`,
+    through another alias or from outside torch -- is seen by the next
+    evaluation.  Only the packed buffer itself is cached, so steady-state calls
+    allocate nothing."""
+    buf = _packed_buffer(m, p)
+    _, ws, bs = _param_arrays(p)
+    _lib.check(_lib.load().rdv_mlp_pack(C.byref(p.desc), ws, bs, C.c_void_p(buf.data_ptr()),
+                                        C.c_void_p(current_stream_handle())), "mlp pack")
     return buf
 
 
@@ -180,10 +215,20 @@ def evaluate_map(m: Map, x) -> RDVObject:
 
 
 def _launch(m: Map, p: ChainPlan, x_ptr: int, y_ptr: int, rows: int) -> None:
-    packed = packed_params(m, p)
-    _lib.check(_lib.load().rdv_mlp_forward(C.byref(p.desc), C.c_void_p(packed.data_ptr()), C.c_void_p(x_ptr),
-                                           C.c_void_p(y_ptr), C.c_int64(rows),
-                                           C.c_void_p(current_stream_handle())), "mlp forward")
+    """One rdv_mlp_forward_unpacked call: the layers' parameters are read at
+    this call (a chain with a compile-time kernel converts them in the kernel;
+    any other is packed into m's cached buffer first, in the same call)."""
+    lib = _lib.load()
+    if p.ws_bytes is None:
+        nb = int(lib.rdv_mlp_unpacked_workspace_bytes(C.byref(p.desc)))
+        if nb < 0:
+            _lib.check(nb, "mlp")
+        p.ws_bytes = nb
+    _, ws, bs = _param_arrays(p)
+    wsp = _packed_buffer(m, p).data_ptr() if p.ws_bytes else None
+    _lib.check(lib.rdv_mlp_forward_unpacked(C.byref(p.desc), ws, bs, C.c_void_p(x_ptr), C.c_void_p(y_ptr),
+                                            C.c_int64(rows), C.c_void_p(wsp), C.c_int64(p.ws_bytes),
+                                            C.c_void_p(current_stream_handle())), "mlp forward")
 
 
 def launch_map_rows(m: Map, x_ptr: int, y_ptr: int, rows: int) -> None:

@@ -170,6 +170,9 @@ _SIGNATURES = {
     "rdv_mlp_pack": (C.c_int, [C.POINTER(MlpDesc), C.POINTER(C.c_void_p), C.POINTER(C.c_void_p), C.c_void_p,
                                C.c_void_p]),
     "rdv_mlp_forward": (C.c_int, [C.POINTER(MlpDesc), C.c_void_p, C.c_void_p, C.c_void_p, C.c_int64, C.c_void_p]),
+    "rdv_mlp_unpacked_workspace_bytes": (C.c_int64, [C.POINTER(MlpDesc)]),
+    "rdv_mlp_forward_unpacked": (C.c_int, [C.POINTER(MlpDesc), C.POINTER(C.c_void_p), C.POINTER(C.c_void_p),
+                                           C.c_void_p, C.c_void_p, C.c_int64, C.c_void_p, C.c_int64, C.c_void_p]),
     "rdv_mlp_forward_f16_all": (C.c_int, [C.POINTER(MlpDesc), C.c_void_p, C.c_void_p, C.c_void_p, C.c_int64,
                                           C.c_void_p]),
     "rdv_mlp_kernel_name": (C.c_char_p, [C.POINTER(MlpDesc)]),

@@ -53,7 +53,11 @@ const char* generic_f16_name(const rdv_mlp_desc& d, const MlpLayout& lay);
 int launch_mlp_generic_f16(const rdv_mlp_desc& d, const MlpLayout& lay, const void* packed, const float* x, float* y,
                            int64_t nrows, hipStream_t stream);
 int launch_mlp_chain_f32(const rdv_mlp_desc& d, const MlpLayout& lay, const void* packed, const float* x,
-                         float* y, int64_t row0, int64_t nrows, bool force_f32, hipStream_t stream);
+                         float* y, int64_t row0, int64_t nrows, bool force_f32, hipStream_t stream,
+                         const DirectWeights* dw = nullptr);
+int launch_fused_entry_direct(const FusedEntry* e, const rdv_mlp_desc& d, const MlpLayout& lay,
+                              const DirectWeights& dw, const float* x, float* y, int64_t nrows, hipStream_t stream);
+bool direct_fused_ok(const FusedEntry* e, const rdv_mlp_desc& d);
 int launch_mlp_pack(const rdv_mlp_desc& d, const MlpLayout& lay, const float* const* W, const float* const* b,
                     void* packed, hipStream_t stream);
 int prepare_chain_f32(const rdv_mlp_desc& d);
@@ -254,6 +258,51 @@ static int mlp_forward_impl(const rdv_mlp_desc* desc, const void* packed, const 
 int rdv_mlp_forward(const rdv_mlp_desc* desc, const void* packed, const float* x, float* y, int64_t n,
                     void* stream) {
   return mlp_forward_impl(desc, packed, x, y, n, stream, true);
+}
+
+int64_t rdv_mlp_unpacked_workspace_bytes(const rdv_mlp_desc* desc) {
+  MlpLayout lay;
+  int rc = check_mlp(desc, &lay);
+  if (rc != RDV_OK) return rc;
+  if (direct_fused_ok(find_fused(*desc, lay), *desc)) return 0;
+  return lay.total_bytes;
+}
+
+int rdv_mlp_forward_unpacked(const rdv_mlp_desc* desc, const float* const* weights, const float* const* biases,
+                             const float* x, float* y, int64_t n, void* workspace, int64_t workspace_bytes,
+                             void* stream) {
+  MlpLayout lay;
+  int rc = check_mlp(desc, &lay);
+  if (rc != RDV_OK) return rc;
+  if (n < 0) return fail(RDV_ERR_INVALID, "row count must be >= 0");
+  if (!weights || !biases) return fail(RDV_ERR_INVALID, "rdv_mlp_forward_unpacked: NULL parameter array");
+  DirectWeights dw = {};
+  for (int i = 0; i < desc->n_layers; ++i) {
+    if (!weights[i] || !biases[i]) return fail(RDV_ERR_INVALID, "rdv_mlp_forward_unpacked: NULL layer parameter");
+    dw.W[i] = weights[i];
+    dw.b[i] = biases[i];
+  }
+  if (n == 0) return RDV_OK;
+  if (!x || !y) return fail(RDV_ERR_INVALID, "rdv_mlp_forward_unpacked: NULL pointer argument");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const FusedEntry* e = find_fused(*desc, lay);
+  if (!direct_fused_ok(e, *desc)) {  // pack into the workspace, then the packed path
+    if (workspace_bytes < lay.total_bytes || workspace == nullptr)
+      return fail(RDV_ERR_WORKSPACE, "workspace of " + std::to_string(workspace_bytes) + " bytes; this chain needs " +
+                                         std::to_string(lay.total_bytes));
+    if (reinterpret_cast<uintptr_t>(workspace) % 256) return fail(RDV_ERR_INVALID, "workspace must be 256-byte aligned");
+    rc = launch_mlp_pack(*desc, lay, dw.W, dw.b, workspace, s);
+    if (rc != RDV_OK) return rc;
+    return mlp_forward_impl(desc, workspace, x, y, n, stream, true);
+  }
+  const int64_t n_full = (n / 32) * 32;
+  rc = launch_fused_entry_direct(e, *desc, lay, dw, x, y, n_full, s);
+  if (rc != RDV_OK) return rc;
+  if (n > n_full) {
+    rc = prepare_chain_f32(*desc);
+    if (rc == RDV_OK) rc = launch_mlp_chain_f32(*desc, lay, nullptr, x, y, n_full, n - n_full, true, s, &dw);
+  }
+  return rc;
 }
 
 int rdv_mlp_forward_f16_all(const rdv_mlp_desc* desc, const void* packed, const float* x, float* y, int64_t n,

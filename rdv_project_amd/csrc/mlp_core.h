@@ -174,6 +174,202 @@ __device__ __forceinline__ void stage_net_weights(const uint8_t* packed, const M
   }
 }
 
+// Shapes of stage_net_weights_direct for a compile-time network whose hidden
+// widths are whole 32-row tiles (the host checks that: direct_fused_ok): layer
+// q's weights are copied, fp32, into an LDS staging area with a row stride of
+// pitch(q) floats -- the columns the layer reads plus padding that spreads a
+// fragment read's 32 rows over the banks -- and the fragments are then built
+// from there.
+template <class N, int THREADS>
+struct DirectStage {
+  static constexpr int kCols0 = N::kEnc == RDV_ENC_FREQ ? N::kIn * (1 + 2 * N::kOct) : N::kIn;
+  static constexpr int cols(int q) { return q == 0 ? kCols0 : 32 * N::mt(q - 1); }
+  static constexpr int rows(int q) { return q == N::kL - 1 ? N::kOut : 32 * N::mt(q); }
+  static constexpr int pitch(int q) { return q == 0 ? kCols0 + 1 : cols(q) + 4; }
+  static constexpr int base(int q) {
+    int s = 0;
+    for (int i = 0; i < q; ++i) s += rows(i) * pitch(i);
+    return s;
+  }
+  static constexpr int kFloats = base(N::kL);
+  // loads: layer 0 one float per element, later layers one float4
+  static constexpr int items(int q) { return q == 0 ? rows(0) * kCols0 : rows(q) * cols(q) / 4; }
+  static constexpr int load_iters(int q) { return (items(q) + THREADS - 1) / THREADS; }
+  static constexpr int units(int q) { return N::mt(q) * N::kc(q) * 64; }
+  static constexpr int unit_iters(int q) { return (units(q) + THREADS - 1) / THREADS; }
+};
+
+// layer0_slot_feature for a compile-time network, by slot s = 8c + j of lane
+// half hh: a FREQ half's trig slots hold, octave after octave, D sines then D
+// cosines, which is the encoded feature order itself, so feature = D + 2D
+// (first octave of the half) + s with no division; half 0 then holds p.
+template <class N>
+__device__ __forceinline__ int layer0_slot_feature_of(int s, int hh) {
+  constexpr int D = N::kIn;
+  if constexpr (N::kEnc != RDV_ENC_FREQ) {
+    return 16 * (s >> 3) + 8 * hh + (s & 7);
+  } else {
+    constexpr int L = N::kOct, H0 = (L + 1) / 2;
+    const int nh = hh ? L - H0 : H0, kbase = hh ? H0 : 0;
+    if (s < 2 * D * nh) return D + 2 * D * kbase + s;
+    return (hh == 0 && s < 2 * D * H0 + D) ? s - 2 * D * H0 : -1;
+  }
+}
+
+// Copy of layer Q's weights into the staging area: coalesced global loads
+// (consecutive threads, consecutive elements), all issued before the writes.
+template <class N, int THREADS, int Q>
+__device__ __forceinline__ void direct_copy_layer(const DirectWeights& dw, const MlpLayout& lay, float* st) {
+  using S = DirectStage<N, THREADS>;
+  constexpr int I = S::items(Q), K = S::load_iters(Q), C = S::cols(Q);
+  const int tid = int(threadIdx.x);
+  const float* W = dw.W[Q];
+  if constexpr (Q == 0) {
+    const int in_w = lay.in_w[0];
+    float v[K];
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const int e0 = k * THREADS + tid;
+      const int e = e0 < I ? e0 : I - 1;
+      const int m = e / C, col = e - m * C;
+      v[k] = W[int64_t(m) * in_w + col];
+    }
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const int e = k * THREADS + tid;
+      if (e < I) {
+        const int m = e / C, col = e - m * C;
+        st[S::base(0) + m * S::pitch(0) + col] = v[k];
+      }
+    }
+  } else {
+    constexpr int C4 = C / 4;
+    f32x4 v[K];
+    if ((reinterpret_cast<uintptr_t>(W) & 15) == 0) {
+      const f32x4* W4 = reinterpret_cast<const f32x4*>(W);
+#pragma unroll
+      for (int k = 0; k < K; ++k) {
+        const int e0 = k * THREADS + tid;
+        v[k] = W4[e0 < I ? e0 : I - 1];  // rows are exactly C floats: the flat float4 index
+      }
+    } else {  // a buffer off 16-byte alignment: the same elements, one float at a time
+#pragma unroll
+      for (int k = 0; k < K; ++k) {
+        const int e0 = k * THREADS + tid;
+        const float* p = W + 4 * int64_t(e0 < I ? e0 : I - 1);
+        v[k] = f32x4{p[0], p[1], p[2], p[3]};
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const int e = k * THREADS + tid;
+      if (e < I) {
+        const int m = e / C4, c4 = e - m * C4;
+        *reinterpret_cast<f32x4*>(st + S::base(Q) + m * S::pitch(Q) + 4 * c4) = v[k];
+      }
+    }
+  }
+}
+
+// Fragment units of layer Q from the staging area (the packer's slot mapping,
+// mlp_pack.hip): a hidden layer's unit is two runs of four consecutive columns
+// (the chunk_sigma quartets), two 16-byte reads; layer 0's follow its encoding.
+template <class N, int THREADS, int Q>
+__device__ __forceinline__ void direct_build_layer(const float* st, half8* sw) {
+  using S = DirectStage<N, THREADS>;
+  constexpr int U = S::units(Q), K = S::unit_iters(Q);
+  const int tid = int(threadIdx.x);
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    const int u = k * THREADS + tid;
+    if (u < U) {
+      const int f = u >> 6, lane = u & 63;
+      const int t = f / N::kc(Q), c = f - t * N::kc(Q);
+      const int m = 32 * t + (lane & 31), hh = lane >> 5;
+      const bool row_ok = m < S::rows(Q);
+      const float* r = st + S::base(Q) + (row_ok ? m : 0) * S::pitch(Q);
+      half8 v;
+      if constexpr (Q == 0) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const int ka = layer0_slot_feature_of<N>(8 * c + j, hh);
+          const float x = r[ka >= 0 ? ka : 0];
+          v[j] = half_t(row_ok && ka >= 0 ? x : 0.0f);
+        }
+      } else {
+        const int col0 = 16 * c + 4 * hh;  // columns col0 .. +3 and col0 + 8 .. +11
+        const f32x4 lo = *reinterpret_cast<const f32x4*>(r + col0);
+        const f32x4 hi = *reinterpret_cast<const f32x4*>(r + col0 + 8);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          v[j] = half_t(row_ok ? lo[j] : 0.0f);
+          v[4 + j] = half_t(row_ok ? hi[j] : 0.0f);
+        }
+      }
+      sw[N::frag_base(Q) * 64 + u] = v;
+    }
+  }
+}
+
+template <class N, int THREADS, int Q>
+struct DirectLayers {
+  __device__ __forceinline__ static void copy(const DirectWeights& dw, const MlpLayout& lay, float* st) {
+    direct_copy_layer<N, THREADS, Q>(dw, lay, st);
+    if constexpr (Q + 1 < N::kL) DirectLayers<N, THREADS, Q + 1>::copy(dw, lay, st);
+  }
+  __device__ __forceinline__ static void build(const float* st, half8* sw) {
+    direct_build_layer<N, THREADS, Q>(st, sw);
+    if constexpr (Q + 1 < N::kL) DirectLayers<N, THREADS, Q + 1>::build(st, sw);
+  }
+};
+
+// stage_net_weights for parameters read straight from the layers' fp32 buffers
+// (no packed block): the weights are copied into the staging area `st`
+// (DirectStage::kFloats floats), then every fragment unit is built from there.
+// Returns whether any of this thread's biases is non-zero (the block ORs them
+// in place of the packer's header flags).  Contains a block barrier.
+template <class N, int THREADS>
+__device__ __forceinline__ bool stage_net_weights_direct(const DirectWeights& dw, const MlpLayout& lay, float* sb,
+                                                         half8* sw, float* st) {
+  constexpr int kBPer = (N::kBias + THREADS - 1) / THREADS;
+  const int tid = int(threadIdx.x);
+  float b[kBPer];
+#pragma unroll
+  for (int k = 0; k < kBPer; ++k) {
+    const int i0 = k * THREADS + tid;
+    const int i = i0 < N::kBias ? i0 : N::kBias - 1;
+    int q = 0;
+#pragma unroll
+    for (int qq = 1; qq < N::kL; ++qq)
+      if (i >= N::bias_base(qq)) q = qq;
+    const float* Bq = dw.b[0];
+    int bb = 0;
+#pragma unroll
+    for (int qq = 1; qq < N::kL; ++qq)
+      if (q == qq) {
+        Bq = dw.b[qq];
+        bb = N::bias_base(qq);
+      }
+    const int o = i - bb;
+    const bool ok = o < lay.out_w[q];
+    b[k] = Bq[ok ? o : 0];
+    b[k] = ok ? b[k] : 0.0f;
+  }
+  DirectLayers<N, THREADS, 0>::copy(dw, lay, st);
+  __syncthreads();
+  DirectLayers<N, THREADS, 0>::build(st, sw);
+  bool nz = false;
+#pragma unroll
+  for (int k = 0; k < kBPer; ++k) {
+    const int i = k * THREADS + tid;
+    if (i < N::kBias) {
+      sb[i] = b[k];
+      nz = nz || b[k] != 0.0f;
+    }
+  }
+  return nz;
+}
+
 // A wave's view of the block's LDS copy of the A fragments: fragment f is a
 // conflict-free 1 KiB line, one ds_read_b128 per lane, read right before its MFMA.
 struct LdsWeights {

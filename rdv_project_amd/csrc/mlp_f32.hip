@@ -24,6 +24,8 @@ struct ChainF32Args {
   int encoding, enc_d, enc_l;
   int act[RDV_MLP_MAX_LAYERS];
   int prec[RDV_MLP_MAX_LAYERS];
+  int direct;        // 1: parameters from dw (the layers' own fp32 buffers), not the packed block
+  DirectWeights dw;
   MlpLayout lay;
 };
 
@@ -59,8 +61,10 @@ __global__ __launch_bounds__(64) void mlp_chain_f32_kernel(ChainF32Args a) {
   float* nxt = buf1;
   for (int li = 0; li < a.lay.n_layers; ++li) {
     const int iw = a.lay.in_w[li], ow = a.lay.out_w[li];
-    const float* __restrict__ W = reinterpret_cast<const float*>(a.packed + a.lay.w32_off[li]);
-    const float* __restrict__ B = reinterpret_cast<const float*>(a.packed + a.lay.b32_off[li]);
+    const float* __restrict__ W =
+        a.direct ? a.dw.W[li] : reinterpret_cast<const float*>(a.packed + a.lay.w32_off[li]);
+    const float* __restrict__ B =
+        a.direct ? a.dw.b[li] : reinterpret_cast<const float*>(a.packed + a.lay.b32_off[li]);
     const bool f16 = a.prec[li] == RDV_PREC_F16 && !a.force_f32;
     const int act = a.act[li];
     if (live) {
@@ -114,9 +118,11 @@ int prepare_chain_f32(const rdv_mlp_desc& d) {
 
 int launch_mlp_chain_f32(const rdv_mlp_desc& d, const MlpLayout& lay, const void* packed,
                          const float* x, float* y, int64_t row0, int64_t nrows, bool force_f32,
-                         hipStream_t stream) {
+                         hipStream_t stream, const DirectWeights* dw) {
   if (nrows <= 0) return RDV_OK;
-  ChainF32Args a;
+  ChainF32Args a = {};
+  a.direct = dw != nullptr ? 1 : 0;
+  if (dw != nullptr) a.dw = *dw;
   a.x = x;
   a.y = y;
   a.packed = static_cast<const uint8_t*>(packed);

@@ -19,8 +19,9 @@ namespace rdv {
 struct FusedArgs {
   const float* x;
   float* y;
-  const uint8_t* packed;
-  int64_t nrows;  // rows evaluated by this launch (starting at x / y)
+  const uint8_t* packed;  // the packed block (DIRECT kernels: unused)
+  DirectWeights dw;       // the layers' fp32 parameters (DIRECT kernels)
+  int64_t nrows;          // rows evaluated by this launch (starting at x / y)
   int act[RDV_MLP_MAX_LAYERS];
   MlpLayout lay;
 };
@@ -49,7 +50,10 @@ struct FusedArgs {
 constexpr int kWaves2 = 8;
 constexpr int kThreads2 = 64 * kWaves2;
 
-template <class N, bool RELU, int HEAD_ACT>
+//  - DIRECT: the block builds its LDS fragments from the layers' fp32 buffers
+//    (stage_net_weights_direct) instead of copying a packed block, so a caller
+//    holding only nn.Linear-layout parameters needs no separate pack launch.
+template <class N, bool RELU, int HEAD_ACT, bool DIRECT = false>
 __global__ __launch_bounds__(kThreads2, 1) void mlp_fused_f16_kernel(FusedArgs a) {
   constexpr int D = N::kIn;
   constexpr int LL = N::kL - 1;
@@ -58,6 +62,7 @@ __global__ __launch_bounds__(kThreads2, 1) void mlp_fused_f16_kernel(FusedArgs a
   __shared__ half8 sw[N::kFrags * 64];
   __shared__ float sx[kWaves2][2][D * 64];  // each wave's input pair tiles (double buffer), [d][row]
   __shared__ int s_next;
+  __shared__ float sst[DIRECT ? DirectStage<N, kThreads2>::kFloats : 1];  // DIRECT: fp32 weight staging
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int h = lane >> 5, col = lane & 31;
@@ -67,7 +72,8 @@ __global__ __launch_bounds__(kThreads2, 1) void mlp_fused_f16_kernel(FusedArgs a
   const int64_t t_begin = int64_t(blockIdx.x) * per_block;
   const int64_t t_end = t_begin + per_block < ntiles ? t_begin + per_block : ntiles;
   const int nt = int(t_end > t_begin ? t_end - t_begin : 0);
-  const bool has_bias = (reinterpret_cast<const MlpPackHeader*>(a.packed)->flags & kMlpHasBias) != 0;
+  bool has_bias = false;
+  if constexpr (!DIRECT) has_bias = packed_has_bias(a.packed);
 
   // DMA of pair tile lt (64 rows, lane l -> row l, clamped to the last row) into buffer `buf`
   const int64_t last = a.nrows - 1;
@@ -93,9 +99,15 @@ __global__ __launch_bounds__(kThreads2, 1) void mlp_fused_f16_kernel(FusedArgs a
   int cur = wave;
   dma_tile(cur, 0);
 
-  stage_net_weights<N, kThreads2>(a.packed, a.lay, sb, sw);
-  if (threadIdx.x == 0) s_next = kWaves2;
-  __syncthreads();
+  if constexpr (DIRECT) {
+    const bool nz = stage_net_weights_direct<N, kThreads2>(a.dw, a.lay, sb, sw, sst);
+    if (threadIdx.x == 0) s_next = kWaves2;
+    has_bias = __syncthreads_or(nz ? 1 : 0) != 0;
+  } else {
+    stage_net_weights<N, kThreads2>(a.packed, a.lay, sb, sw);
+    if (threadIdx.x == 0) s_next = kWaves2;
+    __syncthreads();
+  }
 
   auto claim = [&]() {
     int t = 0;
@@ -161,7 +173,7 @@ using NetFreq3x6_64x2_4 = Net<RDV_ENC_FREQ, 3, 6, 4, 3, 2, 2, 1>;     // enc(39-
 
 typedef int (*FusedLauncher)(const FusedArgs&, int64_t nrows, hipStream_t);
 
-template <class N, bool RELU, int HEAD_ACT>
+template <class N, bool RELU, int HEAD_ACT, bool DIRECT = false>
 int launch_fused(const FusedArgs& a, int64_t nrows, hipStream_t stream) {
   if (nrows <= 0) return RDV_OK;
   DeviceInfo di;
@@ -171,7 +183,7 @@ int launch_fused(const FusedArgs& a, int64_t nrows, hipStream_t stream) {
   int64_t blocks = di.cu_count;
   const int64_t need = ((nrows + 63) / 64 + kWaves2 - 1) / kWaves2;
   if (need < blocks) blocks = need;
-  mlp_fused_f16_kernel<N, RELU, HEAD_ACT><<<dim3(unsigned(blocks)), dim3(kThreads2), 0, stream>>>(a);
+  mlp_fused_f16_kernel<N, RELU, HEAD_ACT, DIRECT><<<dim3(unsigned(blocks)), dim3(kThreads2), 0, stream>>>(a);
   RDV_HIP_TRY(hipGetLastError());
   return RDV_OK;
 }
@@ -179,7 +191,8 @@ int launch_fused(const FusedArgs& a, int64_t nrows, hipStream_t stream) {
 struct FusedEntry {
   int enc, in, oct, out, L, kc0, hidden_act, head_act;
   int mt[RDV_MLP_MAX_LAYERS];
-  FusedLauncher fn;
+  FusedLauncher fn;         // packed parameters
+  FusedLauncher fn_direct;  // the layers' fp32 parameters
   const char* name;
 };
 
@@ -196,6 +209,7 @@ FusedEntry entry(const char* name) {
   e.kc0 = N::kc(0);
   for (int i = 0; i < N::kL; ++i) e.mt[i] = N::mt(i);
   e.fn = &launch_fused<N, RELU, HEAD_ACT>;
+  e.fn_direct = &launch_fused<N, RELU, HEAD_ACT, true>;
   e.name = name;
   return e;
 }
@@ -237,9 +251,21 @@ const FusedEntry* find_fused(const rdv_mlp_desc& d, const MlpLayout& lay) {
 
 const char* fused_name(const FusedEntry* e) { return e ? e->name : nullptr; }
 
+// Can the DIRECT kernel of `e` read the chain's parameters?  Its staging copies
+// whole rows of the later layers: every hidden width must be a whole number of
+// 32-row tiles (the instantiated widths; a narrower layer sharing a tile count
+// takes the packed path).  Layer 0's rows hold at least the encoded features
+// (check_mlp ensures it).
+bool direct_fused_ok(const FusedEntry* e, const rdv_mlp_desc& d) {
+  if (e == nullptr) return false;
+  for (int i = 1; i < d.n_layers; ++i)
+    if (d.dims[i] != 32 * e->mt[i - 1]) return false;
+  return true;
+}
+
 int launch_fused_entry(const FusedEntry* e, const rdv_mlp_desc& d, const MlpLayout& lay, const void* packed,
                        const float* x, float* y, int64_t nrows, hipStream_t stream) {
-  FusedArgs a;
+  FusedArgs a = {};
   a.x = x;
   a.y = y;
   a.packed = static_cast<const uint8_t*>(packed);
@@ -247,6 +273,19 @@ int launch_fused_entry(const FusedEntry* e, const rdv_mlp_desc& d, const MlpLayo
   for (int i = 0; i < RDV_MLP_MAX_LAYERS; ++i) a.act[i] = i < d.n_layers ? d.act[i] : 0;
   a.lay = lay;
   return e->fn(a, nrows, stream);
+}
+
+int launch_fused_entry_direct(const FusedEntry* e, const rdv_mlp_desc& d, const MlpLayout& lay,
+                              const DirectWeights& dw, const float* x, float* y, int64_t nrows, hipStream_t stream) {
+  FusedArgs a = {};
+  a.x = x;
+  a.y = y;
+  a.packed = nullptr;
+  a.dw = dw;
+  a.nrows = nrows;
+  for (int i = 0; i < RDV_MLP_MAX_LAYERS; ++i) a.act[i] = i < d.n_layers ? d.act[i] : 0;
+  a.lay = lay;
+  return e->fn_direct(a, nrows, stream);
 }
 
 }  // namespace rdv

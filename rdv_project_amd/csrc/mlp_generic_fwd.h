@@ -57,7 +57,7 @@ __global__ __launch_bounds__(64 * gen_waves<MT>(), 1) void mlp_generic_f16_kerne
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int h0 = lane >> 5, col = lane & 31;
-  const bool has_bias = (reinterpret_cast<const MlpPackHeader*>(a.packed)->flags & kMlpHasBias) != 0;
+  const bool has_bias = packed_has_bias(a.packed);
 
   const half8* wsrc0;
   const float* bsrc0;

@@ -43,12 +43,25 @@
 namespace rdv {
 
 // First 256 bytes of a packed block.
+// Each word is written by exactly one thread of the single pack launch, so no
+// word needs clearing first: layer_bias[i] by the block that packs layer i's
+// bias, the rest by layer 0's.
 struct MlpPackHeader {
-  uint32_t magic;  // kMlpPackMagic once packed
-  uint32_t flags;  // kMlpHasBias: some bias element is non-zero
+  uint32_t magic;                             // kMlpPackMagic once packed
+  uint32_t reserved;
+  uint32_t layer_bias[RDV_MLP_MAX_LAYERS];  // 1: layer i has a non-zero bias element (0 past the last layer)
 };
-constexpr uint32_t kMlpPackMagic = 0x52445631u;  // "RDV1"
-constexpr uint32_t kMlpHasBias = 1u;
+constexpr uint32_t kMlpPackMagic = 0x52445632u;  // "RDV2"
+
+// Whether any layer of a packed block has a non-zero bias (the kernels then
+// seed their accumulators with the biases; otherwise MFMA's zero C operand).
+__host__ __device__ inline bool packed_has_bias(const uint8_t* packed) {
+  const MlpPackHeader* h = reinterpret_cast<const MlpPackHeader*>(packed);
+  uint32_t any = 0;
+#pragma unroll
+  for (int i = 0; i < RDV_MLP_MAX_LAYERS; ++i) any |= h->layer_bias[i];
+  return any != 0;
+}
 constexpr int64_t kMlpHeaderBytes = 256;
 
 struct MlpLayout {
@@ -65,6 +78,14 @@ struct MlpLayout {
   int64_t w32_off[RDV_MLP_MAX_LAYERS];
   int64_t b32_off[RDV_MLP_MAX_LAYERS];
   int64_t total_bytes;
+};
+
+// The layers' own parameters for the kernels that read them without a packed
+// block: W[i] row-major fp32 [dims[i+1], dims[i]] (nn.Linear layout), b[i] fp32
+// [dims[i+1]], device pointers.
+struct DirectWeights {
+  const float* W[RDV_MLP_MAX_LAYERS];
+  const float* b[RDV_MLP_MAX_LAYERS];
 };
 
 __host__ __device__ inline int div_up(int a, int b) { return (a + b - 1) / b; }

@@ -214,7 +214,7 @@ __global__ __launch_bounds__(kEaThreads, 1) void render_ea_kernel(RenderArgs a) 
   const int64_t nrays = ea_ray_count(a);
   const BlockRays br(nrays, false);
   const int nr = br.count;
-  const bool has_bias = (reinterpret_cast<const MlpPackHeader*>(a.packed)->flags & kMlpHasBias) != 0;
+  const bool has_bias = packed_has_bias(a.packed);
   stage_weights<N, kEaThreads>(a.packed, a.lay, sb, sw, &s_next);
 
   auto claim = [&]() {
@@ -662,7 +662,7 @@ __global__ __launch_bounds__(kRenderThreads, 1) void raymarch_transmittance_kern
   __shared__ int s_next;
   const int lane = threadIdx.x & 63;
   const int h = lane >> 5;
-  const bool has_bias = (reinterpret_cast<const MlpPackHeader*>(a.packed)->flags & kMlpHasBias) != 0;
+  const bool has_bias = packed_has_bias(a.packed);
   stage_weights<N, kRenderThreads>(a.packed, a.lay, sb, sw, &s_next);
   raymarch_rays(a, &s_next, [&](const float (&xc)[3]) {
     f32x16 fin[N::kMaxMT];
@@ -687,7 +687,7 @@ __global__ __launch_bounds__(64 * gen_waves<MT>(), 1) void raymarch_generic_kern
   const GenNet& g = ga.net;
   const int lane = threadIdx.x & 63;
   const int h = lane >> 5;
-  const bool has_bias = (reinterpret_cast<const MlpPackHeader*>(a.packed)->flags & kMlpHasBias) != 0;
+  const bool has_bias = packed_has_bias(a.packed);
   const half8* w0;
   const float* b0;
   gen_sources<LDSW>(a.packed, g, smem, &w0, &b0);
@@ -807,7 +807,7 @@ __global__ __launch_bounds__(64 * gen_waves<MT>(), 1) void ratiotracking_generic
   const GenNet& g = ga.net;
   const int lane = threadIdx.x & 63;
   const int h = lane >> 5, col = lane & 31;
-  const bool has_bias = (reinterpret_cast<const MlpPackHeader*>(ga.packed)->flags & kMlpHasBias) != 0;
+  const bool has_bias = packed_has_bias(ga.packed);
   const half8* w0;
   const float* b0;
   gen_sources<LDSW>(ga.packed, g, smem, &w0, &b0);
@@ -894,7 +894,7 @@ __global__ __launch_bounds__(64 * gen_waves<MT>(), 1) void render_ea_generic_ker
   const int64_t nrays = ea_ray_count(a);
   const BlockRays br(nrays, false);
   const int nr = br.count;
-  const bool has_bias = (reinterpret_cast<const MlpPackHeader*>(a.packed)->flags & kMlpHasBias) != 0;
+  const bool has_bias = packed_has_bias(a.packed);
   const half8* w0;
   const float* b0;
   gen_sources<LDSW>(a.packed, g, smem, &w0, &b0);

@@ -558,7 +558,7 @@ __device__ __forceinline__ void volume_profile_body(const VpGenArgs& ga) {
   const GenNet& g = ga.net;
   const int lane = threadIdx.x & 63;
   const int h = lane >> 5, col = lane & 31;
-  const bool has_bias = (reinterpret_cast<const MlpPackHeader*>(ga.packed)->flags & kMlpHasBias) != 0;
+  const bool has_bias = packed_has_bias(ga.packed);
   const half8* w0;
   const float* b0;
   gen_sources<LDSW>(ga.packed, g, smem, &w0, &b0);

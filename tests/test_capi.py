@@ -88,10 +88,21 @@ def test_packed_bytes_layout():
                 64 * 4, 32 * 4,              # padded fp32 biases
                 64 * 3 * 4, 4 * 64 * 4,      # fp32 weight copies
                 64 * 4, 4 * 4]               # fp32 bias copies
-    off = 256  # header (magic, flags)
+    off = 256  # header (magic, per-layer bias flags)
     for s in sections:  # every section starts 256-byte aligned
         off = (off + s + 255) // 256 * 256
     assert n == off
+    # exact fp32 layers hold fp32 fragments for v_mfma_f32_32x32x2f32: MT x KB (32-row K blocks) x 4 KiB
+    n32 = lib.rdv_mlp_packed_bytes(C.byref(_desc([3, 64, 4], precs=[0, 0])))
+    sections[0:2] = [2 * 1 * 4 * 1024, 1 * 2 * 4 * 1024]
+    off = 256
+    for s in sections:
+        off = (off + s + 255) // 256 * 256
+    assert n32 == off
+    # the unpacked entry needs no workspace where a compile-time kernel serves the chain
+    assert lib.rdv_mlp_unpacked_workspace_bytes(C.byref(_desc([3, 64, 64, 64, 64, 4], acts=[1, 1, 1, 1, 0]))) == 0
+    assert lib.rdv_mlp_unpacked_workspace_bytes(C.byref(_desc([3, 64, 4]))) == n
+    assert lib.rdv_mlp_unpacked_workspace_bytes(C.byref(_desc([3, 64, 4], precs=[0, 0]))) == n32
 
 
 def test_kernel_selection_names():

@@ -263,6 +263,60 @@ def test_generic_prefetched_and_scalar_inputs_agree_bitwise():
     _assert_fp16_parity(ya[:2048].cpu().numpy(), ref[:2048], "prefetched input")
 
 
+@pytest.mark.parametrize("case", ["c1", "c2", "c1_bias", "generic"])
+@pytest.mark.parametrize("n", [4096, 1000, 31])
+def test_unpacked_entry_matches_packed_path(case, n):
+    """rdv_mlp_forward_unpacked (the layers' own fp32 buffers, converted inside
+    the compile-time kernel, or packed into a workspace for other chains) gives
+    the bits of rdv_mlp_pack + rdv_mlp_forward, tail rows included."""
+    import ctypes as C
+    from rdv_project_amd import _chain as CH, _lib
+    enc = None
+    if case.startswith("c1"):
+        x, layers = WL.c1(n)
+        acts = ["relu"] * 4 + ["none"]
+        if case == "c1_bias":
+            layers = [(w, torch.rand(w.shape[0], generator=WL.gen(i)) * 0.2 - 0.1) for i, (w, _) in enumerate(layers)]
+    elif case == "c2":
+        x, layers = WL.c2(n)
+        acts = ["relu"] * 3 + ["none"]
+        enc = rdv.FrequencyEncoding(3, WL.C2_OCTAVES, pad_to=WL.C2_PAD)
+    else:
+        g = WL.gen(23)
+        dims = [20, 96, 40, 6]
+        x = torch.rand(n, 20, generator=g) * 2 - 1
+        layers = [((torch.rand(dims[i + 1], dims[i], generator=g) * 2 - 1) / dims[i] ** 0.5,
+                   torch.rand(dims[i + 1], generator=g) * 0.2 - 0.1) for i in range(3)]
+        acts = ["relu", "relu", "none"]
+    m = _chain(layers, acts, enc=enc)
+    xd = x.cuda()
+    lib = _lib.load()
+    p = CH.plan_chain(m, int(x.shape[1]))
+    packed = CH.packed_params(m, p)
+    ya = torch.empty(n, p.out_features, device="cuda")
+    _lib.check(lib.rdv_mlp_forward(C.byref(p.desc), C.c_void_p(packed.data_ptr()), C.c_void_p(xd.data_ptr()),
+                                   C.c_void_p(ya.data_ptr()), C.c_int64(n), None))
+    nb = int(lib.rdv_mlp_unpacked_workspace_bytes(C.byref(p.desc)))
+    assert (nb == 0) == (case != "generic")
+    _, ws, bs = CH._param_arrays(p)
+    yb = torch.full_like(ya, float("nan"))
+    if nb:
+        raw = torch.empty(nb + 256, dtype=torch.uint8, device="cuda")
+        wsp = raw.data_ptr() + (-raw.data_ptr()) % 256
+        assert lib.rdv_mlp_forward_unpacked(C.byref(p.desc), ws, bs, C.c_void_p(xd.data_ptr()),
+                                            C.c_void_p(yb.data_ptr()), C.c_int64(n), C.c_void_p(wsp),
+                                            C.c_int64(nb - 256), None) == _lib.RDV_ERR_WORKSPACE
+    else:
+        wsp = None
+    _lib.check(lib.rdv_mlp_forward_unpacked(C.byref(p.desc), ws, bs, C.c_void_p(xd.data_ptr()),
+                                            C.c_void_p(yb.data_ptr()), C.c_int64(n), C.c_void_p(wsp),
+                                            C.c_int64(nb), None))
+    torch.cuda.synchronize()
+    assert torch.equal(ya, yb)
+    y = m(rdv.wrap(xd)).as_tensor("torch")  # the API path takes the unpacked entry
+    assert torch.equal(y, ya)
+
+
 def test_output_buffer_cached_per_structure_and_shape():
     x, layers = WL.c1(256)
     m1 = _chain(layers, ["relu"] * 4 + ["none"])
