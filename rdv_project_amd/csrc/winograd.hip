@@ -3,7 +3,8 @@
 // Replaces Conv2DTensorOpWinograd3x3 (src/rdv/domain/nn.py:1002-1087,
 // src/rdv/shaders/tensors/conv2d_tensor_op_winograd3x3.h:95-178) with the same
 // numerics: U = G g G^T in fp32 rounded to fp16 (nn.py:522-538); per tile and
-// input channel V = B^T d B in fp32 rounded to fp16 (.h:59-78, 136); 16
+// input channel V = B^T d B in fp32 rounded to fp16 (.h:59-78, 136; the
+// pipelined kernel's matrix-core sum of the same four terms, below); 16
 // channel-reduction GEMMs with fp32 accumulation (.h:142-161); Y = A^T M A in
 // fp32 plus the fp32 bias (.h:80-93, 169-173); optional ReLU epilogue.
 //
@@ -407,11 +408,11 @@ __device__ __forceinline__ void wg_dma16(const void* src, uint32_t lds_wave) {
       : "memory");
 }
 
+__device__ __forceinline__ void wg_st16(void* p, half_t v) {
+  asm volatile("global_store_short %0, %1, off nt" ::"v"(p), "v"(__builtin_bit_cast(uint16_t, v)) : "memory");
+}
 __device__ __forceinline__ void wg_st32(void* p, uint32_t v) {
   asm volatile("global_store_dword %0, %1, off nt" ::"v"(p), "v"(v) : "memory");
-}
-__device__ __forceinline__ void wg_st64(void* p, f32x2 v) {
-  asm volatile("global_store_dwordx2 %0, %1, off nt" ::"v"(p), "v"(v) : "memory");
 }
 __device__ __forceinline__ void wg_st128(void* p, f32x4 v) {
   asm volatile("global_store_dwordx4 %0, %1, off nt\n\ts_nop 0" ::"v"(p), "v"(v) : "memory");
@@ -449,29 +450,15 @@ __device__ __forceinline__ void wg_static_for(std::integer_sequence<int, I...>, 
 }
 
 // LDS reads issued from inline assembly, so the compiler neither sinks them to
-// their use nor waits for them itself: the role that issues them waits with
-// s_waitcnt lgkmcnt and names the registers it completes (no use of them can
-// be scheduled above the wait).  That role issues no other LDS read, and keeps
-// at most 15 in flight (the counter's range).
-template <int OFF>
-__device__ __forceinline__ uint32_t wg_lds_u32(uint32_t addr) {
-  uint32_t v;
-  asm volatile("ds_read_b32 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF));
-  return v;
-}
+// their use nor waits for them itself: the GEMM role, which issues them, waits
+// with s_waitcnt lgkmcnt and names the registers it completes (no use of them
+// can be scheduled above the wait).  That role issues no other LDS read, and
+// keeps at most 15 in flight (the counter's range).
 template <int OFF>
 __device__ __forceinline__ half8 wg_lds_frag(uint32_t addr) {
   half8 v;
   asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF));
   return v;
-}
-template <int N>
-__device__ __forceinline__ void wg_lds_wait(uint32_t (&w)[4][3]) {
-  asm volatile("s_waitcnt lgkmcnt(%12)"
-               : "+v"(w[0][0]), "+v"(w[0][1]), "+v"(w[0][2]), "+v"(w[1][0]), "+v"(w[1][1]), "+v"(w[1][2]),
-                 "+v"(w[2][0]), "+v"(w[2][1]), "+v"(w[2][2]), "+v"(w[3][0]), "+v"(w[3][1]), "+v"(w[3][2])
-               : "i"(N)
-               : "memory");
 }
 template <int N, int KC>
 __device__ __forceinline__ void wg_lds_wait(half8 (&f)[2][KC]) {
@@ -484,6 +471,10 @@ __device__ __forceinline__ void wg_lds_wait(half8 (&f)[2][KC]) {
 // wg_gemm for the pipelined kernel: the same products and inverse transform in
 // the same order, with the V fragments read two groups ahead of their use (a
 // group: column b = G / 2 of the 4 x 4 domain, rows 2 (G % 2) + 0..1, every kc).
+// The operands are swapped (A = V, B = U: the two fragment layouts are the
+// same), so D is [tile][channel]: lane l holds tiles 4 (l / 16) + 0..3 of
+// channel 16 g + l % 16, and a lane's outputs of one row are 8 consecutive
+// columns of one channel.
 template <int KC>
 __device__ __forceinline__ void wg_gemm_pipe(const half8 (&u)[16][KC], const half8* sv, int lane, f32x4 (&yv)[2][2]) {
   const uint32_t addr = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(sv + lane));
@@ -514,7 +505,7 @@ __device__ __forceinline__ void wg_gemm_pipe(const half8 (&u)[16][KC], const hal
       f32x4 acc = {};
 #pragma unroll
       for (int kc = 0; kc < KC; ++kc)
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(u[4 * (ra0 + r) + b][kc], fr[G % 3][r][kc], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(fr[G % 3][r][kc], u[4 * (ra0 + r) + b][kc], acc, 0, 0, 0);
       ma[ra0 + r] = acc;
     }
     if constexpr (G % 2 == 1) {
@@ -545,76 +536,6 @@ __device__ __forceinline__ void wg_gemm_pipe(const half8 (&u)[16][KC], const hal
   yv[1][1] = y11;
 }
 
-// x +/- y for two fp16 operands, each the high (HI) or low half of its dword, in
-// one v_fma_mix_f32 (x * 1.0 +/- y, the operands widened exactly, one fp32
-// rounding): the value of converting both to fp32 and adding, without the two
-// conversions.
-template <int HI, bool SUB>
-__device__ __forceinline__ float wg_mix(uint32_t x, uint32_t y) {
-  float r;
-  if constexpr (HI && SUB)
-    asm("v_fma_mix_f32 %0, %1, 1.0, -%2 op_sel:[1,0,1] op_sel_hi:[1,0,1]" : "=v"(r) : "v"(x), "v"(y));
-  else if constexpr (HI)
-    asm("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel:[1,0,1] op_sel_hi:[1,0,1]" : "=v"(r) : "v"(x), "v"(y));
-  else if constexpr (SUB)
-    asm("v_fma_mix_f32 %0, %1, 1.0, -%2 op_sel_hi:[1,0,1]" : "=v"(r) : "v"(x), "v"(y));
-  else
-    asm("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel_hi:[1,0,1]" : "=v"(r) : "v"(x), "v"(y));
-  return r;
-}
-
-// 4 x 4 transpose of 32-bit elements within each quad of lanes: lane k (lane %
-// 4) ends with element k of quad lanes 0..3, in that order.  Two exchange stages
-// through DPP quad permutes (partner lane k ^ 1, then k ^ 2).
-__device__ __forceinline__ void wg_quad_transpose(uint32_t (&e)[4], int k) {
-  uint32_t t[4];
-#pragma unroll
-  for (int c = 0; c < 4; ++c) {
-    const uint32_t x = __builtin_amdgcn_update_dpp(0u, e[c ^ 1], 0xB1, 0xF, 0xF, true);  // quad_perm 1,0,3,2
-    t[c] = ((c ^ k) & 1) ? x : e[c];
-  }
-#pragma unroll
-  for (int c = 0; c < 4; ++c) {
-    const uint32_t x = __builtin_amdgcn_update_dpp(0u, t[c ^ 2], 0x4E, 0xF, 0xF, true);  // quad_perm 2,3,0,1
-    e[c] = ((c ^ k) & 2) ? x : t[c];
-  }
-}
-
-// Stores of one tile's 2x2 outputs for this lane's 4 channels (after bias /
-// ReLU) through wg_st*: CHW issues 8 instructions, HWC 4.
-__device__ __forceinline__ void wg_store_asm(const f32x4 (&yv)[2][2], const WinogradArgs& a, int img, int co0,
-                                             int oh, int ow) {
-  const int hw = a.H * a.W;
-  if (a.out_layout == RDV_LAYOUT_CHW) {
-#pragma unroll
-    for (int jj = 0; jj < 4; ++jj)
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const int64_t o = (int64_t(img) * a.cout + co0 + jj) * hw + int64_t(oh + i) * a.W + ow;
-        if (a.out_dtype == RDV_DTYPE_F16) {
-          const half2v hv = {half_t(yv[i][0][jj]), half_t(yv[i][1][jj])};
-          wg_st32(static_cast<half_t*>(a.y) + o, __builtin_bit_cast(uint32_t, hv));
-        } else {
-          const f32x2 fv = {yv[i][0][jj], yv[i][1][jj]};
-          wg_st64(static_cast<float*>(a.y) + o, fv);
-        }
-      }
-  } else {
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int64_t o = (int64_t(img) * hw + int64_t(oh + i) * a.W + ow + j) * a.cout + co0;
-        if (a.out_dtype == RDV_DTYPE_F16) {
-          const half4 hv = {half_t(yv[i][j][0]), half_t(yv[i][j][1]), half_t(yv[i][j][2]), half_t(yv[i][j][3])};
-          wg_st64(static_cast<half_t*>(a.y) + o, __builtin_bit_cast(f32x2, hv));
-        } else {
-          wg_st128(static_cast<float*>(a.y) + o, yv[i][j]);
-        }
-      }
-  }
-}
-
 // ------------------------------------------------------- pipelined kernel
 // winograd3x3_pipe_kernel: each 8-wave block (one per CU) walks a vertical strip
 // of one image, 32 output columns (16 tiles) by rows_per_item tile rows, top to
@@ -628,11 +549,15 @@ __device__ __forceinline__ void wg_store_asm(const f32x4 (&yv)[2][2], const Wino
 //     buffer (s - 1) % 2.
 // Step s = 0 .. R ends with one barrier.  Each role's vector-memory stream is
 // its own (DMAs only; U's loads then stores only), so the input role's waits
-// count its DMA instructions alone.  The V transform is one (tile, 4-channel)
-// unit per input-role thread: 4 x 4 fp16 patch reads from the ring, the
-// reference's fp32 operation order (the first stage widens the fp16 inputs
-// inside v_fma_mix_f32), fp16 rounding, and 16 8-byte writes in B-fragment
-// order.
+// count its DMA instructions alone.  The V transform runs on the matrix cores:
+// one v_mfma_f32_16x16x16_f16 per (channel, 16 tiles) multiplies the patches by
+// the 16 x 16 matrix of B^T (x) B^T (entries 0 and +-1, so the products are
+// exact), and each lane rounds its 4 positions x 8 channels to fp16 and writes
+// 4 B fragments.  Each V value is a sum of four +-d terms.  The reference forms
+// it as (d_i +- d_j) +- (d_k +- d_l) in fp32; both give the same fp32 value
+// whenever the partial sums are exact, which holds when the four fp16 inputs
+// lie within a factor 2^12 of each other (or are zero).  Otherwise the two can
+// differ by fp32 rounding before V's fp16 rounding.
 constexpr int kPipeSlots = 4;
 template <int KC>
 struct WgPipeLds {
@@ -669,9 +594,6 @@ __global__ __launch_bounds__(512, 1) void winograd3x3_pipe_kernel(WinogradArgs a
 
   if (role == 1) {
     // ================= input role
-    // the input role issues first where both roles are ready (measured 2-4% faster
-    // than equal priority, and than the GEMM role first)
-    __builtin_amdgcn_s_setprio(3);
     const uint32_t ring_lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(ring));
     int Ld = 0;  // this wave's DMA instructions per pair
 #pragma unroll
@@ -695,8 +617,22 @@ __global__ __launch_bounds__(512, 1) void winograd3x3_pipe_kernel(WinogradArgs a
         }
       }
     };
-    const int vt = tid - 256;  // this thread's (tile, 4-channel) unit
-    const int n = vt & 15, qd = vt >> 4;
+    // V = B^T d B as one v_mfma_f32_16x16x16_f16 per channel and 16 tiles:
+    // V[p][tile] = sum_k T[p][k] d[k][tile] with p = 4a + b the transform-domain
+    // position, k = 4i + j the patch position (row i, column j) and
+    // T[p][k] = B^T[a][i] B^T[b][j] in {0, +-1}.  Lane (q, n) holds the A row
+    // p = n, columns k = 4q .. 4q + 3 of T; the B column of tile n, patch row q;
+    // and D rows p = 4q .. 4q + 3 of tile n.
+    const int n = lane & 15, qr = lane >> 4;
+    half4 tfrag;
+    {
+      // B^T = {{1, 0, -1, 0}, {0, 1, 1, 0}, {0, -1, 1, 0}, {0, 1, 0, -1}}, entry
+      // (r, c) as a 2-bit two's-complement field at bit 2 (4 r + c)
+      auto bt = [](int r, int c) { return int(0xc41c1431u << (30 - 2 * (4 * r + c))) >> 30; };
+      const int a0 = n >> 2, b0 = n & 3;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) tfrag[j] = half_t(float(bt(a0, qr) * bt(b0, j)));
+    }
     for (int64_t item = blockIdx.x; item < a.items; item += gridDim.x) {
       int img, seg, tr0;
       decode(item, img, seg, tr0);
@@ -706,64 +642,42 @@ __global__ __launch_bounds__(512, 1) void winograd3x3_pipe_kernel(WinogradArgs a
       __syncthreads();
       for (int s = 0; s <= R; ++s) {
         if (s < R) {
-          // ---- V = B^T d B of tile row s (pairs s, s + 1) per (tile, 4 channels)
-          if (qd < CH / 4) {
+          // ---- V = B^T d B of tile row s (pairs s, s + 1): wave w transforms the
+          // 8-channel groups w, w + 4, .. of the 16 tiles.  Columns 2n-1 .. 2n+2 of
+          // tile n are halves 2n+7 .. 2n+10 of a staged row = the high half of dword
+          // n+3, dword n+4 and the low half of dword n+5; patch rows 0, 1 are rows
+          // of pair s (slot sa), rows 2, 3 of pair s + 1 (slot sb).
+          {
             const int sa = s % kPipeSlots, sb = (s + 1) % kPipeSlots;
-            // columns 2n-1 .. 2n+2 of the tile = halves 2n+7 .. 2n+10 of a staged
-            // row = dwords n+3 .. n+5; input rows 0, 1 in slot sa, rows 2, 3 in sb.
-            // Read i (0..47) is dword i % 3 of row (i % 12) / 3 of channel i / 12.
-            // 15 go out first; once channel c's 12 have landed, the reads up to
-            // 15 past them are issued, and channel c is transformed under them.
-            const uint32_t at = ring_lds + uint32_t(4 * qd * kRowBytes + 4 * (n + 3));
-            const uint32_t base0 = at + uint32_t(sa * kSlotBytes), base1 = at + uint32_t(sb * kSlotBytes);
-            uint32_t wv[4][4][3];
-            auto reads = [&](auto lo, auto hi) {
-              constexpr int L = decltype(lo)::value, H = decltype(hi)::value;
-              wg_static_for(std::make_integer_sequence<int, H - L>{}, [&](auto ii) {
-                constexpr int i = L + decltype(ii)::value, c = i / 12, dr = (i % 12) / 3, k = i % 3;
-                wv[c][dr][k] = wg_lds_u32<((dr & 1) * CH + c) * kRowBytes + 4 * k>(dr < 2 ? base0 : base1);
-              });
-            };
-            reads(std::integral_constant<int, 0>{}, std::integral_constant<int, 15>{});
-            half4 hv[16];
-            wg_static_for(std::make_integer_sequence<int, 4>{}, [&](auto cc) {
-              constexpr int c = decltype(cc)::value;
-              wg_lds_wait<c < 3 ? 3 : 0>(wv[c]);
-              if constexpr (c < 3)
-                reads(std::integral_constant<int, 15 + 12 * c>{}, std::integral_constant<int, (27 + 12 * c < 48 ? 27 + 12 * c : 48)>{});
-              // m = B^T d, in fp32 from the fp16 inputs: d[dr][cj] is the high half
-              // of dword 0 (cj = 0), the low / high half of dword 1 (cj = 1, 2) or
-              // the low half of dword 2 (cj = 3) of row dr
-              float m[4][4];
-              wg_static_for(std::make_integer_sequence<int, 4>{}, [&](auto jc) {
-                constexpr int cj = decltype(jc)::value, wd = (cj + 1) / 2, hi = (cj + 1) % 2;
-                m[0][cj] = wg_mix<hi, true>(wv[c][0][wd], wv[c][2][wd]);   // d0 - d2
-                m[1][cj] = wg_mix<hi, false>(wv[c][1][wd], wv[c][2][wd]);  // d1 + d2
-                m[2][cj] = wg_mix<hi, true>(wv[c][2][wd], wv[c][1][wd]);   // d2 - d1
-                m[3][cj] = wg_mix<hi, true>(wv[c][1][wd], wv[c][3][wd]);   // d1 - d3
-              });
-#pragma unroll
-              for (int r = 0; r < 4; ++r) {
-                float vv[4];
-                vv[0] = m[r][0] - m[r][2];
-                vv[1] = m[r][1] + m[r][2];
-                vv[2] = m[r][2] - m[r][1];
-                vv[3] = m[r][1] - m[r][3];
-#pragma unroll
-                for (int b = 0; b < 4; ++b) {
-                  float v = vv[b];
-                  asm volatile("" : "+v"(v));  // fp32 result first, then fp16 (no fused fma_mix rounding)
-                  hv[4 * r + b][c] = half_t(v);
-                }
-              }
-            });
+            const uint32_t* rowp = reinterpret_cast<const uint32_t*>(
+                                       smem + (qr < 2 ? sa : sb) * kSlotBytes + (qr & 1) * CH * kRowBytes) +
+                                   n + 3;
             half8* sv = svb + (s & 1) * LD::kSvHalf8;
-            const int ci0 = 4 * qd;
-            const int kc = ci0 / 32, k = ci0 % 32;
-            const int flane = (k / 8) * 16 + n, j0 = k % 8;
+            const f32x4 zero4 = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-            for (int p = 0; p < 16; ++p)
-              *reinterpret_cast<half4*>(reinterpret_cast<half_t*>(&sv[(p * KC + kc) * 64 + flane]) + j0) = hv[p];
+            for (int gi = 0; gi < CH / 32; ++gi) {
+              const int c0 = 8 * (w + 4 * gi);  // the group's first channel
+              f32x4 vacc[8];
+#pragma unroll
+              for (int cc = 0; cc < 8; ++cc) {
+                const uint32_t* rp = rowp + (c0 + cc) * (kRowBytes / 4);
+                const uint32_t d0 = rp[0], d1 = rp[1], d2 = rp[2];
+                const uint32_t lo = __builtin_amdgcn_alignbit(d1, d0, 16);  // columns 0, 1
+                const uint32_t hi = __builtin_amdgcn_alignbit(d2, d1, 16);  // columns 2, 3
+                const half4 bfrag = __builtin_bit_cast(half4, (uint32_t __attribute__((ext_vector_type(2)))){lo, hi});
+                vacc[cc] = __builtin_amdgcn_mfma_f32_16x16x16f16(tfrag, bfrag, zero4, 0, 0, 0);
+              }
+              // lane (qr, n): positions 4 qr + j of tile n for the group's 8 channels,
+              // rounded to fp16: one B fragment (8 consecutive channels) per position
+              const int kc = c0 / 32, flane = ((c0 % 32) / 8) * 16 + n;
+#pragma unroll
+              for (int j = 0; j < 4; ++j) {
+                half8 h;
+#pragma unroll
+                for (int cc = 0; cc < 8; ++cc) h[cc] = half_t(vacc[cc][j]);
+                sv[((4 * qr + j) * KC + kc) * 64 + flane] = h;
+              }
+            }
           }
           // pair s + 3 into the slot pair s - 1 used (read by step s - 1, before its barrier)
           if (s + 3 <= R) dma_pair(img, seg, tr0 + s + 3, (s + 3) % kPipeSlots);
@@ -779,48 +693,74 @@ __global__ __launch_bounds__(512, 1) void winograd3x3_pipe_kernel(WinogradArgs a
   // ================= GEMM role: wave w owns output channels 16 (4 blockIdx.y + w) + 0..15
   const int g = blockIdx.y * 4 + w;
   const bool active = 16 * g < a.cout;
-  // Bias, ReLU and the stores of tile row tr's outputs yv (after wg_gemm_pipe).
-  auto finish_row = [&](f32x4 (&yv)[2][2], const f32x4& bias, int img, int seg, int tr) {
-    const int n = lane & 15;
-    const int tc = seg * kWgTiles + n;
-    const int co0 = 16 * g + 4 * (lane >> 4);
+  // Bias, ReLU and the stores of tile row tr's outputs yv (after wg_gemm_pipe):
+  // lane (q, c) holds channel co = 16 g + c of tiles 4 q + 0..3 of the strip.
+  // W % 8 == 0, so those four tiles are all inside the image or all outside.
+  const int co = 16 * g + (lane & 15);
+  auto finish_row = [&](f32x4 (&yv)[2][2], float bias, int img, int seg, int tr) {
+    const int tq = seg * kWgTiles + 4 * (lane >> 4);  // the lane's first tile
+    if (tq >= a.W / 2) return;
 #pragma unroll
-    for (int jj = 0; jj < 4; ++jj)
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int jx = 0; jx < 2; ++jx) yv[i][jx] += bias;
+    const int hw = a.H * a.W;
+    if (a.out_layout == RDV_LAYOUT_CHW) {
+      const int64_t o = (int64_t(img) * a.cout + co) * hw + int64_t(2 * tr) * a.W + 2 * tq;
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        if (a.out_dtype == RDV_DTYPE_F16) {
+          // ReLU after the fp16 rounding, two values per instruction (max(x, 0)
+          // commutes with a monotonic rounding that maps 0 to 0)
+          uint32_t hv[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) hv[j] = __builtin_bit_cast(uint32_t, half2v{half_t(yv[i][0][j]), half_t(yv[i][1][j])});
+          if (a.relu) {
+            // volatile: a branch on the uniform flag, not a per-lane select of both results
+#pragma unroll
+            for (int j = 0; j < 4; ++j) asm volatile("v_pk_max_f16 %0, %1, 0" : "=v"(hv[j]) : "v"(hv[j]));
+          }
+          wg_st128(static_cast<half_t*>(a.y) + o + int64_t(i) * a.W, __builtin_bit_cast(f32x4, hv));
+        } else {
+          f32x4 v0, v1;
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            v0[2 * j] = yv[i][0][j];
+            v0[2 * j + 1] = yv[i][1][j];
+            v1[2 * j] = yv[i][0][j + 2];
+            v1[2 * j + 1] = yv[i][1][j + 2];
+          }
+          if (a.relu) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              v0[e] = fmaxf(v0[e], 0.0f);
+              v1[e] = fmaxf(v1[e], 0.0f);
+            }
+          }
+          float* dst = static_cast<float*>(a.y) + o + int64_t(i) * a.W;
+          wg_st128(dst, v0);
+          wg_st128(dst + 4, v1);
+        }
+      }
+    } else {
+      // channels-last: one element per (pixel, channel); the 16 lanes of a tile
+      // quad write 16 consecutive channels of each pixel
 #pragma unroll
       for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int jx = 0; jx < 2; ++jx) {
-          float val = yv[i][jx][jj] + bias[jj];
-          if (a.relu) val = fmaxf(val, 0.0f);
-          yv[i][jx][jj] = val;
-        }
-    if (a.out_layout == RDV_LAYOUT_CHW && a.out_dtype == RDV_DTYPE_F16) {
-      // lane 4q + k of the 16 tile lanes takes channel co0 + k of tiles 4q .. 4q+3
-      // (8 consecutive fp16 columns of each output row): two 16-byte stores
-      // instead of eight 4-byte ones.  W % 8 == 0, so a quad's tiles are all
-      // inside the image or all outside.
-      uint32_t r0[4], r1[4];
+        for (int j = 0; j < 4; ++j)
 #pragma unroll
-      for (int jj = 0; jj < 4; ++jj) {
-        r0[jj] = __builtin_bit_cast(uint32_t, half2v{half_t(yv[0][0][jj]), half_t(yv[0][1][jj])});
-        r1[jj] = __builtin_bit_cast(uint32_t, half2v{half_t(yv[1][0][jj]), half_t(yv[1][1][jj])});
-      }
-      const int k = lane & 3;
-      wg_quad_transpose(r0, k);
-      wg_quad_transpose(r1, k);
-      const int tq = tc - k;  // the quad's first tile
-      if (tq < a.W / 2) {
-        half_t* dst = static_cast<half_t*>(a.y) + (int64_t(img) * a.cout + co0 + k) * (int64_t(a.H) * a.W) +
-                      int64_t(2 * tr) * a.W + 2 * tq;
-        wg_st128(dst, __builtin_bit_cast(f32x4, r0));
-        wg_st128(dst + a.W, __builtin_bit_cast(f32x4, r1));
-      }
-    } else if (tc < a.W / 2) {
-      wg_store_asm(yv, a, img, co0, 2 * tr, 2 * tc);
+          for (int jx = 0; jx < 2; ++jx) {
+            float v = yv[i][jx][j];
+            if (a.relu) v = fmaxf(v, 0.0f);
+            const int64_t o = (int64_t(img) * hw + int64_t(2 * tr + i) * a.W + 2 * (tq + j) + jx) * a.cout + co;
+            if (a.out_dtype == RDV_DTYPE_F16) wg_st16(static_cast<half_t*>(a.y) + o, half_t(v));
+            else wg_st32(static_cast<float*>(a.y) + o, __builtin_bit_cast(uint32_t, v));
+          }
     }
   };
   // The GEMMs, inverse transform, bias, ReLU and stores of tile row tr from sv buffer `buf`.
-  auto gemm_row = [&](const half8 (&uu)[16][KC], const f32x4& bias, int img, int seg, int tr, int buf) {
+  auto gemm_row = [&](const half8 (&uu)[16][KC], float bias, int img, int seg, int tr, int buf) {
     f32x4 yv[2][2];
     wg_gemm_pipe(uu, svb + buf * LD::kSvHalf8, lane, yv);
     finish_row(yv, bias, img, seg, tr);
@@ -839,7 +779,9 @@ __global__ __launch_bounds__(512, 1) void winograd3x3_pipe_kernel(WinogradArgs a
   if (any) __syncthreads();
   const int g_n = (a.cout + 15) / 16;
   const int gu = active ? g : 0;
-  const f32x4 bias = wg_lane_bias(a, gu, lane);
+  // this lane's channel bias (unconditional load: a zero block for a null bias, or a clamped index)
+  const float* bsrc = a.bias ? a.bias : reinterpret_cast<const float*>(g_wg_zero16);
+  const float bias = bsrc[a.bias && co < a.cout ? co : 0];
   half8 u[16][KC];
   wg_static_for(std::make_integer_sequence<int, 8>{}, [&](auto gc) {
     constexpr int G = decltype(gc)::value, b = G / 2, ra0 = 2 * (G % 2);
