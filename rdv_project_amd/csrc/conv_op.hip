@@ -81,6 +81,14 @@ __device__ __forceinline__ float w_at(const ConvArgs& a, int o, int k) {
   return a.w[(int64_t(o) * a.cin + ci) * (a.kh * a.kw) + tap];
 }
 
+// Physical position of slot ln (0..63) of output tile t's filter fragment in
+// LDS: the two low bits XOR (ln / 16 + t) % 4.  The staging writes of a wave
+// (slots 16 kq + 4 j + e of every t and kq for one e) then spread over every
+// bank instead of four (a 16-way conflict), and a fragment's 64 slots stay a
+// permutation of themselves, so its reads (lane l reads slot l) remain
+// conflict-free.
+__device__ __forceinline__ int cv_swz(int t, int ln) { return ln ^ (((ln >> 4) + t) & 3); }
+
 // w block [o0, o0 + ob) x K [k0, k0 + kp) into LDS, fragment order: slot
 // ((t * nkc + c) * 64 + lane) = 16 bytes, out o0 + 16 t + lane % 16, K
 // k0 + c kK + (lane / 16) kLane + 0 .. kLane-1 (fp16 halves or fp32 floats);
@@ -111,7 +119,7 @@ __device__ void cv_stage(const ConvArgs& a, int o0, int k0, int nkc, f32x4* sw, 
         for (int i = 0; i < 4; ++i) v[i] = k + i < a.K ? w_at(a, o, k + i) : 0.0f;
       }
     }
-    sw[s] = v;
+    sw[(t * nkc + c) * 64 + cv_swz(t, ln)] = v;
   }
   for (int i = tid; i < a.ob; i += nthr) sb[i] = (a.bias != nullptr && o0 + i < a.cout) ? a.bias[o0 + i] : 0.0f;
 }
@@ -150,7 +158,7 @@ __device__ void cv_stage_rows(const ConvArgs& a, int o0, int k0, int nkc, f32x4*
 #pragma unroll
         for (int i = 0; i < 4; ++i) v[i] = r[i][e];
       }
-      sw[(t * nkc + c) * 64 + kq * 16 + 4 * j + e] = v;
+      sw[(t * nkc + c) * 64 + cv_swz(t, kq * 16 + 4 * j + e)] = v;
     }
   }
   for (int i = threadIdx.x; i < a.ob; i += kCvThreads)
@@ -234,7 +242,7 @@ __device__ __forceinline__ void cv_mma(const f32x4* sw, int nt, int nkc, int c, 
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
       if (t < nt) {
-        const half8 wh = __builtin_bit_cast(half8, sw[(t * nkc + c) * 64 + lane]);
+        const half8 wh = __builtin_bit_cast(half8, sw[(t * nkc + c) * 64 + cv_swz(t, lane)]);
 #pragma unroll
         for (int rr = 0; rr < kCvRT; ++rr)
           acc[rr][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wh, xb[rr], acc[rr][t], 0, 0, 0);
@@ -247,7 +255,7 @@ __device__ __forceinline__ void cv_mma(const f32x4* sw, int nt, int nkc, int c, 
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
       if (t < nt) {
-        const f32x4 wv = sw[(t * nkc + c) * 64 + lane];
+        const f32x4 wv = sw[(t * nkc + c) * 64 + cv_swz(t, lane)];
 #pragma unroll
         for (int s = 0; s < 4; ++s)
 #pragma unroll
@@ -382,23 +390,33 @@ struct TileArgs {
 // do not delay this batch's waits.
 template <int NT, class Mid>
 __device__ void cv_stage_filter(const ConvArgs& a, int o0, int nkc, f32x4* sw, float* sb, Mid&& mid) {
+  // the bias first: the oldest load, so that waiting for it waits for nothing else
+  static_assert(16 * NT <= kCvThreads, "one bias per thread");
+  const int bi = int(threadIdx.x);
+  const float bv = (bi < 16 * NT && a.bias != nullptr && o0 + bi < a.cout) ? a.bias[o0 + bi] : 0.0f;
   // group gi: four outputs 4 cg .. (cg = gi % 4 NT: output tile t = cg / 4, j = cg % 4) of rows
   // k .. k + 7 (k = 32 c + 8 kq, kq = (gi / 4 NT) % 4, c = gi / 16 NT).  Consecutive lanes take
   // consecutive 16-byte pieces of a row, so a wave's load covers whole rows of the filter block.
+  // Every block reads the same filter at the same time: each starts at its own
+  // K row (a rotation of the group index by whole rows), so that the blocks of
+  // an XCD spread their requests over the L2 channels instead of queueing on
+  // the same lines.
   const int groups = NT * nkc * 16;
+  const int rot = int(blockIdx.x * 7u % unsigned(4 * nkc)) * (4 * NT);
+  auto rotated = [&](int gi) { return gi + rot < groups ? gi + rot : gi + rot - groups; };
   bool ran = false;
   for (int g0 = int(threadIdx.x); g0 < groups || !ran; g0 += kFiltBatch * kCvThreads) {
     f32x4 r[kFiltBatch][8];
 #pragma unroll
     for (int u = 0; u < kFiltBatch; ++u) {
-      const int gi = g0 + u * kCvThreads;
+      const int g = g0 + u * kCvThreads, gi = rotated(g);
       const int cg = gi % (4 * NT), rest = gi / (4 * NT);
       const int t = cg >> 2, j = cg & 3, kq = rest & 3, c = rest >> 2;
       const int o = o0 + 16 * t + 4 * j;
       const int k = c * 32 + kq * 8;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        const bool ok = gi < groups && o < a.cout && k + i < a.K;
+        const bool ok = g < groups && o < a.cout && k + i < a.K;
         const int64_t off = ok ? int64_t(k + i) * a.cout + o : 0;
         r[u][i] = *reinterpret_cast<const f32x4*>(a.w + off);
         if (!ok) r[u][i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -410,8 +428,8 @@ __device__ void cv_stage_filter(const ConvArgs& a, int o0, int nkc, f32x4* sw, f
     }
 #pragma unroll
     for (int u = 0; u < kFiltBatch; ++u) {
-      const int gi = g0 + u * kCvThreads;
-      if (gi < groups) {
+      const int gi = rotated(g0 + u * kCvThreads);
+      if (g0 + u * kCvThreads < groups) {
         const int cg = gi % (4 * NT), rest = gi / (4 * NT);
         const int t = cg >> 2, j = cg & 3, kq = rest & 3, c = rest >> 2;
 #pragma unroll
@@ -419,13 +437,12 @@ __device__ void cv_stage_filter(const ConvArgs& a, int o0, int nkc, f32x4* sw, f
           half8 h;
 #pragma unroll
           for (int i = 0; i < 8; ++i) h[i] = half_t(r[u][i][e]);
-          sw[(t * nkc + c) * 64 + kq * 16 + 4 * j + e] = __builtin_bit_cast(f32x4, h);
+          sw[(t * nkc + c) * 64 + cv_swz(t, kq * 16 + 4 * j + e)] = __builtin_bit_cast(f32x4, h);
         }
       }
     }
   }
-  for (int i = threadIdx.x; i < 16 * NT; i += kCvThreads)
-    sb[i] = (a.bias != nullptr && o0 + i < a.cout) ? a.bias[o0 + i] : 0.0f;
+  if (bi < 16 * NT) sb[bi] = bv;
 }
 
 template <int NT>
@@ -532,7 +549,7 @@ __global__ __launch_bounds__(kCvThreads, 1) void conv_tile_kernel(TileArgs ta) {
       for (int j = 0; j < kTileNB; ++j)
         xb[j] = *reinterpret_cast<const half8*>(wrow + o + (j >> 1) * jstride + (j & 1) * 16 * ta.ps);
 #pragma unroll
-      for (int t = 0; t < NT; ++t) wb[t] = __builtin_bit_cast(half8, sw[(t * nkc + cc) * 64 + lane]);
+      for (int t = 0; t < NT; ++t) wb[t] = __builtin_bit_cast(half8, sw[(t * nkc + cc) * 64 + cv_swz(t, lane)]);
       advance();
     };
     auto mma = [&](const half8 (&xb)[kTileNB], const half8 (&wb)[NT]) {
@@ -651,6 +668,11 @@ int launch_conv2d(const rdv_conv2d_desc& d, const float* x, const float* w, cons
   // spatial tiles: fp16, whole 32-channel chunks per tap, an RSCK filter of
   // 16-byte rows, one output block, and the haloed window plus the filter block in LDS
   if (f16 && vec && a.w_rows && d.cin % 32 == 0 && d.cout % 16 == 0 && passes == 1 && a.n_ob == 1) {
+    const int64_t tiles = int64_t((d.H + kTileH - 1) / kTileH) * ((d.W + kTileW - 1) / kTileW);
+    if (tiles > 0x7fffffff) return fail(RDV_ERR_UNSUPPORTED, "grid too large");
+    const size_t filt = size_t(ob / 16) * (K / 32) * 64 * sizeof(f32x4) + size_t(ob) * sizeof(float);
+    const int ti = ob / 16 - 1;  // the kernels' NT is the exact tile count
+    const int64_t grid = std::min<int64_t>(tiles, dev.cu_count);
     TileArgs ta;
     ta.c = a;
     ta.c.kp = K;
@@ -658,13 +680,10 @@ int launch_conv2d(const rdv_conv2d_desc& d, const float* x, const float* w, cons
     ta.win_h = kTileH + d.kh - 1;
     ta.ps = 2 * d.cin + 16;
     ta.win_bytes = (ta.win_w * ta.win_h * ta.ps + 15) / 16 * 16;
-    const size_t tlds = size_t(ta.win_bytes) + size_t(ob / 16) * (K / 32) * 64 * sizeof(f32x4) + size_t(ob) * sizeof(float);
+    const size_t tlds = size_t(ta.win_bytes) + filt;
     if (tlds <= size_t(156) * 1024) {
       ta.tiles_w = (d.W + kTileW - 1) / kTileW;
-      const int64_t tiles = int64_t((d.H + kTileH - 1) / kTileH) * ta.tiles_w;
-      if (tiles > 0x7fffffff) return fail(RDV_ERR_UNSUPPORTED, "grid too large");
       ta.tiles = int(tiles);
-      const int ti = ob / 16 - 1;  // the kernel's NT is the exact tile count
       static const void* const tfns[8] = {
           reinterpret_cast<const void*>(&conv_tile_kernel<1>), reinterpret_cast<const void*>(&conv_tile_kernel<2>),
           reinterpret_cast<const void*>(&conv_tile_kernel<3>), reinterpret_cast<const void*>(&conv_tile_kernel<4>),
@@ -675,7 +694,6 @@ int launch_conv2d(const rdv_conv2d_desc& d, const float* x, const float* w, cons
         RDV_HIP_TRY(hipFuncSetAttribute(tfns[ti], hipFuncAttributeMaxDynamicSharedMemorySize, 156 * 1024));
         tattr[ti] = true;
       }
-      const int64_t grid = std::min<int64_t>(tiles, dev.cu_count);
       void* tparams[] = {&ta};
       RDV_HIP_TRY(hipLaunchKernel(tfns[ti], dim3(static_cast<unsigned>(grid)), dim3(kCvThreads), tparams, tlds, stream));
       return RDV_OK;
