@@ -58,11 +58,20 @@ __global__ __launch_bounds__(kThreads2, 1) void mlp_fused_f16_kernel(FusedArgs a
   constexpr int D = N::kIn;
   constexpr int LL = N::kL - 1;
   constexpr int MTO = N::mt(LL);
-  __shared__ float sb[N::kBias];
-  __shared__ half8 sw[N::kFrags * 64];
-  __shared__ float sx[kWaves2][2][D * 64];  // each wave's input pair tiles (double buffer), [d][row]
-  __shared__ int s_next;
-  __shared__ float sst[DIRECT ? DirectStage<N, kThreads2>::kFloats : 1];  // DIRECT: fp32 weight staging
+  // One LDS block carved by hand, the input tiles first: their LDS-DMA target
+  // (M0) must stay below 64 KiB, and the DIRECT staging area makes the block
+  // larger than that (separate __shared__ arrays are placed by the compiler).
+  constexpr int kSxBytes = kWaves2 * 2 * D * 64 * 4;
+  constexpr int kSwBytes = N::kFrags * 64 * 16;
+  constexpr int kSbBytes = (N::kBias * 4 + 15) / 16 * 16;
+  constexpr int kSstBytes = DIRECT ? DirectStage<N, kThreads2>::kFloats * 4 : 0;
+  static_assert(kSxBytes <= 65536, "the input tiles' DMA addresses must be below 64 KiB");
+  __shared__ __attribute__((aligned(16))) uint8_t lds[kSxBytes + kSwBytes + kSbBytes + kSstBytes + 16];
+  auto& sx = *reinterpret_cast<float (*)[kWaves2][2][D * 64]>(lds);  // each wave's input pair tiles, [d][row]
+  half8* const sw = reinterpret_cast<half8*>(lds + kSxBytes);
+  float* const sb = reinterpret_cast<float*>(lds + kSxBytes + kSwBytes);
+  float* const sst = reinterpret_cast<float*>(lds + kSxBytes + kSwBytes + kSbBytes);  // DIRECT: fp32 weight staging
+  int& s_next = *reinterpret_cast<int*>(lds + kSxBytes + kSwBytes + kSbBytes + kSstBytes);
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int h = lane >> 5, col = lane & 31;

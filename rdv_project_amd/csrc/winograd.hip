@@ -564,6 +564,8 @@ struct WgPipeLds {
   static constexpr int kSlotBytes = 2 * 32 * KC * kRowBytes;
   static constexpr int kSvHalf8 = 16 * KC * 64;
   static constexpr int kBytes = kPipeSlots * kSlotBytes + 2 * kSvHalf8 * 16;
+  // the ring is the DMA target (M0 addresses): it starts the block and must end below 64 KiB
+  static_assert(kPipeSlots * kSlotBytes <= 65536, "DMA ring past 64 KiB");
 };
 
 template <int KC>
