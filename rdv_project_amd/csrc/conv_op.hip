@@ -358,23 +358,30 @@ __global__ __launch_bounds__(kCvThreads) void conv_op_kernel(ConvArgs a) {
 
 // ------------------------------------------------------------ spatial tiles
 // The fp16 path for a filter block that fits LDS next to a haloed input tile
-// (cin % 32 == 0, cout <= 128): a block owns TH x TW tiles of output pixels in
-// turn.  Each tile's (TH + KH - 1) x (TW + KW - 1) x cin input window is
-// converted to fp16 into LDS once (zero outside the image) and every tap reads
-// its B fragments from there, so x crosses the load path about
+// (cin % 32 == 0, cout = 16 NT <= 128): a block owns TH x TW tiles of output
+// pixels in turn.  Each tile's (TH + KH - 1) x (TW + KW - 1) x cin input window
+// is converted to fp16 into LDS once (zero outside the image) and every tap
+// reads its B fragments from there, so x crosses the load path about
 // (TH + KH - 1)(TW + KW - 1) / (TH TW) times instead of KH KW times.  The
-// filter block is staged once per launch, its loads issued in one round next
-// to the first window's, and the next tile's window loads are in flight (in
+// filter is staged once per launch, its loads issued in one round next to the
+// first window's, and the next tile's window loads are in flight (in
 // registers) while the current tile's MFMAs run.  Wave w computes output rows
 // 2w and 2w + 1 of the tile, 32 columns each (N blocks j = 0..3: row 2w + j / 2,
 // columns 16 (j % 2) ..: four blocks share every filter fragment read) against
 // every 16-channel output tile.  K runs over taps in (kh, kw) order and 32-channel
 // chunks within a tap: the filter staging's K order.
-constexpr int kTileH = 8;     // output rows per tile (two per wave)
-constexpr int kTileW = 32;    // output columns per tile
-constexpr int kTileNB = 4;    // N blocks per wave
-constexpr int kWinBatch = 22; // window loads per thread held across a tile (a 3x3, 64-channel window: 21.25)
-constexpr int kFiltBatch = 5; // filter groups per thread and round (64 -> 64 3x3: 4.5)
+//
+// Both stagings are written for few instructions per load, because at one wave
+// per SIMD their instruction count, not the memory system, sets the prologue's
+// length: filter loads take immediate offsets from one address per 8-row group,
+// and window loads are buffer loads whose descriptor covers one image row, so a
+// column or row outside the image reads zero with no per-lane test.
+constexpr int kTileH = 8;      // output rows per tile (two per wave)
+constexpr int kTileW = 32;     // output columns per tile
+constexpr int kTileNB = 4;     // N blocks per wave
+constexpr int kWinSlots = 23;  // window units per wave held across a tile (a 3x3, 64-channel window: 90 / 4)
+constexpr int kFiltA = 3;      // filter groups per thread in the first round (64 -> 64 3x3: 4.5 in all)
+constexpr int kFiltB = 2;      // filter groups per thread in each later round
 
 struct TileArgs {
   ConvArgs c;
@@ -382,67 +389,97 @@ struct TileArgs {
   int win_w, win_h;    // input window: kTileW + kw - 1, kTileH + kh - 1
   int ps;              // LDS bytes per window pixel: 2 cin + 16 (spreads a wave's reads over every bank)
   int win_bytes;       // window bytes, rounded up to 16
+  int rp;              // 16-byte fp32 pieces per window row: win_w cin / 4
+  int upr;             // 64-piece units per window row: ceil(rp / 64), >= 4
+  int units;           // units per window: win_h upr
+  int row_bytes;       // bytes per image row: W cin 4 (< 2^31)
+  unsigned cq_magic;   // ceil(2^32 / (cin / 4)): p / (cin / 4) == umulhi(p, cq_magic) for every p < rp
+  int stage_out;       // output rows staged through the window's LDS (2 NT KiB per wave fit in it)
 };
 
-// The RSCK filter block [o0, o0 + 16 NT) x every K into LDS in fragment order
-// (as cv_stage_rows), each thread's groups kFiltBatch at a time; between the
-// loads and their conversion, `mid` runs (the first window's loads), so those
-// do not delay this batch's waits.
-template <int NT, class Mid>
-__device__ void cv_stage_filter(const ConvArgs& a, int o0, int nkc, f32x4* sw, float* sb, Mid&& mid) {
-  // the bias first: the oldest load, so that waiting for it waits for nothing else
-  static_assert(16 * NT <= kCvThreads, "one bias per thread");
-  const int bi = int(threadIdx.x);
-  const float bv = (bi < 16 * NT && a.bias != nullptr && o0 + bi < a.cout) ? a.bias[o0 + bi] : 0.0f;
-  // group gi: four outputs 4 cg .. (cg = gi % 4 NT: output tile t = cg / 4, j = cg % 4) of rows
-  // k .. k + 7 (k = 32 c + 8 kq, kq = (gi / 4 NT) % 4, c = gi / 16 NT).  Consecutive lanes take
-  // consecutive 16-byte pieces of a row, so a wave's load covers whole rows of the filter block.
-  // Every block reads the same filter at the same time: each starts at its own
-  // K row (a rotation of the group index by whole rows), so that the blocks of
-  // an XCD spread their requests over the L2 channels instead of queueing on
-  // the same lines.
-  const int groups = NT * nkc * 16;
-  const int rot = int(blockIdx.x * 7u % unsigned(4 * nkc)) * (4 * NT);
-  auto rotated = [&](int gi) { return gi + rot < groups ? gi + rot : gi + rot - groups; };
-  bool ran = false;
-  for (int g0 = int(threadIdx.x); g0 < groups || !ran; g0 += kFiltBatch * kCvThreads) {
-    f32x4 r[kFiltBatch][8];
+// The RSCK filter (16 NT outputs, every K row) into LDS in fragment order
+// (slot (t nkc + c) 64 + lane as cv_stage_rows writes it) plus the bias.
+// Group gi: outputs 4 cg .. 4 cg + 3 (cg = gi % 4 NT: tile t = cg / 4, j = cg % 4)
+// of K rows 8 rb .. 8 rb + 7 (rb = gi / 4 NT: chunk c = rb / 4, kq = rb % 4) --
+// eight 16-byte loads at a fixed stride from one address, transposed in
+// registers into four lanes' 8-row fragments.  A round gives each thread NB
+// groups: group g0 + u kCvThreads + tid of round g0.  Every block reads the same
+// filter at the same time: each starts at its own row block (a rotation `rot`
+// of the group index), so that the blocks of an XCD spread their requests over
+// the L2 channels instead of queueing on the same lines.  Past the last group a
+// thread takes the last one again: it loads and writes the same bytes as that
+// group's owner, so no test guards the conversion (one that the compiler sinks
+// the loads below, behind a full wait).
+struct CtFilter {
+  int groups, rot, nkc;
+  __device__ int group(int g0, int u) const {
+    const int gi = min(g0 + u * kCvThreads + int(threadIdx.x), groups - 1) + rot;
+    return gi < groups ? gi : gi - groups;
+  }
+};
+
+template <int NT, int NB>
+__device__ __forceinline__ void ct_filter_issue(const CtFilter& f, const float* __restrict__ w, int g0,
+                                                f32x4 (&r)[NB][8]) {
+  constexpr int kG = 4 * NT, kRow = 16 * NT;
 #pragma unroll
-    for (int u = 0; u < kFiltBatch; ++u) {
-      const int g = g0 + u * kCvThreads, gi = rotated(g);
-      const int cg = gi % (4 * NT), rest = gi / (4 * NT);
-      const int t = cg >> 2, j = cg & 3, kq = rest & 3, c = rest >> 2;
-      const int o = o0 + 16 * t + 4 * j;
-      const int k = c * 32 + kq * 8;
+  for (int u = 0; u < NB; ++u) {
+    const int gi = f.group(g0, u);
+    const float* src = w + ((gi / kG) * 8 * kRow + 4 * (gi % kG));
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const bool ok = g < groups && o < a.cout && k + i < a.K;
-        const int64_t off = ok ? int64_t(k + i) * a.cout + o : 0;
-        r[u][i] = *reinterpret_cast<const f32x4*>(a.w + off);
-        if (!ok) r[u][i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-      }
-    }
-    if (!ran) {
-      mid();
-      ran = true;
-    }
+    for (int i = 0; i < 8; ++i) r[u][i] = *reinterpret_cast<const f32x4*>(src + i * kRow);
+  }
+}
+
+template <int NT, int NB>
+__device__ __forceinline__ void ct_filter_convert(const CtFilter& f, int g0, const f32x4 (&r)[NB][8], f32x4* sw) {
+  constexpr int kG = 4 * NT;
 #pragma unroll
-    for (int u = 0; u < kFiltBatch; ++u) {
-      const int gi = rotated(g0 + u * kCvThreads);
-      if (g0 + u * kCvThreads < groups) {
-        const int cg = gi % (4 * NT), rest = gi / (4 * NT);
-        const int t = cg >> 2, j = cg & 3, kq = rest & 3, c = rest >> 2;
+  for (int u = 0; u < NB; ++u) {
+    const int gi = f.group(g0, u);
+    const int cg = gi % kG, rb = gi / kG;
+    const int t = cg >> 2, j = cg & 3, kq = rb & 3, c = rb >> 2;
+    const int s = (kq + t) & 3;  // cv_swz's XOR of the slot's two low bits
+    f32x4* dst = sw + (t * f.nkc + c) * 64 + kq * 16 + 4 * j;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          half8 h;
+    for (int e = 0; e < 4; ++e) {
+      half8 h;
 #pragma unroll
-          for (int i = 0; i < 8; ++i) h[i] = half_t(r[u][i][e]);
-          sw[(t * nkc + c) * 64 + cv_swz(t, kq * 16 + 4 * j + e)] = __builtin_bit_cast(f32x4, h);
-        }
-      }
+      for (int i = 0; i < 8; ++i) h[i] = half_t(r[u][i][e]);
+      dst[e ^ s] = __builtin_bit_cast(f32x4, h);
     }
   }
-  if (bi < 16 * NT) sb[bi] = bv;
+}
+
+// The filter's first round (kFiltA groups per thread), then `mid` (the first
+// window's loads), then that round's conversion, then rounds of kFiltB groups:
+// the first round and the window together fill the registers, and the later
+// rounds' loads run while the window's are still in flight.
+template <int NT, class Mid>
+__device__ void ct_stage_filter(const float* __restrict__ w, const float* __restrict__ bias, int nkc, f32x4* sw,
+                                float* sb, Mid&& mid) {
+  constexpr int kRow = 16 * NT;  // floats per K row
+  static_assert(kRow <= kCvThreads, "one bias per thread");
+  const int tid = int(threadIdx.x);
+  // the bias first: the oldest load, so that waiting for it waits for nothing else
+  const float bv = (tid < kRow && bias != nullptr) ? bias[tid] : 0.0f;
+  CtFilter f;
+  f.groups = nkc * 16 * NT;
+  f.rot = int(blockIdx.x * 7u % unsigned(4 * nkc)) * (4 * NT);
+  f.nkc = nkc;
+  {
+    f32x4 r[kFiltA][8];
+    ct_filter_issue<NT>(f, w, 0, r);
+    __builtin_amdgcn_sched_barrier(0);
+    mid();
+    ct_filter_convert<NT>(f, 0, r, sw);
+  }
+  for (int g0 = kFiltA * kCvThreads; g0 < f.groups; g0 += kFiltB * kCvThreads) {
+    f32x4 r[kFiltB][8];
+    ct_filter_issue<NT>(f, w, g0, r);
+    ct_filter_convert<NT>(f, g0, r, sw);
+  }
+  if (tid < kRow) sb[tid] = bv;
 }
 
 template <int NT>
@@ -456,60 +493,93 @@ __global__ __launch_bounds__(kCvThreads, 1) void conv_tile_kernel(TileArgs ta) {
   const int lane = threadIdx.x & 63;
   const int q = lane >> 4, n = lane & 15;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int o0 = (blockIdx.x % a.n_ob) * a.ob;
-  const int64_t tstride = gridDim.x / a.n_ob;
-  const int cq = a.cin / 4;  // 16-byte groups of 4 channels per pixel
-  const int groups = ta.win_h * ta.win_w * cq;
+  const int tstride = int(gridDim.x);  // one output block (n_ob == 1) on this path
+  const int wrow_bytes = ta.win_w * ta.ps;  // LDS bytes per window row
 
-  // one window batch: groups [base, base + kWinBatch kCvThreads) of `tile`, fp32 in registers
-  f32x4 raw[kWinBatch];
-  int dst[kWinBatch];
-  auto load_batch = [&](int64_t tile, int base) {
-    const int th = int(tile / ta.tiles_w), tw = int(tile % ta.tiles_w);
-    const int h0 = th * kTileH, w0 = tw * kTileW;
+  // Window unit u (< ta.units) is 64 consecutive 16-byte pieces of window row
+  // u / upr: pieces 64 (u % upr) .. + 63, piece p holding channels 4 (p % cq) ..
+  // + 3 of window column p / cq (cq = cin / 4).  Wave w loads units w, w + 4, ..:
+  // slot s of a batch starting at slot s0 is unit w + 4 (s0 + s).  A unit is one
+  // buffer load per lane from a descriptor over its image row alone (no records
+  // for a row outside the image), so pieces left or right of the image read
+  // zero; lanes past the row's last piece load and are not committed.
+  f32x4 raw[kWinSlots];
+  auto unit_rc = [&](int s0, int& r, int& c) {
+    // (an opaque zero: the slots' row and column walk is not hoisted out of the
+    // tile loop, where its 23 steps would be kept in spilled scalar registers)
+    int z;
+    asm volatile("s_mov_b32 %0, 0" : "=s"(z));
+    const int u = wave + 4 * (s0 + z);
+    r = u / ta.upr;
+    c = u - r * ta.upr;
+  };
+  auto win_issue = [&](int tile, int s0) {
+    const int th = tile / ta.tiles_w, tw = tile - th * ta.tiles_w;
+    const int cshift = (tw * kTileW - a.pw) * a.cin * 4;  // bytes; negative at the left edge
+    const int64_t rstep = int64_t(a.W) * a.cin * 4;      // bytes per image row
+    int r, c;
+    unit_rc(s0, r, c);
+    int ih = th * kTileH - a.ph + r;
+    uint64_t row = uint64_t(a.x) + uint64_t(int64_t(ih) * rstep);  // image row ih (any ih: no records outside)
+    int u = wave + 4 * s0;
+    // every slot loads (a unit past the window, or a row outside the image, has no records and reads
+    // zero), so the counts of loads in flight are exact and the waits for older loads stay narrow
 #pragma unroll
-    for (int i = 0; i < kWinBatch; ++i) {
-      const int gi = base + i * kCvThreads + int(threadIdx.x);
-      const int pix = gi / cq, g4 = gi - pix * cq;
-      const int r = pix / ta.win_w, cc = pix - r * ta.win_w;
-      const int ih = h0 + r - a.ph, iw = w0 + cc - a.pw;
-      const bool in = gi < groups && ih >= 0 && ih < a.H && iw >= 0 && iw < a.W;
-      const int64_t off = in ? (int64_t(ih) * a.W + iw) * a.cin + 4 * g4 : 0;
-      raw[i] = *reinterpret_cast<const f32x4*>(a.x + off);
-      if (!in) raw[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-      dst[i] = gi < groups ? pix * ta.ps + 8 * g4 : -1;
+    for (int s = 0; s < kWinSlots; ++s) {
+      const int nrec = (u < ta.units && unsigned(ih) < unsigned(a.H)) ? ta.row_bytes : 0;
+      const auto rs = __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(row), 0, nrec, 0x00020000);
+      raw[s] = __builtin_bit_cast(
+          f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, unsigned(16 * lane + (c * 1024 + cshift)), 0, 0));
+      u += 4;
+      c += 4;
+      if (c >= ta.upr) {
+        c -= ta.upr;
+        ++ih;
+        row += uint64_t(rstep);
+      }
     }
   };
-  auto commit_batch = [&]() {
+  auto win_commit = [&](int s0) {
+    int r, c;
+    unit_rc(s0, r, c);
 #pragma unroll
-    for (int i = 0; i < kWinBatch; ++i) {
-      if (dst[i] >= 0) {
-        half4 hv;
+    for (int s = 0; s < kWinSlots; ++s) {
+      if (wave + 4 * (s0 + s) < ta.units) {
+        const int p = 64 * c + lane;
+        if (p < ta.rp) {
+          // window pixel p / cq at (p / cq) ps, its 4-channel group p % cq at 8 (p % cq): 8 p + 16 (p / cq)
+          const int col = int(__umulhi(unsigned(p), ta.cq_magic));
+          half4 hv;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) hv[j] = half_t(raw[i][j]);
-        *reinterpret_cast<half4*>(win + dst[i]) = hv;
+          for (int j = 0; j < 4; ++j) hv[j] = half_t(raw[s][j]);
+          *reinterpret_cast<half4*>(win + r * wrow_bytes + 8 * p + 16 * col) = hv;
+        }
+      }
+      c += 4;
+      if (c >= ta.upr) {
+        c -= ta.upr;
+        ++r;
       }
     }
   };
 
-  int64_t tile = blockIdx.x / a.n_ob;
+  int tile = int(blockIdx.x);  // tiles < 2^31 (checked on the host)
   // the filter's first round of loads, then the first window's (or its first batch), then the conversions
-  cv_stage_filter<NT>(a, o0, nkc, sw, sb, [&]() {
-    if (tile < ta.tiles) load_batch(tile, 0);
-  });
+  // (the grid has at most one block per tile, so every block has a first tile)
+  ct_stage_filter<NT>(a.w, a.bias, nkc, sw, sb, [&]() { win_issue(tile, 0); });
   for (; tile < ta.tiles; tile += tstride) {
-    const int th = int(tile / ta.tiles_w), tw = int(tile % ta.tiles_w);
+    const int th = tile / ta.tiles_w, tw = tile - th * ta.tiles_w;
     const int h0 = th * kTileH, w0 = tw * kTileW;
     // this tile's window into LDS: the batch in flight, and any further batches now
-    commit_batch();
-    for (int base = kWinBatch * kCvThreads; base < groups; base += kWinBatch * kCvThreads) {
-      load_batch(tile, base);
-      commit_batch();
+    win_commit(0);
+    for (int s0 = kWinSlots; 4 * s0 < ta.units; s0 += kWinSlots) {
+      win_issue(tile, s0);
+      win_commit(s0);
     }
     __syncthreads();
     // the next tile's window loads run under this tile's MFMAs
-    const int64_t next = tile + tstride;
-    if (next < ta.tiles) load_batch(next, 0);  // (its first batch, when the window needs more than one)
+    const int next = tile + tstride;  // (tiles <= 2^30 and the grid is at most one block per CU)
+    if (next < ta.tiles) win_issue(next, 0);  // (its first batch, when the window needs more than one)
     f32x4 acc[kTileNB][NT];
     {
       const f32x4* sb4 = reinterpret_cast<const f32x4*>(sb);
@@ -521,36 +591,45 @@ __global__ __launch_bounds__(kCvThreads, 1) void conv_tile_kernel(TileArgs ta) {
       }
     }
     // lane (q, n) of N block j reads window pixel (2 wave + j / 2 + kh, 16 (j % 2) + n + kw),
-    // channels 32 kc + 8 q .. + 7.  Two register sets alternate: chunk c + 1's
-    // fragments are read into one while chunk c's MFMAs run on the other; a
-    // scheduling barrier keeps the reads ahead of those MFMAs.
-    const uint8_t* wrow = win + (2 * wave * ta.win_w + n) * ta.ps + 16 * q;
-    const int jstride = ta.win_w * ta.ps;
+    // channels 32 kc + 8 q .. + 7, and of output tile t filter slot (t nkc + chunk) 64 +
+    // cv_swz(t, lane).  Each fragment's LDS address lives in a register of its own and
+    // moves by a uniform step per chunk (channels first, then taps along the row, then
+    // rows), so a chunk's reads need no address arithmetic.  Two register sets
+    // alternate: chunk c + 1's fragments are read into one while chunk c's MFMAs run on
+    // the other, and a scheduling barrier keeps the reads ahead of those MFMAs.  Every
+    // read is unconditional: past the last chunk the addresses stay on it (a re-read,
+    // unused), so the waits before each MFMA group count exactly the reads in flight.
     const int kcs = a.cin / 32;
-    int kc = 0, kw = 0;
-    int off = 0;  // window byte offset of the chunk read next: (kh win_w + kw) ps + 64 kc
-    auto advance = [&]() {  // channels first, then taps along the row, then rows
-      if (++kc == kcs) {
-        kc = 0;
-        if (++kw == a.kw) {
-          kw = 0;
-          off += (ta.win_w - a.kw + 1) * ta.ps - 64 * (kcs - 1);
-        } else {
-          off += ta.ps - 64 * (kcs - 1);
+    unsigned xo[kTileNB], wo[NT];
+    {
+      const unsigned xb0 = unsigned((2 * wave * ta.win_w + n) * ta.ps + 16 * q);
+#pragma unroll
+      for (int j = 0; j < kTileNB; ++j) xo[j] = xb0 + unsigned((j >> 1) * wrow_bytes + (j & 1) * 16 * ta.ps);
+#pragma unroll
+      for (int t = 0; t < NT; ++t) wo[t] = unsigned(ta.win_bytes + (t * nkc * 64 + cv_swz(t, lane)) * 16);
+    }
+    int kc = 0, kw = 0, cn = 0;  // the next read's channel chunk, tap column and chunk index
+    auto frags = [&](half8 (&xb)[kTileNB], half8 (&wb)[NT]) {
+#pragma unroll
+      for (int j = 0; j < kTileNB; ++j) xb[j] = *reinterpret_cast<const half8*>(win + xo[j]);
+#pragma unroll
+      for (int t = 0; t < NT; ++t) wb[t] = *reinterpret_cast<const half8*>(win + wo[t]);
+      if (++cn < nkc) {
+        int d = 64;
+        if (++kc == kcs) {
+          kc = 0;
+          if (++kw == a.kw) {
+            kw = 0;
+            d = (ta.win_w - a.kw + 1) * ta.ps - 64 * (kcs - 1);
+          } else {
+            d = ta.ps - 64 * (kcs - 1);
+          }
         }
-      } else {
-        off += 64;
+#pragma unroll
+        for (int j = 0; j < kTileNB; ++j) xo[j] += unsigned(d);
+#pragma unroll
+        for (int t = 0; t < NT; ++t) wo[t] += 1024u;
       }
-    };
-    auto frags = [&](int c, half8 (&xb)[kTileNB], half8 (&wb)[NT]) {
-      const int o = c < nkc ? off : 0;  // past the last chunk: re-read chunk 0 (in bounds, unused)
-      const int cc = c < nkc ? c : 0;
-#pragma unroll
-      for (int j = 0; j < kTileNB; ++j)
-        xb[j] = *reinterpret_cast<const half8*>(wrow + o + (j >> 1) * jstride + (j & 1) * 16 * ta.ps);
-#pragma unroll
-      for (int t = 0; t < NT; ++t) wb[t] = __builtin_bit_cast(half8, sw[(t * nkc + cc) * 64 + cv_swz(t, lane)]);
-      advance();
     };
     auto mma = [&](const half8 (&xb)[kTileNB], const half8 (&wb)[NT]) {
 #pragma unroll
@@ -560,15 +639,57 @@ __global__ __launch_bounds__(kCvThreads, 1) void conv_tile_kernel(TileArgs ta) {
           acc[j][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wb[t], xb[j], acc[j][t], 0, 0, 0);
     };
     half8 xa[kTileNB], wa[NT], xb2[kTileNB], wb2[NT];
-    frags(0, xa, wa);
-    for (int c = 0; c < nkc; c += 2) {
-      frags(c + 1, xb2, wb2);
+    frags(xa, wa);
+    int c = 0;
+    for (; c + 2 <= nkc; c += 2) {
+      frags(xb2, wb2);  // chunk c + 1
       __builtin_amdgcn_sched_barrier(0);
-      mma(xa, wa);
-      if (c + 1 < nkc) {
-        frags(c + 2, xa, wa);
-        __builtin_amdgcn_sched_barrier(0);
-        mma(xb2, wb2);
+      mma(xa, wa);      // chunk c
+      frags(xa, wa);    // chunk c + 2 (a re-read of the last chunk when there is none)
+      __builtin_amdgcn_sched_barrier(0);
+      mma(xb2, wb2);    // chunk c + 1
+    }
+    if (c < nkc) mma(xa, wa);  // an odd chunk count's last chunk
+    if (a.relu) {
+#pragma unroll
+      for (int j = 0; j < kTileNB; ++j)
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc[j][t][e] = fmaxf(acc[j][t][e], 0.0f);
+    }
+    if constexpr ((NT & (NT - 1)) == 0) {
+      if (ta.stage_out) {
+        // Each output row (32 pixels x 16 NT channels, contiguous in y) goes out in
+        // 1 KiB stores of consecutive lanes: wave w stages row 2 w + h in 2 NT KiB of
+        // the window's LDS (every wave is done reading it after this barrier), a
+        // pixel's 16-byte units XORed by the pixel's low bits so that the writes
+        // (16 pixels a stride apart) and the reads (one pixel's units) both spread
+        // over the banks; one wave writes and reads its own slot, in order.
+        __syncthreads();
+        constexpr int U = 4 * NT;  // 16-byte units per pixel
+        uint8_t* slot = win + wave * (2048 * NT);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+#pragma unroll
+          for (int jj = 0; jj < 2; ++jj) {
+            const int px = 16 * jj + n;
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+              *reinterpret_cast<f32x4*>(slot + px * (64 * NT) + 16 * ((4 * t + q) ^ (px & (U - 1)))) =
+                  acc[2 * h + jj][t];
+          }
+          const int oh = h0 + 2 * wave + h;
+#pragma unroll
+          for (int k = 0; k < 2 * NT; ++k) {
+            const int px = k * (16 / NT) + lane / U, u = lane % U;
+            const f32x4 v = *reinterpret_cast<const f32x4*>(slot + px * (64 * NT) + 16 * (u ^ (px & (U - 1))));
+            if (oh < a.H && w0 + px < a.W)
+              __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(a.y + (int64_t(oh) * a.W + w0 + px) * a.cout + 4 * u));
+          }
+        }
+        __syncthreads();  // every wave is done with this window
+        continue;
       }
     }
 #pragma unroll
@@ -577,17 +698,8 @@ __global__ __launch_bounds__(kCvThreads, 1) void conv_tile_kernel(TileArgs ta) {
       if (oh < a.H && ow < a.W) {
         float* yr = a.y + (int64_t(oh) * a.W + ow) * a.cout;
 #pragma unroll
-        for (int t = 0; t < NT; ++t) {
-          const int col = o0 + 16 * t + 4 * q;
-          if (col < a.cout) {
-            f32x4 v = acc[j][t];
-            if (a.relu) {
-#pragma unroll
-              for (int e = 0; e < 4; ++e) v[e] = fmaxf(v[e], 0.0f);
-            }
-            *reinterpret_cast<f32x4*>(yr + col) = v;
-          }
-        }
+        for (int t = 0; t < NT; ++t)
+          __builtin_nontemporal_store(acc[j][t], reinterpret_cast<f32x4*>(yr + 16 * t + 4 * q));
       }
     }
     __syncthreads();  // every wave is done with this window
@@ -667,9 +779,11 @@ int launch_conv2d(const rdv_conv2d_desc& d, const float* x, const float* w, cons
   a.w_rows = d.w_layout == RDV_WLAYOUT_RSCK && d.cout % 4 == 0 && reinterpret_cast<uintptr_t>(w) % 16 == 0 ? 1 : 0;
   // spatial tiles: fp16, whole 32-channel chunks per tap, an RSCK filter of
   // 16-byte rows, one output block, and the haloed window plus the filter block in LDS
-  if (f16 && vec && a.w_rows && d.cin % 32 == 0 && d.cout % 16 == 0 && passes == 1 && a.n_ob == 1) {
+  // (and image rows whose bytes a buffer descriptor's 31-bit record count covers)
+  if (f16 && vec && a.w_rows && d.cin % 32 == 0 && d.cout % 16 == 0 && passes == 1 && a.n_ob == 1 &&
+      int64_t(d.W) * d.cin * 4 < (int64_t(1) << 31)) {
     const int64_t tiles = int64_t((d.H + kTileH - 1) / kTileH) * ((d.W + kTileW - 1) / kTileW);
-    if (tiles > 0x7fffffff) return fail(RDV_ERR_UNSUPPORTED, "grid too large");
+    if (tiles > (int64_t(1) << 30)) return fail(RDV_ERR_UNSUPPORTED, "grid too large");
     const size_t filt = size_t(ob / 16) * (K / 32) * 64 * sizeof(f32x4) + size_t(ob) * sizeof(float);
     const int ti = ob / 16 - 1;  // the kernels' NT is the exact tile count
     const int64_t grid = std::min<int64_t>(tiles, dev.cu_count);
@@ -680,6 +794,12 @@ int launch_conv2d(const rdv_conv2d_desc& d, const float* x, const float* w, cons
     ta.win_h = kTileH + d.kh - 1;
     ta.ps = 2 * d.cin + 16;
     ta.win_bytes = (ta.win_w * ta.win_h * ta.ps + 15) / 16 * 16;
+    ta.rp = ta.win_w * (d.cin / 4);
+    ta.upr = (ta.rp + 63) / 64;
+    ta.units = ta.win_h * ta.upr;
+    ta.row_bytes = int(int64_t(d.W) * d.cin * 4);
+    ta.cq_magic = unsigned(((uint64_t(1) << 32) + unsigned(d.cin / 4) - 1) / unsigned(d.cin / 4));
+    ta.stage_out = ta.win_bytes >= kCvWaves * 2048 * (ob / 16) ? 1 : 0;
     const size_t tlds = size_t(ta.win_bytes) + filt;
     if (tlds <= size_t(156) * 1024) {
       ta.tiles_w = (d.W + kTileW - 1) / kTileW;

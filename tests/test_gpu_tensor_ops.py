@@ -310,17 +310,20 @@ def test_direct_conv_variants_match_oracle(cls, f16, shape):
     _check_conv(op.as_type("torch").cpu().numpy(), x, w, b, H, W, f16, f"{cls.__name__}{shape}")
 
 
-def test_direct_conv_against_torch_full_size():
-    """64 -> 64 3x3 on a 256 x 256 image (the Winograd benchmark's shape) on
-    the fp16 path against torch's fp32 conv of the fp16-rounded operands."""
-    H = W = 256
-    x, w, b = _conv_case(H, W, 64, 64, 3, 3, seed=5)
+@pytest.mark.parametrize("H,W,C,K", [
+    (256, 256, 64, 64),   # the Winograd benchmark's shape: one spatial tile per block
+    (392, 616, 32, 32),   # 49 x 20 tiles: every block walks several, ragged in both directions
+])
+def test_direct_conv_against_torch_full_size(H, W, C, K):
+    """C -> K 3x3 on the fp16 path against torch's fp32 conv of the
+    fp16-rounded operands."""
+    x, w, b = _conv_case(H, W, C, K, 3, 3, seed=5)
     op = rdv.Conv2DTensorOpSimple3x3(x.cuda(), w.cuda(), b.cuda(), H, W)
     got = op.as_type("torch").cpu()
     # reference on the CPU in float64 (the GPU's fp32 conv may take a reduced-precision path)
-    xt = x.half().double().reshape(1, H, W, 64).permute(0, 3, 1, 2)
+    xt = x.half().double().reshape(1, H, W, C).permute(0, 3, 1, 2)
     wt = w.half().double().permute(3, 2, 0, 1).contiguous()
-    ref = torch.nn.functional.conv2d(xt, wt, b.double(), padding=1).permute(0, 2, 3, 1).reshape(H * W, 64).float()
+    ref = torch.nn.functional.conv2d(xt, wt, b.double(), padding=1).permute(0, 2, 3, 1).reshape(H * W, K).float()
     err = (got - ref).abs().max().item()
     assert err <= 2e-4 * max(1.0, ref.abs().max().item()), f"max |err| {err}"
 
