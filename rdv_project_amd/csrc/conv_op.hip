@@ -379,9 +379,17 @@ __global__ __launch_bounds__(kCvThreads) void conv_op_kernel(ConvArgs a) {
 constexpr int kTileH = 8;      // output rows per tile (two per wave)
 constexpr int kTileW = 32;     // output columns per tile
 constexpr int kTileNB = 4;     // N blocks per wave
-constexpr int kWinSlots = 23;  // window units per wave held across a tile (a 3x3, 64-channel window: 90 / 4)
-constexpr int kFiltA = 3;      // filter groups per thread in the first round (64 -> 64 3x3: 4.5 in all)
-constexpr int kFiltB = 2;      // filter groups per thread in each later round
+constexpr int kCtMath = 4;       // waves that run the MFMAs (one per SIMD)
+// Threads per block: 8 waves, two per SIMD, so that the staging's instruction
+// latencies overlap -- up to 5 output tiles, where the MFMA waves' registers
+// fit in half a SIMD's file; 4 waves above.
+template <int NT>
+constexpr int ct_threads() { return NT <= 5 ? 512 : 256; }
+// window units per wave held across a tile (a 3x3, 64-channel window has 90)
+template <int NT>
+constexpr int ct_win_slots() { return (92 + ct_threads<NT>() / 64 - 1) / (ct_threads<NT>() / 64); }
+constexpr int kFiltA = 3;        // filter groups per thread in the first round (64 -> 64 3x3: 2.25 in all)
+constexpr int kFiltB = 2;        // filter groups per thread in each later round
 
 struct TileArgs {
   ConvArgs c;
@@ -403,23 +411,24 @@ struct TileArgs {
 // of K rows 8 rb .. 8 rb + 7 (rb = gi / 4 NT: chunk c = rb / 4, kq = rb % 4) --
 // eight 16-byte loads at a fixed stride from one address, transposed in
 // registers into four lanes' 8-row fragments.  A round gives each thread NB
-// groups: group g0 + u kCvThreads + tid of round g0.  Every block reads the same
+// groups: group g0 + u THREADS + tid of round g0.  Every block reads the same
 // filter at the same time: each starts at its own row block (a rotation `rot`
 // of the group index), so that the blocks of an XCD spread their requests over
 // the L2 channels instead of queueing on the same lines.  Past the last group a
 // thread takes the last one again: it loads and writes the same bytes as that
 // group's owner, so no test guards the conversion (one that the compiler sinks
 // the loads below, behind a full wait).
+template <int THREADS>
 struct CtFilter {
   int groups, rot, nkc;
   __device__ int group(int g0, int u) const {
-    const int gi = min(g0 + u * kCvThreads + int(threadIdx.x), groups - 1) + rot;
+    const int gi = min(g0 + u * THREADS + int(threadIdx.x), groups - 1) + rot;
     return gi < groups ? gi : gi - groups;
   }
 };
 
-template <int NT, int NB>
-__device__ __forceinline__ void ct_filter_issue(const CtFilter& f, const float* __restrict__ w, int g0,
+template <int NT, int NB, class F>
+__device__ __forceinline__ void ct_filter_issue(const F& f, const float* __restrict__ w, int g0,
                                                 f32x4 (&r)[NB][8]) {
   constexpr int kG = 4 * NT, kRow = 16 * NT;
 #pragma unroll
@@ -431,8 +440,8 @@ __device__ __forceinline__ void ct_filter_issue(const CtFilter& f, const float* 
   }
 }
 
-template <int NT, int NB>
-__device__ __forceinline__ void ct_filter_convert(const CtFilter& f, int g0, const f32x4 (&r)[NB][8], f32x4* sw) {
+template <int NT, int NB, class F>
+__device__ __forceinline__ void ct_filter_convert(const F& f, int g0, const f32x4 (&r)[NB][8], f32x4* sw) {
   constexpr int kG = 4 * NT;
 #pragma unroll
   for (int u = 0; u < NB; ++u) {
@@ -459,11 +468,12 @@ template <int NT, class Mid>
 __device__ void ct_stage_filter(const float* __restrict__ w, const float* __restrict__ bias, int nkc, f32x4* sw,
                                 float* sb, Mid&& mid) {
   constexpr int kRow = 16 * NT;  // floats per K row
-  static_assert(kRow <= kCvThreads, "one bias per thread");
+  constexpr int kThreads = ct_threads<NT>();
+  static_assert(kRow <= kThreads, "one bias per thread");
   const int tid = int(threadIdx.x);
   // the bias first: the oldest load, so that waiting for it waits for nothing else
   const float bv = (tid < kRow && bias != nullptr) ? bias[tid] : 0.0f;
-  CtFilter f;
+  CtFilter<kThreads> f;
   f.groups = nkc * 16 * NT;
   f.rot = int(blockIdx.x * 7u % unsigned(4 * nkc)) * (4 * NT);
   f.nkc = nkc;
@@ -474,7 +484,7 @@ __device__ void ct_stage_filter(const float* __restrict__ w, const float* __rest
     mid();
     ct_filter_convert<NT>(f, 0, r, sw);
   }
-  for (int g0 = kFiltA * kCvThreads; g0 < f.groups; g0 += kFiltB * kCvThreads) {
+  for (int g0 = kFiltA * kThreads; g0 < f.groups; g0 += kFiltB * kThreads) {
     f32x4 r[kFiltB][8];
     ct_filter_issue<NT>(f, w, g0, r);
     ct_filter_convert<NT>(f, g0, r, sw);
@@ -483,7 +493,8 @@ __device__ void ct_stage_filter(const float* __restrict__ w, const float* __rest
 }
 
 template <int NT>
-__global__ __launch_bounds__(kCvThreads, 1) void conv_tile_kernel(TileArgs ta) {
+__global__ __launch_bounds__(ct_threads<NT>(), 1) void conv_tile_kernel(TileArgs ta) {
+  constexpr int kCtWaves = ct_threads<NT>() / 64, kWinSlots = ct_win_slots<NT>();
   const ConvArgs& a = ta.c;
   extern __shared__ f32x4 cv_smem[];
   const int nkc = a.K / 32;
@@ -498,8 +509,8 @@ __global__ __launch_bounds__(kCvThreads, 1) void conv_tile_kernel(TileArgs ta) {
 
   // Window unit u (< ta.units) is 64 consecutive 16-byte pieces of window row
   // u / upr: pieces 64 (u % upr) .. + 63, piece p holding channels 4 (p % cq) ..
-  // + 3 of window column p / cq (cq = cin / 4).  Wave w loads units w, w + 4, ..:
-  // slot s of a batch starting at slot s0 is unit w + 4 (s0 + s).  A unit is one
+  // + 3 of window column p / cq (cq = cin / 4).  Wave w of W loads units w, w + W,
+  // ..: slot s of a batch starting at slot s0 is unit w + W (s0 + s).  A unit is one
   // buffer load per lane from a descriptor over its image row alone (no records
   // for a row outside the image), so pieces left or right of the image read
   // zero; lanes past the row's last piece load and are not committed.
@@ -509,10 +520,12 @@ __global__ __launch_bounds__(kCvThreads, 1) void conv_tile_kernel(TileArgs ta) {
     // tile loop, where its 23 steps would be kept in spilled scalar registers)
     int z;
     asm volatile("s_mov_b32 %0, 0" : "=s"(z));
-    const int u = wave + 4 * (s0 + z);
+    const int u = wave + kCtWaves * (s0 + z);
     r = u / ta.upr;
     c = u - r * ta.upr;
   };
+  // a slot's step of kCtWaves units: sr rows and sc columns, then one carry at most
+  const int sr = kCtWaves / ta.upr, sc = kCtWaves - sr * ta.upr;
   auto win_issue = [&](int tile, int s0) {
     const int th = tile / ta.tiles_w, tw = tile - th * ta.tiles_w;
     const int cshift = (tw * kTileW - a.pw) * a.cin * 4;  // bytes; negative at the left edge
@@ -521,7 +534,7 @@ __global__ __launch_bounds__(kCvThreads, 1) void conv_tile_kernel(TileArgs ta) {
     unit_rc(s0, r, c);
     int ih = th * kTileH - a.ph + r;
     uint64_t row = uint64_t(a.x) + uint64_t(int64_t(ih) * rstep);  // image row ih (any ih: no records outside)
-    int u = wave + 4 * s0;
+    int u = wave + kCtWaves * s0;
     // every slot loads (a unit past the window, or a row outside the image, has no records and reads
     // zero), so the counts of loads in flight are exact and the waits for older loads stay narrow
 #pragma unroll
@@ -530,8 +543,10 @@ __global__ __launch_bounds__(kCvThreads, 1) void conv_tile_kernel(TileArgs ta) {
       const auto rs = __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(row), 0, nrec, 0x00020000);
       raw[s] = __builtin_bit_cast(
           f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, unsigned(16 * lane + (c * 1024 + cshift)), 0, 0));
-      u += 4;
-      c += 4;
+      u += kCtWaves;
+      c += sc;
+      ih += sr;
+      row += uint64_t(sr * rstep);
       if (c >= ta.upr) {
         c -= ta.upr;
         ++ih;
@@ -544,7 +559,7 @@ __global__ __launch_bounds__(kCvThreads, 1) void conv_tile_kernel(TileArgs ta) {
     unit_rc(s0, r, c);
 #pragma unroll
     for (int s = 0; s < kWinSlots; ++s) {
-      if (wave + 4 * (s0 + s) < ta.units) {
+      if (wave + kCtWaves * (s0 + s) < ta.units) {
         const int p = 64 * c + lane;
         if (p < ta.rp) {
           // window pixel p / cq at (p / cq) ps, its 4-channel group p % cq at 8 (p % cq): 8 p + 16 (p / cq)
@@ -555,7 +570,8 @@ __global__ __launch_bounds__(kCvThreads, 1) void conv_tile_kernel(TileArgs ta) {
           *reinterpret_cast<half4*>(win + r * wrow_bytes + 8 * p + 16 * col) = hv;
         }
       }
-      c += 4;
+      c += sc;
+      r += sr;
       if (c >= ta.upr) {
         c -= ta.upr;
         ++r;
@@ -572,7 +588,7 @@ __global__ __launch_bounds__(kCvThreads, 1) void conv_tile_kernel(TileArgs ta) {
     const int h0 = th * kTileH, w0 = tw * kTileW;
     // this tile's window into LDS: the batch in flight, and any further batches now
     win_commit(0);
-    for (int s0 = kWinSlots; 4 * s0 < ta.units; s0 += kWinSlots) {
+    for (int s0 = kWinSlots; kCtWaves * s0 < ta.units; s0 += kWinSlots) {
       win_issue(tile, s0);
       win_commit(s0);
     }
@@ -581,6 +597,7 @@ __global__ __launch_bounds__(kCvThreads, 1) void conv_tile_kernel(TileArgs ta) {
     const int next = tile + tstride;  // (tiles <= 2^30 and the grid is at most one block per CU)
     if (next < ta.tiles) win_issue(next, 0);  // (its first batch, when the window needs more than one)
     f32x4 acc[kTileNB][NT];
+    if (wave < kCtMath) {  // the MFMAs: waves 0 .. 3, one per SIMD
     {
       const f32x4* sb4 = reinterpret_cast<const f32x4*>(sb);
 #pragma unroll
@@ -658,6 +675,7 @@ __global__ __launch_bounds__(kCvThreads, 1) void conv_tile_kernel(TileArgs ta) {
 #pragma unroll
           for (int e = 0; e < 4; ++e) acc[j][t][e] = fmaxf(acc[j][t][e], 0.0f);
     }
+    }  // the MFMAs
     if constexpr ((NT & (NT - 1)) == 0) {
       if (ta.stage_out) {
         // Each output row (32 pixels x 16 NT channels, contiguous in y) goes out in
@@ -669,6 +687,7 @@ __global__ __launch_bounds__(kCvThreads, 1) void conv_tile_kernel(TileArgs ta) {
         __syncthreads();
         constexpr int U = 4 * NT;  // 16-byte units per pixel
         uint8_t* slot = win + wave * (2048 * NT);
+        if (wave < kCtMath) {
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
 #pragma unroll
@@ -688,18 +707,21 @@ __global__ __launch_bounds__(kCvThreads, 1) void conv_tile_kernel(TileArgs ta) {
               __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(a.y + (int64_t(oh) * a.W + w0 + px) * a.cout + 4 * u));
           }
         }
+        }
         __syncthreads();  // every wave is done with this window
         continue;
       }
     }
+    if (wave < kCtMath) {
 #pragma unroll
-    for (int j = 0; j < kTileNB; ++j) {
-      const int oh = h0 + 2 * wave + (j >> 1), ow = w0 + 16 * (j & 1) + n;
-      if (oh < a.H && ow < a.W) {
-        float* yr = a.y + (int64_t(oh) * a.W + ow) * a.cout;
+      for (int j = 0; j < kTileNB; ++j) {
+        const int oh = h0 + 2 * wave + (j >> 1), ow = w0 + 16 * (j & 1) + n;
+        if (oh < a.H && ow < a.W) {
+          float* yr = a.y + (int64_t(oh) * a.W + ow) * a.cout;
 #pragma unroll
-        for (int t = 0; t < NT; ++t)
-          __builtin_nontemporal_store(acc[j][t], reinterpret_cast<f32x4*>(yr + 16 * t + 4 * q));
+          for (int t = 0; t < NT; ++t)
+            __builtin_nontemporal_store(acc[j][t], reinterpret_cast<f32x4*>(yr + 16 * t + 4 * q));
+        }
       }
     }
     __syncthreads();  // every wave is done with this window
@@ -799,7 +821,9 @@ int launch_conv2d(const rdv_conv2d_desc& d, const float* x, const float* w, cons
     ta.units = ta.win_h * ta.upr;
     ta.row_bytes = int(int64_t(d.W) * d.cin * 4);
     ta.cq_magic = unsigned(((uint64_t(1) << 32) + unsigned(d.cin / 4) - 1) / unsigned(d.cin / 4));
-    ta.stage_out = ta.win_bytes >= kCvWaves * 2048 * (ob / 16) ? 1 : 0;
+    ta.stage_out = ta.win_bytes >= kCtMath * 2048 * (ob / 16) ? 1 : 0;
+    static const int tthreads[8] = {ct_threads<1>(), ct_threads<2>(), ct_threads<3>(), ct_threads<4>(),
+                                    ct_threads<5>(), ct_threads<6>(), ct_threads<7>(), ct_threads<8>()};
     const size_t tlds = size_t(ta.win_bytes) + filt;
     if (tlds <= size_t(156) * 1024) {
       ta.tiles_w = (d.W + kTileW - 1) / kTileW;
@@ -815,7 +839,7 @@ int launch_conv2d(const rdv_conv2d_desc& d, const float* x, const float* w, cons
         tattr[ti] = true;
       }
       void* tparams[] = {&ta};
-      RDV_HIP_TRY(hipLaunchKernel(tfns[ti], dim3(static_cast<unsigned>(grid)), dim3(kCvThreads), tparams, tlds, stream));
+      RDV_HIP_TRY(hipLaunchKernel(tfns[ti], dim3(static_cast<unsigned>(grid)), dim3(tthreads[ti]), tparams, tlds, stream));
       return RDV_OK;
     }
   }
