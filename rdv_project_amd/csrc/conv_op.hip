@@ -365,10 +365,11 @@ __global__ __launch_bounds__(kCvThreads) void conv_op_kernel(ConvArgs a) {
 // (TH + KH - 1)(TW + KW - 1) / (TH TW) times instead of KH KW times.  The
 // filter is staged once per launch, its loads issued in one round next to the
 // first window's, and the next tile's window loads are in flight (in
-// registers) while the current tile's MFMAs run.  Wave w computes output rows
-// 2w and 2w + 1 of the tile, 32 columns each (N blocks j = 0..3: row 2w + j / 2,
-// columns 16 (j % 2) ..: four blocks share every filter fragment read) against
-// every 16-channel output tile.  K runs over taps in (kh, kw) order and 32-channel
+// registers) while the current tile's MFMAs run.  MFMA wave w (of four)
+// computes output rows 2w and 2w + 1 of the tile, 32 columns each (N blocks
+// j = 0..3: row 2w + j / 2, columns 16 (j % 2) ..: four blocks share every filter
+// fragment read) against every 16-channel output tile; eight MFMA waves of one
+// row each measured no faster (their LDS reads per MFMA grow by half).  K runs over taps in (kh, kw) order and 32-channel
 // chunks within a tap: the filter staging's K order.
 //
 // Both stagings are written for few instructions per load, because at one wave
@@ -376,15 +377,16 @@ __global__ __launch_bounds__(kCvThreads) void conv_op_kernel(ConvArgs a) {
 // length: filter loads take immediate offsets from one address per 8-row group,
 // and window loads are buffer loads whose descriptor covers one image row, so a
 // column or row outside the image reads zero with no per-lane test.
-constexpr int kTileH = 8;      // output rows per tile (two per wave)
+constexpr int kTileH = 8;      // output rows per tile
 constexpr int kTileW = 32;     // output columns per tile
-constexpr int kTileNB = 4;     // N blocks per wave
-constexpr int kCtMath = 4;       // waves that run the MFMAs (one per SIMD)
 // Threads per block: 8 waves, two per SIMD, so that the staging's instruction
 // latencies overlap -- up to 5 output tiles, where the MFMA waves' registers
 // fit in half a SIMD's file; 4 waves above.
 template <int NT>
 constexpr int ct_threads() { return NT <= 5 ? 512 : 256; }
+// waves that run the MFMAs, each on kTileH / ct_math() output rows
+template <int NT>
+constexpr int ct_math() { return 4; }
 // window units per wave held across a tile (a 3x3, 64-channel window has 90)
 template <int NT>
 constexpr int ct_win_slots() { return (92 + ct_threads<NT>() / 64 - 1) / (ct_threads<NT>() / 64); }
@@ -495,6 +497,7 @@ __device__ void ct_stage_filter(const float* __restrict__ w, const float* __rest
 template <int NT>
 __global__ __launch_bounds__(ct_threads<NT>(), 1) void conv_tile_kernel(TileArgs ta) {
   constexpr int kCtWaves = ct_threads<NT>() / 64, kWinSlots = ct_win_slots<NT>();
+  constexpr int kMath = ct_math<NT>(), kRows = kTileH / kMath, kNB = 2 * kRows;  // MFMA waves, their rows, N blocks
   const ConvArgs& a = ta.c;
   extern __shared__ f32x4 cv_smem[];
   const int nkc = a.K / 32;
@@ -596,18 +599,18 @@ __global__ __launch_bounds__(ct_threads<NT>(), 1) void conv_tile_kernel(TileArgs
     // the next tile's window loads run under this tile's MFMAs
     const int next = tile + tstride;  // (tiles <= 2^30 and the grid is at most one block per CU)
     if (next < ta.tiles) win_issue(next, 0);  // (its first batch, when the window needs more than one)
-    f32x4 acc[kTileNB][NT];
-    if (wave < kCtMath) {  // the MFMAs: waves 0 .. 3, one per SIMD
+    f32x4 acc[kNB][NT];
+    if (wave < kMath) {  // the MFMAs
     {
       const f32x4* sb4 = reinterpret_cast<const f32x4*>(sb);
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
         const f32x4 b = sb4[t * 4 + q];
 #pragma unroll
-        for (int j = 0; j < kTileNB; ++j) acc[j][t] = b;
+        for (int j = 0; j < kNB; ++j) acc[j][t] = b;
       }
     }
-    // lane (q, n) of N block j reads window pixel (2 wave + j / 2 + kh, 16 (j % 2) + n + kw),
+    // lane (q, n) of N block j reads window pixel (kRows wave + j / 2 + kh, 16 (j % 2) + n + kw),
     // channels 32 kc + 8 q .. + 7, and of output tile t filter slot (t nkc + chunk) 64 +
     // cv_swz(t, lane).  Each fragment's LDS address lives in a register of its own and
     // moves by a uniform step per chunk (channels first, then taps along the row, then
@@ -617,18 +620,18 @@ __global__ __launch_bounds__(ct_threads<NT>(), 1) void conv_tile_kernel(TileArgs
     // read is unconditional: past the last chunk the addresses stay on it (a re-read,
     // unused), so the waits before each MFMA group count exactly the reads in flight.
     const int kcs = a.cin / 32;
-    unsigned xo[kTileNB], wo[NT];
+    unsigned xo[kNB], wo[NT];
     {
-      const unsigned xb0 = unsigned((2 * wave * ta.win_w + n) * ta.ps + 16 * q);
+      const unsigned xb0 = unsigned((kRows * wave * ta.win_w + n) * ta.ps + 16 * q);
 #pragma unroll
-      for (int j = 0; j < kTileNB; ++j) xo[j] = xb0 + unsigned((j >> 1) * wrow_bytes + (j & 1) * 16 * ta.ps);
+      for (int j = 0; j < kNB; ++j) xo[j] = xb0 + unsigned((j >> 1) * wrow_bytes + (j & 1) * 16 * ta.ps);
 #pragma unroll
       for (int t = 0; t < NT; ++t) wo[t] = unsigned(ta.win_bytes + (t * nkc * 64 + cv_swz(t, lane)) * 16);
     }
     int kc = 0, kw = 0, cn = 0;  // the next read's channel chunk, tap column and chunk index
-    auto frags = [&](half8 (&xb)[kTileNB], half8 (&wb)[NT]) {
+    auto frags = [&](half8 (&xb)[kNB], half8 (&wb)[NT]) {
 #pragma unroll
-      for (int j = 0; j < kTileNB; ++j) xb[j] = *reinterpret_cast<const half8*>(win + xo[j]);
+      for (int j = 0; j < kNB; ++j) xb[j] = *reinterpret_cast<const half8*>(win + xo[j]);
 #pragma unroll
       for (int t = 0; t < NT; ++t) wb[t] = *reinterpret_cast<const half8*>(win + wo[t]);
       if (++cn < nkc) {
@@ -643,19 +646,19 @@ __global__ __launch_bounds__(ct_threads<NT>(), 1) void conv_tile_kernel(TileArgs
           }
         }
 #pragma unroll
-        for (int j = 0; j < kTileNB; ++j) xo[j] += unsigned(d);
+        for (int j = 0; j < kNB; ++j) xo[j] += unsigned(d);
 #pragma unroll
         for (int t = 0; t < NT; ++t) wo[t] += 1024u;
       }
     };
-    auto mma = [&](const half8 (&xb)[kTileNB], const half8 (&wb)[NT]) {
+    auto mma = [&](const half8 (&xb)[kNB], const half8 (&wb)[NT]) {
 #pragma unroll
       for (int t = 0; t < NT; ++t)
 #pragma unroll
-        for (int j = 0; j < kTileNB; ++j)
+        for (int j = 0; j < kNB; ++j)
           acc[j][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wb[t], xb[j], acc[j][t], 0, 0, 0);
     };
-    half8 xa[kTileNB], wa[NT], xb2[kTileNB], wb2[NT];
+    half8 xa[kNB], wa[NT], xb2[kNB], wb2[NT];
     frags(xa, wa);
     int c = 0;
     for (; c + 2 <= nkc; c += 2) {
@@ -669,7 +672,7 @@ __global__ __launch_bounds__(ct_threads<NT>(), 1) void conv_tile_kernel(TileArgs
     if (c < nkc) mma(xa, wa);  // an odd chunk count's last chunk
     if (a.relu) {
 #pragma unroll
-      for (int j = 0; j < kTileNB; ++j)
+      for (int j = 0; j < kNB; ++j)
 #pragma unroll
         for (int t = 0; t < NT; ++t)
 #pragma unroll
@@ -678,44 +681,40 @@ __global__ __launch_bounds__(ct_threads<NT>(), 1) void conv_tile_kernel(TileArgs
     }  // the MFMAs
     if constexpr ((NT & (NT - 1)) == 0) {
       if (ta.stage_out) {
-        // Each output row (32 pixels x 16 NT channels, contiguous in y) goes out in
-        // 1 KiB stores of consecutive lanes: wave w stages row 2 w + h in 2 NT KiB of
-        // the window's LDS (every wave is done reading it after this barrier), a
-        // pixel's 16-byte units XORed by the pixel's low bits so that the writes
-        // (16 pixels a stride apart) and the reads (one pixel's units) both spread
-        // over the banks; one wave writes and reads its own slot, in order.
+        // Each N block's outputs (16 pixels x 16 NT channels, contiguous in y) go out
+        // in 1 KiB stores of consecutive lanes: the wave stages them in NT KiB of the
+        // window's LDS (every wave is done reading it after this barrier), a pixel's
+        // 16-byte units XORed by the pixel's low bits so that the writes (16 pixels a
+        // stride apart) and the reads (one pixel's units) both spread over the banks;
+        // one wave writes and reads its own slot, in order.
         __syncthreads();
         constexpr int U = 4 * NT;  // 16-byte units per pixel
-        uint8_t* slot = win + wave * (2048 * NT);
-        if (wave < kCtMath) {
+        uint8_t* slot = win + wave * (1024 * NT);
+        if (wave < kMath) {
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-#pragma unroll
-          for (int jj = 0; jj < 2; ++jj) {
-            const int px = 16 * jj + n;
+          for (int j = 0; j < kNB; ++j) {
 #pragma unroll
             for (int t = 0; t < NT; ++t)
-              *reinterpret_cast<f32x4*>(slot + px * (64 * NT) + 16 * ((4 * t + q) ^ (px & (U - 1)))) =
-                  acc[2 * h + jj][t];
-          }
-          const int oh = h0 + 2 * wave + h;
+              *reinterpret_cast<f32x4*>(slot + n * (64 * NT) + 16 * ((4 * t + q) ^ (n & (U - 1)))) = acc[j][t];
+            const int oh = h0 + kRows * wave + (j >> 1), pw0 = w0 + 16 * (j & 1);
 #pragma unroll
-          for (int k = 0; k < 2 * NT; ++k) {
-            const int px = k * (16 / NT) + lane / U, u = lane % U;
-            const f32x4 v = *reinterpret_cast<const f32x4*>(slot + px * (64 * NT) + 16 * (u ^ (px & (U - 1))));
-            if (oh < a.H && w0 + px < a.W)
-              __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(a.y + (int64_t(oh) * a.W + w0 + px) * a.cout + 4 * u));
+            for (int k = 0; k < NT; ++k) {
+              const int px = k * (16 / NT) + lane / U, u = lane % U;
+              const f32x4 v = *reinterpret_cast<const f32x4*>(slot + px * (64 * NT) + 16 * (u ^ (px & (U - 1))));
+              if (oh < a.H && pw0 + px < a.W)
+                __builtin_nontemporal_store(
+                    v, reinterpret_cast<f32x4*>(a.y + (int64_t(oh) * a.W + pw0 + px) * a.cout + 4 * u));
+            }
           }
-        }
         }
         __syncthreads();  // every wave is done with this window
         continue;
       }
     }
-    if (wave < kCtMath) {
+    if (wave < kMath) {
 #pragma unroll
-      for (int j = 0; j < kTileNB; ++j) {
-        const int oh = h0 + 2 * wave + (j >> 1), ow = w0 + 16 * (j & 1) + n;
+      for (int j = 0; j < kNB; ++j) {
+        const int oh = h0 + kRows * wave + (j >> 1), ow = w0 + 16 * (j & 1) + n;
         if (oh < a.H && ow < a.W) {
           float* yr = a.y + (int64_t(oh) * a.W + ow) * a.cout;
 #pragma unroll
@@ -821,7 +820,9 @@ int launch_conv2d(const rdv_conv2d_desc& d, const float* x, const float* w, cons
     ta.units = ta.win_h * ta.upr;
     ta.row_bytes = int(int64_t(d.W) * d.cin * 4);
     ta.cq_magic = unsigned(((uint64_t(1) << 32) + unsigned(d.cin / 4) - 1) / unsigned(d.cin / 4));
-    ta.stage_out = ta.win_bytes >= kCtMath * 2048 * (ob / 16) ? 1 : 0;
+    static const int tmath[8] = {ct_math<1>(), ct_math<2>(), ct_math<3>(), ct_math<4>(),
+                                 ct_math<5>(), ct_math<6>(), ct_math<7>(), ct_math<8>()};
+    ta.stage_out = ta.win_bytes >= tmath[ti] * 1024 * (ob / 16) ? 1 : 0;
     static const int tthreads[8] = {ct_threads<1>(), ct_threads<2>(), ct_threads<3>(), ct_threads<4>(),
                                     ct_threads<5>(), ct_threads<6>(), ct_threads<7>(), ct_threads<8>()};
     const size_t tlds = size_t(ta.win_bytes) + filt;
