@@ -378,6 +378,18 @@ struct LdsWeights {
   __device__ __forceinline__ half8 get(int f) const { return sw[f * 64 + lane]; }
 };
 
+// The same with fragments F0 .. F0 + NR - 1 held in registers for the life of
+// the wave (read from LDS once): an MFMA whose A operand needs no LDS read
+// leaves the LDS to the others (reads and MFMAs of a CU contend).  The index
+// is a compile-time constant after unrolling, so the choice costs nothing.
+template <int F0, int NR>
+struct RegLdsWeights {
+  const half8* sw;
+  int lane;
+  half8 r[NR > 0 ? NR : 1];
+  __device__ __forceinline__ half8 get(int f) const { return (f >= F0 && f < F0 + NR) ? r[f - F0] : sw[f * 64 + lane]; }
+};
+
 // BIAS: the accumulators were seeded with the bias; otherwise the first K
 // chunk starts from MFMA's zero C operand (all biases zero: nothing to load).
 template <class N, int l, bool BIAS, class WS>

@@ -33,10 +33,11 @@ struct FusedArgs {
 // staggered by half a layer (run_pair, mlp_core.h): the fp32 -> fp16 hand-off
 // of one tile is interleaved with the MFMAs of the other, so VALU and matrix
 // work overlap within the wave.
-//  - Weights: the block copies the packed A fragments into LDS once; every MFMA
-//    reads its fragment with one conflict-free ds_read_b128.  (2048 waves each
-//    pulling the same 26 KiB straight from L2 serialised on a few hot lines for
-//    ~3 us.)
+//  - Weights: the block copies the packed A fragments into LDS once (2048
+//    waves each pulling the same 26 KiB straight from L2 serialised on a few hot
+//    lines for ~3 us); each wave then reads its first 26 fragments into
+//    registers, and every MFMA on a later one reads its fragment with one
+//    conflict-free ds_read_b128.
 //  - Input: at the top of an iteration a wave claims its next pair tile and
 //    DMAs its 64 rows from HBM straight into a wave-private LDS buffer
 //    (global_load_lds_dword, one per input column: lane l's row lands at
@@ -124,6 +125,16 @@ __global__ __launch_bounds__(kThreads2, 1) void mlp_fused_f16_kernel(FusedArgs a
     return __builtin_amdgcn_readfirstlane(t);
   };
 
+  // The first 26 A fragments (every one of C2's chain) in registers, read from
+  // LDS once: the MFMAs on them leave the LDS to the rest (LDS reads and MFMAs
+  // of a CU contend).  26 keeps every instantiation's registers within a half
+  // SIMD (at most 256 VGPRs, no spills); C2: 23.8 -> 23.0 us per call.
+  constexpr int RF0 = 0;
+  constexpr int RN = N::kFrags < 26 ? N::kFrags : 26;
+  RegLdsWeights<RF0, RN> wr;
+#pragma unroll
+  for (int i = 0; i < RN; ++i) wr.r[i] = sw[(RF0 + i) * 64 + lane];
+
   f32x4 po[2][MTO][4];
   int64_t prow = -1;
   int buf = 0;
@@ -145,7 +156,9 @@ __global__ __launch_bounds__(kThreads2, 1) void mlp_fused_f16_kernel(FusedArgs a
     dma_tile(nxt, buf ^ 1);
     f32x16 accA[N::kMaxMT], accB[N::kMaxMT];
     half8 bA[N::kMaxKC], bB[N::kMaxKC];
-    const LdsWeights ws{sw + opaque_zero(), lane};
+    RegLdsWeights<RF0, RN> ws = wr;
+    ws.sw = sw + opaque_zero();
+    ws.lane = lane;
     build_input<N>(pA, h, bA);
     if (has_bias) {
       run_pair<N, 0, RELU, true>(ws, pB, h, bA, bB, accA, accB, sb + opaque_zero());
