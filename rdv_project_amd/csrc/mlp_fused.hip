@@ -128,9 +128,13 @@ __global__ __launch_bounds__(kThreads2, 1) void mlp_fused_f16_kernel(FusedArgs a
   // The first 26 A fragments (every one of C2's chain) in registers, read from
   // LDS once: the MFMAs on them leave the LDS to the rest (LDS reads and MFMAs
   // of a CU contend).  26 keeps every instantiation's registers within a half
-  // SIMD (at most 256 VGPRs, no spills); C2: 23.8 -> 23.0 us per call.
-  constexpr int RF0 = 0;
-  constexpr int RN = N::kFrags < 26 ? N::kFrags : 26;
+  // SIMD (at most 256 VGPRs, no spills); C2: 22.9 -> 22.3 us per call.  The
+  // DIRECT kernels keep the hidden layers' first 16 (their staging needs more
+  // registers; 24.8 -> 24.4 us, and 25.0 us with all 26).
+  constexpr int RH0 = N::kL > 2 ? N::frag_base(1) : 0;
+  constexpr int RHN = N::kL > 2 ? N::frag_base(N::kL - 1) - RH0 : 0;
+  constexpr int RF0 = DIRECT ? RH0 : 0;
+  constexpr int RN = DIRECT ? (RHN < 16 ? RHN : 16) : (N::kFrags < 26 ? N::kFrags : 26);
   RegLdsWeights<RF0, RN> wr;
 #pragma unroll
   for (int i = 0; i < RN; ++i) wr.r[i] = sw[(RF0 + i) * 64 + lane];
