@@ -404,6 +404,7 @@ struct TileArgs {
   int units;           // units per window: win_h upr
   int row_bytes;       // bytes per image row: W cin 4 (< 2^31)
   unsigned cq_magic;   // ceil(2^32 / (cin / 4)): p / (cin / 4) == umulhi(p, cq_magic) for every p < rp
+  unsigned upr_magic;  // ceil(2^32 / upr): u / upr == umulhi(u, upr_magic) for every unit index u used
   int stage_out;       // output rows staged through the window's LDS (2 NT KiB per wave fit in it)
 };
 
@@ -518,66 +519,54 @@ __global__ __launch_bounds__(ct_threads<NT>(), 1) void conv_tile_kernel(TileArgs
   // for a row outside the image), so pieces left or right of the image read
   // zero; lanes past the row's last piece load and are not committed.
   f32x4 raw[kWinSlots];
-  auto unit_rc = [&](int s0, int& r, int& c) {
-    // (an opaque zero: the slots' row and column walk is not hoisted out of the
-    // tile loop, where its 23 steps would be kept in spilled scalar registers)
-    int z;
-    asm volatile("s_mov_b32 %0, 0" : "=s"(z));
-    const int u = wave + kCtWaves * (s0 + z);
-    r = u / ta.upr;
-    c = u - r * ta.upr;
+  // The slots' unit arithmetic (row, column, descriptor) runs on the vector ALU
+  // from a per-lane copy of the uniform unit index, and only the descriptor's
+  // fields go back to scalar registers: the walk is uniform, but the CU's eight
+  // waves share one scalar ALU, and in scalar form this walk made it the CU's
+  // busiest unit.  (The copy is an asm move, so the compiler cannot fold it
+  // back to scalar code.)
+  auto vcopy = [](int v) {
+    int r;
+    asm volatile("v_mov_b32 %0, %1" : "=v"(r) : "s"(v));
+    return r;
   };
-  // a slot's step of kCtWaves units: sr rows and sc columns, then one carry at most
-  const int sr = kCtWaves / ta.upr, sc = kCtWaves - sr * ta.upr;
   auto win_issue = [&](int tile, int s0) {
     const int th = tile / ta.tiles_w, tw = tile - th * ta.tiles_w;
     const int cshift = (tw * kTileW - a.pw) * a.cin * 4;  // bytes; negative at the left edge
     const int64_t rstep = int64_t(a.W) * a.cin * 4;      // bytes per image row
-    int r, c;
-    unit_rc(s0, r, c);
-    int ih = th * kTileH - a.ph + r;
-    uint64_t row = uint64_t(a.x) + uint64_t(int64_t(ih) * rstep);  // image row ih (any ih: no records outside)
-    int u = wave + kCtWaves * s0;
+    const int ih0 = th * kTileH - a.ph;
+    const int u0 = vcopy(wave + kCtWaves * s0);
     // every slot loads (a unit past the window, or a row outside the image, has no records and reads
     // zero), so the counts of loads in flight are exact and the waits for older loads stay narrow
 #pragma unroll
     for (int s = 0; s < kWinSlots; ++s) {
+      const int u = u0 + kCtWaves * s;
+      const int r = int(__umulhi(unsigned(u), ta.upr_magic)), c = u - r * ta.upr;
+      const int ih = ih0 + r;
       const int nrec = (u < ta.units && unsigned(ih) < unsigned(a.H)) ? ta.row_bytes : 0;
-      const auto rs = __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(row), 0, nrec, 0x00020000);
+      const uint64_t row = uint64_t(a.x) + uint64_t(int64_t(ih) * rstep);  // image row ih (no records outside)
+      const uint32_t rlo = __builtin_amdgcn_readfirstlane(uint32_t(row));
+      const uint32_t rhi = __builtin_amdgcn_readfirstlane(uint32_t(row >> 32));
+      const auto rs = __builtin_amdgcn_make_buffer_rsrc(
+          reinterpret_cast<void*>((uint64_t(rhi) << 32) | rlo), 0, __builtin_amdgcn_readfirstlane(nrec), 0x00020000);
       raw[s] = __builtin_bit_cast(
-          f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, unsigned(16 * lane + (c * 1024 + cshift)), 0, 0));
-      u += kCtWaves;
-      c += sc;
-      ih += sr;
-      row += uint64_t(sr * rstep);
-      if (c >= ta.upr) {
-        c -= ta.upr;
-        ++ih;
-        row += uint64_t(rstep);
-      }
+          f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, unsigned(16 * lane + c * 1024 + cshift), 0, 0));
     }
   };
   auto win_commit = [&](int s0) {
-    int r, c;
-    unit_rc(s0, r, c);
+    const int u0 = vcopy(wave + kCtWaves * s0);
 #pragma unroll
     for (int s = 0; s < kWinSlots; ++s) {
-      if (wave + kCtWaves * (s0 + s) < ta.units) {
-        const int p = 64 * c + lane;
-        if (p < ta.rp) {
-          // window pixel p / cq at (p / cq) ps, its 4-channel group p % cq at 8 (p % cq): 8 p + 16 (p / cq)
-          const int col = int(__umulhi(unsigned(p), ta.cq_magic));
-          half4 hv;
+      const int u = u0 + kCtWaves * s;
+      const int r = int(__umulhi(unsigned(u), ta.upr_magic)), c = u - r * ta.upr;
+      const int p = 64 * c + lane;
+      if (u < ta.units && p < ta.rp) {
+        // window pixel p / cq at (p / cq) ps, its 4-channel group p % cq at 8 (p % cq): 8 p + 16 (p / cq)
+        const int col = int(__umulhi(unsigned(p), ta.cq_magic));
+        half4 hv;
 #pragma unroll
-          for (int j = 0; j < 4; ++j) hv[j] = half_t(raw[s][j]);
-          *reinterpret_cast<half4*>(win + r * wrow_bytes + 8 * p + 16 * col) = hv;
-        }
-      }
-      c += sc;
-      r += sr;
-      if (c >= ta.upr) {
-        c -= ta.upr;
-        ++r;
+        for (int j = 0; j < 4; ++j) hv[j] = half_t(raw[s][j]);
+        *reinterpret_cast<half4*>(win + r * wrow_bytes + 8 * p + 16 * col) = hv;
       }
     }
   };
@@ -820,6 +809,7 @@ int launch_conv2d(const rdv_conv2d_desc& d, const float* x, const float* w, cons
     ta.units = ta.win_h * ta.upr;
     ta.row_bytes = int(int64_t(d.W) * d.cin * 4);
     ta.cq_magic = unsigned(((uint64_t(1) << 32) + unsigned(d.cin / 4) - 1) / unsigned(d.cin / 4));
+    ta.upr_magic = unsigned(((uint64_t(1) << 32) + unsigned(ta.upr) - 1) / unsigned(ta.upr));
     static const int tmath[8] = {ct_math<1>(), ct_math<2>(), ct_math<3>(), ct_math<4>(),
                                  ct_math<5>(), ct_math<6>(), ct_math<7>(), ct_math<8>()};
     ta.stage_out = ta.win_bytes >= tmath[ti] * 1024 * (ob / 16) ? 1 : 0;
