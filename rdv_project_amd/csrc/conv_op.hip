@@ -398,7 +398,7 @@ struct TileArgs {
   int tiles_w, tiles;  // column tiles per row band, tiles in all
   int win_w, win_h;    // input window: kTileW + kw - 1, kTileH + kh - 1
   int ps;              // LDS bytes per window pixel: 2 cin + 16 (spreads a wave's reads over every bank)
-  int win_bytes;       // window bytes, rounded up to 16
+  int win_bytes;       // window bytes, rounded up to 16, plus 16 spare bytes at the end
   int rp;              // 16-byte fp32 pieces per window row: win_w cin / 4
   int upr;             // 64-piece units per window row: ceil(rp / 64), >= 4
   int units;           // units per window: win_h upr
@@ -560,14 +560,15 @@ __global__ __launch_bounds__(ct_threads<NT>(), 1) void conv_tile_kernel(TileArgs
       const int u = u0 + kCtWaves * s;
       const int r = int(__umulhi(unsigned(u), ta.upr_magic)), c = u - r * ta.upr;
       const int p = 64 * c + lane;
-      if (u < ta.units && p < ta.rp) {
-        // window pixel p / cq at (p / cq) ps, its 4-channel group p % cq at 8 (p % cq): 8 p + 16 (p / cq)
-        const int col = int(__umulhi(unsigned(p), ta.cq_magic));
-        half4 hv;
+      // window pixel p / cq at (p / cq) ps, its 4-channel group p % cq at 8 (p % cq): 8 p + 16 (p / cq);
+      // a lane past the row's pieces (or a slot past the window) writes the spare 8 bytes after the
+      // window instead, so the write needs no exec mask
+      const int col = int(__umulhi(unsigned(p), ta.cq_magic));
+      const int dst = (u < ta.units && p < ta.rp) ? r * wrow_bytes + 8 * p + 16 * col : ta.win_bytes - 16;
+      half4 hv;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) hv[j] = half_t(raw[s][j]);
-        *reinterpret_cast<half4*>(win + r * wrow_bytes + 8 * p + 16 * col) = hv;
-      }
+      for (int j = 0; j < 4; ++j) hv[j] = half_t(raw[s][j]);
+      *reinterpret_cast<half4*>(win + dst) = hv;
     }
   };
 
@@ -803,7 +804,7 @@ int launch_conv2d(const rdv_conv2d_desc& d, const float* x, const float* w, cons
     ta.win_w = kTileW + d.kw - 1;
     ta.win_h = kTileH + d.kh - 1;
     ta.ps = 2 * d.cin + 16;
-    ta.win_bytes = (ta.win_w * ta.win_h * ta.ps + 15) / 16 * 16;
+    ta.win_bytes = (ta.win_w * ta.win_h * ta.ps + 15) / 16 * 16 + 16;
     ta.rp = ta.win_w * (d.cin / 4);
     ta.upr = (ta.rp + 63) / 64;
     ta.units = ta.win_h * ta.upr;
