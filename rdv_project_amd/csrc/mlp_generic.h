@@ -17,6 +17,7 @@
 #ifndef RDV_MLP_GENERIC_H
 #define RDV_MLP_GENERIC_H
 
+#include "mlp_core.h"
 #include "mlp_layout.h"
 #include "rdv_common.h"
 
@@ -41,7 +42,28 @@ struct GenNet {
   int n_bias;                   // floats spanned by the bias sections (with alignment gaps)
   int max_mt;                   // largest mt[l]
   int64_t frag_off0, bias_off0; // byte offsets of layer 0's sections in the packed block
+  int fast;                     // 1: the chain is GenFieldNet with its compact layout (gen_field_row0's compiled path)
 };
+
+// The extinction chain the marching kernels carry most often, 3 -> 64 -> 64 ->
+// 64 -> 1 with ReLU hidden layers, as a compile-time network: its evaluation
+// runs no shape logic (the run-time chain's per-layer switches and loops are
+// scalar instructions, and a CU's eight waves share one scalar ALU).
+using GenFieldNet = Net<RDV_ENC_NONE, 3, 0, 1, 1, 2, 2, 2, 1>;
+
+// Whether g is network N with N's fragment and bias offsets, fp16 layers and
+// ReLU between layers (the head's activation is applied separately).
+template <class N>
+inline bool gen_matches(const GenNet& g) {
+  if (g.L != N::kL || g.enc != N::kEnc || g.D != N::kIn || g.out != N::kOut) return false;
+  for (int l = 0; l < N::kL; ++l) {
+    if (g.mt[l] != N::mt(l) || g.kc[l] != N::kc(l) || g.frag[l] != N::frag_base(l) || g.bias[l] != N::bias_base(l) ||
+        g.f32[l] != 0)
+      return false;
+    if (l + 1 < N::kL && g.act[l] != RDV_ACT_RELU) return false;
+  }
+  return true;
+}
 
 inline void gen_net(const rdv_mlp_desc& d, const MlpLayout& lay, GenNet* g) {
   g->L = d.n_layers;
@@ -67,6 +89,7 @@ inline void gen_net(const rdv_mlp_desc& d, const MlpLayout& lay, GenNet* g) {
   const int last = d.n_layers - 1;
   g->n_frag = int((lay.frag_off[last] - lay.frag_off[0]) / 1024) + lay.frag_units[last];
   g->n_bias = int((lay.bias_off[last] - lay.bias_off[0]) / 4) + 32 * lay.mt[last];
+  g->fast = gen_matches<GenFieldNet>(*g) ? 1 : 0;
 }
 
 // Waves per block of the kernels built on gen_chain: 8 per CU (2 per SIMD);

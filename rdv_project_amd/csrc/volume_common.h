@@ -114,6 +114,23 @@ __device__ __forceinline__ float gen_field_row0(const GenNet& g, const half8* w0
   auto wf = [&](int f) { return wsrc[f * 64 + lane]; };
   auto get = [&](int d) { return d == 0 ? p[0] : (d == 1 ? p[1] : p[2]); };
   float v = 0.0f;
+  if constexpr (!F32L && MT >= 2) {
+    if (g.fast) {  // GenFieldNet (gen_net checked the shape and layout): the compiled chain
+      using N = GenFieldNet;
+      const LdsWeights ws{wsrc, lane};
+      half8 b[N::kMaxKC];
+      f32x16 acc0[N::kMaxMT], acc1[N::kMaxMT];
+      build_input<N>(p, h, b);
+      if (has_bias) {
+        load_bias<N, 0>(acc0, b0 + z, h);
+        run_chain<N, 0, true, true>(ws, b, acc0, acc1, b0 + z, h);
+      } else {
+        run_chain<N, 0, true, false>(ws, b, acc0, acc1, b0, h);
+      }
+      // the last layer's result is in set (kL - 1) % 2
+      return gen_head_act(act, 0, (N::kL - 1) % 2 == 0 ? acc0[0][0] : acc1[0][0]);
+    }
+  }
   auto sink = [&](const auto& acc) { v = gen_head_act(act, 0, acc[0][0]); };
   if constexpr (F32L) {
     gen_chain_mixed<MT>(g, GenCtx{b0 + z, has_bias, h}, wf, get, sink);
