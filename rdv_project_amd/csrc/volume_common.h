@@ -141,6 +141,29 @@ __device__ __forceinline__ float gen_field_row0(const GenNet& g, const half8* w0
   return v;
 }
 
+// GenFieldNet's head value at 64 points, one per lane (the 64-ray kernels):
+// tile A holds the points of lanes 0-31 and tile B those of lanes 32-63, run as
+// a staggered pair (run_pair).  Layer 0 reads 3 features, all in a lane's low
+// K half, so lanes 32-63 give zeros to both tiles' B fragments and lanes 0-31
+// give tile B the point of lane + 32.  Row 0 of column n is in lane n of each
+// tile's D; tile B's goes back to lane n + 32.
+__device__ __forceinline__ float gen_field_pair64(const half8* w0, const float* b0, bool has_bias, int lane, int h,
+                                                  const float (&p)[3], int act) {
+  using N = GenFieldNet;
+  const int z = opaque_zero();
+  const LdsWeights ws{w0 + z, lane};
+  float ps[3];
+#pragma unroll
+  for (int i = 0; i < 3; ++i) ps[i] = __shfl_xor(p[i], 32);
+  half8 bA[N::kMaxKC], bB[N::kMaxKC];
+  f32x16 accA[N::kMaxMT], accB[N::kMaxMT];
+  build_input<N>(p, h, bA);
+  if (has_bias) run_pair<N, 0, true, true>(ws, ps, h, bA, bB, accA, accB, b0 + z);
+  else run_pair<N, 0, true, false>(ws, ps, h, bA, bB, accA, accB, b0);
+  const float vb = __shfl_xor(accB[0][0], 32);
+  return gen_head_act(act, 0, h == 0 ? accA[0][0] : vb);
+}
+
 // voxel_majorant_field.h: the majorant of the voxel holding x and the distance
 // along w to that voxel's exit.
 __device__ __forceinline__ float voxel_majorant(const float* __restrict__ grid, int mw, int mh, int md,

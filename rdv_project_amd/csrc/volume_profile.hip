@@ -549,8 +549,11 @@ struct VpGenArgs {
 };
 
 // One block's rays (DDA: VolumeProfileDDA's marches, a compile-time choice so that
-// VolumeProfile's kernel carries none of the walk's state).
-template <int MT, bool LDSW, bool DDA, bool F32L>
+// VolumeProfile's kernel carries none of the walk's state).  W64: 64 rays per
+// wave, one per lane, with GenFieldNet evaluated for both 32-point tiles at once
+// (gen_field_pair64); otherwise 32 per wave, lanes l and l + 32 carrying the same
+// ray (the chain's two K halves of one MFMA column).
+template <int MT, bool LDSW, bool DDA, bool F32L, bool W64 = false>
 __device__ __forceinline__ void volume_profile_body(const VpGenArgs& ga) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   __shared__ int s_next;
@@ -585,7 +588,8 @@ __device__ __forceinline__ void volume_profile_body(const VpGenArgs& ga) {
   bool exhausted = false;  // the block's range has run dry
   float q[3] = {0.0f, 0.0f, 0.0f};
   float sigma = 0.0f;
-  const uint64_t below = (uint64_t(1) << col) - 1;
+  const uint64_t below = (uint64_t(1) << (W64 ? lane : col)) - 1;
+  const bool owner = W64 || h == 0;  // the lane whose ballot bit stands for its ray
   for (;;) {
     for (;;) {
       if (ray >= 0 && !pending) {
@@ -594,12 +598,12 @@ __device__ __forceinline__ void volume_profile_body(const VpGenArgs& ga) {
         if (!pending) ray = -1;
       }
       const bool idle = ray < 0 && !exhausted;
-      const uint64_t want = __builtin_amdgcn_ballot_w64(h == 0 && idle);
+      const uint64_t want = __builtin_amdgcn_ballot_w64(owner && idle);
       if (want == 0) break;
       int base = 0;
       if (lane == 0) base = atomicAdd(&s_next, __builtin_popcountll(want));
       base = __builtin_amdgcn_readfirstlane(base);
-      if (idle) {  // both halves see the same `want` bits of the h == 0 lanes
+      if (idle) {  // (32 rays per wave: both halves see the same `want` bits of the h == 0 lanes)
         const int k = base + __builtin_popcountll(want & below);
         if (k < nr) {
           ray = br.ray(k);
@@ -614,12 +618,17 @@ __device__ __forceinline__ void volume_profile_body(const VpGenArgs& ga) {
         }
       }
     }
-    if (__builtin_amdgcn_ballot_w64(h == 0 && pending) == 0) break;  // every column is out of work
+    if (__builtin_amdgcn_ballot_w64(owner && pending) == 0) break;  // every ray is out of work
     float p[3];
 #pragma unroll
     for (int i = 0; i < 3; ++i) p[i] = pending ? q[i] : 0.0f;
-    float s = gen_field_row0<MT, F32L>(g, w0, b0, has_bias, lane, h, p, act);
-    s = __shfl(s, col);  // the value of lane col (row 0 of its column)
+    float s;
+    if constexpr (W64) {
+      s = gen_field_pair64(w0, b0, has_bias, lane, h, p, act);
+    } else {
+      s = gen_field_row0<MT, F32L>(g, w0, b0, has_bias, lane, h, p, act);
+      s = __shfl(s, col);  // the value of lane col (row 0 of its column)
+    }
     if (pending) {
       sigma = s;
       has = true;
@@ -636,6 +645,19 @@ __global__ __launch_bounds__(64 * gen_waves<MT>(), 1) void volume_profile_kernel
 template <int MT, bool LDSW, bool F32L = false>
 __global__ __launch_bounds__(64 * gen_waves<MT>(), 1) void volume_profile_dda_kernel(VpGenArgs ga) {
   volume_profile_body<MT, LDSW, true, F32L>(ga);
+}
+
+// 64 rays per wave for the chains that are GenFieldNet (GenNet::fast), weights in LDS.
+template <bool DDA>
+__global__ __launch_bounds__(64 * gen_waves<2>(), 1) void volume_profile64_kernel(VpGenArgs ga) {
+  volume_profile_body<2, true, DDA, false, true>(ga);
+}
+
+// Launch of volume_profile64_kernel<DDA> (64 rays per wave).
+template <bool DDA>
+static int launch_volume_profile64(const VpGenArgs& ga, int64_t nrays, int cu, hipStream_t stream) {
+  return launch_gen_field<VpGenArgs, 2, true>(&volume_profile64_kernel<DDA>, ga, (nrays + 63) / 64, cu,
+                                               gen_lds_bytes(ga.net), stream);
 }
 
 // volume_profile.h:155-160 for the rows that reached a depth.
@@ -722,6 +744,10 @@ int launch_volume_profile(const rdv_mlp_desc& d, const MlpLayout& lay, const voi
   a.dd = dda_d;
   ga.packed = static_cast<const uint8_t*>(packed);
   gen_net(d, lay, &ga.net);
+  // GenFieldNet: 64 rays per wave
+  if (!mixed && ga.net.fast && gen_lds_bytes(ga.net) <= kGenFieldLdsCap)
+    return dda_grid != nullptr ? launch_volume_profile64<true>(ga, nrays, di.cu_count, stream)
+                               : launch_volume_profile64<false>(ga, nrays, di.cu_count, stream);
   // 32 rays per wave
   if (dda_grid != nullptr) return launch_volume_profile_dda_any(ga, (nrays + 31) / 32, di.cu_count, mixed, stream);
   if (mixed) RDV_GEN_FIELD_DISPATCH_MIXED(volume_profile_kernel, ga, (nrays + 31) / 32, di.cu_count, ga.net, stream);
