@@ -290,11 +290,18 @@ __device__ __forceinline__ void direct_build_layer(const float* st, half8* sw) {
       const float* r = st + S::base(Q) + (row_ok ? m : 0) * S::pitch(Q);
       half8 v;
       if constexpr (Q == 0) {
+        // Slots past the row's kCols0 columns (a raw input narrower than its
+        // 16-wide K chunk) are zero: the staging row holds only those columns
+        // and its pitch padding is never written, so reading on would pick up
+        // a neighbour row or whatever an earlier kernel left in the LDS (a
+        // value beyond fp16 range turns 0 * Inf into NaN, which ReLU then
+        // maps to 0 for every point).
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
           const int ka = layer0_slot_feature_of<N>(8 * c + j, hh);
-          const float x = r[ka >= 0 ? ka : 0];
-          v[j] = half_t(row_ok && ka >= 0 ? x : 0.0f);
+          const bool ok = row_ok && ka >= 0 && ka < S::kCols0;
+          const float x = r[ok ? ka : 0];
+          v[j] = half_t(ok ? x : 0.0f);
         }
       } else {
         const int col0 = 16 * c + 4 * hh;  // columns col0 .. +3 and col0 + 8 .. +11

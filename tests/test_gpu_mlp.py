@@ -59,6 +59,26 @@ def test_c1_full_config_matches_oracle():
     _assert_fp16_parity(y, ref, "C1")
 
 
+def test_c1_after_a_kernel_that_leaves_infinities_in_lds():
+    """Regression: the one-launch kernel that builds its fragments from the
+    layers' fp32 buffers once read layer 0's unused K slots (features 3..15 of
+    a 3-wide input) from LDS it had not written.  Where an earlier kernel left
+    values beyond fp16 range there, 0 * Inf = NaN and ReLU turned every point's
+    output into 0.  A 3x3 conv whose operands are all 1e5 (fp16 infinity)
+    first runs on every CU; the chain must still match the oracle."""
+    H = W = 256
+    C = K = 64
+    op = rdv.Conv2DTensorOpSimple3x3(torch.full((H * W, C), 1e5).cuda(), torch.full((3, 3, C, K), 1e5).cuda(),
+                                     torch.zeros(K).cuda(), H, W)
+    op.evaluate()
+    torch.cuda.synchronize()
+    x, layers = WL.c1()
+    acts = ["relu"] * 4 + ["none"]
+    y = _chain(layers, acts)(rdv.wrap(x.cuda())).as_tensor("torch").cpu().numpy()
+    ref = O.mlp_forward(x.numpy(), _np_layers(layers), acts, ["f16"] * 5)
+    _assert_fp16_parity(y, ref, "C1 after the conv")
+
+
 def test_c2_full_config_matches_oracle():
     x, layers = WL.c2()
     acts = ["relu"] * 3 + ["none"]
