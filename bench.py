@@ -157,7 +157,8 @@ def bench_volume_profile(steps, warmup):
         "workload": "VolumeProfile over 512x512 C4 camera rays: extinction 3->64->64->64->1 softplus (fp16 MFMA, "
                     "seed 11), 8^3 voxel majorant, density_scale 4, thresholds (0.9, 0.5, 0.1), step 0.004, g 0.3, "
                     "4 environment samples, constant RGB environment and albedo",
-        "kernels": "volume_profile_kernel + volume_profile_finish_kernel",
+        "kernels": "volume_profile64_kernel (the chain compiled for this shape, 64 rays per wave) + "
+                   "volume_profile_finish_kernel",
         "ms_per_call": round(ev, 3),
         "Mrays_per_s": round(n / (ev * 1e-3) / 1e6, 2),
         "valid_fraction": round(valid, 4),
@@ -167,7 +168,8 @@ def bench_volume_profile(steps, warmup):
                 "mean_S": round(float(out[:, -1].double().mean()), 4),
                 "variant": "VolumeProfileDDA, majorant_grid = the same 8^3 MajorantGrid"},
         "bound": "per-ray state machine (two fixed-step marches, the light ray's march, four ratio-tracked "
-                 "environment rays); one chain evaluation per step for the 32 rays of a wave",
+                 "environment rays); one chain evaluation per step for the 64 rays of a wave, as two staggered "
+                 "32-point tiles",
     }
 
 
