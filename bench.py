@@ -32,6 +32,7 @@ sys.path.insert(0, ROOT)
 
 METRIC = "fused-MLP Mpoints/s (w64, 2^20 pts) + % fp16 MFMA peak; Winograd conv TFLOP/s"
 PEAK_FP16_TFLOPS = 2500.0  # MI355X dense fp16 MFMA
+PEAK_FP32_TFLOPS = 157.3   # MI355X fp32 (vector and matrix)
 PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
 C2_FLOP_PER_POINT = 2 * (48 * 64 + 64 * 64 + 64 * 64 + 64 * 4)  # 23,040 (declared padded shapes)
 C1_FLOP_PER_POINT = 2 * (3 * 64 + 3 * 64 * 64 + 64 * 4)          # 25,472
@@ -58,15 +59,16 @@ def _log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def _mlp_setup(x_cpu, layers, acts, enc=None, rotate=ROTATE):
-    """Builds the rdv chain, packs it, and returns (desc, packed, rotating x/y sets)."""
+def _mlp_setup(x_cpu, layers, acts, enc=None, rotate=ROTATE, f16=True):
+    """Builds the rdv chain (LinearFast layers, or exact-fp32 Linear ones with
+    f16=False), packs it, and returns (desc, packed, rotating x/y sets)."""
     import torch
     import rdv_project_amd as rdv
     from rdv_project_amd import _chain
 
     m = enc
     for (w, b), a in zip(layers, acts):
-        lin = rdv.linear(w.cuda(), b.cuda(), f16=True)
+        lin = rdv.linear(w.cuda(), b.cuda(), f16=f16)
         m = lin if m is None else m >> lin
         if a == "relu":
             m = m >> rdv.relu
@@ -203,11 +205,11 @@ def _time_launches(launch, steps: int, warmup: int, prewarm_s: float | None = No
     return wall, ev
 
 
-def bench_mlp(x_cpu, layers, acts, enc, steps, warmup, rotate=ROTATE):
+def bench_mlp(x_cpu, layers, acts, enc, steps, warmup, rotate=ROTATE, f16=True):
     import torch
     from rdv_project_amd import _lib
     lib = _lib.load()
-    m, p, packed, xs, ys = _mlp_setup(x_cpu, layers, acts, enc, rotate)
+    m, p, packed, xs, ys = _mlp_setup(x_cpu, layers, acts, enc, rotate, f16)
     n = x_cpu.shape[0]
     stream = C.c_void_p(torch.cuda.current_stream().cuda_stream)
     dptr = C.byref(p.desc)
@@ -585,6 +587,27 @@ def bench_generic_mlp(steps, warmup):
     }
 
 
+def bench_f32_chain(steps, warmup):
+    """The exact-fp32 Linear chain (Linear layers, every product and sum in fp32 in the reference's order):
+    C1's network and points, 3 -> 64 -> 64 -> 64 -> 64 -> 4, ReLU, 65,536 points."""
+    from rdv_project_amd import workloads as WL
+    x, layers = WL.c1()
+    n = x.shape[0]
+    acts = ["relu"] * 4 + ["none"]
+    wall, ev, name = bench_mlp(x, layers, acts, None, steps, warmup, rotate=4, f16=False)
+    flop = C1_FLOP_PER_POINT * n
+    return {
+        "workload": "exact-fp32 Linear chain: C1's 65,536 points U[-1,1]^3 (seed 0), 3 -> 64 -> 64 -> 64 -> 64 -> 4, "
+                    "ReLU, Kaiming-uniform weights (seed 1), fp32 products and sums in the reference's order",
+        "kernel": name,
+        "us_per_call": round(ev * 1e3, 2),
+        "wall_us_per_call": round(wall * 1e3, 2),
+        "Mpoints_per_s": round(n / (ev * 1e-3) / 1e6, 1),
+        "TFLOP_s": round(flop / (ev * 1e-3) / 1e12, 2),
+        "fp32_vector_peak_pct": round(100 * flop / (ev * 1e-3) / 1e12 / PEAK_FP32_TFLOPS, 2),
+    }
+
+
 def bench_volumes(steps, warmup):
     """Ratio-tracking transmittance (RatiotrackingTransmittance with a VoxelMajorantField) over the C4 camera's
     512 x 512 rays: extinction = a 3 -> 64 -> 64 -> 64 -> 1 softplus LinearFast chain (Kaiming-uniform fp16,
@@ -766,6 +789,8 @@ def main() -> int:
         _log("generic MLP")
         extras["generic_mlp"] = bench_generic_mlp(max(args.steps // 5, 10), args.warmup)
         _log(f"generic MLP {extras['generic_mlp']}")
+        extras["f32_chain"] = bench_f32_chain(max(args.steps // 20, 10), 3)
+        _log(f"fp32 chain {extras['f32_chain']}")
         _log("ratio tracking")
         extras["ratiotracking"] = bench_volumes(max(args.steps // 20, 10), 3)
         _log(f"ratio tracking {extras['ratiotracking']}")

@@ -61,6 +61,7 @@ bool direct_fused_ok(const FusedEntry* e, const rdv_mlp_desc& d);
 int launch_mlp_pack(const rdv_mlp_desc& d, const MlpLayout& lay, const float* const* W, const float* const* b,
                     void* packed, hipStream_t stream);
 int prepare_chain_f32(const rdv_mlp_desc& d);
+const char* chain_f32_name(const rdv_mlp_desc& d, const MlpLayout& lay);
 int64_t winograd_weight_bytes(int cin, int cout);
 int launch_winograd_transform_weight(const void* w, int w_layout, int w_dtype, int cin, int cout, void* U,
                                      hipStream_t stream);
@@ -726,7 +727,7 @@ const char* rdv_mlp_kernel_name(const rdv_mlp_desc* desc) {
   if (check_mlp(desc, &lay) != RDV_OK) return "";
   const FusedEntry* e = find_fused(*desc, lay);
   if (e) return fused_name(e);
-  return generic_f16_supported(*desc) ? generic_f16_name(*desc, lay) : "mlp_chain_f32_kernel";
+  return generic_f16_supported(*desc) ? generic_f16_name(*desc, lay) : chain_f32_name(*desc, lay);
 }
 
 }  // extern "C"

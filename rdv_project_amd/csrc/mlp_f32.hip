@@ -1,4 +1,4 @@
-// Generic chain kernel: one thread per row, every layer on the vector ALUs.
+// Chain kernels on the vector ALUs: one thread's arithmetic per row and output.
 //
 // This is the reference's per-thread evaluation order made explicit:
 //  - Linear (src/rdv/shaders/maps/linear.h:36-43):  acc = b[o]; acc += x[k] * W[o][k]
@@ -93,6 +93,159 @@ __global__ __launch_bounds__(64) void mlp_chain_f32_kernel(ChainF32Args a) {
   }
 }
 
+// ------------------------------------------------------------ register rows
+// The same arithmetic, per output, in the same order, for chains whose widths
+// are all at most 64 and whose weights fit in LDS beside the activations:
+//  - persistent blocks of 8 waves (two per SIMD: a row's 64 inputs and the
+//    weight reads in flight take more than the 128 registers of four); 2 row
+//    groups of 64 rows (one row per lane), and in each group 4 waves splitting
+//    a layer's outputs (o = 4j + og);
+//  - a row's layer input sits in 64 registers, its weights are read from LDS
+//    as 16-byte broadcasts (one address per wave), so each FMA costs no LDS
+//    access of its own (the one-thread-per-row kernel above reads an LDS input
+//    per FMA and runs one wave per SIMD);
+//  - a layer's outputs go through LDS to the group's 4 waves (two barriers).
+constexpr int kF32RegWaves = 8;
+constexpr int kF32RegGroups = kF32RegWaves / 4;
+constexpr int kF32RegRows = 64 * kF32RegGroups;  // rows per block and iteration
+constexpr int kF32RegWidth = 64;
+constexpr int kF32RegActStride = kF32RegWidth + 1;  // rows of the activation buffer: conflict-free by lane
+
+struct ChainF32RegArgs {
+  const float* x;
+  float* y;
+  const uint8_t* packed;
+  int64_t row0, nrows;
+  int L;
+  int encoding, enc_d, enc_l;
+  int in_w[RDV_MLP_MAX_LAYERS], out_w[RDV_MLP_MAX_LAYERS];
+  int act[RDV_MLP_MAX_LAYERS];
+  int f16[RDV_MLP_MAX_LAYERS];   // LinearFast emulation (fp16 operands, sum from zero, bias last)
+  int woff[RDV_MLP_MAX_LAYERS];  // LDS float offset of layer l's weights, rows of wstride floats
+  int wstride[RDV_MLP_MAX_LAYERS];
+  int boff[RDV_MLP_MAX_LAYERS];  // LDS float offset of layer l's bias
+  int w_floats;                  // floats of the weight and bias area
+  int direct;
+  DirectWeights dw;
+  MlpLayout lay;
+};
+
+// Output o of layer rows wr[0 .. iw) . cur, in the reference's order (Linear:
+// acc = b; acc += x[k] * W[o][k]; LinearFast: products of fp16 operands summed
+// from zero, then the bias).  KQ = ceil(iw / 4) 16-byte weight reads.
+template <int KQ, bool F16>
+__device__ __forceinline__ float f32reg_dot(const float (&cur)[kF32RegWidth], const float* wr, int iw, float bias) {
+  float acc = F16 ? 0.0f : bias;
+#pragma unroll
+  for (int q = 0; q < KQ; ++q) {
+    const f32x4 w = *reinterpret_cast<const f32x4*>(wr + 4 * q);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int k = 4 * q + j;
+      float t;
+      if constexpr (F16) t = fmaf(float(half_t(cur[k])), float(half_t(w[j])), acc);
+      else t = fmaf(cur[k], w[j], acc);
+      acc = (q + 1 < KQ || k < iw) ? t : acc;
+    }
+  }
+  return F16 ? acc + bias : acc;
+}
+
+template <int KQ, bool F16>
+__device__ __forceinline__ void f32reg_layer(const ChainF32RegArgs& a, int l, const float (&cur)[kF32RegWidth],
+                                             const float* sW, float* act_row, float* yrow, int og) {
+  const int iw = a.in_w[l], ow = a.out_w[l], act = a.act[l];
+  const float* W = sW + a.woff[l];
+  const float* B = sW + a.boff[l];
+  const int ws = a.wstride[l];
+  for (int o = og; o < ow; o += 4) {
+    const float v = apply_act(act, o, f32reg_dot<KQ, F16>(cur, W + o * ws, iw, B[o]));
+    if (yrow != nullptr) yrow[o] = v;
+    else act_row[o] = v;
+  }
+}
+
+__global__ __launch_bounds__(64 * kF32RegWaves, 1) void mlp_chain_f32_reg_kernel(ChainF32RegArgs a) {
+  extern __shared__ __attribute__((aligned(16))) float smem_f32[];
+  float* const sW = smem_f32;
+  float* const sAct = smem_f32 + a.w_floats;  // [kF32RegGroups][64 rows][kF32RegActStride]
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int rg = wave >> 2, og = wave & 3;
+
+  // weights (rows padded to wstride, zeros in the padding) and biases into LDS
+  for (int l = 0; l < a.L; ++l) {
+    const float* W = a.direct ? a.dw.W[l] : reinterpret_cast<const float*>(a.packed + a.lay.w32_off[l]);
+    const float* B = a.direct ? a.dw.b[l] : reinterpret_cast<const float*>(a.packed + a.lay.b32_off[l]);
+    const int iw = a.in_w[l], ow = a.out_w[l], ws = a.wstride[l];
+    for (int i = threadIdx.x; i < ow * ws; i += blockDim.x) {
+      const int o = i / ws, k = i - o * ws;
+      sW[a.woff[l] + i] = k < iw ? W[int64_t(o) * iw + k] : 0.0f;
+    }
+    for (int i = threadIdx.x; i < ow; i += blockDim.x) sW[a.boff[l] + i] = B[i];
+  }
+  __syncthreads();
+
+  float* const act_row = sAct + (rg * 64 + lane) * kF32RegActStride;
+  const int in0 = a.in_w[0], D = a.enc_d;
+  for (int64_t base = int64_t(blockIdx.x) * kF32RegRows; base < a.nrows; base += int64_t(gridDim.x) * kF32RegRows) {
+    const int64_t r = base + rg * 64 + lane;
+    const bool live = r < a.nrows;
+    const int64_t row = a.row0 + (live ? r : a.nrows - 1);
+    // layer-0 input, encoded if requested and zero padded to in0, by the group's first wave
+    if (og == 0) {
+      const float* xr = a.x + row * D;
+      if (a.encoding == RDV_ENC_FREQ) {
+        for (int d = 0; d < D; ++d) act_row[d] = xr[d];
+        for (int k = 0; k < a.enc_l; ++k)
+          for (int d = 0; d < D; ++d) {
+            const float t = ldexpf(xr[d], k);  // 2^k p, exact
+            act_row[D + 2 * D * k + d] = sinpif(t);
+            act_row[D + 2 * D * k + D + d] = cospif(t);
+          }
+        for (int f = D * (1 + 2 * a.enc_l); f < in0; ++f) act_row[f] = 0.0f;
+      } else {
+        for (int f = 0; f < in0; ++f) act_row[f] = f < D ? xr[f] : 0.0f;
+      }
+    }
+    __syncthreads();
+    for (int l = 0; l < a.L; ++l) {
+      float cur[kF32RegWidth];
+#pragma unroll
+      for (int k = 0; k < kF32RegWidth; ++k) cur[k] = act_row[k];
+      __syncthreads();  // every wave of the group holds the layer input before it is overwritten
+      float* yrow = (l + 1 == a.L && live) ? a.y + row * a.out_w[l] : nullptr;
+      if (l + 1 == a.L && !live) {
+        // a dead row's last layer is not evaluated
+      } else {
+        const int kq = (a.in_w[l] + 3) >> 2;
+        const bool f16 = a.f16[l] != 0;
+#define RDV_F32REG(KQ) \
+  if (f16) f32reg_layer<KQ, true>(a, l, cur, sW, act_row, yrow, og); else f32reg_layer<KQ, false>(a, l, cur, sW, act_row, yrow, og)
+        switch (kq) {
+          case 1: RDV_F32REG(1); break;
+          case 2: RDV_F32REG(2); break;
+          case 3: RDV_F32REG(3); break;
+          case 4: RDV_F32REG(4); break;
+          case 5: RDV_F32REG(5); break;
+          case 6: RDV_F32REG(6); break;
+          case 7: RDV_F32REG(7); break;
+          case 8: RDV_F32REG(8); break;
+          case 9: RDV_F32REG(9); break;
+          case 10: RDV_F32REG(10); break;
+          case 11: RDV_F32REG(11); break;
+          case 12: RDV_F32REG(12); break;
+          case 13: RDV_F32REG(13); break;
+          case 14: RDV_F32REG(14); break;
+          case 15: RDV_F32REG(15); break;
+          default: RDV_F32REG(16); break;
+        }
+#undef RDV_F32REG
+      }
+      __syncthreads();  // the layer's outputs are in LDS for the group
+    }
+  }
+}
+
 static size_t chain_lds_bytes(const rdv_mlp_desc& d) {
   int maxw = 0;
   for (int i = 0; i <= d.n_layers; ++i) maxw = d.dims[i] > maxw ? d.dims[i] : maxw;
@@ -114,6 +267,29 @@ int prepare_chain_f32(const rdv_mlp_desc& d) {
     raised = true;
   }
   return RDV_OK;
+}
+
+// Whether mlp_chain_f32_reg_kernel serves the chain (every width at most 64,
+// weights, biases and the activation rows within gfx950's 160 KiB of LDS per
+// block), and the LDS bytes it then takes.
+constexpr size_t kF32RegLdsCap = 160 * 1024;
+bool chain_f32_reg_fits(const rdv_mlp_desc& d, const MlpLayout& lay, size_t* lds_bytes) {
+  int64_t floats = 0;
+  for (int l = 0; l < d.n_layers; ++l) {
+    const int iw = lay.in_w[l], ow = lay.out_w[l];
+    if (iw > kF32RegWidth || ow > kF32RegWidth) return false;
+    floats += int64_t(ow) * ((iw + 3) & ~3) + ((ow + 3) & ~3);
+  }
+  const size_t lds = size_t(floats) * 4 + size_t(kF32RegGroups) * 64 * kF32RegActStride * 4;
+  if (lds > kF32RegLdsCap) return false;
+  if (lds_bytes != nullptr) *lds_bytes = lds;
+  return true;
+}
+
+// The kernel that evaluates the chain on the vector ALUs for row counts of at
+// least kF32RegRows (fewer rows, and the fp32 tail group, take the row kernel).
+const char* chain_f32_name(const rdv_mlp_desc& d, const MlpLayout& lay) {
+  return chain_f32_reg_fits(d, lay, nullptr) ? "mlp_chain_f32_reg_kernel" : "mlp_chain_f32_kernel";
 }
 
 int launch_mlp_chain_f32(const rdv_mlp_desc& d, const MlpLayout& lay, const void* packed,
@@ -140,6 +316,54 @@ int launch_mlp_chain_f32(const rdv_mlp_desc& d, const MlpLayout& lay, const void
     a.prec[i] = i < d.n_layers ? d.prec[i] : 0;
   }
   a.lay = lay;
+  size_t reg_lds = 0;
+  if (nrows >= kF32RegRows && chain_f32_reg_fits(d, lay, &reg_lds)) {  // the register kernel
+    ChainF32RegArgs ra = {};
+    int off = 0;
+    for (int l = 0; l < d.n_layers; ++l) {
+      const int iw = lay.in_w[l], ow = lay.out_w[l];
+      ra.in_w[l] = iw;
+      ra.out_w[l] = ow;
+      ra.act[l] = d.act[l];
+      ra.f16[l] = (d.prec[l] == RDV_PREC_F16 && !force_f32) ? 1 : 0;
+      ra.wstride[l] = (iw + 3) & ~3;
+      ra.woff[l] = off;
+      off += ow * ra.wstride[l];
+      ra.boff[l] = off;
+      off += (ow + 3) & ~3;
+    }
+    const size_t lds = reg_lds;
+    DeviceInfo di;
+    int rc = device_info(&di);
+    if (rc != RDV_OK) return rc;
+    if (lds > di.lds_per_block) return fail(RDV_ERR_UNSUPPORTED, "the fp32 chain needs more LDS than the device has");
+    {
+      static bool raised = false;
+      if (!raised) {
+        RDV_HIP_TRY(hipFuncSetAttribute(reinterpret_cast<const void*>(&mlp_chain_f32_reg_kernel),
+                                        hipFuncAttributeMaxDynamicSharedMemorySize, int(di.lds_per_block)));
+        raised = true;
+      }
+      ra.x = x;
+      ra.y = y;
+      ra.packed = a.packed;
+      ra.row0 = row0;
+      ra.nrows = nrows;
+      ra.L = d.n_layers;
+      ra.encoding = d.encoding;
+      ra.enc_d = d.in_features;
+      ra.enc_l = d.enc_octaves;
+      ra.w_floats = off;
+      ra.direct = a.direct;
+      ra.dw = a.dw;
+      ra.lay = lay;
+      int64_t blocks = (nrows + kF32RegRows - 1) / kF32RegRows;
+      if (blocks > di.cu_count) blocks = di.cu_count;
+      mlp_chain_f32_reg_kernel<<<dim3(unsigned(blocks)), dim3(64 * kF32RegWaves), lds, stream>>>(ra);
+      RDV_HIP_TRY(hipGetLastError());
+      return RDV_OK;
+    }
+  }
   const size_t lds = chain_lds_bytes(d);
   const int64_t blocks = (nrows + 63) / 64;
   mlp_chain_f32_kernel<<<dim3(unsigned(blocks)), dim3(64), lds, stream>>>(a);

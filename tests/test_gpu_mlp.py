@@ -151,7 +151,7 @@ def test_golden_vectors(path):
 
 @pytest.mark.parametrize("dims,f16,n,kernel", [
     ([5, 37, 19, 7], True, 1000, "mlp_generic_f16<2,lds>"),          # odd widths, partial tiles and chunks
-    ([3, 64, 64, 4], False, 1000, "mlp_chain_f32_kernel"),            # exact fp32 Linear chain
+    ([3, 64, 64, 4], False, 1000, "mlp_chain_f32_reg_kernel"),        # exact fp32 Linear chain
     ([64, 128, 128, 16], True, 1000, "mlp_generic_f16<4,lds>"),
     ([64, 128, 128, 16], True, 40_000, "mlp_generic_f16<4,lds>"),     # several tiles per wave
     ([17, 96, 200, 33], True, 777, "mlp_generic_f16<8,lds>"),         # 3, 7 and 2 M tiles
@@ -180,6 +180,40 @@ def test_generic_chains(dims, f16, n, kernel):
     from rdv_project_amd import _chain as CH, _lib
     p = CH.plan_chain(m, dims[0])
     assert _lib.load().rdv_mlp_kernel_name(p.desc).decode() == kernel
+
+
+@pytest.mark.parametrize("dims,precs,enc", [
+    ([3, 64, 64, 64, 64, 4], ["f32"] * 5, None),                   # C1's network, exact fp32 Linear layers
+    ([5, 37, 19, 7], ["f32"] * 3, None),                            # odd widths: a tail quartet in every layer
+    ([3, 48, 64, 4], ["f32", "f16", "f32"], None),                  # a LinearFast layer between Linear ones
+    ([39, 64, 64, 4], ["f32"] * 3, 6),                              # FREQ(6) encoding of 3 inputs
+])
+def test_f32_chain_register_kernel_equals_row_kernel(dims, precs, enc):
+    """Chains that are not all LinearFast run on the vector ALUs in the
+    reference's per-output order: 128 rows or more on the register kernel,
+    fewer on the one-thread-per-row kernel.  Rows 0..95 of a 5,000-row call
+    must equal, bit for bit, the same rows evaluated alone (three whole groups
+    of 32, so the same LinearFast rule), and the oracle."""
+    g = WL.gen(41)
+    d_in = 3 if enc else dims[0]
+    layers = [((torch.rand(dims[i + 1], dims[i], generator=g) * 2 - 1) / dims[i] ** 0.5 * 1.7,
+               torch.rand(dims[i + 1], generator=g) * 0.2 - 0.1) for i in range(len(dims) - 1)]
+    acts = ["relu"] * (len(dims) - 2) + ["none"]
+    x = torch.rand(5000, d_in, generator=g) * 2 - 1
+    encoder = rdv.FrequencyEncoding(3, enc) if enc else None
+    m = _chain(layers, acts, f16=[p == "f16" for p in precs], enc=encoder)
+    y = m(x.cuda()).as_tensor("torch").cpu().numpy().copy()
+    y_small = m(x[:96].contiguous().cuda()).as_tensor("torch").cpu().numpy()
+    assert np.array_equal(y[:96], y_small)
+    ref = O.mlp_forward(x.numpy(), _np_layers(layers), acts, precs, encoding=(enc, None) if enc else None)
+    if all(p == "f32" for p in precs):
+        # the encoding's fp32 sinpi / cospi against the oracle's float64 sin / cos rounded to fp32
+        tol = dict(rtol=1e-4, atol=1e-5) if enc else dict(rtol=1e-5, atol=1e-6)
+        np.testing.assert_allclose(y, ref, **tol)
+    else:
+        _assert_fp16_parity(y, ref, str(dims))
+    from rdv_project_amd import _chain as CH, _lib
+    assert _lib.load().rdv_mlp_kernel_name(CH.plan_chain(m, d_in).desc).decode() == "mlp_chain_f32_reg_kernel"
 
 
 @pytest.mark.parametrize("acts", [
