@@ -130,25 +130,38 @@ struct ChainF32RegArgs {
   MlpLayout lay;
 };
 
-// Output o of layer rows wr[0 .. iw) . cur, in the reference's order (Linear:
-// acc = b; acc += x[k] * W[o][k]; LinearFast: products of fp16 operands summed
-// from zero, then the bias).  KQ = ceil(iw / 4) 16-byte weight reads.
+// Outputs of a layer in the reference's order (Linear: acc = b; acc += x[k] *
+// W[o][k]; LinearFast: products of fp16 operands summed from zero, then the
+// bias), KQ = ceil(iw / 4) 16-byte weight reads per output.
+// Outputs o and o2 together: two independent FMA chains, so each chain's
+// dependent FMAs interleave with the other's.
 template <int KQ, bool F16>
-__device__ __forceinline__ float f32reg_dot(const float (&cur)[kF32RegWidth], const float* wr, int iw, float bias) {
-  float acc = F16 ? 0.0f : bias;
+__device__ __forceinline__ void f32reg_dot2(const float (&cur)[kF32RegWidth], const float* wr, const float* wr2,
+                                            int iw, float bias, float bias2, float& out, float& out2) {
+  float acc = F16 ? 0.0f : bias, acc2 = F16 ? 0.0f : bias2;
 #pragma unroll
   for (int q = 0; q < KQ; ++q) {
     const f32x4 w = *reinterpret_cast<const f32x4*>(wr + 4 * q);
+    const f32x4 w2 = *reinterpret_cast<const f32x4*>(wr2 + 4 * q);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int k = 4 * q + j;
-      float t;
-      if constexpr (F16) t = fmaf(float(half_t(cur[k])), float(half_t(w[j])), acc);
-      else t = fmaf(cur[k], w[j], acc);
-      acc = (q + 1 < KQ || k < iw) ? t : acc;
+      float t, t2;
+      if constexpr (F16) {
+        const float c = float(half_t(cur[k]));
+        t = fmaf(c, float(half_t(w[j])), acc);
+        t2 = fmaf(c, float(half_t(w2[j])), acc2);
+      } else {
+        t = fmaf(cur[k], w[j], acc);
+        t2 = fmaf(cur[k], w2[j], acc2);
+      }
+      const bool in = q + 1 < KQ || k < iw;
+      acc = in ? t : acc;
+      acc2 = in ? t2 : acc2;
     }
   }
-  return F16 ? acc + bias : acc;
+  out = F16 ? acc + bias : acc;
+  out2 = F16 ? acc2 + bias2 : acc2;
 }
 
 template <int KQ, bool F16>
@@ -158,10 +171,15 @@ __device__ __forceinline__ void f32reg_layer(const ChainF32RegArgs& a, int l, co
   const float* W = sW + a.woff[l];
   const float* B = sW + a.boff[l];
   const int ws = a.wstride[l];
-  for (int o = og; o < ow; o += 4) {
-    const float v = apply_act(act, o, f32reg_dot<KQ, F16>(cur, W + o * ws, iw, B[o]));
-    if (yrow != nullptr) yrow[o] = v;
-    else act_row[o] = v;
+  for (int o = og; o < ow; o += 8) {
+    const int o2 = o + 4 < ow ? o + 4 : o;  // a lone last output is computed twice
+    float v, v2;
+    f32reg_dot2<KQ, F16>(cur, W + o * ws, W + o2 * ws, iw, B[o], B[o2], v, v2);
+    v = apply_act(act, o, v);
+    v2 = apply_act(act, o2, v2);
+    float* dst = yrow != nullptr ? yrow : act_row;
+    dst[o] = v;
+    dst[o2] = v2;
   }
 }
 
