@@ -96,18 +96,17 @@ __global__ __launch_bounds__(64) void mlp_chain_f32_kernel(ChainF32Args a) {
 // ------------------------------------------------------------ register rows
 // The same arithmetic, per output, in the same order, for chains whose widths
 // are all at most 64 and whose weights fit in LDS beside the activations:
-//  - persistent blocks of 8 waves (two per SIMD: a row's 64 inputs and the
-//    weight reads in flight take more than the 128 registers of four); 2 row
-//    groups of 64 rows (one row per lane), and in each group 4 waves splitting
-//    a layer's outputs (o = 4j + og);
-//  - a row's layer input sits in 64 registers, its weights are read from LDS
-//    as 16-byte broadcasts (one address per wave), so each FMA costs no LDS
-//    access of its own (the one-thread-per-row kernel above reads an LDS input
-//    per FMA and runs one wave per SIMD);
+//  - persistent blocks of 8 waves (two per SIMD); 2 row groups of 128 rows, two
+//    rows per lane (r and r + 64), and in each group 4 waves splitting a
+//    layer's outputs (o = 4j + og);
+//  - a lane's two layer inputs sit in 2 x 64 registers and its weights are read
+//    from LDS as 16-byte broadcasts (one address per wave), each weight serving
+//    both rows: a broadcast still returns 16 bytes to every lane, so the LDS
+//    return path, not the FMAs, bounds a one-row-per-lane layout;
 //  - a layer's outputs go through LDS to the group's 4 waves (two barriers).
 constexpr int kF32RegWaves = 8;
 constexpr int kF32RegGroups = kF32RegWaves / 4;
-constexpr int kF32RegRows = 64 * kF32RegGroups;  // rows per block and iteration
+constexpr int kF32RegRows = 128 * kF32RegGroups;  // rows per block and iteration
 constexpr int kF32RegWidth = 64;
 constexpr int kF32RegActStride = kF32RegWidth + 1;  // rows of the activation buffer: conflict-free by lane
 
@@ -130,63 +129,78 @@ struct ChainF32RegArgs {
   MlpLayout lay;
 };
 
-// Outputs of a layer in the reference's order (Linear: acc = b; acc += x[k] *
-// W[o][k]; LinearFast: products of fp16 operands summed from zero, then the
-// bias), KQ = ceil(iw / 4) 16-byte weight reads per output.
-// Outputs o and o2 together: two independent FMA chains, so each chain's
-// dependent FMAs interleave with the other's.
+// Output o of two rows (inputs c0, c1) in the reference's order (Linear:
+// acc = b; acc += x[k] * W[o][k]; LinearFast: products of fp16 operands summed
+// from zero, then the bias; the caller has rounded c0 / c1), KQ = ceil(iw / 4)
+// 16-byte weight reads.
 template <int KQ, bool F16>
-__device__ __forceinline__ void f32reg_dot2(const float (&cur)[kF32RegWidth], const float* wr, const float* wr2,
-                                            int iw, float bias, float bias2, float& out, float& out2) {
-  float acc = F16 ? 0.0f : bias, acc2 = F16 ? 0.0f : bias2;
+__device__ __forceinline__ void f32reg_dot(const float (&c0)[kF32RegWidth], const float (&c1)[kF32RegWidth],
+                                           const float* wr, int iw, float bias, float& out0, float& out1) {
+  float a0 = F16 ? 0.0f : bias, a1 = F16 ? 0.0f : bias;
 #pragma unroll
   for (int q = 0; q < KQ; ++q) {
     const f32x4 w = *reinterpret_cast<const f32x4*>(wr + 4 * q);
-    const f32x4 w2 = *reinterpret_cast<const f32x4*>(wr2 + 4 * q);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int k = 4 * q + j;
-      float t, t2;
-      if constexpr (F16) {
-        const float c = float(half_t(cur[k]));
-        t = fmaf(c, float(half_t(w[j])), acc);
-        t2 = fmaf(c, float(half_t(w2[j])), acc2);
+      float t0, t1;
+      if constexpr (F16) {  // c0 / c1 already rounded to fp16 by the caller
+        const float wh = float(half_t(w[j]));
+        t0 = fmaf(c0[k], wh, a0);
+        t1 = fmaf(c1[k], wh, a1);
       } else {
-        t = fmaf(cur[k], w[j], acc);
-        t2 = fmaf(cur[k], w2[j], acc2);
+        t0 = fmaf(c0[k], w[j], a0);
+        t1 = fmaf(c1[k], w[j], a1);
       }
       const bool in = q + 1 < KQ || k < iw;
-      acc = in ? t : acc;
-      acc2 = in ? t2 : acc2;
+      a0 = in ? t0 : a0;
+      a1 = in ? t1 : a1;
     }
   }
-  out = F16 ? acc + bias : acc;
-  out2 = F16 ? acc2 + bias2 : acc2;
+  out0 = F16 ? a0 + bias : a0;
+  out1 = F16 ? a1 + bias : a1;
 }
 
+// Layer l for the lane's two rows; outputs to dst0 / dst1 (null: not stored).
 template <int KQ, bool F16>
-__device__ __forceinline__ void f32reg_layer(const ChainF32RegArgs& a, int l, const float (&cur)[kF32RegWidth],
-                                             const float* sW, float* act_row, float* yrow, int og) {
+__device__ __forceinline__ void f32reg_layer(const ChainF32RegArgs& a, int l, const float (&c0)[kF32RegWidth],
+                                             const float (&c1)[kF32RegWidth], const float* sW, float* dst0,
+                                             float* dst1, int og) {
   const int iw = a.in_w[l], ow = a.out_w[l], act = a.act[l];
   const float* W = sW + a.woff[l];
   const float* B = sW + a.boff[l];
   const int ws = a.wstride[l];
-  for (int o = og; o < ow; o += 8) {
-    const int o2 = o + 4 < ow ? o + 4 : o;  // a lone last output is computed twice
-    float v, v2;
-    f32reg_dot2<KQ, F16>(cur, W + o * ws, W + o2 * ws, iw, B[o], B[o2], v, v2);
-    v = apply_act(act, o, v);
-    v2 = apply_act(act, o2, v2);
-    float* dst = yrow != nullptr ? yrow : act_row;
-    dst[o] = v;
-    dst[o2] = v2;
+#pragma nounroll
+  for (int o = og; o < ow; o += 4) {
+    float v0, v1;
+    f32reg_dot<KQ, F16>(c0, c1, W + o * ws, iw, B[o], v0, v1);
+    if (dst0 != nullptr) dst0[o] = apply_act(act, o, v0);
+    if (dst1 != nullptr) dst1[o] = apply_act(act, o, v1);
+  }
+}
+
+// Layer-0 input of one row (encoded if requested, zero padded to in0) into act_row.
+__device__ __forceinline__ void f32reg_input(const ChainF32RegArgs& a, int64_t row, float* act_row) {
+  const int in0 = a.in_w[0], D = a.enc_d;
+  const float* xr = a.x + row * D;
+  if (a.encoding == RDV_ENC_FREQ) {
+    for (int d = 0; d < D; ++d) act_row[d] = xr[d];
+    for (int k = 0; k < a.enc_l; ++k)
+      for (int d = 0; d < D; ++d) {
+        const float t = ldexpf(xr[d], k);  // 2^k p, exact
+        act_row[D + 2 * D * k + d] = sinpif(t);
+        act_row[D + 2 * D * k + D + d] = cospif(t);
+      }
+    for (int f = D * (1 + 2 * a.enc_l); f < in0; ++f) act_row[f] = 0.0f;
+  } else {
+    for (int f = 0; f < in0; ++f) act_row[f] = f < D ? xr[f] : 0.0f;
   }
 }
 
 __global__ __launch_bounds__(64 * kF32RegWaves, 1) void mlp_chain_f32_reg_kernel(ChainF32RegArgs a) {
   extern __shared__ __attribute__((aligned(16))) float smem_f32[];
   float* const sW = smem_f32;
-  float* const sAct = smem_f32 + a.w_floats;  // [kF32RegGroups][64 rows][kF32RegActStride]
+  float* const sAct = smem_f32 + a.w_floats;  // [kF32RegGroups][128 rows][kF32RegActStride]
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int rg = wave >> 2, og = wave & 3;
 
@@ -203,62 +217,59 @@ __global__ __launch_bounds__(64 * kF32RegWaves, 1) void mlp_chain_f32_reg_kernel
   }
   __syncthreads();
 
-  float* const act_row = sAct + (rg * 64 + lane) * kF32RegActStride;
-  const int in0 = a.in_w[0], D = a.enc_d;
+  float* const act0 = sAct + (rg * 128 + lane) * kF32RegActStride;
+  float* const act1 = act0 + 64 * kF32RegActStride;
   for (int64_t base = int64_t(blockIdx.x) * kF32RegRows; base < a.nrows; base += int64_t(gridDim.x) * kF32RegRows) {
-    const int64_t r = base + rg * 64 + lane;
-    const bool live = r < a.nrows;
-    const int64_t row = a.row0 + (live ? r : a.nrows - 1);
-    // layer-0 input, encoded if requested and zero padded to in0, by the group's first wave
-    if (og == 0) {
-      const float* xr = a.x + row * D;
-      if (a.encoding == RDV_ENC_FREQ) {
-        for (int d = 0; d < D; ++d) act_row[d] = xr[d];
-        for (int k = 0; k < a.enc_l; ++k)
-          for (int d = 0; d < D; ++d) {
-            const float t = ldexpf(xr[d], k);  // 2^k p, exact
-            act_row[D + 2 * D * k + d] = sinpif(t);
-            act_row[D + 2 * D * k + D + d] = cospif(t);
-          }
-        for (int f = D * (1 + 2 * a.enc_l); f < in0; ++f) act_row[f] = 0.0f;
-      } else {
-        for (int f = 0; f < in0; ++f) act_row[f] = f < D ? xr[f] : 0.0f;
-      }
+    const int64_t r0 = base + rg * 128 + lane, r1 = r0 + 64;
+    const bool live0 = r0 < a.nrows, live1 = r1 < a.nrows;
+    const int64_t row0 = a.row0 + (live0 ? r0 : a.nrows - 1);
+    const int64_t row1 = a.row0 + (live1 ? r1 : a.nrows - 1);
+    if (og == 0) {  // the group's first wave writes the layer-0 inputs
+      f32reg_input(a, row0, act0);
+      f32reg_input(a, row1, act1);
     }
     __syncthreads();
     for (int l = 0; l < a.L; ++l) {
-      float cur[kF32RegWidth];
+      float c0[kF32RegWidth], c1[kF32RegWidth];
 #pragma unroll
-      for (int k = 0; k < kF32RegWidth; ++k) cur[k] = act_row[k];
-      __syncthreads();  // every wave of the group holds the layer input before it is overwritten
-      float* yrow = (l + 1 == a.L && live) ? a.y + row * a.out_w[l] : nullptr;
-      if (l + 1 == a.L && !live) {
-        // a dead row's last layer is not evaluated
-      } else {
-        const int kq = (a.in_w[l] + 3) >> 2;
-        const bool f16 = a.f16[l] != 0;
-#define RDV_F32REG(KQ) \
-  if (f16) f32reg_layer<KQ, true>(a, l, cur, sW, act_row, yrow, og); else f32reg_layer<KQ, false>(a, l, cur, sW, act_row, yrow, og)
-        switch (kq) {
-          case 1: RDV_F32REG(1); break;
-          case 2: RDV_F32REG(2); break;
-          case 3: RDV_F32REG(3); break;
-          case 4: RDV_F32REG(4); break;
-          case 5: RDV_F32REG(5); break;
-          case 6: RDV_F32REG(6); break;
-          case 7: RDV_F32REG(7); break;
-          case 8: RDV_F32REG(8); break;
-          case 9: RDV_F32REG(9); break;
-          case 10: RDV_F32REG(10); break;
-          case 11: RDV_F32REG(11); break;
-          case 12: RDV_F32REG(12); break;
-          case 13: RDV_F32REG(13); break;
-          case 14: RDV_F32REG(14); break;
-          case 15: RDV_F32REG(15); break;
-          default: RDV_F32REG(16); break;
-        }
-#undef RDV_F32REG
+      for (int k = 0; k < kF32RegWidth; ++k) {
+        c0[k] = act0[k];
+        c1[k] = act1[k];
       }
+      __syncthreads();  // every wave of the group holds the layer input before it is overwritten
+      const bool last = l + 1 == a.L;
+      float* d0 = last ? (live0 ? a.y + row0 * a.out_w[l] : nullptr) : act0;
+      float* d1 = last ? (live1 ? a.y + row1 * a.out_w[l] : nullptr) : act1;
+      const int kq = (a.in_w[l] + 3) >> 2;
+      const bool f16 = a.f16[l] != 0;
+      if (f16) {  // a LinearFast layer's inputs in fp16, rounded once for all of its outputs
+#pragma unroll
+        for (int k = 0; k < kF32RegWidth; ++k) {
+          c0[k] = float(half_t(c0[k]));
+          c1[k] = float(half_t(c1[k]));
+        }
+      }
+#define RDV_F32REG(KQ) \
+  if (f16) f32reg_layer<KQ, true>(a, l, c0, c1, sW, d0, d1, og); else f32reg_layer<KQ, false>(a, l, c0, c1, sW, d0, d1, og)
+      switch (kq) {
+        case 1: RDV_F32REG(1); break;
+        case 2: RDV_F32REG(2); break;
+        case 3: RDV_F32REG(3); break;
+        case 4: RDV_F32REG(4); break;
+        case 5: RDV_F32REG(5); break;
+        case 6: RDV_F32REG(6); break;
+        case 7: RDV_F32REG(7); break;
+        case 8: RDV_F32REG(8); break;
+        case 9: RDV_F32REG(9); break;
+        case 10: RDV_F32REG(10); break;
+        case 11: RDV_F32REG(11); break;
+        case 12: RDV_F32REG(12); break;
+        case 13: RDV_F32REG(13); break;
+        case 14: RDV_F32REG(14); break;
+        case 15: RDV_F32REG(15); break;
+        default: RDV_F32REG(16); break;
+      }
+#undef RDV_F32REG
       __syncthreads();  // the layer's outputs are in LDS for the group
     }
   }
@@ -298,7 +309,7 @@ bool chain_f32_reg_fits(const rdv_mlp_desc& d, const MlpLayout& lay, size_t* lds
     if (iw > kF32RegWidth || ow > kF32RegWidth) return false;
     floats += int64_t(ow) * ((iw + 3) & ~3) + ((ow + 3) & ~3);
   }
-  const size_t lds = size_t(floats) * 4 + size_t(kF32RegGroups) * 64 * kF32RegActStride * 4;
+  const size_t lds = size_t(floats) * 4 + size_t(kF32RegGroups) * 128 * kF32RegActStride * 4;
   if (lds > kF32RegLdsCap) return false;
   if (lds_bytes != nullptr) *lds_bytes = lds;
   return true;
