@@ -209,9 +209,15 @@ __global__ __launch_bounds__(64 * kF32RegWaves, 1) void mlp_chain_f32_reg_kernel
     const float* W = a.direct ? a.dw.W[l] : reinterpret_cast<const float*>(a.packed + a.lay.w32_off[l]);
     const float* B = a.direct ? a.dw.b[l] : reinterpret_cast<const float*>(a.packed + a.lay.b32_off[l]);
     const int iw = a.in_w[l], ow = a.out_w[l], ws = a.wstride[l];
-    for (int i = threadIdx.x; i < ow * ws; i += blockDim.x) {
-      const int o = i / ws, k = i - o * ws;
-      sW[a.woff[l] + i] = k < iw ? W[int64_t(o) * iw + k] : 0.0f;
+    if (iw == ws && (reinterpret_cast<uintptr_t>(W) & 15) == 0) {  // rows of whole quartets: a float4 copy
+      const f32x4* W4 = reinterpret_cast<const f32x4*>(W);
+      f32x4* d4 = reinterpret_cast<f32x4*>(sW + a.woff[l]);
+      for (int i = threadIdx.x; i < ow * iw / 4; i += blockDim.x) d4[i] = W4[i];
+    } else {
+      for (int i = threadIdx.x; i < ow * ws; i += blockDim.x) {
+        const int o = i / ws, k = i - o * ws;
+        sW[a.woff[l] + i] = k < iw ? W[int64_t(o) * iw + k] : 0.0f;
+      }
     }
     for (int i = threadIdx.x; i < ow; i += blockDim.x) sW[a.boff[l] + i] = B[i];
   }
