@@ -190,7 +190,7 @@ def test_generic_chains(dims, f16, n, kernel):
 ])
 def test_f32_chain_register_kernel_equals_row_kernel(dims, precs, enc):
     """Chains that are not all LinearFast run on the vector ALUs in the
-    reference's per-output order: 128 rows or more on the register kernel,
+    reference's per-output order: 256 rows or more on the register kernel,
     fewer on the one-thread-per-row kernel.  Rows 0..95 of a 5,000-row call
     must equal, bit for bit, the same rows evaluated alone (three whole groups
     of 32, so the same LinearFast rule), and the oracle."""
