@@ -178,7 +178,10 @@ __global__ __launch_bounds__(64 * gen_waves<MT>(), 1) void mlp_generic_f16_kerne
 #pragma unroll
               for (int jj = 0; jj < 4; ++jj) v[jj] = gen_head_act(act, r0 + jj, acc[tt][4 * q + jj]);
               if (a.vec_out) {
-                __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(yr + r0));
+                // a cached store: the two lane halves write alternate 16-byte pieces of each
+                // row, and the L2 merges them into whole lines (non-temporal stores left
+                // half lines: 1.40x the output bytes)
+                *reinterpret_cast<f32x4*>(yr + r0) = v;
               } else {
 #pragma unroll
                 for (int jj = 0; jj < 4; ++jj)
