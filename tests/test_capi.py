@@ -112,8 +112,10 @@ def test_kernel_selection_names():
     assert lib.rdv_mlp_kernel_name(C.byref(
         _desc([48, 64, 64, 64, 4], acts=[1, 1, 1, 0], enc=_lib.ENC_FREQ, octaves=6, in_features=3))) \
         .decode() == "mlp_fused_f16<freq3x6,64x3,4>"
-    # fp32 layers and unlisted shapes go to the generic kernel
+    # fp32 layers go to the vector-ALU chain kernels (register rows up to 64 wide), unlisted
+    # LinearFast shapes to the generic kernel
     assert lib.rdv_mlp_kernel_name(C.byref(_desc([3, 64, 4], precs=[0, 0]))).decode() == "mlp_chain_f32_reg_kernel"
+    assert lib.rdv_mlp_kernel_name(C.byref(_desc([3, 128, 4], precs=[0, 0]))).decode() == "mlp_chain_f32_kernel"
     assert lib.rdv_mlp_kernel_name(C.byref(_desc([5, 37, 19]))).decode() == "mlp_generic_f16<2,lds>"
     assert lib.rdv_mlp_kernel_name(C.byref(_desc([3, 256, 256, 4]))).decode() == "mlp_generic_f16<8,global>"
 
