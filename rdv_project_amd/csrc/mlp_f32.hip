@@ -108,7 +108,9 @@ constexpr int kF32RegWaves = 8;
 constexpr int kF32RegGroups = kF32RegWaves / 4;
 constexpr int kF32RegRows = 128 * kF32RegGroups;  // rows per block and iteration
 constexpr int kF32RegWidth = 64;
-constexpr int kF32RegActStride = kF32RegWidth + 1;  // rows of the activation buffer: conflict-free by lane
+// Rows of the activation buffer: 16-byte aligned, so a layer's inputs come back as 16 ds_read_b128 per row
+// (lane rows 272 bytes apart: every 16 lanes cover all 64 banks, the full rate of a 16-byte read).
+constexpr int kF32RegActStride = kF32RegWidth + 4;
 
 struct ChainF32RegArgs {
   const float* x;
@@ -238,9 +240,14 @@ __global__ __launch_bounds__(64 * kF32RegWaves, 1) void mlp_chain_f32_reg_kernel
     for (int l = 0; l < a.L; ++l) {
       float c0[kF32RegWidth], c1[kF32RegWidth];
 #pragma unroll
-      for (int k = 0; k < kF32RegWidth; ++k) {
-        c0[k] = act0[k];
-        c1[k] = act1[k];
+      for (int q = 0; q < kF32RegWidth / 4; ++q) {
+        const f32x4 v0 = *reinterpret_cast<const f32x4*>(act0 + 4 * q);
+        const f32x4 v1 = *reinterpret_cast<const f32x4*>(act1 + 4 * q);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          c0[4 * q + j] = v0[j];
+          c1[4 * q + j] = v1[j];
+        }
       }
       __syncthreads();  // every wave of the group holds the layer input before it is overwritten
       const bool last = l + 1 == a.L;
