@@ -24,6 +24,7 @@ from .core import (
     wrap,
 )
 from .maths import (
+    BatchGridEvaluator,
     Composite,
     Constant,
     Grid,

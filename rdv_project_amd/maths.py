@@ -356,6 +356,33 @@ class GridEvaluator(Main):
         _render.evaluate_grid(self.g, out=out)
 
 
+class BatchGridEvaluator(Main):
+    """Evaluates `grid` at a batch of integer index vectors `input` ([rows, IN],
+    int32 or another integer type; an RDVObject or a torch tensor) into
+    `output` ([rows, OUT] fp32), one thread per index vector; dispatch(evaluator,
+    rows) runs it (reference: maths:815-844, shaders/grids/batch_grid_evaluator.h)."""
+
+    def __init__(self, grid, input, output) -> None:
+        self.g = grid
+        self.input = input
+        self.output = output
+
+    def set_direct(self, g, input, output) -> None:
+        self.g, self.input, self.output = g, input, output
+
+    def _dispatch(self, threads: int) -> None:
+        from . import _render
+        from .core import launch_scope
+        idx, _, rows = _render._batch_indices(self.g, self.input)
+        if threads != rows:
+            raise AssertionError(f"BatchGridEvaluator dispatches one thread per index vector ({rows}), got {threads}")
+        out = self.output if isinstance(self.output, RDVObject) else wrap(self.output)
+        if tuple(out.shape)[-1:] != (int(self.g.OUT),) or _math.prod(out.shape) != rows * int(self.g.OUT):
+            raise AssertionError(f"output must hold {rows} rows of {int(self.g.OUT)} floats, got {tuple(out.shape)}")
+        with launch_scope():
+            _render._batch_values(self.g, idx, rows, out.device_ptr, {})
+
+
 class TensorOpEvaluator(Main):
     """Re-runs a TensorOperation's kernel over its own result buffer
     (reference: maths:1382-1399)."""

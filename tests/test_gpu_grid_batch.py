@@ -134,3 +134,19 @@ def test_camera_sensor_batches_match_the_full_frame():
     rays = R.camera_rays(W, H, WL.c4_pose().reshape(1, 9).numpy())[i[:, 0], i[:, 1], i[:, 2]].astype(np.float32)
     ref = R.render_ea(rays, [(w.numpy(), b.numpy()) for w, b in layers], 64)
     np.testing.assert_allclose(img, ref, rtol=1e-3, atol=1e-5)
+
+
+def test_batch_grid_evaluator_through_dispatch():
+    """BatchGridEvaluator(grid, input, output) run by rdv.dispatch(evaluator, rows)
+    (the reference's evaluator object, maths:815-844) writes the caller's
+    output buffer with the values Grid.__call__(indices) returns."""
+    cam = rdv.Cameras(33, 17, POSES.cuda(), fov=0.7)
+    idx = _indices(cam.shape, 257, seed=3).cuda()
+    want = cam(idx).as_tensor("torch").clone()
+    out = torch.full((257, 6), float("nan"), device="cuda")
+    ev = rdv.BatchGridEvaluator(cam, idx, out)
+    rdv.dispatch(ev, 257)
+    torch.cuda.synchronize()
+    assert torch.equal(out, want)
+    with pytest.raises(AssertionError):
+        rdv.dispatch(ev, 256)  # one thread per index vector
